@@ -1,0 +1,271 @@
+"""Benchmark of the packed-ternary hot path on one MI355X.
+
+Headline (``value``): the decode GEMV (K2) at the north-star shape, Llama-3-8B
+gate 4096 -> 14336, M = 1 token, bf16 activations, in HBM GB/s of algorithmic
+bytes.  A "step" is one GEMV call on a fresh weight matrix: the weights rotate
+through enough copies (> 2x the 256 MB Infinity Cache) that every call streams
+from HBM, and the launches of a round are captured in a HIP graph so that the
+GPU runs them back to back.  Inputs are resident in HBM before timing starts.
+
+Also reported: the prefill GEMM (K3) at M = 2048 tokens, gate_up 4096 -> 28672
+(TFLOP/s against the dense bf16 MFMA peak), K1 pack at 8192 x 3072, and the
+reference CPU gemm_ternary (oracle/_ref, compiled from the reference sources)
+timed on a bounded sample of the same GEMV workload on this host.
+
+Prints ONE JSON line on stdout; progress goes to stderr.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBPS = 8000.0          # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0       # dense bf16 MFMA
+MALL_BYTES = 256 << 20
+
+METRIC = ("ternary GEMV HBM GB/s (% of peak) + prefill GEMM TFLOP/s (% MFMA peak), 1 GPU")
+
+
+def log(msg: str) -> None:
+    sys.stderr.write(f"[bench] {msg}\n")
+    sys.stderr.flush()
+
+
+def gemv_bytes(m: int, n: int, k: int, x_bytes: int = 2, beta: bool = False,
+               bias: bool = False) -> int:
+    """16*N*ceil(K/48) packed weights + activations + C write (+ C read) (+ bias)."""
+    limbs = (k + 47) // 48
+    return 16 * n * limbs + x_bytes * m * k + 4 * m * n * (2 if beta else 1) + (4 * n if bias else 0)
+
+
+def make_weights(torch, ops, lib, n: int, k: int, copies: int, dev, seed: int):
+    g = torch.Generator(dev).manual_seed(seed)
+    out = []
+    for _ in range(copies):
+        w = torch.randn((n, k), generator=g, device=dev)   # effective W/0.02 ~ N(0, 1)
+        out.append(ops.quantize_pack(w, 0.45, lib.THR_CPP))
+        del w
+    return out
+
+
+def time_graph(torch, launch, buffers, steps: int, warmup: int) -> float:
+    """Captures one launch per buffer into a graph, replays it; returns ms per launch."""
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for i in range(min(warmup, len(buffers)) or 1):
+            launch(buffers[i % len(buffers)])
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for b in buffers:
+            launch(b)
+    torch.cuda.synchronize()
+    reps = max(1, -(-steps // len(buffers)))
+    for _ in range(max(1, warmup // len(buffers))):
+        graph.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        for _ in range(reps):
+            graph.replay()
+        end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / (reps * len(buffers))
+
+
+def cpu_reference_gemv(n: int, k: int, budget_s: float):
+    """Reference gemm_ternary (the compiled reference CPU path) on the same GEMV workload:
+    W (n x L limbs) times one packed activation column, timed over row blocks until
+    `budget_s` has elapsed or all rows are done.  Returns (GB/s of packed weights, detail)."""
+    import numpy as np
+
+    import oracle
+
+    ref = oracle.ref()
+    kind = "reference"
+    if ref is None:
+        ref = oracle.ref("generic")
+    if ref is None:
+        kind = "port"
+    rng = np.random.default_rng(0)
+    limbs = (k + 47) // 48
+    w = rng.standard_normal((n, k)).astype(np.float32)
+    wp = oracle.pack_rows(w, 0.45, 0)                                   # (n, L, 16)
+    x = rng.standard_normal((1, k)).astype(np.float32)
+    xp = oracle.pack_cols(x, np.float32(oracle.torch_threshold(0.5)), 1)  # (L, 1, 16)
+    c = np.zeros((n, 1), np.float32)
+    block = 256
+    rows_done = 0
+    t0 = time.perf_counter()
+    while rows_done < n and time.perf_counter() - t0 < budget_s:
+        r1 = min(n, rows_done + block)
+        if kind == "reference":
+            ref.gemm_ternary_rows(wp, xp, c, n, 1, limbs * 48, rows_done, r1)
+        else:
+            c[rows_done:r1] = oracle.gemm_limb(wp[rows_done:r1], xp, c[rows_done:r1],
+                                               r1 - rows_done, 1, limbs * 48)
+        rows_done = r1
+    dt = time.perf_counter() - t0
+    nbytes = 16 * rows_done * limbs
+    variant = ref.variant if kind == "reference" else "oracle C restatement"
+    simd = ref.simd_path() if kind == "reference" else "scalar"
+    return nbytes / dt / 1e9, {
+        "kind": kind, "rows": rows_done, "seconds": dt, "limb_products": rows_done * limbs,
+        "variant": variant, "simd": simd,
+    }
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2048)
+    ap.add_argument("--warmup", type=int, default=64)
+    ap.add_argument("--cpu-budget", type=float, default=12.0,
+                    help="seconds of single-core reference CPU work for the baseline")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", choices=["gemv", "gemm", "pack"], default=None,
+                    help="time one kernel only (for profiling runs)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the packed-ternary path is a single-GPU kernel set "
+              "(multi-GPU sharding is a design note only); run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from t81lib_amd import _lib, ops
+
+    if not torch.cuda.is_available() or not _lib.available():
+        print("bench.py needs a gfx950 GPU and libt81_hip.so", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    result: dict = {}
+
+    # ---------------------------------------------------------- K2 decode GEMV --
+    M, K, N = 1, 4096, 14336
+    wbytes = 16 * N * ((K + 47) // 48)
+    copies = max(8, -(-2 * MALL_BYTES // wbytes) + 4)
+    gemv_ms = None
+    if args.only in (None, "gemv"):
+        log(f"GEMV {K}->{N} M={M}: {copies} weight copies of {wbytes / 1e6:.1f} MB")
+        wbufs = make_weights(torch, ops, _lib, N, K, copies, dev, seed=1)
+        x = torch.randn((M, K), device=dev).to(torch.bfloat16)
+        out = torch.empty((M, N), device=dev)
+        launch = lambda wb: ops.ternary_matmul(x, wb, K, c=out, kernel=2)  # noqa: E731
+        gemv_ms = time_graph(torch, launch, wbufs, args.steps, args.warmup)
+        del wbufs
+        torch.cuda.empty_cache()
+        log(f"GEMV {gemv_ms * 1e3:.2f} us/call")
+
+    # --------------------------------------------------------- K3 prefill GEMM --
+    GM, GK, GN = 2048, 4096, 28672
+    gemm_ms = None
+    if args.only in (None, "gemm"):
+        log(f"GEMM M={GM} {GK}->{GN}")
+        gw = make_weights(torch, ops, _lib, GN, GK, 2, dev, seed=2)
+        gx = torch.randn((GM, GK), device=dev).to(torch.bfloat16)
+        gout = torch.empty((GM, GN), device=dev)
+        glaunch = lambda wb: ops.ternary_matmul(gx, wb, GK, c=gout, kernel=3)  # noqa: E731
+        gsteps = max(4, min(64, args.steps // 32))
+        gemm_ms = time_graph(torch, glaunch, gw, gsteps, 4)
+        del gw, gx, gout
+        torch.cuda.empty_cache()
+        log(f"GEMM {gemm_ms:.3f} ms/call")
+
+    # ------------------------------------------------------------- K1 pack --
+    PR, PC = 8192, 3072
+    pack_ms = None
+    if args.only in (None, "pack"):
+        pbytes = 4 * PR * PC + 16 * PR * ((PC + 47) // 48)
+        pcopies = max(4, -(-2 * MALL_BYTES // pbytes) + 2)
+        srcs = [torch.randn((PR, PC), device=dev) * 0.02 for _ in range(pcopies)]
+        pout = torch.empty((PR, (PC + 47) // 48, 16), dtype=torch.uint8, device=dev)
+        plaunch = lambda s: ops.quantize_pack(s, 0.45, _lib.THR_CPP, out=pout)  # noqa: E731
+        pack_ms = time_graph(torch, plaunch, srcs, max(64, args.steps // 8), 8)
+        del srcs
+        torch.cuda.empty_cache()
+        log(f"pack {pack_ms * 1e3:.2f} us/call")
+
+    # ------------------------------------------------------------ CPU baseline --
+    cpu = None
+    if not args.no_cpu and args.only is None:
+        log("reference CPU gemm_ternary on the GEMV workload (1 core)")
+        gbps, detail = cpu_reference_gemv(N, K, args.cpu_budget)
+        cpu = {
+            "value": gbps, "unit": "GB/s", "cores": 1, "kind": detail["kind"],
+            "sample": (f"reference gemm_ternary_cpu_impl ({detail['variant']}, SIMD "
+                       f"{detail['simd']}) on {detail['rows']} of {N} weight rows x "
+                       f"{(K + 47) // 48} limbs x 1 packed activation column = "
+                       f"{detail['limb_products']} limb products in {detail['seconds']:.2f} s; "
+                       f"GB/s of packed weights streamed; host {cpu_model()}, "
+                       f"nproc {os.cpu_count()}"),
+        }
+
+    gbytes = gemv_bytes(M, N, K)
+    line: dict = {
+        "metric": METRIC,
+        "value": (gbytes / (gemv_ms * 1e-3) / 1e9) if gemv_ms else None,
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": gemv_ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: W ~ N(0,1) (the effective W/0.02) ternarized at 0.45, x ~ N(0,1) bf16",
+        "config": {"workload": f"decode GEMV K2, {K}->{N} (Llama-3-8B gate), M={M}, bf16 x, "
+                               f"fp32 out, alpha=1 beta=0, {copies} rotating weight copies",
+                   "M": M, "K": K, "N": N, "parallelism": "none (1 GPU)"},
+    }
+    if gemv_ms:
+        achieved = gbytes / (gemv_ms * 1e-3) / 1e9
+        line["roofline"] = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS,
+                            "unit": "GB/s", "frac": achieved / HBM_PEAK_GBPS, "traffic": None}
+        line["tokens_per_s_equiv"] = M / (gemv_ms * 1e-3)
+    if cpu:
+        line["cpu_baseline"] = cpu
+    if gemm_ms:
+        flops = 2.0 * GM * GN * GK
+        tflops = flops / (gemm_ms * 1e-3) / 1e12
+        line["gemm"] = {
+            "workload": f"prefill GEMM K3, M={GM}, {GK}->{GN} (Llama-3-8B gate_up), bf16 x",
+            "ms": gemm_ms, "tflops": tflops, "tokens_per_s_equiv": GM / (gemm_ms * 1e-3),
+            "roofline": {"bound": "mfma", "achieved": tflops, "peak": BF16_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": tflops / BF16_PEAK_TFLOPS},
+        }
+    if pack_ms:
+        pbytes = 4 * PR * PC + 16 * PR * ((PC + 47) // 48)
+        gbs = pbytes / (pack_ms * 1e-3) / 1e9
+        line["pack"] = {"workload": f"K1 quantize+pack {PR}x{PC} fp32", "us": pack_ms * 1e3,
+                        "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBPS,
+                                     "unit": "GB/s", "frac": gbs / HBM_PEAK_GBPS}}
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

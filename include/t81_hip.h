@@ -1,0 +1,131 @@
+/*
+ * include/t81_hip.h -- C ABI of libt81_hip.so, the MI355X (gfx950) backend of
+ * t81lib's packed-ternary GEMM path.
+ *
+ * Plain C: pointers, sizes and an opaque stream handle (a hipStream_t, or NULL
+ * for the null stream).  No function throws.  Every entry point validates its
+ * arguments on the host, enqueues its kernels on `stream` and returns without
+ * synchronising; results are ordered with later work on the same stream.
+ * Device pointers must come from the same device that is current on the
+ * calling thread.  Returns T81_HIP_OK or a negative T81_HIP_E* code; the text
+ * of the last error on the calling thread is t81_hip_last_error().
+ *
+ * Packed-limb layout (the reference's, include/t81/core/limb.hpp:145-181 and
+ * docs/t81lib-spec-v0.1.0.md:179-234): a limb is 16 bytes holding 48 trits,
+ * byte j = 13 + t[3j] + 3*t[3j+1] + 9*t[3j+2] (values 0..26).  A packed
+ * matrix of `rows` x `cols` trits is rows x L x 16 bytes, L = ceil(cols/48),
+ * row-major; trits past `cols` are 0 (byte 13 for a fully padded triple).
+ */
+#ifndef T81_HIP_H
+#define T81_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* return codes */
+#define T81_HIP_OK 0
+#define T81_HIP_EINVAL_SHAPE (-1)     /* negative or inconsistent dimensions      */
+#define T81_HIP_EINVAL_K48 (-2)       /* K not a multiple of 48 (limb GEMM)       */
+#define T81_HIP_EINVAL_THRESHOLD (-3) /* threshold outside (0, 1] (C++ form)      */
+#define T81_HIP_EINVAL_DTYPE (-4)     /* unsupported dtype / alpha-beta combo     */
+#define T81_HIP_EINVAL_POINTER (-5)   /* NULL where data is required              */
+#define T81_HIP_EHIP (-6)             /* HIP runtime error (text in last_error)   */
+#define T81_HIP_ENODEV (-7)           /* no gfx950 device                         */
+
+/* element types of activations / float inputs */
+#define T81_DTYPE_F32 0
+#define T81_DTYPE_BF16 1
+#define T81_DTYPE_I8 2
+#define T81_DTYPE_F16 3
+
+/* threshold forms of the quantizer */
+#define T81_THR_CPP 0   /* python/bindings.cpp:405-414: >=thr -> +1 else <=-thr -> -1; */
+                        /* thr must lie in (0, 1] (bindings.cpp:419-421, 463-465)      */
+#define T81_THR_TORCH 1 /* t81/torch/__init__.py:44-50: thr clamped to [0, 0.9999] by */
+                        /* the caller (in double, then float32); -1 wins on ties       */
+
+/* 1 if a gfx950 device is present and usable, else 0.  Never fails.
+ * Replaces: t81::linalg::detail::rocm_available(), include/t81/linalg/gemm_gpu.hpp:70-72. */
+int t81_hip_available(void);
+
+/* Text of the last error returned on the calling thread ("" if none). */
+const char *t81_hip_last_error(void);
+
+/* K1 -- threshold-quantize a rows x cols float matrix (row-major, dtype
+ * T81_DTYPE_F32/BF16/F16) and pack it row-wise into out (rows x L x 16 bytes).
+ * Bit-exact with the reference packer.
+ * Replaces: pack_dense_matrix, python/bindings.cpp:460-517 (thr_mode T81_THR_CPP);
+ *           TernaryTensor.from_float / _quantize_tensor + _pack_rowwise,
+ *           t81/torch/__init__.py:214-231, 44-50, 68-80 (thr_mode T81_THR_TORCH). */
+int t81_hip_quantize_pack(const void *w, int w_dtype, uint8_t *out, int64_t rows, int64_t cols,
+                          float threshold, int thr_mode, void *stream);
+
+/* Elementwise quantize of `count` floats to int8 trits.
+ * Replaces: quantize_to_trits, python/bindings.cpp:416-445. */
+int t81_hip_quantize(const void *src, int dtype, int8_t *out, int64_t count, float threshold,
+                     int thr_mode, void *stream);
+
+/* Column-wise pack of activations: x is tokens x K (row-major), out is
+ * L x tokens x 16 bytes holding limb l of column n of x^T at (l*tokens+n)*16.
+ * Replaces: TernaryTensor._pack_rhs_for_gemm / _pack_columnwise,
+ *           t81/torch/__init__.py:257-262, 83-97. */
+int t81_hip_pack_cols(const void *x, int x_dtype, uint8_t *out, int64_t tokens, int64_t k,
+                      float threshold, int thr_mode, void *stream);
+
+/* Unpack rows x limbs_per_row x 16 bytes into a rows x cols int8 trit matrix
+ * (cols <= 48 * limbs_per_row).  Bytes > 26 decode to unspecified trits; call
+ * t81_hip_validate_packed first where the input is untrusted.
+ * Replaces: unpack_packed_limbs, python/bindings.cpp:640-686, and
+ *           _limbs_to_trits, t81/torch/__init__.py:100-112. */
+int t81_hip_unpack(const uint8_t *packed, int8_t *out, int64_t rows, int64_t limbs_per_row,
+                   int64_t cols, void *stream);
+
+/* Counts bytes > 26 in `count` packed bytes; *bad_count (device int32) is
+ * overwritten.  Mirrors the check of limb::from_bytes, limb.hpp:160-168. */
+int t81_hip_validate_packed(const uint8_t *packed, int64_t count, int32_t *bad_count,
+                            void *stream);
+
+/* K2/K3 -- ternary matmul, dot-product semantics over the packed weights:
+ *     C[m, n] = alpha * sum_{k<K} X[m, k] * T[n, k] + beta * C[m, n] + bias[n]
+ * X is M x K row-major (x_dtype F32 or BF16; C is float32 M x N) or I8 (C is
+ * int32 M x N, exact; requires alpha == 1, beta in {0, 1}, bias == NULL,
+ * K <= 131071).  W is N x L x 16 packed bytes.  beta == 0 does not read C.
+ * bias may be NULL.  M <= 16 runs the decode GEMV kernel (K2), larger M the
+ * prefill GEMM kernel (K3).
+ * Replaces: the hot path of TernaryTensor.matmul_input / t8.nn.Linear
+ *           (t81/torch/__init__.py:241-246, t81/nn/linear.py:53-70) with the
+ *           trit-dot reading of gemm_ternary (t81/torch/__init__.py:291-304). */
+int t81_hip_ternary_matmul(const void *x, int x_dtype, const uint8_t *w, void *c, int64_t m,
+                           int64_t n, int64_t k, float alpha, float beta, const float *bias,
+                           void *stream);
+
+/* Same, forcing the kernel: which = 2 (K2 GEMV, M <= 16) or 3 (K3 GEMM). */
+int t81_hip_ternary_matmul_kernel(int which, const void *x, int x_dtype, const uint8_t *w,
+                                  void *c, int64_t m, int64_t n, int64_t k, float alpha,
+                                  float beta, const float *bias, void *stream);
+
+/* K4 -- the reference's literal gemm_ternary: A (M x K/48 limbs), B (K/48 x N
+ * limbs), C (M x N float32, read and written):
+ *     C[i,j] = float( C[i,j]*beta + sum_l alpha * V(A[i,l]) * V(B[l,j]) )
+ * with V the limb's balanced-ternary integer value, each product formed
+ * exactly and converted as low + high * 3^48 through the reference's tryte
+ * tables, accumulated in double with l ascending (no FMA contraction).
+ * Bit-exact with src/linalg/gemm_cpu.cpp:8-71 (including +-inf outputs).
+ * Replaces: t81::linalg::detail::rocm_gemm_ternary, gemm_gpu.hpp:131-140 and
+ *           src/linalg/gemm_rocm.cpp:335-396 (device pointers instead of spans). */
+int t81_hip_gemm_ternary_limb(const uint8_t *a, const uint8_t *b, float *c, int m, int n, int k,
+                              float alpha, float beta, void *stream);
+
+/* Host-only test hook, no device needed: writes the 16 x 27 tryte-contribution
+ * table K4 uses (constant-evaluated like build_tryte_contributions,
+ * include/t81/linalg/gemm.hpp:28-41), so it can be compared bit for bit. */
+void t81_hip_limb_tryte_table(double *out);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* T81_HIP_H */

@@ -1,0 +1,363 @@
+"""CPU checkers for the packed-ternary path -- TEST INFRASTRUCTURE ONLY.
+
+``oracle`` wraps two shared libraries built by ``oracle/Makefile``:
+
+* ``liboracle.so`` -- the C restatement of the reference algorithm
+  (``oracle/t81_oracle.c``; every function cites the reference lines it
+  restates);
+* ``_ref/libt81ref_*.so`` -- the reference's own ``gemm_cpu.cpp`` and limb
+  headers compiled from ``/root/reference`` (present only where that tree
+  was available at build time), reached through ``oracle/ref_driver.cpp``.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py`` may import this package.  The product package ``t81lib_amd``
+never imports it and has no CPU fallback.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from typing import Optional
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+_ORACLE_SO = os.path.join(HERE, "liboracle.so")
+REF_DIR = os.path.join(HERE, "_ref")
+
+TRITS = 48
+TRYTES = 16
+
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+_i8p = ctypes.POINTER(ctypes.c_int8)
+_f32p = ctypes.POINTER(ctypes.c_float)
+_f64p = ctypes.POINTER(ctypes.c_double)
+_i64p = ctypes.POINTER(ctypes.c_int64)
+
+
+def build(reference: bool = True) -> None:
+    """Runs oracle/Makefile (the reference build only when its tree exists)."""
+    targets = ["oracle"]
+    if reference and os.path.isdir("/root/reference/src/linalg"):
+        targets.append("ref")
+    subprocess.run(["make", "-s", "-C", HERE, *targets], check=True)
+
+
+def _ptr(a: np.ndarray, typ):
+    return a.ctypes.data_as(typ)
+
+
+def _load_oracle() -> ctypes.CDLL:
+    if not os.path.exists(_ORACLE_SO):
+        build(reference=False)
+    lib = ctypes.CDLL(_ORACLE_SO)
+    lib.orc_quantize_trit.restype = ctypes.c_int8
+    lib.orc_quantize_trit.argtypes = [ctypes.c_float, ctypes.c_float, ctypes.c_int]
+    lib.orc_torch_threshold.restype = ctypes.c_float
+    lib.orc_torch_threshold.argtypes = [ctypes.c_double]
+    lib.orc_tryte_of.restype = ctypes.c_uint8
+    lib.orc_tryte_of.argtypes = [ctypes.c_int] * 3
+    lib.orc_trits_of.argtypes = [ctypes.c_uint8, _i8p]
+    lib.orc_pack_rows.argtypes = [_f32p, ctypes.c_int64, ctypes.c_int64, ctypes.c_float,
+                                  ctypes.c_int, _u8p]
+    lib.orc_pack_trits_rows.argtypes = [_i8p, ctypes.c_int64, ctypes.c_int64, _u8p]
+    lib.orc_pack_cols.argtypes = [_f32p, ctypes.c_int64, ctypes.c_int64, ctypes.c_float,
+                                  ctypes.c_int, _u8p]
+    lib.orc_unpack.restype = ctypes.c_int
+    lib.orc_unpack.argtypes = [_u8p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, _i8p]
+    lib.orc_mul_wide.argtypes = [_u8p, _u8p, _u8p, _u8p]
+    lib.orc_tryte_table.argtypes = [_f64p]
+    lib.orc_limb_to_double.restype = ctypes.c_double
+    lib.orc_limb_to_double.argtypes = [_u8p]
+    lib.orc_multiply_to_double.restype = ctypes.c_double
+    lib.orc_multiply_to_double.argtypes = [_u8p, _u8p]
+    lib.orc_gemm_limb.restype = ctypes.c_int
+    lib.orc_gemm_limb.argtypes = [_u8p, _u8p, _f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                  ctypes.c_float, ctypes.c_float]
+    lib.orc_trit_matmul_f64.argtypes = [_f64p, ctypes.c_int64, ctypes.c_int64, _u8p,
+                                        ctypes.c_int64, _i8p, _f64p]
+    lib.orc_trit_matmul_abs_f64.argtypes = lib.orc_trit_matmul_f64.argtypes
+    lib.orc_trit_matmul_i64.argtypes = [_i8p, ctypes.c_int64, ctypes.c_int64, _u8p,
+                                        ctypes.c_int64, _i8p, _i64p]
+    return lib
+
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        _lib = _load_oracle()
+    return _lib
+
+
+# ------------------------------------------------------------------ codec --
+def tryte_of(t0: int, t1: int, t2: int) -> int:
+    return int(lib().orc_tryte_of(t0, t1, t2))
+
+
+def trits_of(u: int) -> tuple[int, int, int]:
+    out = np.zeros(3, np.int8)
+    lib().orc_trits_of(u, _ptr(out, _i8p))
+    return tuple(int(v) for v in out)
+
+
+def quantize_trit(v: float, thr: float, mode: int = 0) -> int:
+    return int(lib().orc_quantize_trit(v, thr, mode))
+
+
+def torch_threshold(thr: float) -> float:
+    return float(lib().orc_torch_threshold(thr))
+
+
+def pack_rows(w: np.ndarray, thr: float, mode: int = 0) -> np.ndarray:
+    """(rows, cols) float32 -> (rows, L, 16) uint8, reference pack_dense_matrix."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    rows, cols = w.shape
+    L = (cols + TRITS - 1) // TRITS
+    out = np.empty((rows, L, TRYTES), np.uint8)
+    lib().orc_pack_rows(_ptr(w, _f32p), rows, cols, thr, mode, _ptr(out, _u8p))
+    return out
+
+
+def pack_trits_rows(t: np.ndarray) -> np.ndarray:
+    t = np.ascontiguousarray(t, dtype=np.int8)
+    rows, cols = t.shape
+    L = (cols + TRITS - 1) // TRITS
+    out = np.empty((rows, L, TRYTES), np.uint8)
+    lib().orc_pack_trits_rows(_ptr(t, _i8p), rows, cols, _ptr(out, _u8p))
+    return out
+
+
+def pack_cols(x: np.ndarray, thr: float = 0.5, mode: int = 1) -> np.ndarray:
+    """(tokens, K) float32 -> (L, tokens, 16) uint8, reference _pack_columnwise of x^T."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    tokens, k = x.shape
+    L = (k + TRITS - 1) // TRITS
+    out = np.empty((L, tokens, TRYTES), np.uint8)
+    lib().orc_pack_cols(_ptr(x, _f32p), tokens, k, thr, mode, _ptr(out, _u8p))
+    return out
+
+
+def unpack(packed: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    packed = np.ascontiguousarray(packed, dtype=np.uint8)
+    L = packed.shape[1]
+    out = np.zeros((rows, cols), np.int8)
+    rc = lib().orc_unpack(_ptr(packed, _u8p), rows, L, cols, _ptr(out, _i8p))
+    if rc != 0:
+        raise ValueError(f"unpack rejected input (code {rc})")
+    return out
+
+
+# ------------------------------------------------------------------- limb --
+def mul_wide(a: np.ndarray, b: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    a = np.ascontiguousarray(a, np.uint8)
+    b = np.ascontiguousarray(b, np.uint8)
+    lo = np.empty(16, np.uint8)
+    hi = np.empty(16, np.uint8)
+    lib().orc_mul_wide(_ptr(a, _u8p), _ptr(b, _u8p), _ptr(lo, _u8p), _ptr(hi, _u8p))
+    return lo, hi
+
+
+def tryte_table() -> np.ndarray:
+    out = np.empty(16 * 27, np.float64)
+    lib().orc_tryte_table(_ptr(out, _f64p))
+    return out.reshape(16, 27)
+
+
+def limb_to_double(a: np.ndarray) -> float:
+    a = np.ascontiguousarray(a, np.uint8)
+    return float(lib().orc_limb_to_double(_ptr(a, _u8p)))
+
+
+def multiply_to_double(a: np.ndarray, b: np.ndarray) -> float:
+    a = np.ascontiguousarray(a, np.uint8)
+    b = np.ascontiguousarray(b, np.uint8)
+    return float(lib().orc_multiply_to_double(_ptr(a, _u8p), _ptr(b, _u8p)))
+
+
+def gemm_limb(A: np.ndarray, B: np.ndarray, C: np.ndarray, M: int, N: int, K: int,
+              alpha: float = 1.0, beta: float = 0.0) -> np.ndarray:
+    """Reference gemm_ternary semantics; returns a new C (input C is not modified)."""
+    A = np.ascontiguousarray(A, np.uint8)
+    B = np.ascontiguousarray(B, np.uint8)
+    out = np.array(C, dtype=np.float32, copy=True, order="C")
+    rc = lib().orc_gemm_limb(_ptr(A, _u8p), _ptr(B, _u8p), _ptr(out, _f32p), M, N, K,
+                             alpha, beta)
+    if rc != 0:
+        raise ValueError("gemm_ternary shape rejected")
+    return out
+
+
+# --------------------------------------------------------------- trit-dot --
+def trit_matmul_f64(x: np.ndarray, w_packed: np.ndarray, K: int) -> np.ndarray:
+    """out[m, n] = sum_k x[m, k] * T[n, k] in float64."""
+    x = np.ascontiguousarray(x, np.float64)
+    w_packed = np.ascontiguousarray(w_packed, np.uint8)
+    M = x.shape[0]
+    N = w_packed.shape[0]
+    out = np.empty((M, N), np.float64)
+    scratch = np.empty(max(K, 1), np.int8)
+    lib().orc_trit_matmul_f64(_ptr(x, _f64p), M, K, _ptr(w_packed, _u8p), N,
+                              _ptr(scratch, _i8p), _ptr(out, _f64p))
+    return out
+
+
+def trit_matmul_abs_f64(x: np.ndarray, w_packed: np.ndarray, K: int) -> np.ndarray:
+    """out[m, n] = sum_k |x[m, k] * T[n, k]| -- the scale of the fp tolerances."""
+    x = np.ascontiguousarray(x, np.float64)
+    w_packed = np.ascontiguousarray(w_packed, np.uint8)
+    M = x.shape[0]
+    N = w_packed.shape[0]
+    out = np.empty((M, N), np.float64)
+    scratch = np.empty(max(K, 1), np.int8)
+    lib().orc_trit_matmul_abs_f64(_ptr(x, _f64p), M, K, _ptr(w_packed, _u8p), N,
+                                  _ptr(scratch, _i8p), _ptr(out, _f64p))
+    return out
+
+
+def trit_matmul_i64(x: np.ndarray, w_packed: np.ndarray, K: int) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.int8)
+    w_packed = np.ascontiguousarray(w_packed, np.uint8)
+    M = x.shape[0]
+    N = w_packed.shape[0]
+    out = np.empty((M, N), np.int64)
+    scratch = np.empty(max(K, 1), np.int8)
+    lib().orc_trit_matmul_i64(_ptr(x, _i8p), M, K, _ptr(w_packed, _u8p), N,
+                              _ptr(scratch, _i8p), _ptr(out, _i64p))
+    return out
+
+
+# ------------------------------------------------ the compiled reference --
+def _cpu_has_avx512f() -> bool:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("flags"):
+                    return " avx512f" in line
+    except OSError:
+        pass
+    return False
+
+
+class Ref:
+    """The reference's own CPU path (oracle/_ref), or None where it was not built."""
+
+    def __init__(self, lib: ctypes.CDLL, variant: str):
+        self.lib = lib
+        self.variant = variant
+        lib.t81ref_tryte_table.argtypes = [_f64p]
+        for name in ("t81ref_mul_wide", "t81ref_mul_wide_scalar"):
+            fn = getattr(lib, name)
+            fn.restype = ctypes.c_int
+            fn.argtypes = [_u8p, _u8p, _u8p, _u8p]
+        lib.t81ref_limb_to_double.restype = ctypes.c_double
+        lib.t81ref_limb_to_double.argtypes = [_u8p]
+        lib.t81ref_multiply_to_double.restype = ctypes.c_double
+        lib.t81ref_multiply_to_double.argtypes = [_u8p, _u8p]
+        lib.t81ref_limb_from_value.restype = ctypes.c_int
+        lib.t81ref_limb_from_value.argtypes = [ctypes.c_longlong, _u8p]
+        lib.t81ref_limb_from_trits.restype = ctypes.c_int
+        lib.t81ref_limb_from_trits.argtypes = [_i8p, _u8p]
+        lib.t81ref_limb_min_max.argtypes = [_u8p, _u8p]
+        lib.t81ref_random_limbs.argtypes = [ctypes.c_ulonglong, ctypes.c_int, _u8p]
+        lib.t81ref_gemm_ternary.restype = ctypes.c_int
+        lib.t81ref_gemm_ternary.argtypes = [_u8p, _u8p, _f32p, ctypes.c_int, ctypes.c_int,
+                                            ctypes.c_int, ctypes.c_float, ctypes.c_float]
+        lib.t81ref_gemm_ternary_rows.restype = ctypes.c_int
+        lib.t81ref_gemm_ternary_rows.argtypes = [_u8p, _u8p, _f32p, ctypes.c_int, ctypes.c_int,
+                                                 ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                                 ctypes.c_float, ctypes.c_float]
+        lib.t81ref_simd_path.restype = ctypes.c_char_p
+
+    def tryte_table(self) -> np.ndarray:
+        out = np.empty(16 * 27, np.float64)
+        self.lib.t81ref_tryte_table(_ptr(out, _f64p))
+        return out.reshape(16, 27)
+
+    def mul_wide(self, a, b, scalar: bool = False):
+        a = np.ascontiguousarray(a, np.uint8)
+        b = np.ascontiguousarray(b, np.uint8)
+        lo = np.empty(16, np.uint8)
+        hi = np.empty(16, np.uint8)
+        fn = self.lib.t81ref_mul_wide_scalar if scalar else self.lib.t81ref_mul_wide
+        if fn(_ptr(a, _u8p), _ptr(b, _u8p), _ptr(lo, _u8p), _ptr(hi, _u8p)) != 0:
+            raise ValueError("reference mul_wide rejected input")
+        return lo, hi
+
+    def limb_to_double(self, a) -> float:
+        a = np.ascontiguousarray(a, np.uint8)
+        return float(self.lib.t81ref_limb_to_double(_ptr(a, _u8p)))
+
+    def multiply_to_double(self, a, b) -> float:
+        a = np.ascontiguousarray(a, np.uint8)
+        b = np.ascontiguousarray(b, np.uint8)
+        return float(self.lib.t81ref_multiply_to_double(_ptr(a, _u8p), _ptr(b, _u8p)))
+
+    def limb_from_value(self, v: int) -> np.ndarray:
+        out = np.empty(16, np.uint8)
+        if self.lib.t81ref_limb_from_value(v, _ptr(out, _u8p)) != 0:
+            raise ValueError("value out of range")
+        return out
+
+    def limb_from_trits(self, t) -> np.ndarray:
+        t = np.ascontiguousarray(t, np.int8)
+        out = np.empty(16, np.uint8)
+        if self.lib.t81ref_limb_from_trits(_ptr(t, _i8p), _ptr(out, _u8p)) != 0:
+            raise ValueError("invalid trits")
+        return out
+
+    def limb_min_max(self):
+        lo = np.empty(16, np.uint8)
+        hi = np.empty(16, np.uint8)
+        self.lib.t81ref_limb_min_max(_ptr(lo, _u8p), _ptr(hi, _u8p))
+        return lo, hi
+
+    def random_limbs(self, seed: int, count: int) -> np.ndarray:
+        out = np.empty((count, 16), np.uint8)
+        self.lib.t81ref_random_limbs(seed, count, _ptr(out, _u8p))
+        return out
+
+    def gemm_ternary(self, A, B, C, M, N, K, alpha=1.0, beta=0.0) -> np.ndarray:
+        A = np.ascontiguousarray(A, np.uint8)
+        B = np.ascontiguousarray(B, np.uint8)
+        out = np.array(C, dtype=np.float32, copy=True, order="C")
+        rc = self.lib.t81ref_gemm_ternary(_ptr(A, _u8p), _ptr(B, _u8p), _ptr(out, _f32p),
+                                          M, N, K, alpha, beta)
+        if rc != 0:
+            raise ValueError(f"reference gemm_ternary rejected the call ({rc})")
+        return out
+
+    def gemm_ternary_rows(self, A, B, C, M, N, K, r0, r1, alpha=1.0, beta=0.0) -> None:
+        """In-place over rows [r0, r1) of C (used by the CPU baseline)."""
+        rc = self.lib.t81ref_gemm_ternary_rows(_ptr(A, _u8p), _ptr(B, _u8p), _ptr(C, _f32p),
+                                               M, N, K, r0, r1, alpha, beta)
+        if rc != 0:
+            raise ValueError(f"reference gemm_ternary rejected the call ({rc})")
+
+    def simd_path(self) -> str:
+        return self.lib.t81ref_simd_path().decode()
+
+
+_ref_cache: dict = {}
+
+
+def ref(variant: Optional[str] = None) -> Optional[Ref]:
+    """Loads oracle/_ref/libt81ref_<variant>.so; variant defaults to avx512 when
+    the host supports it (the C++ library build), else generic."""
+    if variant is None:
+        variant = "avx512" if _cpu_has_avx512f() else "generic"
+    if variant == "avx512" and not _cpu_has_avx512f():
+        return None
+    if variant in _ref_cache:
+        return _ref_cache[variant]
+    path = os.path.join(REF_DIR, f"libt81ref_{variant}.so")
+    if not os.path.exists(path):
+        _ref_cache[variant] = None
+        return None
+    r = Ref(ctypes.CDLL(path), variant)
+    _ref_cache[variant] = r
+    return r

@@ -1,0 +1,243 @@
+// t81lib_amd/csrc/abi.hip -- the extern "C" boundary of libt81_hip.so (include/t81_hip.h).
+//
+// Every entry point: validates on the host (the reference's checks and messages,
+// cited per function), checks that the current device is a gfx950, enqueues on
+// the caller's stream and returns.  No exceptions cross the boundary, no memory
+// is allocated, nothing is synchronised.
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <climits>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/t81_hip.h"
+#include "t81_kernels.hpp"
+
+namespace t81hip {
+void host_tryte_table(double *out);
+}
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string &msg) {
+    g_last_error = msg;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char *where) {
+    return fail(T81_HIP_EHIP, std::string(where) + ": " + hipGetErrorString(e));
+}
+
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_arch_state[kMaxDevices];  // 0 unknown, 1 gfx950, -1 other
+
+// Checks the current device once per device id: the kernels are built for gfx950 only.
+int require_device(const char *where) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, where);
+    if (dev < 0 || dev >= kMaxDevices) return fail(T81_HIP_ENODEV, "device index out of range");
+    int state = g_arch_state[dev].load(std::memory_order_relaxed);
+    if (state == 0) {
+        hipDeviceProp_t prop;
+        e = hipGetDeviceProperties(&prop, dev);
+        if (e != hipSuccess) return hip_fail(e, where);
+        state = std::strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : -1;
+        g_arch_state[dev].store(state, std::memory_order_relaxed);
+    }
+    if (state != 1) return fail(T81_HIP_ENODEV, std::string(where) + ": device is not gfx950");
+    return T81_HIP_OK;
+}
+
+int finish(hipError_t e, const char *where) {
+    if (e != hipSuccess) return hip_fail(e, where);
+    g_last_error.clear();
+    return T81_HIP_OK;
+}
+
+bool float_dtype(int d) { return d == T81_DTYPE_F32 || d == T81_DTYPE_BF16 || d == T81_DTYPE_F16; }
+
+// python/bindings.cpp:419-421 / 463-465 (C++ form); t81/torch/__init__.py:45 (torch form,
+// clamped by the caller -- here only range-checked).
+int check_threshold(float thr, int mode) {
+    if (mode == T81_THR_CPP) {
+        if (thr <= 0.0f || thr > 1.0f)
+            return fail(T81_HIP_EINVAL_THRESHOLD, "threshold must be between 0 (exclusive) and 1");
+        return T81_HIP_OK;
+    }
+    if (mode == T81_THR_TORCH) {
+        if (!(thr >= 0.0f && thr <= 1.0f))
+            return fail(T81_HIP_EINVAL_THRESHOLD,
+                        "torch-form threshold must already be clamped to [0, 0.9999]");
+        return T81_HIP_OK;
+    }
+    return fail(T81_HIP_EINVAL_THRESHOLD, "unknown threshold mode");
+}
+
+int check_matmul(const void *x, int x_dtype, const uint8_t *w, void *c, int64_t m, int64_t n,
+                 int64_t k, float alpha, float beta, const float *bias) {
+    if (m < 0 || n < 0 || k < 0)
+        return fail(T81_HIP_EINVAL_SHAPE, "gemm_ternary dimensions must be non-negative");
+    if (m > INT_MAX / 2 || n > (int64_t(1) << 40) || k > (int64_t(1) << 31))
+        return fail(T81_HIP_EINVAL_SHAPE, "ternary_matmul dimensions too large");
+    if (x_dtype != T81_DTYPE_F32 && x_dtype != T81_DTYPE_BF16 && x_dtype != T81_DTYPE_I8)
+        return fail(T81_HIP_EINVAL_DTYPE, "activations must be float32, bfloat16 or int8");
+    if (x_dtype == T81_DTYPE_I8) {
+        if (alpha != 1.0f || !(beta == 0.0f || beta == 1.0f) || bias != nullptr)
+            return fail(T81_HIP_EINVAL_DTYPE,
+                        "int8 activations produce exact int32: alpha must be 1, beta 0 or 1, "
+                        "no bias");
+        if (k > 131071)
+            return fail(T81_HIP_EINVAL_SHAPE, "int8 activations require K <= 131071 (exact sums)");
+    }
+    if ((m > 0 && k > 0 && x == nullptr) || (n > 0 && k > 0 && w == nullptr) ||
+        (m > 0 && n > 0 && c == nullptr))
+        return fail(T81_HIP_EINVAL_POINTER, "null data pointer");
+    if (reinterpret_cast<uintptr_t>(w) % 16 != 0)
+        return fail(T81_HIP_EINVAL_POINTER, "packed weights must be 16-byte aligned");
+    const uintptr_t elem = x_dtype == T81_DTYPE_F32 ? 4 : (x_dtype == T81_DTYPE_BF16 ? 2 : 1);
+    if (reinterpret_cast<uintptr_t>(x) % elem != 0 || reinterpret_cast<uintptr_t>(c) % 4 != 0 ||
+        reinterpret_cast<uintptr_t>(bias) % 4 != 0)
+        return fail(T81_HIP_EINVAL_POINTER, "misaligned activation, output or bias pointer");
+    return T81_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int t81_hip_available(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return 0;
+    return require_device("t81_hip_available") == T81_HIP_OK ? 1 : 0;
+}
+
+const char *t81_hip_last_error(void) { return g_last_error.c_str(); }
+
+int t81_hip_quantize_pack(const void *w, int w_dtype, uint8_t *out, int64_t rows, int64_t cols,
+                          float threshold, int thr_mode, void *stream) {
+    if (int rc = check_threshold(threshold, thr_mode)) return rc;
+    if (rows < 0 || cols < 0) return fail(T81_HIP_EINVAL_SHAPE, "rows and cols must be non-negative");
+    if (!float_dtype(w_dtype)) return fail(T81_HIP_EINVAL_DTYPE, "weights must be a float dtype");
+    if (rows > 0 && cols > 0 && (w == nullptr || out == nullptr))
+        return fail(T81_HIP_EINVAL_POINTER, "null data pointer");
+    if (reinterpret_cast<uintptr_t>(out) % 4 != 0 ||
+        reinterpret_cast<uintptr_t>(w) % (w_dtype == T81_DTYPE_F32 ? 4 : 2) != 0)
+        return fail(T81_HIP_EINVAL_POINTER, "misaligned input or output pointer");
+    if (int rc = require_device("t81_hip_quantize_pack")) return rc;
+    return finish(t81hip::launch_quantize_pack_rows(w, w_dtype, out, rows, cols, threshold,
+                                                    thr_mode == T81_THR_TORCH,
+                                                    static_cast<hipStream_t>(stream)),
+                  "t81_hip_quantize_pack");
+}
+
+int t81_hip_quantize(const void *src, int dtype, int8_t *out, int64_t count, float threshold,
+                     int thr_mode, void *stream) {
+    if (int rc = check_threshold(threshold, thr_mode)) return rc;
+    if (count < 0) return fail(T81_HIP_EINVAL_SHAPE, "count must be non-negative");
+    if (!float_dtype(dtype)) return fail(T81_HIP_EINVAL_DTYPE, "input must be a float dtype");
+    if (count > 0 && (src == nullptr || out == nullptr))
+        return fail(T81_HIP_EINVAL_POINTER, "null data pointer");
+    if (int rc = require_device("t81_hip_quantize")) return rc;
+    return finish(t81hip::launch_quantize(src, dtype, out, count, threshold,
+                                          thr_mode == T81_THR_TORCH,
+                                          static_cast<hipStream_t>(stream)),
+                  "t81_hip_quantize");
+}
+
+int t81_hip_pack_cols(const void *x, int x_dtype, uint8_t *out, int64_t tokens, int64_t k,
+                      float threshold, int thr_mode, void *stream) {
+    if (int rc = check_threshold(threshold, thr_mode)) return rc;
+    if (tokens < 0 || k < 0) return fail(T81_HIP_EINVAL_SHAPE, "dimensions must be non-negative");
+    if (!float_dtype(x_dtype)) return fail(T81_HIP_EINVAL_DTYPE, "input must be a float dtype");
+    if (tokens > 0 && k > 0 && (x == nullptr || out == nullptr))
+        return fail(T81_HIP_EINVAL_POINTER, "null data pointer");
+    if (reinterpret_cast<uintptr_t>(out) % 4 != 0 ||
+        reinterpret_cast<uintptr_t>(x) % (x_dtype == T81_DTYPE_F32 ? 4 : 2) != 0)
+        return fail(T81_HIP_EINVAL_POINTER, "misaligned input or output pointer");
+    if (int rc = require_device("t81_hip_pack_cols")) return rc;
+    return finish(t81hip::launch_quantize_pack_cols(x, x_dtype, out, tokens, k, threshold,
+                                                    thr_mode == T81_THR_TORCH,
+                                                    static_cast<hipStream_t>(stream)),
+                  "t81_hip_pack_cols");
+}
+
+// python/bindings.cpp:643-661: non-negative sizes, cols within the packed capacity.
+int t81_hip_unpack(const uint8_t *packed, int8_t *out, int64_t rows, int64_t limbs_per_row,
+                   int64_t cols, void *stream) {
+    if (rows < 0 || cols < 0 || limbs_per_row < 0)
+        return fail(T81_HIP_EINVAL_SHAPE, "rows and cols must be non-negative");
+    if (cols > limbs_per_row * 48)
+        return fail(T81_HIP_EINVAL_SHAPE, "cols exceeds packed trit capacity");
+    if (rows > 0 && cols > 0 && (packed == nullptr || out == nullptr))
+        return fail(T81_HIP_EINVAL_POINTER, "null data pointer");
+    if (int rc = require_device("t81_hip_unpack")) return rc;
+    return finish(t81hip::launch_unpack(packed, out, rows, limbs_per_row, cols,
+                                        static_cast<hipStream_t>(stream)),
+                  "t81_hip_unpack");
+}
+
+int t81_hip_validate_packed(const uint8_t *packed, int64_t count, int32_t *bad_count,
+                            void *stream) {
+    if (count < 0) return fail(T81_HIP_EINVAL_SHAPE, "count must be non-negative");
+    if (bad_count == nullptr || (count > 0 && packed == nullptr))
+        return fail(T81_HIP_EINVAL_POINTER, "null data pointer");
+    if (int rc = require_device("t81_hip_validate_packed")) return rc;
+    return finish(t81hip::launch_validate(packed, count, bad_count,
+                                          static_cast<hipStream_t>(stream)),
+                  "t81_hip_validate_packed");
+}
+
+int t81_hip_ternary_matmul_kernel(int which, const void *x, int x_dtype, const uint8_t *w,
+                                  void *c, int64_t m, int64_t n, int64_t k, float alpha,
+                                  float beta, const float *bias, void *stream) {
+    if (int rc = check_matmul(x, x_dtype, w, c, m, n, k, alpha, beta, bias)) return rc;
+    if (which == 2 && m > 16) return fail(T81_HIP_EINVAL_SHAPE, "the GEMV kernel takes M <= 16");
+    if (which != 2 && which != 3) return fail(T81_HIP_EINVAL_SHAPE, "kernel must be 2 or 3");
+    if (int rc = require_device("t81_hip_ternary_matmul")) return rc;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t e;
+    if (which == 2)
+        e = t81hip::launch_gemv(x, x_dtype, w, c, static_cast<int>(m), n, k, alpha, beta, bias, s);
+    else
+        e = t81hip::launch_gemm(x, x_dtype, w, c, m, n, k, alpha, beta, bias, s);
+    return finish(e, "t81_hip_ternary_matmul");
+}
+
+int t81_hip_ternary_matmul(const void *x, int x_dtype, const uint8_t *w, void *c, int64_t m,
+                           int64_t n, int64_t k, float alpha, float beta, const float *bias,
+                           void *stream) {
+    return t81_hip_ternary_matmul_kernel(m <= 16 ? 2 : 3, x, x_dtype, w, c, m, n, k, alpha, beta,
+                                         bias, stream);
+}
+
+// include/t81/linalg/gemm_gpu.hpp:171-190: dimension, K % 48 and (implicitly, through
+// the caller's buffers) span checks; M == 0 or N == 0 is a no-op.
+int t81_hip_gemm_ternary_limb(const uint8_t *a, const uint8_t *b, float *c, int m, int n, int k,
+                              float alpha, float beta, void *stream) {
+    if (m < 0 || n < 0 || k < 0)
+        return fail(T81_HIP_EINVAL_SHAPE, "gemm_ternary dimensions must be non-negative");
+    if (k % 48 != 0) return fail(T81_HIP_EINVAL_K48, "gemm_ternary requires K divisible by 48");
+    if (m == 0 || n == 0) {
+        g_last_error.clear();
+        return T81_HIP_OK;
+    }
+    if (c == nullptr || (k > 0 && (a == nullptr || b == nullptr)))
+        return fail(T81_HIP_EINVAL_POINTER, "null data pointer");
+    if (reinterpret_cast<uintptr_t>(a) % 16 != 0 || reinterpret_cast<uintptr_t>(b) % 16 != 0 ||
+        reinterpret_cast<uintptr_t>(c) % 4 != 0)
+        return fail(T81_HIP_EINVAL_POINTER, "limb buffers must be 16-byte aligned");
+    if (int rc = require_device("t81_hip_gemm_ternary_limb")) return rc;
+    return finish(t81hip::launch_gemm_limb(a, b, c, m, n, k / 48, alpha, beta,
+                                           static_cast<hipStream_t>(stream)),
+                  "t81_hip_gemm_ternary_limb");
+}
+
+void t81_hip_limb_tryte_table(double *out) { t81hip::host_tryte_table(out); }
+
+}  // extern "C"

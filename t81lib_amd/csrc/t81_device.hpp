@@ -1,0 +1,87 @@
+// t81lib_amd/csrc/t81_device.hpp -- device-side helpers shared by the gfx950 kernels.
+//
+// Tryte code (include/t81/core/detail/lut.hpp:13-49): byte u = 13 + t0 + 3*t1 + 9*t2,
+// i.e. the base-3 digits of u are t_i + 1.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace t81hip {
+
+constexpr int kTrits = 48;
+constexpr int kTrytes = 16;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+__host__ __device__ constexpr int trit_of(int u, int p) {
+    return p == 0 ? (u % 3) - 1 : (p == 1 ? ((u / 3) % 3) - 1 : (u / 9) - 1);
+}
+
+__host__ __device__ constexpr uint32_t bf16_bits_of_trit(int t) {
+    return t > 0 ? 0x3F80u : (t < 0 ? 0xBF80u : 0u);
+}
+
+// ---------------------------------------------------------------------------
+// Decode tables in LDS.  For a byte u (one tryte = trits t0,t1,t2):
+//   E[u] = { bf16(t0) | bf16(t1) << 16,  bf16(t2) }
+//   F[u] = { bf16(t0) << 16,             bf16(t1) | bf16(t2) << 16 }
+// Two consecutive bytes (a, b) hold trits 0..5 of a 6-trit run; the three
+// natural-order bf16 pairs are E[a].x, E[a].y | F[b].x and F[b].y.  Entries are
+// 8 bytes, so a byte value u addresses offset 8u; u < 32 for every valid byte,
+// which lets (word << 3) place each byte's 8u in its own 8-bit field.  The
+// field is masked to 8 bits, so even an invalid byte (> 26) addresses at most
+// 255 + 8 bytes past a table start: the region below is zero-filled to cover it.
+constexpr int kLutE = 0;                    // byte offset of E
+constexpr int kLutF = 256;                  // byte offset of F
+constexpr int kLutBytes = 256 + 256 + 16;   // F start + max field + one entry
+
+__device__ __forceinline__ void lut_init(uint8_t *lds, int tid, int nthreads) {
+    uint32_t *w = reinterpret_cast<uint32_t *>(lds);
+    for (int i = tid; i < kLutBytes / 4; i += nthreads) w[i] = 0u;
+    __syncthreads();
+    for (int u = tid; u < 27; u += nthreads) {
+        const uint32_t b0 = bf16_bits_of_trit(trit_of(u, 0));
+        const uint32_t b1 = bf16_bits_of_trit(trit_of(u, 1));
+        const uint32_t b2 = bf16_bits_of_trit(trit_of(u, 2));
+        w[(kLutE + 8 * u) / 4 + 0] = b0 | (b1 << 16);
+        w[(kLutE + 8 * u) / 4 + 1] = b2;
+        w[(kLutF + 8 * u) / 4 + 0] = b0 << 16;
+        w[(kLutF + 8 * u) / 4 + 1] = b1 | (b2 << 16);
+    }
+    __syncthreads();
+}
+
+// Decodes one packed dword (4 bytes = 12 trits, natural order) into 6 dwords of
+// bf16 pairs: out[i] = { bf16(t[2i]), bf16(t[2i+1]) }.
+__device__ __forceinline__ void decode_dword(const uint8_t *lds, uint32_t w, uint32_t *out) {
+    const uint32_t w8 = w << 3;
+    const uint32_t a0 = w8 & 0xFFu;
+    const uint32_t a1 = (w8 >> 8) & 0xFFu;
+    const uint32_t a2 = (w8 >> 16) & 0xFFu;
+    const uint32_t a3 = w8 >> 24;
+    const uint2 e0 = *reinterpret_cast<const uint2 *>(lds + kLutE + a0);
+    const uint2 f1 = *reinterpret_cast<const uint2 *>(lds + kLutF + a1);
+    const uint2 e2 = *reinterpret_cast<const uint2 *>(lds + kLutE + a2);
+    const uint2 f3 = *reinterpret_cast<const uint2 *>(lds + kLutF + a3);
+    out[0] = e0.x;
+    out[1] = e0.y | f1.x;
+    out[2] = f1.y;
+    out[3] = e2.x;
+    out[4] = e2.y | f3.x;
+    out[5] = f3.y;
+}
+
+__device__ __forceinline__ uint16_t bf16_bits_rne(float f) {
+    // round-to-nearest-even float -> bf16 (NaN kept quiet)
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float bf16_bits_to_float(uint32_t b) { return __uint_as_float(b << 16); }
+
+}  // namespace t81hip

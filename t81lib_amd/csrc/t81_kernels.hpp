@@ -1,0 +1,40 @@
+// t81lib_amd/csrc/t81_kernels.hpp -- host-side launchers of the gfx950 kernels.
+// Shapes and pointers are validated by the C ABI (abi.hip) before any launcher runs;
+// launchers only enqueue work on the given stream.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace t81hip {
+
+constexpr int kDtypeF32 = 0;
+constexpr int kDtypeBF16 = 1;
+constexpr int kDtypeI8 = 2;
+constexpr int kDtypeF16 = 3;
+
+// pack.hip
+hipError_t launch_quantize_pack_rows(const void *w, int dtype, uint8_t *out, int64_t rows,
+                                     int64_t cols, float thr, int torch_form, hipStream_t s);
+hipError_t launch_quantize_pack_cols(const void *x, int dtype, uint8_t *out, int64_t tokens,
+                                     int64_t k, float thr, int torch_form, hipStream_t s);
+hipError_t launch_quantize(const void *src, int dtype, int8_t *out, int64_t count, float thr,
+                           int torch_form, hipStream_t s);
+hipError_t launch_unpack(const uint8_t *packed, int8_t *out, int64_t rows, int64_t limbs,
+                         int64_t cols, hipStream_t s);
+hipError_t launch_validate(const uint8_t *packed, int64_t count, int32_t *bad, hipStream_t s);
+
+// gemv.hip (K2): M <= 16
+hipError_t launch_gemv(const void *x, int x_dtype, const uint8_t *w, void *c, int m, int64_t n,
+                       int64_t k, float alpha, float beta, const float *bias, hipStream_t s);
+
+// gemm.hip (K3): any M
+hipError_t launch_gemm(const void *x, int x_dtype, const uint8_t *w, void *c, int64_t m,
+                       int64_t n, int64_t k, float alpha, float beta, const float *bias,
+                       hipStream_t s);
+
+// limb.hip (K4)
+hipError_t launch_gemm_limb(const uint8_t *a, const uint8_t *b, float *c, int m, int n,
+                            int k_limbs, float alpha, float beta, hipStream_t s);
+
+}  // namespace t81hip

@@ -1,0 +1,160 @@
+"""The reference's ``t81lib`` extension-module surface for the packed path, on the GPU.
+
+Same names, argument meanings, defaults and exception types as the pybind11
+module (python/bindings.cpp:759-765 constants, :769-810 ``gemm_ternary``,
+:405-517 quantize/pack, :640-686 unpack).  Arguments may be NumPy arrays /
+buffers (copied to the GPU, results copied back -- the host-span contract of
+``rocm_gemm_ternary``, src/linalg/gemm_rocm.cpp:335-396) or GPU torch tensors
+(used in place, no copies).  Every computation runs on the GPU; there is no
+CPU path.
+"""
+
+from __future__ import annotations
+
+from typing import Any
+
+import numpy as np
+import torch
+
+from . import _lib, ops
+
+TRITS_PER_LIMB = 48
+TRYTES_PER_LIMB = 16
+BYTES_PER_LIMB = 16
+HAS_CUDA_BACKEND = False
+HAS_METAL_BACKEND = False
+
+
+def _has_rocm() -> bool:
+    return _lib.available()
+
+
+def __getattr__(name: str) -> Any:
+    if name == "HAS_ROCM_BACKEND":  # evaluated lazily: probing the device initialises HIP
+        return _has_rocm()
+    raise AttributeError(name)
+
+
+def _device() -> torch.device:
+    if not torch.cuda.is_available():
+        raise _lib.T81HipError("t81lib_amd needs a gfx950 GPU; none is visible")
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+def _as_device(obj: Any, dtype: torch.dtype) -> tuple[torch.Tensor, bool]:
+    """(tensor on the GPU, was_host)."""
+    if isinstance(obj, torch.Tensor):
+        if obj.device.type == "cuda":
+            return obj, False
+        return obj.to(device=_device()), True
+    arr = np.asarray(obj)
+    return torch.from_numpy(np.ascontiguousarray(arr)).to(device=_device()), True
+
+
+def _packed_bytes(obj: Any) -> tuple[torch.Tensor, bool]:
+    """Packed limbs from a uint8 array/tensor, a V16 array, or any byte buffer."""
+    if isinstance(obj, torch.Tensor):
+        if obj.dtype != torch.uint8:
+            raise ValueError("packed limbs must be uint8")
+        t, host = _as_device(obj, torch.uint8)
+        return t.contiguous().reshape(-1), host
+    arr = np.asarray(memoryview(obj) if not isinstance(obj, np.ndarray) else obj)
+    arr = np.ascontiguousarray(arr).view(np.uint8).reshape(-1)
+    return torch.from_numpy(arr).to(device=_device()), True
+
+
+def gemm_ternary(A: Any, B: Any, C: Any, M: int, N: int, K: int, alpha: float = 1.0,
+                 beta: float = 0.0) -> None:
+    """Packed-limb GEMM, reference semantics (limb-integer products, fp64 sums).
+
+    C (M x N float32) is read and overwritten in place, like the reference.
+    """
+    if M < 0 or N < 0 or K < 0:
+        raise ValueError("gemm_ternary dimensions must be non-negative")
+    if K % TRITS_PER_LIMB != 0:
+        raise ValueError("K must be divisible by the limb trit count")
+    kl = K // TRITS_PER_LIMB
+    a, _ = _packed_bytes(A)
+    b, _ = _packed_bytes(B)
+    if a.numel() != M * kl * BYTES_PER_LIMB:
+        raise ValueError("A span size does not match (M, K / 48)")
+    if b.numel() != kl * N * BYTES_PER_LIMB:
+        raise ValueError("B span size does not match (K / 48, N)")
+    if isinstance(C, torch.Tensor) and C.device.type == "cuda":
+        if C.dtype != torch.float32 or tuple(C.shape) != (M, N) or not C.is_contiguous():
+            raise ValueError("C tensor shape must match (M, N)")
+        ops.gemm_limb(a, b, C, M, N, K, alpha, beta)
+        return
+    if isinstance(C, torch.Tensor):
+        host = C
+        if host.dtype != torch.float32 or host.numel() != M * N:
+            raise ValueError("C tensor shape must match (M, N)")
+        c = host.to(device=_device()).contiguous().reshape(M, N)
+        ops.gemm_limb(a, b, c, M, N, K, alpha, beta)
+        host.copy_(c.reshape(host.shape).cpu())
+        return
+    view = np.asarray(C if isinstance(C, np.ndarray) else memoryview(C)).reshape(-1)
+    if view.dtype != np.float32 or view.size != M * N:
+        raise ValueError("C tensor shape must match (M, N)")
+    c = torch.from_numpy(np.ascontiguousarray(view).copy()).to(device=_device()).reshape(M, N)
+    ops.gemm_limb(a, b, c, M, N, K, alpha, beta)
+    view[...] = c.cpu().numpy().reshape(-1)
+
+
+def _threshold_cpp(threshold: float) -> float:
+    if threshold <= 0.0 or threshold > 1.0:
+        raise ValueError("threshold must be between 0 (exclusive) and 1")
+    return float(threshold)
+
+
+def _return_like(result: torch.Tensor, was_host: bool):
+    return result.cpu().numpy() if was_host else result
+
+
+def quantize_to_trits(values: Any, threshold: float = 0.5):
+    """Float array -> int8 trits in {-1, 0, 1} (python/bindings.cpp:416-445)."""
+    thr = _threshold_cpp(threshold)
+    t, host = _as_device(values, torch.float32)
+    if t.ndim == 0:
+        raise ValueError("expected at least one dimension for quantization")
+    return _return_like(ops.quantize(t, thr, _lib.THR_CPP), host)
+
+
+def dequantize_trits(trits: Any):
+    """Trit tensor -> float32 (python/bindings.cpp:447-458)."""
+    t, host = _as_device(trits, torch.int8)
+    return _return_like(t.to(torch.int8).to(torch.float32), host)
+
+
+def pack_dense_matrix(matrix: Any, threshold: float = 0.5):
+    """2-D float array -> (rows, limbs, 16) uint8 packed limbs (python/bindings.cpp:460-517)."""
+    thr = _threshold_cpp(threshold)
+    t, host = _as_device(matrix, torch.float32)
+    if t.ndim != 2:
+        raise ValueError("pack_dense_matrix expects a 2D array")
+    return _return_like(ops.quantize_pack(t, thr, _lib.THR_CPP), host)
+
+
+def unpack_packed_limbs(packed: Any, rows: int, cols: int):
+    """(rows, limbs, 16) uint8 -> (rows, cols) int8 trits (python/bindings.cpp:640-686)."""
+    if rows < 0 or cols < 0:
+        raise ValueError("rows and cols must be non-negative")
+    t, host = _as_device(packed, torch.uint8)
+    if t.ndim != 3:
+        raise ValueError("packed limbs must be a 3D array")
+    if t.shape[0] != rows:
+        raise ValueError("row count mismatch")
+    if t.shape[2] != BYTES_PER_LIMB:
+        raise ValueError("packed limb innermost dimension must equal limb byte width")
+    if cols > t.shape[1] * TRITS_PER_LIMB:
+        raise ValueError("cols exceeds packed trit capacity")
+    if ops.count_invalid_bytes(t):
+        raise ValueError("limb bytes must encode canonical trytes")
+    return _return_like(ops.unpack(t, rows, cols), host)
+
+
+__all__ = [
+    "TRITS_PER_LIMB", "TRYTES_PER_LIMB", "BYTES_PER_LIMB", "HAS_CUDA_BACKEND",
+    "HAS_METAL_BACKEND", "gemm_ternary", "quantize_to_trits", "dequantize_trits",
+    "pack_dense_matrix", "unpack_packed_limbs",
+]

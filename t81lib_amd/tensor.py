@@ -1,0 +1,220 @@
+"""``TernaryTensor`` and the ``trit`` dtype marker, GPU-resident.
+
+Mirrors t81/torch/__init__.py:115-304 (``trit``, ``TernaryTensor.from_float``,
+``update_from_float``, ``matmul_input``, ``torch.matmul``/``torch.mm``
+interception, autograd through ``_TernaryGemmFunction``), with the packed limbs
+kept on the GPU and packed once by the K1 kernel instead of per call on the
+host.  Two readings of ``matmul_input`` are available:
+
+* ``semantics="trit_dot"`` (default) -- y = x @ T^T over the packed trits, the
+  reading every other consumer of the packed weights uses (the reference's own
+  backward, t81/torch/__init__.py:291-304; training forward
+  t81/nn/linear.py:43-45).  Runs K2 (M <= 16) or K3.
+* ``semantics="reference_limb"`` -- the reference's literal path
+  (t81/torch/__init__.py:241-276): activations quantized at 0.5, packed
+  column-wise, multiplied as limb integers by K4; bit-exact with the
+  reference CPU ``gemm_ternary``, including its +-inf outputs.
+"""
+
+from __future__ import annotations
+
+import warnings
+from typing import Callable, Optional
+
+import torch
+
+from . import _lib, ops
+
+
+class TritDtype:
+    __slots__ = ()
+
+    def __repr__(self) -> str:
+        return "t81.trit"
+
+
+trit = TritDtype()
+
+SEMANTICS = ("trit_dot", "reference_limb")
+
+
+def _to_gpu_float(tensor: torch.Tensor) -> torch.Tensor:
+    """Counterpart of _to_cpu_float (t81/torch/__init__.py:53-65): this build keeps
+    everything on the GPU, so host tensors are moved there (with a warning)."""
+    if tensor.is_meta:
+        raise NotImplementedError(
+            "t81.trit does not support meta tensors; load weights on CPU or disable offload.")
+    if tensor.device.type != "cuda":
+        if not torch.cuda.is_available():
+            raise _lib.T81HipError("t81lib_amd needs a gfx950 GPU; none is visible")
+        warnings.warn(
+            f"t81.trit runs on the GPU; moving tensor from {tensor.device} to cuda.",
+            RuntimeWarning, stacklevel=3)
+        tensor = tensor.detach().to(device="cuda")
+    tensor = tensor.detach()
+    if tensor.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        tensor = tensor.to(torch.float32)
+    return tensor.contiguous()
+
+
+class TernaryTensor(torch.Tensor):
+    """A (rows, cols) ternary matrix held as packed limbs (rows, ceil(cols/48), 16) on the GPU."""
+
+    @staticmethod
+    def __new__(cls, packed: torch.Tensor, shape: tuple[int, int], *, k_actual: int,
+                k_limbs: int, float_source: Optional[torch.Tensor] = None,
+                threshold: float = 0.5, semantics: str = "trit_dot") -> "TernaryTensor":
+        if semantics not in SEMANTICS:
+            raise ValueError(f"semantics must be one of {SEMANTICS}")
+        t = torch.Tensor._make_wrapper_subclass(cls, shape, dtype=torch.float32,
+                                                device=packed.device, requires_grad=False)
+        t._packed = packed
+        t._rows = int(shape[0])
+        t._k_actual = int(k_actual)
+        t._k_limbs = int(k_limbs)
+        t._float_source = float_source
+        t._threshold = ops.torch_threshold(threshold)
+        t._semantics = semantics
+        return t
+
+    @property
+    def dtype(self) -> TritDtype:  # type: ignore[override]
+        return trit
+
+    @property
+    def packed(self) -> torch.Tensor:
+        """The (rows, L, 16) uint8 limb buffer (reference layout)."""
+        return self._packed
+
+    def __repr__(self) -> str:  # type: ignore[override]
+        return f"TernaryTensor(shape={tuple(self.shape)}, trits_per_row={self._k_actual})"
+
+    @staticmethod
+    def _ensure_2d(tensor: torch.Tensor) -> torch.Tensor:
+        if tensor.ndim != 2:
+            raise ValueError("t81.trit tensors currently only support 2D matrices")
+        return tensor
+
+    @classmethod
+    def from_float(cls, source: torch.Tensor, quantize: bool = True, threshold: float = 0.5,
+                   semantics: str = "trit_dot") -> "TernaryTensor":
+        """t81/torch/__init__.py:214-231: clamp, threshold (torch form), pack row-wise."""
+        src = _to_gpu_float(cls._ensure_2d(source))
+        rows, cols = src.shape
+        k_limbs = ops.limbs_for(cols)
+        if quantize:
+            packed = ops.quantize_pack(src, ops.torch_threshold(threshold), _lib.THR_TORCH)
+        else:
+            packed = _pack_exact_trits(src)
+        return cls(packed, (rows, cols), k_actual=cols, k_limbs=k_limbs, float_source=src,
+                   threshold=threshold, semantics=semantics)
+
+    def update_from_float(self, source: torch.Tensor) -> None:
+        """t81/torch/__init__.py:233-239: re-quantize into the existing buffer."""
+        src = _to_gpu_float(self._ensure_2d(source))
+        if tuple(src.shape) != (self._rows, self._k_actual):
+            raise ValueError("source shape does not match the ternary tensor")
+        ops.quantize_pack(src, self._threshold, _lib.THR_TORCH, out=self._packed)
+        self._float_source = src
+
+    def trits(self) -> torch.Tensor:
+        """(rows, cols) int8 trits (GPU unpack kernel)."""
+        return ops.unpack(self._packed, self._rows, self._k_actual)
+
+    def matmul_input(self, input: torch.Tensor, bias: Optional[torch.Tensor] = None
+                     ) -> torch.Tensor:
+        """input (tokens, cols) -> (tokens, rows): input @ T^T (+ bias), float32."""
+        if input.ndim != 2:
+            raise ValueError("t81.trit linear helpers expect 2D activations")
+        rhs = input.transpose(-2, -1)
+        out = _TernaryGemmFunction.apply(self, rhs)
+        out = out.transpose(-2, -1)
+        if bias is not None:
+            out = out + bias.to(device=out.device, dtype=torch.float32)
+        return out
+
+    def linear(self, x: torch.Tensor, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """Inference fast path: x (tokens, cols) -> (tokens, rows) with the bias fused."""
+        if self._semantics != "trit_dot":
+            return self.matmul_input(x, bias=bias)
+        x = _activations(x)
+        return ops.ternary_matmul(x, self._packed, self._k_actual, bias=bias)
+
+    @classmethod
+    def __torch_function__(cls, func: Callable, types, args=(), kwargs=None):
+        kwargs = kwargs or {}
+        if func in (torch.matmul, torch.mm):
+            lhs, rhs = args
+            if isinstance(lhs, TernaryTensor):
+                return _TernaryGemmFunction.apply(lhs, rhs)
+        # metadata (shape, device, ...) falls through to the default; real compute on the
+        # storage-less wrapper fails loudly in __torch_dispatch__.
+        return super().__torch_function__(func, types, args, kwargs)
+
+    @classmethod
+    def __torch_dispatch__(cls, func, types, args=(), kwargs=None):
+        raise NotImplementedError(
+            f"TernaryTensor holds packed trits only; it supports matmul/mm/matmul_input, "
+            f"not {func}")
+
+    # -- the two forward readings; rhs is (cols, tokens), result (rows, tokens) --
+    def _compute_gemm(self, rhs: torch.Tensor) -> torch.Tensor:
+        if rhs.shape[0] != self._k_actual:
+            raise ValueError("rhs dimension does not match ternary weight width")
+        if self._semantics == "trit_dot":
+            x = _activations(rhs.transpose(0, 1))
+            return ops.ternary_matmul(x, self._packed, self._k_actual).transpose(0, 1)
+        # reference_limb: t81/torch/__init__.py:257-276
+        tokens = rhs.shape[1]
+        packed_rhs = ops.pack_cols(rhs.transpose(0, 1).float().contiguous(), 0.5, _lib.THR_TORCH)
+        out = torch.zeros((self._rows, tokens), dtype=torch.float32, device=rhs.device)
+        ops.gemm_limb(self._packed, packed_rhs, out, self._rows, tokens, self._k_limbs * 48)
+        return out
+
+
+def _activations(x: torch.Tensor) -> torch.Tensor:
+    if x.device.type != "cuda":
+        raise ValueError("activations must be on the GPU")
+    if x.dtype not in (torch.float32, torch.bfloat16, torch.int8):
+        x = x.float()
+    return x.contiguous()
+
+
+def _pack_exact_trits(src: torch.Tensor) -> torch.Tensor:
+    """quantize=False (t81/torch/__init__.py:222): values are taken as int8 trits."""
+    as_int = src.to(torch.int8)
+    if bool(((as_int < -1) | (as_int > 1)).any()):
+        raise ValueError("limb trits must be -1..1")
+    return ops.quantize_pack(as_int.to(torch.float32), 0.5, _lib.THR_TORCH)
+
+
+class _TernaryGemmFunction(torch.autograd.Function):
+    """Forward T @ rhs; backward grad_rhs = T^T @ grad (t81/torch/__init__.py:279-304)."""
+
+    @staticmethod
+    def forward(ctx, ternary_weight: TernaryTensor, rhs: torch.Tensor) -> torch.Tensor:
+        device = rhs.device
+        if device.type != "cuda":
+            rhs_gpu = _to_gpu_float(rhs)
+        else:
+            rhs_gpu = rhs
+        ctx.ternary = ternary_weight
+        ctx.rhs_device = device
+        ctx.rhs_dtype = rhs.dtype
+        out = ternary_weight._compute_gemm(rhs_gpu)
+        if device.type != "cuda":
+            out = out.to(device)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_output: torch.Tensor) -> tuple[None, torch.Tensor]:
+        t: TernaryTensor = ctx.ternary
+        weight = t.trits().to(torch.float32)  # (rows, cols)
+        grad = grad_output.to(device=weight.device, dtype=torch.float32)
+        grad_rhs = weight.transpose(0, 1).matmul(grad)
+        if ctx.rhs_device.type != "cuda":
+            grad_rhs = grad_rhs.to(ctx.rhs_device)
+        return None, grad_rhs
+
+
+__all__ = ["trit", "TritDtype", "TernaryTensor", "SEMANTICS"]

@@ -1,0 +1,66 @@
+"""Shared test setup.
+
+Markers: ``gpu`` tests need a gfx950 device and the built libt81_hip.so; they
+compare the HIP path with the CPU oracle (oracle/) through the C ABI.
+Everything else runs on the CPU: the oracle against the golden vectors of the
+compiled reference, host-side validation, and the library's exports.
+"""
+
+from __future__ import annotations
+
+import os
+import sys
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+GOLDEN = os.path.join(ROOT, "tests", "golden", "ref_vectors.npz")
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs a gfx950 GPU and the built libt81_hip.so")
+
+
+@pytest.fixture(scope="session")
+def golden():
+    return np.load(GOLDEN)
+
+
+@pytest.fixture(scope="session")
+def orc():
+    import oracle
+
+    if not os.path.exists(os.path.join(ROOT, "oracle", "liboracle.so")):
+        oracle.build(reference=False)
+    return oracle
+
+
+@pytest.fixture(scope="session")
+def gpu():
+    """The torch CUDA device; fails (does not skip) when a gpu-marked test has no GPU,
+    so a silent CPU pass is impossible."""
+    import torch
+
+    from t81lib_amd import _lib
+
+    if not torch.cuda.is_available():
+        pytest.fail("gpu-marked test run without a visible GPU")
+    _lib.lib()
+    if not _lib.available():
+        pytest.fail(f"libt81_hip reports no gfx950 device: {_lib.last_error()}")
+    return torch.device("cuda", 0)
+
+
+def fp_tolerance_ok(got, ref, scale, rtol, atol=1e-6):
+    """|got - ref| <= rtol * scale + atol elementwise, scale = sum_k |alpha x_k t_k| + |beta c| + |bias|
+    (a relative tolerance on the terms that were summed, so cancellation in a sum does not
+    demand more than the inputs carry)."""
+    got = np.asarray(got, np.float64)
+    err = np.abs(got - ref)
+    bound = rtol * scale + atol
+    bad = ~(err <= bound)
+    return (not bad.any()), float((err / np.maximum(scale, 1e-30)).max(initial=0.0)), int(bad.sum())

@@ -1,0 +1,122 @@
+"""Writes tests/golden/ref_vectors.npz from the reference's own compiled CPU path.
+
+Run in a container that has /root/reference (``make -C oracle ref`` builds
+oracle/_ref/libt81ref_*.so from the reference sources).  The fixture holds
+inputs and the outputs the reference code produced for them; it is data, not
+source.  Vectors:
+
+* ``table``                  16x27 tryte contributions (include/t81/linalg/gemm.hpp:28-41)
+* ``mw_a``/``mw_b``/``mw_lo``/``mw_hi``/``mw_prod``
+                             limb::mul_wide and multiply_to_double on the inputs of
+                             tests/unit/test_limb_basic.cpp:68-116 (9 fixed limbs, all
+                             pairs; 1000 random pairs, mt19937_64(0xdeadbeef))
+* ``ft_trits``/``ft_bytes``  limb::from_trits on random trit vectors (the tryte code)
+* ``g<i>_*``                 gemm_ternary_cpu_impl (src/linalg/gemm_cpu.cpp:8-71) cases
+* ``emb_*``                  gemm_ternary on one-value-per-limb embeddings: small integers
+                             as limbs, which turns the limb GEMM into an exact integer GEMM
+                             (the cross-check of the trit-dot oracle)
+"""
+
+from __future__ import annotations
+
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
+
+import oracle  # noqa: E402
+
+
+def main() -> None:
+    oracle.build(reference=True)
+    ref = oracle.ref("generic")
+    if ref is None:
+        raise SystemExit("oracle/_ref/libt81ref_generic.so is not built (needs /root/reference)")
+    out: dict[str, np.ndarray] = {}
+    out["table"] = ref.tryte_table()
+
+    # test_limb_basic.cpp:68-78 fixed values, then its seeded random limbs
+    lo_min, hi_max = ref.limb_min_max()
+    fixed = [ref.limb_from_value(v) for v in (0, 1, -1, 42, -42, 1234, -1234)]
+    fixed += [lo_min, hi_max]
+    a_list, b_list = [], []
+    for x in fixed:
+        for y in fixed:
+            a_list.append(x)
+            b_list.append(y)
+    rnd = ref.random_limbs(0xDEADBEEF, 2000)
+    a_list += [rnd[2 * i] for i in range(1000)]
+    b_list += [rnd[2 * i + 1] for i in range(1000)]
+    mw_a = np.stack(a_list).astype(np.uint8)
+    mw_b = np.stack(b_list).astype(np.uint8)
+    lo = np.empty_like(mw_a)
+    hi = np.empty_like(mw_a)
+    prod = np.empty(len(mw_a), np.float64)
+    for i in range(len(mw_a)):
+        lo[i], hi[i] = ref.mul_wide(mw_a[i], mw_b[i])
+        prod[i] = ref.multiply_to_double(mw_a[i], mw_b[i])
+    out.update(mw_a=mw_a, mw_b=mw_b, mw_lo=lo, mw_hi=hi, mw_prod=prod)
+
+    rng = np.random.default_rng(81)
+    ft_trits = rng.integers(-1, 2, size=(256, 48), dtype=np.int8)
+    ft_trits[0] = 0
+    ft_trits[1] = 1
+    ft_trits[2] = -1
+    out["ft_trits"] = ft_trits
+    out["ft_bytes"] = np.stack([ref.limb_from_trits(t) for t in ft_trits])
+
+    cases = []
+    # the two known-answer cases of tests/python/test_bindings.py:16-38
+    cases.append(("zero", np.full((2, 1, 16), 13, np.uint8), np.full((1, 3, 16), 13, np.uint8),
+                  np.zeros((2, 3), np.float32), 2, 3, 48, 1.0, 0.0))
+    cases.append(("beta", np.full((2, 1, 16), 13, np.uint8), np.full((1, 3, 16), 13, np.uint8),
+                  np.full((2, 3), 2.0, np.float32), 2, 3, 48, 0.0, 0.5))
+    # full-range limbs: products overflow float32 -> +-inf (double sums stay finite)
+    M, N, KL = 9, 13, 3
+    cases.append(("full", rng.integers(0, 27, (M, KL, 16), dtype=np.uint8),
+                  rng.integers(0, 27, (KL, N, 16), dtype=np.uint8),
+                  rng.standard_normal((M, N)).astype(np.float32), M, N, KL * 48, 0.5, 1.0))
+    # low trytes only: finite, rounding-sensitive outputs
+    for nz, alpha, beta in ((3, 1.0, 0.0), (5, 0.37, -0.7), (8, -1.25, 2.0), (11, 3.0, 0.0)):
+        A = np.full((M, KL, 16), 13, np.uint8)
+        B = np.full((KL, N, 16), 13, np.uint8)
+        A[..., :nz] = rng.integers(0, 27, (M, KL, nz))
+        B[..., :nz] = rng.integers(0, 27, (KL, N, nz))
+        cases.append((f"low{nz}", A, B, rng.standard_normal((M, N)).astype(np.float32), M, N,
+                      KL * 48, alpha, beta))
+    # NaN in C with beta = 0 still propagates (accum = C * beta, gemm_cpu.cpp:37-38)
+    C = np.zeros((M, N), np.float32)
+    C[0, 0] = np.nan
+    A = np.full((M, 1, 16), 13, np.uint8)
+    A[..., 0] = rng.integers(0, 27, (M, 1))
+    B = np.full((1, N, 16), 13, np.uint8)
+    B[..., 0] = rng.integers(0, 27, (1, N))
+    cases.append(("nan", A, B, C, M, N, 48, 1.0, 0.0))
+    for i, (name, A, B, C, M_, N_, K_, al, be) in enumerate(cases):
+        out[f"g{i}_A"] = A
+        out[f"g{i}_B"] = B
+        out[f"g{i}_C"] = C
+        out[f"g{i}_shape"] = np.array([M_, N_, K_], np.int64)
+        out[f"g{i}_ab"] = np.array([al, be], np.float32)
+        out[f"g{i}_out"] = ref.gemm_ternary(A, B, C, M_, N_, K_, al, be)
+    out["g_names"] = np.array([c[0] for c in cases])
+
+    # one value per limb: T (N x K) trits and X (M x K) int8 -> sum_k X[m,k] T[n,k]
+    Mx, Nx, Kx = 5, 7, 37
+    T = rng.integers(-1, 2, (Nx, Kx), dtype=np.int8)
+    X = rng.integers(-128, 128, (Mx, Kx)).astype(np.int8)
+    A = np.stack([[ref.limb_from_value(int(v)) for v in row] for row in T])          # (N, K)
+    B = np.stack([[ref.limb_from_value(int(v)) for v in col] for col in X.T])        # (K, M)
+    emb = ref.gemm_ternary(A, B, np.zeros((Nx, Mx), np.float32), Nx, Mx, Kx * 48)
+    out.update(emb_T=T, emb_X=X, emb_out=emb)
+
+    path = os.path.join(HERE, "ref_vectors.npz")
+    np.savez_compressed(path, **out)
+    print(f"wrote {path} ({os.path.getsize(path)} bytes, SIMD path {ref.simd_path()})")
+
+
+if __name__ == "__main__":
+    main()

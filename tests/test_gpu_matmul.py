@@ -1,0 +1,209 @@
+"""K2 (GEMV, M <= 16) and K3 (GEMM) against the trit-dot oracle.
+
+Integer activations: bit-exact int32.  Float activations: elementwise
+|y - ref| <= rtol * (|alpha| sum_k |x_k t_k| + |beta c| + |bias|) + 1e-6 with
+rtol = 1e-3 for float32 and 1e-2 for bfloat16 activations (the north-star
+tolerances, relative to the magnitude of the summed terms).  Full-size configs
+are checked on a seeded sample of outputs plus linearity.
+"""
+
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from t81lib_amd import _lib, ops
+from conftest import fp_tolerance_ok
+
+pytestmark = pytest.mark.gpu
+
+RTOL = {torch.float32: 1e-3, torch.bfloat16: 1e-2}
+
+
+def announce(case: str) -> None:
+    sys.__stderr__.write(f"[gpu case] {case}\n")
+    sys.__stderr__.flush()
+
+
+def make_problem(M, N, K, dtype, seed, zeros=True):
+    g = torch.Generator("cpu").manual_seed(seed)
+    w = torch.randn((N, K), generator=g)            # effective weights W/0.02 ~ N(0,1)
+    if not zeros:
+        w = torch.sign(w) + (w == 0).float()
+    if dtype == torch.int8:
+        x = torch.randint(-128, 128, (M, K), generator=g, dtype=torch.int8)
+    else:
+        x = torch.randn((M, K), generator=g).to(dtype)
+    c = torch.randn((M, N), generator=g)
+    bias = torch.randn((N,), generator=g)
+    return w, x, c, bias
+
+
+def oracle_matmul(orc, x, packed_np, K, alpha, beta, c, bias, rows=None, cols=None):
+    """Reference y (float64) and tolerance scale on the selected tokens/rows."""
+    xs = x if rows is None else x[rows]
+    pk = packed_np if cols is None else packed_np[cols]
+    xd = xs.to(torch.float64).numpy()
+    acc = orc.trit_matmul_f64(xd, pk, K)
+    scale_acc = orc.trit_matmul_abs_f64(xd, pk, K)
+    cc = c.to(torch.float64).numpy()
+    bb = bias.to(torch.float64).numpy() if bias is not None else None
+    if rows is not None:
+        cc = cc[rows]
+    if cols is not None:
+        cc = cc[:, cols]
+        bb = bb[cols] if bb is not None else None
+    ref = alpha * acc + (beta * cc if beta != 0 else 0)
+    scale = abs(alpha) * scale_acc + (abs(beta) * np.abs(cc) if beta != 0 else 0)
+    if bb is not None:
+        ref = ref + bb
+        scale = scale + np.abs(bb)
+    return ref, scale
+
+
+def run(gpu, w, x, c, bias, K, alpha, beta, use_bias, kernel=None, thr=0.45):
+    packed = ops.quantize_pack(w.to(gpu), thr, _lib.THR_CPP)
+    cg = c.to(gpu).contiguous() if beta != 0 else None
+    out = ops.ternary_matmul(x.to(gpu), packed, K, alpha=alpha, beta=beta, c=cg,
+                             bias=bias.to(gpu) if use_bias else None, kernel=kernel)
+    torch.cuda.synchronize()
+    return packed.cpu().numpy(), out.cpu()
+
+
+SMALL = [
+    # M, N, K
+    (1, 64, 48), (1, 100, 1024), (4, 33, 1000), (16, 257, 3072), (3, 16, 4096), (16, 48, 97),
+    (1, 7, 1), (2, 5, 47),
+    (17, 64, 96), (64, 96, 1024), (100, 200, 300), (128, 512, 4096), (37, 45, 4097),
+]
+
+
+@pytest.mark.parametrize("M,N,K", SMALL)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_float_activations_vs_oracle(gpu, orc, M, N, K, dtype):
+    announce(f"matmul {dtype} M={M} N={N} K={K}")
+    w, x, c, bias = make_problem(M, N, K, dtype, seed=M * 1000 + N + K)
+    for alpha, beta, use_bias in ((1.0, 0.0, False), (0.5, 1.0, True), (-2.0, 0.25, False)):
+        packed, out = run(gpu, w, x, c, bias, K, alpha, beta, use_bias)
+        ref, scale = oracle_matmul(orc, x, packed, K, alpha, beta, c, bias if use_bias else None)
+        ok, worst, nbad = fp_tolerance_ok(out.numpy(), ref, scale, RTOL[dtype])
+        assert ok, f"alpha={alpha} beta={beta}: {nbad} outside, worst rel {worst:.3g}"
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 64, 48), (4, 33, 1000), (16, 257, 3072), (17, 64, 96),
+                                   (64, 96, 1024), (100, 200, 4097), (300, 128, 2048)])
+def test_int8_activations_bit_exact(gpu, orc, M, N, K):
+    announce(f"matmul int8 M={M} N={N} K={K}")
+    w, x, c, bias = make_problem(M, N, K, torch.int8, seed=7 + M + N + K)
+    packed, out = run(gpu, w, x, c, bias, K, 1.0, 0.0, False)
+    want = orc.trit_matmul_i64(x.numpy(), packed, K)
+    assert out.dtype == torch.int32
+    np.testing.assert_array_equal(out.numpy().astype(np.int64), want)
+    # beta = 1 accumulates into an int32 C exactly
+    c0 = torch.randint(-1000, 1000, (M, N), dtype=torch.int32)
+    packed_t = torch.from_numpy(packed).to(gpu)
+    out2 = ops.ternary_matmul(x.to(gpu), packed_t, K, beta=1.0, c=c0.to(gpu))
+    np.testing.assert_array_equal(out2.cpu().numpy().astype(np.int64), want + c0.numpy())
+
+
+@pytest.mark.parametrize("M", [1, 8, 16])
+def test_gemv_and_gemm_kernels_agree(gpu, orc, M):
+    """M <= 16 is valid for both kernels: each must match the oracle on its own."""
+    announce(f"K2 vs K3 M={M}")
+    w, x, c, bias = make_problem(M, 320, 2000, torch.bfloat16, seed=M)
+    for kernel in (2, 3):
+        packed, out = run(gpu, w, x, c, bias, 2000, 1.0, 0.0, True, kernel=kernel)
+        ref, scale = oracle_matmul(orc, x, packed, 2000, 1.0, 0.0, c, bias)
+        ok, worst, nbad = fp_tolerance_ok(out.numpy(), ref, scale, 1e-2)
+        assert ok, f"kernel {kernel}: {nbad} outside, worst {worst:.3g}"
+
+
+def test_unaligned_activations(gpu, orc):
+    announce("matmul unaligned x view")
+    M, N, K = 5, 70, 512
+    w, x, c, bias = make_problem(M, N, K, torch.bfloat16, seed=3)
+    packed = ops.quantize_pack(w.to(gpu), 0.45, _lib.THR_CPP)
+    big = torch.empty(M * K + 1, dtype=torch.bfloat16, device=gpu)
+    big[1:] = x.to(gpu).reshape(-1)
+    xv = big[1:].view(M, K)
+    for kernel in (2, 3):
+        out = ops.ternary_matmul(xv, packed, K, kernel=kernel).cpu()
+        ref, scale = oracle_matmul(orc, x, packed.cpu().numpy(), K, 1.0, 0.0, c, None)
+        ok, worst, nbad = fp_tolerance_ok(out.numpy(), ref, scale, 1e-2)
+        assert ok, f"kernel {kernel}"
+
+
+def test_empty_and_zero_k(gpu):
+    announce("matmul empty / K=0")
+    packed = torch.empty((4, 0, 16), dtype=torch.uint8, device=gpu)
+    out = ops.ternary_matmul(torch.empty((3, 0), device=gpu), packed, 0,
+                             bias=torch.arange(4.0, device=gpu))
+    np.testing.assert_array_equal(out.cpu().numpy(), np.tile(np.arange(4.0), (3, 1)))
+    out = ops.ternary_matmul(torch.empty((0, 48), device=gpu),
+                             torch.empty((4, 1, 16), dtype=torch.uint8, device=gpu), 48)
+    assert out.shape == (0, 4)
+
+
+# ------------------------------------------------------------ full-size configs --
+PHI3 = {"qkv": (3072, 9216), "o": (3072, 3072), "gate_up": (3072, 16384), "down": (8192, 3072)}
+
+
+@pytest.mark.parametrize("layer", list(PHI3))
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_config3_phi3_decode(gpu, orc, layer, M):
+    """Config 3: Phi-3-mini decode shapes, bf16 activations, fp32 bias, full oracle check."""
+    K, N = PHI3[layer]
+    announce(f"config3 {layer} M={M} K={K} N={N}")
+    w, x, c, bias = make_problem(M, N, K, torch.bfloat16, seed=sum(map(ord, layer)) + M)
+    packed, out = run(gpu, w, x, c, bias, K, 1.0, 0.0, True)
+    ref, scale = oracle_matmul(orc, x, packed, K, 1.0, 0.0, c, bias)
+    ok, worst, nbad = fp_tolerance_ok(out.numpy(), ref, scale, 1e-2)
+    assert ok, f"{nbad} outside, worst {worst:.3g}"
+
+
+LLAMA = {"qkv": (4096, 6144), "gate_up": (4096, 28672), "down": (14336, 4096)}
+
+
+@pytest.mark.parametrize("layer", list(LLAMA))
+@pytest.mark.parametrize("M", [512, 2048, 8192])
+def test_config4_llama_prefill_sampled(gpu, orc, layer, M):
+    """Config 4 at full size: a seeded sample of 48 tokens x 96 rows against the oracle for
+    (alpha, beta) = (1, 0) and (0.5, 1), plus linearity in the activations."""
+    K, N = LLAMA[layer]
+    announce(f"config4 {layer} M={M} K={K} N={N}")
+    g = torch.Generator("cpu").manual_seed(M + N)
+    w = torch.randn((N, K), generator=g)
+    x = torch.randn((M, K), generator=g).to(torch.bfloat16)
+    gg = torch.Generator(gpu).manual_seed(M + N)
+    cg_full = torch.randn((M, N), generator=gg, device=gpu)  # C is generated on the GPU
+    packed = ops.quantize_pack(w.to(gpu), 0.45, _lib.THR_CPP)
+    packed_np = packed.cpu().numpy()
+    rows = np.sort(np.random.default_rng(M).choice(M, 48, replace=False))
+    cols = np.sort(np.random.default_rng(N).choice(N, 96, replace=False))
+    rows_t = torch.from_numpy(rows).to(gpu)
+    cols_t = torch.from_numpy(cols).to(gpu)
+    c_sample = cg_full[rows_t][:, cols_t].cpu().double().numpy()
+    xd = x[torch.from_numpy(rows)].double().numpy()
+    acc = orc.trit_matmul_f64(xd, packed_np[cols], K)
+    acc_abs = orc.trit_matmul_abs_f64(xd, packed_np[cols], K)
+    xg = x.to(gpu)
+    for alpha, beta in ((1.0, 0.0), (0.5, 1.0)):
+        cg = cg_full.clone() if beta else None
+        out = ops.ternary_matmul(xg, packed, K, alpha=alpha, beta=beta, c=cg)
+        got = out[rows_t][:, cols_t].cpu().numpy()
+        ref = alpha * acc + beta * c_sample
+        scale = abs(alpha) * acc_abs + abs(beta) * np.abs(c_sample)
+        ok, worst, nbad = fp_tolerance_ok(got, ref, scale, 1e-2)
+        assert ok, f"alpha={alpha}: {nbad} outside, worst {worst:.3g}"
+        del cg, out
+    # linearity: W(x1 + x2) == W x1 + W x2 (exact inputs in fp32, tolerance on the sums)
+    x1 = x[:64].float().to(gpu)
+    x2 = torch.randn((64, K), generator=g).to(gpu)
+    y12 = ops.ternary_matmul(x1 + x2, packed, K, kernel=3)
+    y1 = ops.ternary_matmul(x1, packed, K, kernel=3)
+    y2 = ops.ternary_matmul(x2, packed, K, kernel=3)
+    scale = (x1.abs() + x2.abs()).sum(1, keepdim=True)
+    assert bool(((y12 - y1 - y2).abs() <= 2e-3 * scale + 1e-4).all())
