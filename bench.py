@@ -125,6 +125,43 @@ def cpu_reference_gemv(n: int, k: int, budget_s: float):
     }
 
 
+def run_sweep(torch, ops, lib, dev) -> list:
+    """Decode GEMV (config 3 + the Llama gate/down shapes) and prefill GEMM (config 4)."""
+    rows = []
+    decode = [("phi3.qkv", 3072, 9216), ("phi3.o", 3072, 3072), ("phi3.gate_up", 3072, 16384),
+              ("phi3.down", 8192, 3072), ("llama.gate", 4096, 14336), ("llama.down", 14336, 4096)]
+    for name, k, n in decode:
+        wbytes = 16 * n * ((k + 47) // 48)
+        copies = max(4, -(-2 * MALL_BYTES // wbytes) + 2)
+        wb = make_weights(torch, ops, lib, n, k, copies, dev, seed=3)
+        for m in (1, 4, 16):
+            x = torch.randn((m, k), device=dev).to(torch.bfloat16)
+            out = torch.empty((m, n), device=dev)
+            ms = time_graph(torch, lambda w: ops.ternary_matmul(x, w, k, c=out), wb, 512, 32)
+            gbs = gemv_bytes(m, n, k) / (ms * 1e-3) / 1e9
+            rows.append({"shape": name, "M": m, "K": k, "N": n, "us": ms * 1e3, "GBps": gbs,
+                         "frac_hbm": gbs / HBM_PEAK_GBPS})
+            log(f"gemv {name:14s} M={m:2d} {k:5d}->{n:5d}: {ms * 1e3:7.2f} us  {gbs:7.0f} GB/s")
+        del wb
+        torch.cuda.empty_cache()
+    prefill = [("llama.qkv", 4096, 6144), ("llama.gate_up", 4096, 28672),
+               ("llama.down", 14336, 4096)]
+    for name, k, n in prefill:
+        wb = make_weights(torch, ops, lib, n, k, 2, dev, seed=4)
+        for m in (512, 2048, 8192):
+            x = torch.randn((m, k), device=dev).to(torch.bfloat16)
+            out = torch.empty((m, n), device=dev)
+            ms = time_graph(torch, lambda w: ops.ternary_matmul(x, w, k, c=out), wb, 8, 2)
+            tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+            rows.append({"shape": name, "M": m, "K": k, "N": n, "us": ms * 1e3, "TFLOPs": tf,
+                         "frac_mfma": tf / BF16_PEAK_TFLOPS})
+            log(f"gemm {name:14s} M={m:5d} {k:5d}->{n:5d}: {ms * 1e3:8.1f} us  {tf:7.1f} TFLOP/s")
+            del x, out
+        del wb
+        torch.cuda.empty_cache()
+    return rows
+
+
 def cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -146,6 +183,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", choices=["gemv", "gemm", "pack"], default=None,
                     help="time one kernel only (for profiling runs)")
+    ap.add_argument("--sweep", action="store_true",
+                    help="also time the config-3/4 shapes and print a table on stderr")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the packed-ternary path is a single-GPU kernel set "
@@ -223,6 +262,8 @@ def main() -> int:
                        f"nproc {os.cpu_count()}"),
         }
 
+    sweep = run_sweep(torch, ops, _lib, dev) if args.sweep else None
+
     gbytes = gemv_bytes(M, N, K)
     line: dict = {
         "metric": METRIC,
@@ -263,6 +304,8 @@ def main() -> int:
         line["pack"] = {"workload": f"K1 quantize+pack {PR}x{PC} fp32", "us": pack_ms * 1e3,
                         "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBPS,
                                      "unit": "GB/s", "frac": gbs / HBM_PEAK_GBPS}}
+    if sweep:
+        line["sweep"] = sweep
     print(json.dumps(line), flush=True)
     return 0
 

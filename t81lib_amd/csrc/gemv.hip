@@ -29,201 +29,569 @@ namespace t81hip {
 
 namespace {
 
-constexpr int kWaves = 4;
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 // ---- activation fragments: 8 consecutive X[m, k0 .. k0+8) as bf16 (hi, lo) ----
+// Out-of-range lanes read from kZeroBlock / kPadLimb instead of selecting a value
+// after the load: the loads stay unconditional and nothing has to wait for them
+// until the data is used, so the compiler can count outstanding loads exactly
+// (s_waitcnt vmcnt(n) rather than vmcnt(0)) and the weight ring stays in flight.
+// Both are ordinary (read-only in practice) global arrays: a `const` qualifier would
+// place them in the constant address space and turn the selected loads into flat loads.
+__device__ uint32_t kZeroBlock[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+__device__ uint32_t kPadLimb[4] = {0x0D0D0D0Du, 0x0D0D0D0Du, 0x0D0D0D0Du, 0x0D0D0D0Du};
+
+// Raw bits of 8 activations: bf16 -> a (16 bytes); fp32 -> a, b (32 bytes); int8 -> a.xy.
+struct XRaw {
+    u32x4 a, b;
+};
+
+// kAligned: K % 8 == 0 and x 16-byte aligned (8-byte for int8), so a chunk of 8 is
+// either entirely inside K or entirely past it.
+template <int XT, bool kAligned>
+__device__ __forceinline__ XRaw load_x8_raw(const void *x, int64_t row_off, int64_t k0,
+                                            int64_t K, bool valid) {
+    constexpr int kElem = XT == kDtypeF32 ? 4 : (XT == kDtypeBF16 ? 2 : 1);
+    XRaw raw;
+    if constexpr (kAligned) {
+        const bool ok = valid && k0 < K;
+        const uint8_t *p = ok ? static_cast<const uint8_t *>(x) + (row_off + k0) * kElem
+                              : reinterpret_cast<const uint8_t *>(kZeroBlock);
+        if constexpr (XT == kDtypeBF16) {
+            raw.a = *reinterpret_cast<const u32x4 *>(p);
+        } else if constexpr (XT == kDtypeF32) {
+            raw.a = reinterpret_cast<const u32x4 *>(p)[0];
+            raw.b = reinterpret_cast<const u32x4 *>(p)[1];
+        } else {
+            const uint2 v = *reinterpret_cast<const uint2 *>(p);
+            raw.a = u32x4{v.x, v.y, 0u, 0u};
+        }
+    } else {
+        uint32_t e[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const bool ok = valid && (k0 + i < K);
+            const uint8_t *p = ok ? static_cast<const uint8_t *>(x) + (row_off + k0 + i) * kElem
+                                  : reinterpret_cast<const uint8_t *>(kZeroBlock);
+            if constexpr (XT == kDtypeBF16) e[i] = *reinterpret_cast<const uint16_t *>(p);
+            else if constexpr (XT == kDtypeF32) e[i] = *reinterpret_cast<const uint32_t *>(p);
+            else e[i] = *p;
+        }
+        if constexpr (XT == kDtypeBF16) {
+            raw.a = u32x4{e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16),
+                          e[6] | (e[7] << 16)};
+        } else if constexpr (XT == kDtypeF32) {
+            raw.a = u32x4{e[0], e[1], e[2], e[3]};
+            raw.b = u32x4{e[4], e[5], e[6], e[7]};
+        } else {
+            raw.a = u32x4{e[0] | (e[1] << 8) | (e[2] << 16) | (e[3] << 24),
+                          e[4] | (e[5] << 8) | (e[6] << 16) | (e[7] << 24), 0u, 0u};
+        }
+    }
+    return raw;
+}
+
+// bf16 operands of 8 raw activations: bf16 as is; fp32 as x = hi + lo with
+// hi = bf16(x), lo = bf16(x - hi), |x - hi - lo| <= 2^-18 |x|; int8 exactly.
+template <int XT>
+__device__ __forceinline__ void cvt_x8(const XRaw &raw, bf16x8 &hi, bf16x8 &lo) {
+    const u32x4 zero = {0u, 0u, 0u, 0u};
+    if constexpr (XT == kDtypeBF16) {
+        hi = __builtin_bit_cast(bf16x8, raw.a);
+        lo = __builtin_bit_cast(bf16x8, zero);
+    } else if constexpr (XT == kDtypeF32) {
+        const uint32_t v[8] = {raw.a[0], raw.a[1], raw.a[2], raw.a[3],
+                               raw.b[0], raw.b[1], raw.b[2], raw.b[3]};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float f = __uint_as_float(v[i]);
+            const __bf16 h = static_cast<__bf16>(f);
+            hi[i] = h;
+            lo[i] = static_cast<__bf16>(f - static_cast<float>(h));
+        }
+    } else {
+        const uint32_t w[2] = {raw.a[0], raw.a[1]};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int8_t b = static_cast<int8_t>((w[i / 4] >> (8 * (i % 4))) & 0xFFu);
+            hi[i] = static_cast<__bf16>(static_cast<float>(b));
+        }
+        lo = __builtin_bit_cast(bf16x8, zero);
+    }
+}
+
 template <int XT, bool kAligned>
 __device__ __forceinline__ void load_x8(const void *x, int64_t row_off, int64_t k0, int64_t K,
                                         bool valid, bf16x8 &hi, bf16x8 &lo) {
-    u32x4 zero = {0u, 0u, 0u, 0u};
-    hi = __builtin_bit_cast(bf16x8, zero);
-    lo = hi;
-    if (!valid) return;
-    if constexpr (XT == kDtypeBF16) {
-        const uint16_t *p = static_cast<const uint16_t *>(x) + row_off + k0;
-        if (kAligned && k0 + 8 <= K) {
-            hi = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(p));
-        } else {
-            uint16_t v[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = (k0 + i < K) ? p[i] : static_cast<uint16_t>(0);
-            hi = __builtin_bit_cast(bf16x8, v);
-        }
-    } else if constexpr (XT == kDtypeF32) {
-        const float *p = static_cast<const float *>(x) + row_off + k0;
-        float v[8];
-        if (kAligned && k0 + 8 <= K) {
-            const float4 a = reinterpret_cast<const float4 *>(p)[0];
-            const float4 b = reinterpret_cast<const float4 *>(p)[1];
-            v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-            v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = (k0 + i < K) ? p[i] : 0.0f;
-        }
-        // x = hi + lo with hi = bf16(x), lo = bf16(x - hi): |x - hi - lo| <= 2^-18 |x|
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const __bf16 h = static_cast<__bf16>(v[i]);
-            hi[i] = h;
-            lo[i] = static_cast<__bf16>(v[i] - static_cast<float>(h));
-        }
-    } else {  // int8: exact in bf16
-        const int8_t *p = static_cast<const int8_t *>(x) + row_off + k0;
-        int8_t v[8];
-        if (kAligned && k0 + 8 <= K) {
-            const uint2 raw = *reinterpret_cast<const uint2 *>(p);
-            __builtin_memcpy(v, &raw, 8);
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = (k0 + i < K) ? p[i] : static_cast<int8_t>(0);
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) hi[i] = static_cast<__bf16>(static_cast<float>(v[i]));
-    }
+    cvt_x8<XT>(load_x8_raw<XT, kAligned>(x, row_off, k0, K, valid), hi, lo);
 }
 
+// Limb `limb` of weight row `row`, or the padding limb (all-zero trits) past the
+// matrix or past the caller's limb range [.., limb_end).
 __device__ __forceinline__ u32x4 load_limb(const uint8_t *w, int64_t row, int64_t limb,
-                                           int64_t N, int64_t L) {
-    if (row < N && limb < L) {
-        const u32x4 *p = reinterpret_cast<const u32x4 *>(w + (row * L + limb) * kTrytes);
-        return __builtin_nontemporal_load(p);
-    }
-    const u32x4 pad = {0x0D0D0D0Du, 0x0D0D0D0Du, 0x0D0D0D0Du, 0x0D0D0D0Du};  // all-zero trits
-    return pad;
+                                           int64_t N, int64_t L, int64_t limb_end) {
+    const bool ok = row < N && limb < limb_end && limb < L;
+    const uint8_t *p = ok ? w + (row * L + limb) * kTrytes
+                          : reinterpret_cast<const uint8_t *>(kPadLimb);
+    return *reinterpret_cast<const u32x4 *>(p);
 }
 
-template <int XT, int G, bool kAligned>
-__global__ __launch_bounds__(256) void gemv_kernel(const void *__restrict__ x,
-                                                   const uint8_t *__restrict__ w,
-                                                   void *__restrict__ c, int M, int64_t N,
-                                                   int64_t K, int64_t L, float alpha, float beta,
-                                                   const float *__restrict__ bias) {
+// acc += A x B over the six 8-trit slots of one limb per lane-quarter; pairs[] holds
+// the limb decoded to 24 bf16 pairs (A), bh / bl the activations (lo plane for fp32).
+template <int XT>
+__device__ __forceinline__ floatx4 mfma_pairs(const uint32_t *pairs, const bf16x8 *bh,
+                                              const bf16x8 *bl, floatx4 acc) {
+#pragma unroll
+    for (int j = 0; j < 6; ++j) {
+        const u32x4 araw = {pairs[4 * j], pairs[4 * j + 1], pairs[4 * j + 2], pairs[4 * j + 3]};
+        const bf16x8 a = __builtin_bit_cast(bf16x8, araw);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bh[j], acc, 0, 0, 0);
+        if constexpr (XT == kDtypeF32)
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bl[j], acc, 0, 0, 0);
+    }
+    return acc;
+}
+
+// acc += T(16 rows, one limb per lane-quarter) x B  over the six 8-trit slots of the limb.
+template <int XT>
+__device__ __forceinline__ floatx4 mfma_limb(const uint8_t *lut, u32x4 wl, const bf16x8 *bh,
+                                             const bf16x8 *bl, floatx4 acc) {
+    uint32_t pairs[24];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) decode_dword(lut, wl[d], pairs + 6 * d);
+    return mfma_pairs<XT>(pairs, bh, bl, acc);
+}
+
+
+// Applies alpha / beta / bias to a finished 16x16 tile and stores it.  Lane (m, q)
+// holds rows n0 + 4q + i (i < 4) of token m.
+template <int XT>
+__device__ __forceinline__ void store_tile(floatx4 v, int lane, int M, int64_t N, int64_t n0,
+                                           void *c, float alpha, float beta, const float *bias) {
+    const int r = lane & 15;
+    const int q = lane >> 4;
+    if (r >= M) return;
+    const int64_t nb = n0 + 4 * q;
+    if constexpr (XT == kDtypeI8) {
+        int32_t *cr = static_cast<int32_t *>(c) + static_cast<int64_t>(r) * N;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (nb + i < N) {
+                int32_t y = static_cast<int32_t>(v[i]);
+                if (beta != 0.0f) y += cr[nb + i];
+                cr[nb + i] = y;
+            }
+        }
+    } else {
+        float *cr = static_cast<float *>(c) + static_cast<int64_t>(r) * N;
+        float y[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int64_t n = nb + i;
+            float t = alpha * v[i];
+            if (n < N) {
+                if (beta != 0.0f) t = t + beta * cr[n];
+                if (bias != nullptr) t = t + bias[n];
+            }
+            y[i] = t;
+        }
+        if (nb + 3 < N && (reinterpret_cast<uintptr_t>(cr + nb) & 15u) == 0) {
+            *reinterpret_cast<float4 *>(cr + nb) = make_float4(y[0], y[1], y[2], y[3]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (nb + i < N) cr[nb + i] = y[i];
+        }
+    }
+}
+
+// Sums the per-wave partial tiles of G 16-row groups and stores them.
+template <int XT, int G, int KS>
+__device__ __forceinline__ void reduce_store(floatx4 (&acc)[G], floatx4 *red, int wave, int lane,
+                                             int M, int64_t N, int64_t n0, void *c, float alpha,
+                                             float beta, const float *bias) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) red[(wave * G + g) * 64 + lane] = acc[g];
+    __syncthreads();
+    for (int g = wave; g < G; g += KS) {
+        floatx4 v = red[g * 64 + lane];
+#pragma unroll
+        for (int ww = 1; ww < KS; ++ww) v += red[(ww * G + g) * 64 + lane];
+        store_tile<XT>(v, lane, M, N, n0 + 16 * g, c, alpha, beta, bias);
+    }
+}
+
+// ---------------------------------------------------------------------------------
+// gemv_persistent_kernel: one workgroup of 8 waves per CU slot, looping over 16-row
+// groups (group blockIdx.x, then + gridDim.x, ...).  The activations are the same
+// for every group, so each wave stages its K range once:
+//   1. raw loads of its activation slice (issued before anything else),
+//   2. the first RING weight sub-blocks,
+//   3. zero fill + the slice -> LDS as bf16 (fp32: hi and lo planes; int8: exact),
+//      one barrier,
+// and then streams weight limbs through the ring continuously across groups: the
+// refill for slot f + RING is issued before slot f is decoded, whichever group it
+// belongs to, so the ring never drains at a group boundary.  At the end of each
+// group the 8 partial 16x16 tiles are summed through a double-buffered LDS tile by
+// one wave (rotating with the group) while the other waves go on streaming.
+// Wave w owns limbs [w*L/8, (w+1)*L/8); all waves run nsb = ceil(max range / 4)
+// sub-blocks per group so that the per-group barriers line up.
+//
+// Per-slot overhead is kept to a few instructions: each lane walks its weight limbs
+// with an incrementing pointer (invalid slots read the padding limb), and the B
+// operands are read unconditionally -- lanes of tokens >= M read a zero row, and
+// every staged row is zero past the wave's range.
+constexpr int kWavesP = 8;
+
+template <int XT>
+struct PersistLayout {
+    static constexpr int kPlanes = XT == kDtypeF32 ? 2 : 1;
+    static constexpr int kElem = XT == kDtypeF32 ? 4 : (XT == kDtypeBF16 ? 2 : 1);
+    static constexpr int kChunkVals = 16 / kElem;  // activations per 16-byte load
+};
+
+// Dynamic LDS: red [2][8][64] floatx4 | per wave: planes x (M + 1) rows x row bytes.
+__host__ __device__ inline int persist_row_bytes(int nsb) { return nsb * 4 * kTrits * 2 + 16; }
+constexpr int kPersistRedBytes = 2 * kWavesP * 64 * 16;
+__host__ __device__ inline int persist_wave_bytes(int M, int nsb, int planes) {
+    return planes * (M + 1) * persist_row_bytes(nsb);
+}
+__host__ __device__ inline int persist_lds_bytes(int M, int nsb, int planes) {
+    return kPersistRedBytes + kWavesP * persist_wave_bytes(M, nsb, planes);
+}
+
+template <int XT, int RING, int SU>
+__global__ __launch_bounds__(64 * kWavesP) void gemv_persistent_kernel(
+    const void *__restrict__ x, const uint8_t *__restrict__ w, void *__restrict__ c, int M,
+    int64_t N, int64_t K, int64_t L, int nsb, int x_aligned, float alpha, float beta,
+    const float *__restrict__ bias) {
+    using LY = PersistLayout<XT>;
+    constexpr int kElem = LY::kElem;
+    constexpr int kChunkVals = LY::kChunkVals;
     __shared__ __attribute__((aligned(16))) uint8_t lut[kLutBytes];
-    __shared__ __attribute__((aligned(16))) floatx4 red[kWaves][G][64];
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    floatx4 *red = reinterpret_cast<floatx4 *>(smem);
+    const int row = persist_row_bytes(nsb);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int r = lane & 15;   // A row within a 16-row group / B column (token)
-    const int q = lane >> 4;   // k-quarter
-    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * (16 * G);
-    const int64_t S = (L + 3) / 4;  // 4-limb sub-blocks
+    const int r = lane & 15;
+    const int q = lane >> 4;
+    const int64_t groups = (N + 15) / 16;
+    const int64_t lb = (wave * L) / kWavesP;
+    const int64_t le = ((wave + 1) * L) / kWavesP;
+    const int lw = static_cast<int>(le - lb);
+    const int plane_bytes = (M + 1) * row;
+    uint8_t *xw = smem + kPersistRedBytes + wave * persist_wave_bytes(M, nsb, LY::kPlanes);
+    const int64_t my_groups =
+        groups > blockIdx.x ? (groups - blockIdx.x + gridDim.x - 1) / gridDim.x : 0;
+    const int64_t total_f = my_groups * nsb;
 
+    // 1. raw activation loads: 16-byte chunks of the wave's slice, natural order
+    const int chunks_row = (lw * kTrits + kChunkVals - 1) / kChunkVals;
+    const int chunks = M * chunks_row;
+    u32x4 sraw[SU];
+#pragma unroll
+    for (int i = 0; i < SU; ++i) {
+        const int u = lane + 64 * i;
+        const bool ok = u < chunks;
+        const int uu = ok ? u : 0;
+        const int m = chunks_row > 0 ? uu / chunks_row : 0;
+        const int cu = uu - m * chunks_row;
+        const int64_t k0 = lb * kTrits + static_cast<int64_t>(cu) * kChunkVals;
+        if (x_aligned) {  // K % kChunkVals == 0: a chunk is all inside K or all past it
+            const bool in = ok && k0 < K;
+            const uint8_t *p = in ? static_cast<const uint8_t *>(x) + (m * K + k0) * kElem
+                                  : reinterpret_cast<const uint8_t *>(kZeroBlock);
+            sraw[i] = *reinterpret_cast<const u32x4 *>(p);
+        } else {
+            uint32_t e[kChunkVals];
+#pragma unroll
+            for (int v = 0; v < kChunkVals; ++v) {
+                const bool in = ok && k0 + v < K;
+                const uint8_t *p = in ? static_cast<const uint8_t *>(x) + (m * K + k0 + v) * kElem
+                                      : reinterpret_cast<const uint8_t *>(kZeroBlock);
+                if constexpr (kElem == 4) e[v] = *reinterpret_cast<const uint32_t *>(p);
+                else if constexpr (kElem == 2) e[v] = *reinterpret_cast<const uint16_t *>(p);
+                else e[v] = *p;
+            }
+            uint32_t wd[4];
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                if constexpr (kElem == 4) wd[d] = e[d];
+                else if constexpr (kElem == 2) wd[d] = e[2 * d] | (e[2 * d + 1] << 16);
+                else wd[d] = e[4 * d] | (e[4 * d + 1] << 8) | (e[4 * d + 2] << 16) | (e[4 * d + 3] << 24);
+            }
+            sraw[i] = u32x4{wd[0], wd[1], wd[2], wd[3]};
+        }
+    }
+
+    // 2. the weight ring.  Each lane walks its limbs with a pointer: +4 limbs per
+    //    sub-block, + one group stride per group.  A slot is valid for this lane when
+    //    its limb lies in the wave's range (sb < sb_lim) and its row exists.
+    const int sb_lim = (lw - q + 3) / 4;
+    const int64_t group_step = static_cast<int64_t>(gridDim.x) * 16 * L * kTrytes;
+    const uint8_t *pad = reinterpret_cast<const uint8_t *>(kPadLimb);
+    int64_t rrow = static_cast<int64_t>(blockIdx.x) * 16 + r;  // row of the next refill
+    const uint8_t *rptr = w + (rrow * L + lb + q) * kTrytes;
+    int rsb = 0;
+    auto refill = [&]() -> u32x4 {
+        const bool ok = rsb < sb_lim && rrow < N;
+        const u32x4 v = *reinterpret_cast<const u32x4 *>(ok ? rptr : pad);
+        rptr += 4 * kTrytes;
+        if (++rsb == nsb) {
+            rsb = 0;
+            rptr += group_step - static_cast<int64_t>(nsb) * 4 * kTrytes;
+            rrow += static_cast<int64_t>(gridDim.x) * 16;
+        }
+        return v;
+    };
+    u32x4 ring[RING];
+#pragma unroll
+    for (int i = 0; i < RING; ++i) ring[i] = refill();
+
+    // 3. decode table, zero fill, activations -> LDS (bf16 planes); one barrier
+    lut_fill(lut, tid, 64 * kWavesP);
+    {
+        const int wave_bytes = persist_wave_bytes(M, nsb, LY::kPlanes);
+        const u32x4 z = {0u, 0u, 0u, 0u};
+        for (int b = 16 * lane; b < wave_bytes; b += 64 * 16)
+            *reinterpret_cast<u32x4 *>(xw + b) = z;
+    }
+#pragma unroll
+    for (int i = 0; i < SU; ++i) {
+        const int u = lane + 64 * i;
+        if (u < chunks) {
+            const int m = u / chunks_row;
+            const int cu = u - m * chunks_row;
+            uint8_t *dst = xw + m * row + cu * kChunkVals * 2;
+            if constexpr (XT == kDtypeBF16) {
+                *reinterpret_cast<u32x4 *>(dst) = sraw[i];
+            } else if constexpr (XT == kDtypeF32) {
+                // x = hi + lo, hi = bf16(x), lo = bf16(x - hi): |x - hi - lo| <= 2^-18 |x|
+                uint32_t h[4], l[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float f = __uint_as_float(sraw[i][e]);
+                    h[e] = bf16_bits_rne(f);
+                    l[e] = bf16_bits_rne(f - bf16_bits_to_float(h[e]));
+                }
+                *reinterpret_cast<uint2 *>(dst) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+                *reinterpret_cast<uint2 *>(dst + plane_bytes) =
+                    make_uint2(l[0] | (l[1] << 16), l[2] | (l[3] << 16));
+            } else {  // int8 -> bf16, exact
+                uint32_t o[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const uint32_t wd0 = sraw[i][e / 2];
+                    const int8_t b0 = static_cast<int8_t>((wd0 >> (16 * (e % 2))) & 0xFFu);
+                    const int8_t b1 = static_cast<int8_t>((wd0 >> (16 * (e % 2) + 8)) & 0xFFu);
+                    o[e] = bf16_bits_rne(static_cast<float>(b0)) |
+                           (bf16_bits_rne(static_cast<float>(b1)) << 16);
+                }
+                reinterpret_cast<u32x4 *>(dst)[0] = u32x4{o[0], o[1], o[2], o[3]};
+                reinterpret_cast<u32x4 *>(dst)[1] = u32x4{o[4], o[5], o[6], o[7]};
+            }
+        }
+    }
+    __syncthreads();
+
+    // 4. stream the groups.  Lane (r, q) reads its B operands at xb + sb * 4 limbs:
+    //    row r (or the zero row M), limb q of the sub-block.
+    const uint8_t *xb = xw + (r < M ? r : M) * row + q * kTrits * 2;
+    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+    int64_t gi = 0;
+    int sb = 0;
+    for (int64_t f0 = 0; f0 < total_f; f0 += RING) {
+#pragma unroll
+        for (int i = 0; i < RING; ++i) {
+            // decode slot i before its refill is issued: the refill then reuses the
+            // slot's registers and the ring needs no copies across iterations
+            uint32_t pairs[24];
+#pragma unroll
+            for (int d = 0; d < 4; ++d) decode_dword(lut, ring[i][d], pairs + 6 * d);
+            __builtin_amdgcn_sched_barrier(0);
+            ring[i] = refill();  // unconditional: past the end it reads the padding limb
+            if (f0 + i < total_f) {
+                const uint8_t *src = xb + sb * (4 * kTrits * 2);
+                bf16x8 bh[6], bl[6];
+#pragma unroll
+                for (int j = 0; j < 6; ++j) {
+                    bh[j] = *reinterpret_cast<const bf16x8 *>(src + 16 * j);
+                    if constexpr (XT == kDtypeF32)
+                        bl[j] = *reinterpret_cast<const bf16x8 *>(src + plane_bytes + 16 * j);
+                }
+                acc = mfma_pairs<XT>(pairs, bh, bl, acc);
+                if (++sb == nsb) {  // group gi complete: publish, reduce, store
+                    sb = 0;
+                    floatx4 *buf = red + (gi & 1) * kWavesP * 64;
+                    buf[wave * 64 + lane] = acc;
+                    acc = floatx4{0.f, 0.f, 0.f, 0.f};
+                    __syncthreads();
+                    // the reducing wave rotates: its bias / C loads (if any) drain its own
+                    // ring, so the stall is spread over the waves
+                    if (wave == static_cast<int>(gi % kWavesP)) {
+                        floatx4 v = buf[lane];
+#pragma unroll
+                        for (int ww = 1; ww < kWavesP; ++ww) v += buf[ww * 64 + lane];
+                        const int64_t grp = blockIdx.x + gi * gridDim.x;
+                        store_tile<XT>(v, lane, M, N, grp * 16, c, alpha, beta, bias);
+                    }
+                    ++gi;
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------
+// gemv_stream_kernel: for M * K too large to stage, activations come straight from
+// global memory, fetched one sub-block ahead and issued before the weight prefetch
+// (so waiting for them never drains the weight loads).  Waves split K round-robin.
+template <int XT, int G, bool kAligned>
+__global__ __launch_bounds__(256) void gemv_stream_kernel(const void *__restrict__ x,
+                                                          const uint8_t *__restrict__ w,
+                                                          void *__restrict__ c, int M, int64_t N,
+                                                          int64_t K, int64_t L, float alpha,
+                                                          float beta,
+                                                          const float *__restrict__ bias) {
+    constexpr int KS = 4;
+    __shared__ __attribute__((aligned(16))) uint8_t lut[kLutBytes];
+    __shared__ __attribute__((aligned(16))) floatx4 red[KS * G * 64];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int r = lane & 15;
+    const int q = lane >> 4;
+    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * (16 * G);
+    const int64_t S = (L + 3) / 4;
+
+    const bool xvalid = r < M;
+    const int64_t xrow = static_cast<int64_t>(r) * K;
+    bf16x8 bh[6], bl[6], nh[6], nl[6];
+    int64_t s = wave;
+#pragma unroll
+    for (int j = 0; j < 6; ++j)
+        load_x8<XT, kAligned>(x, xrow, (4 * s + q) * kTrits + 8 * j, K,
+                              xvalid && (4 * s + q) < L, bh[j], bl[j]);
+    u32x4 wcur[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) wcur[g] = load_limb(w, n0 + 16 * g + r, 4 * s + q, N, L, L);
     lut_init(lut, tid, 256);
 
     floatx4 acc[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) acc[g] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    const bool xvalid = r < M;
-    const int64_t xrow = static_cast<int64_t>(r) * K;
-
-    int64_t s = wave;
-    u32x4 wcur[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) wcur[g] = load_limb(w, n0 + 16 * g + r, 4 * s + q, N, L);
-
-    for (; s < S; s += kWaves) {
-        // prefetch the next sub-block's weights while this one is decoded
-        u32x4 wnext[G];
-        const int64_t sn = s + kWaves;
-#pragma unroll
-        for (int g = 0; g < G; ++g) wnext[g] = load_limb(w, n0 + 16 * g + r, 4 * sn + q, N, L);
-
-        const int64_t kbase = (4 * s + q) * kTrits;
-        bf16x8 bh[6], bl[6];
+    for (; s < S; s += KS) {
+        const int64_t sn = s + KS;
 #pragma unroll
         for (int j = 0; j < 6; ++j)
-            load_x8<XT, kAligned>(x, xrow, kbase + 8 * j, K, xvalid && (4 * s + q) < L, bh[j],
-                                  bl[j]);
-
+            load_x8<XT, kAligned>(x, xrow, (4 * sn + q) * kTrits + 8 * j, K,
+                                  xvalid && sn < S && (4 * sn + q) < L, nh[j], nl[j]);
+        u32x4 wnext[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) wnext[g] = load_limb(w, n0 + 16 * g + r, 4 * sn + q, N, L, L);
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-            uint32_t pairs[24];
-#pragma unroll
-            for (int d = 0; d < 4; ++d) decode_dword(lut, wcur[g][d], pairs + 6 * d);
-#pragma unroll
-            for (int j = 0; j < 6; ++j) {
-                const u32x4 araw = {pairs[4 * j], pairs[4 * j + 1], pairs[4 * j + 2],
-                                    pairs[4 * j + 3]};
-                const bf16x8 a = __builtin_bit_cast(bf16x8, araw);
-                acc[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bh[j], acc[g], 0, 0, 0);
-                if constexpr (XT == kDtypeF32)
-                    acc[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bl[j], acc[g], 0, 0, 0);
-            }
+            acc[g] = mfma_limb<XT>(lut, wcur[g], bh, bl, acc[g]);
             wcur[g] = wnext[g];
         }
-    }
-
-    // ---- split-K reduction over the 4 waves, then the epilogue ----
 #pragma unroll
-    for (int g = 0; g < G; ++g) red[wave][g][lane] = acc[g];
-    __syncthreads();
-
-    for (int g = wave; g < G; g += kWaves) {
-        floatx4 v = red[0][g][lane];
-#pragma unroll
-        for (int ww = 1; ww < kWaves; ++ww) v += red[ww][g][lane];
-        if (r >= M) continue;
-        const int64_t nb = n0 + 16 * g + 4 * q;
-        if constexpr (XT == kDtypeI8) {
-            int32_t *cr = static_cast<int32_t *>(c) + static_cast<int64_t>(r) * N;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                if (nb + i < N) {
-                    int32_t y = static_cast<int32_t>(v[i]);
-                    if (beta != 0.0f) y += cr[nb + i];
-                    cr[nb + i] = y;
-                }
-            }
-        } else {
-            float *cr = static_cast<float *>(c) + static_cast<int64_t>(r) * N;
-            float y[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int64_t n = nb + i;
-                float t = alpha * v[i];
-                if (n < N) {
-                    if (beta != 0.0f) t = t + beta * cr[n];
-                    if (bias != nullptr) t = t + bias[n];
-                }
-                y[i] = t;
-            }
-            if (nb + 3 < N && (reinterpret_cast<uintptr_t>(cr + nb) & 15u) == 0) {
-                *reinterpret_cast<float4 *>(cr + nb) = make_float4(y[0], y[1], y[2], y[3]);
-            } else {
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    if (nb + i < N) cr[nb + i] = y[i];
-            }
+        for (int j = 0; j < 6; ++j) {
+            bh[j] = nh[j];
+            bl[j] = nl[j];
         }
     }
+    reduce_store<XT, G, KS>(acc, red, wave, lane, M, N, n0, c, alpha, beta, bias);
 }
 
-template <int XT, int G>
-hipError_t launch_gemv_t(const void *x, const uint8_t *w, void *c, int m, int64_t n, int64_t k,
-                         float alpha, float beta, const float *bias, hipStream_t s) {
-    const int64_t L = (k + kTrits - 1) / kTrits;
+template <int XT, int G, bool kAligned>
+hipError_t launch_stream(const void *x, const uint8_t *w, void *c, int m, int64_t n, int64_t k,
+                         int64_t L, float alpha, float beta, const float *bias, hipStream_t s) {
     const int64_t blocks = (n + 16 * G - 1) / (16 * G);
-    const int elem = XT == kDtypeF32 ? 4 : (XT == kDtypeBF16 ? 2 : 1);
-    const bool aligned = (k % 8 == 0) && (reinterpret_cast<uintptr_t>(x) % (8 * elem) == 0);
-    if (aligned)
-        gemv_kernel<XT, G, true><<<dim3(blocks), dim3(256), 0, s>>>(x, w, c, m, n, k, L, alpha,
-                                                                    beta, bias);
-    else
-        gemv_kernel<XT, G, false><<<dim3(blocks), dim3(256), 0, s>>>(x, w, c, m, n, k, L, alpha,
-                                                                     beta, bias);
+    gemv_stream_kernel<XT, G, kAligned><<<dim3(blocks), dim3(256), 0, s>>>(x, w, c, m, n, k, L,
+                                                                          alpha, beta, bias);
     return hipGetLastError();
 }
 
+int cu_count() {
+    static int cus = 0;
+    if (cus == 0) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
+            cus = v;
+        if (cus <= 0) cus = 256;
+    }
+    return cus;
+}
+
+// Resident workgroups per CU for a persistent instantiation at `lds` bytes (cached;
+// the first call also raises the dynamic-LDS limit when more than 64 KiB is asked).
+template <int XT, int RING, int SU>
+int persist_occupancy(size_t lds) {
+    static size_t cached_lds = 0;
+    static int cached = 0;
+    if (cached > 0 && cached_lds == lds) return cached;
+    auto fn = reinterpret_cast<const void *>(&gemv_persistent_kernel<XT, RING, SU>);
+    if (lds > 64 * 1024)
+        (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  static_cast<int>(lds));
+    int nb = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fn, 64 * kWavesP, lds) != hipSuccess ||
+        nb <= 0)
+        nb = 1;
+    cached_lds = lds;
+    cached = nb;
+    return nb;
+}
+
+template <int XT, int RING, int SU>
+hipError_t launch_persist(const void *x, const uint8_t *w, void *c, int m, int64_t n, int64_t k,
+                          int64_t L, int nsb, size_t lds, bool aligned, float alpha,
+                          float beta, const float *bias, hipStream_t s) {
+    const int64_t groups = (n + 15) / 16;
+    const int occ = persist_occupancy<XT, RING, SU>(lds);
+    const int64_t grid = groups < static_cast<int64_t>(cu_count()) * occ
+                             ? groups
+                             : static_cast<int64_t>(cu_count()) * occ;
+    gemv_persistent_kernel<XT, RING, SU><<<dim3(grid), dim3(64 * kWavesP), lds, s>>>(
+        x, w, c, m, n, k, L, nsb, aligned ? 1 : 0, alpha, beta, bias);
+    return hipGetLastError();
+}
+
+constexpr size_t kMaxPersistLds = 160 * 1024;
+
 template <int XT>
-hipError_t launch_gemv_g(const void *x, const uint8_t *w, void *c, int m, int64_t n, int64_t k,
+hipError_t launch_gemv_x(const void *x, const uint8_t *w, void *c, int m, int64_t n, int64_t k,
                          float alpha, float beta, const float *bias, hipStream_t s) {
-    // more rows per wave amortise the activation loads once several tokens are live
-    if (m <= 4) return launch_gemv_t<XT, 1>(x, w, c, m, n, k, alpha, beta, bias, s);
-    return launch_gemv_t<XT, 2>(x, w, c, m, n, k, alpha, beta, bias, s);
+    using LY = PersistLayout<XT>;
+    const int elem = LY::kElem;
+    const int64_t L = (k + kTrits - 1) / kTrits;
+    const bool aligned = (k % LY::kChunkVals == 0) && (reinterpret_cast<uintptr_t>(x) % 16 == 0);
+    const bool aligned8 = (k % 8 == 0) && (reinterpret_cast<uintptr_t>(x) % (8 * elem) == 0);
+    if (L > 0) {
+        const int lw_max = static_cast<int>((L + kWavesP - 1) / kWavesP);
+        const int nsb = (lw_max + 3) / 4;
+        const int64_t chunks = m * ((lw_max * kTrits + LY::kChunkVals - 1) / LY::kChunkVals);
+        const int su = static_cast<int>((chunks + 63) / 64);
+        const size_t lds = static_cast<size_t>(persist_lds_bytes(m, nsb, LY::kPlanes));
+        if (su <= 4 && lds <= kMaxPersistLds) {
+            if (su <= 1)
+                return launch_persist<XT, 8, 1>(x, w, c, m, n, k, L, nsb, lds, aligned, alpha,
+                                                beta, bias, s);
+            if (su <= 2)
+                return launch_persist<XT, 8, 2>(x, w, c, m, n, k, L, nsb, lds, aligned, alpha,
+                                                beta, bias, s);
+            return launch_persist<XT, 8, 4>(x, w, c, m, n, k, L, nsb, lds, aligned, alpha, beta,
+                                            bias, s);
+        }
+    }
+    if (aligned8) return launch_stream<XT, 2, true>(x, w, c, m, n, k, L, alpha, beta, bias, s);
+    return launch_stream<XT, 2, false>(x, w, c, m, n, k, L, alpha, beta, bias, s);
 }
 
 }  // namespace
@@ -232,9 +600,9 @@ hipError_t launch_gemv(const void *x, int x_dtype, const uint8_t *w, void *c, in
                        int64_t k, float alpha, float beta, const float *bias, hipStream_t s) {
     if (m == 0 || n == 0) return hipSuccess;
     switch (x_dtype) {
-        case kDtypeBF16: return launch_gemv_g<kDtypeBF16>(x, w, c, m, n, k, alpha, beta, bias, s);
-        case kDtypeF32: return launch_gemv_g<kDtypeF32>(x, w, c, m, n, k, alpha, beta, bias, s);
-        default: return launch_gemv_g<kDtypeI8>(x, w, c, m, n, k, alpha, beta, bias, s);
+        case kDtypeBF16: return launch_gemv_x<kDtypeBF16>(x, w, c, m, n, k, alpha, beta, bias, s);
+        case kDtypeF32: return launch_gemv_x<kDtypeF32>(x, w, c, m, n, k, alpha, beta, bias, s);
+        default: return launch_gemv_x<kDtypeI8>(x, w, c, m, n, k, alpha, beta, bias, s);
     }
 }
 

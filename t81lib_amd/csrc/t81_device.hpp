@@ -38,19 +38,31 @@ constexpr int kLutE = 0;                    // byte offset of E
 constexpr int kLutF = 256;                  // byte offset of F
 constexpr int kLutBytes = 256 + 256 + 16;   // F start + max field + one entry
 
-__device__ __forceinline__ void lut_init(uint8_t *lds, int tid, int nthreads) {
-    uint32_t *w = reinterpret_cast<uint32_t *>(lds);
-    for (int i = tid; i < kLutBytes / 4; i += nthreads) w[i] = 0u;
-    __syncthreads();
-    for (int u = tid; u < 27; u += nthreads) {
-        const uint32_t b0 = bf16_bits_of_trit(trit_of(u, 0));
-        const uint32_t b1 = bf16_bits_of_trit(trit_of(u, 1));
-        const uint32_t b2 = bf16_bits_of_trit(trit_of(u, 2));
-        w[(kLutE + 8 * u) / 4 + 0] = b0 | (b1 << 16);
-        w[(kLutE + 8 * u) / 4 + 1] = b2;
-        w[(kLutF + 8 * u) / 4 + 0] = b0 << 16;
-        w[(kLutF + 8 * u) / 4 + 1] = b1 | (b2 << 16);
+// Writes the E/F tables (and the zero fill around them) with one pass: thread i
+// owns word i, so no barrier is needed between fill and entries.  The caller
+// issues the __syncthreads() that publishes the table.
+__device__ __forceinline__ void lut_fill(uint8_t *lds, int tid, int nthreads) {
+    uint32_t *words = reinterpret_cast<uint32_t *>(lds);
+    for (int i = tid; i < kLutBytes / 4; i += nthreads) {
+        const int off = 4 * i;
+        uint32_t v = 0u;
+        const bool in_e = off < kLutF;
+        const int rel = in_e ? off - kLutE : off - kLutF;
+        const int u = rel / 8;
+        const int part = (rel % 8) / 4;
+        if (rel >= 0 && u < 27 && off < kLutF + 8 * 27) {
+            const uint32_t b0 = bf16_bits_of_trit(trit_of(u, 0));
+            const uint32_t b1 = bf16_bits_of_trit(trit_of(u, 1));
+            const uint32_t b2 = bf16_bits_of_trit(trit_of(u, 2));
+            if (in_e) v = part == 0 ? (b0 | (b1 << 16)) : b2;
+            else v = part == 0 ? (b0 << 16) : (b1 | (b2 << 16));
+        }
+        words[i] = v;
     }
+}
+
+__device__ __forceinline__ void lut_init(uint8_t *lds, int tid, int nthreads) {
+    lut_fill(lds, tid, nthreads);
     __syncthreads();
 }
 
