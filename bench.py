@@ -181,8 +181,10 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=12.0,
                     help="seconds of single-core reference CPU work for the baseline")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["gemv", "gemm", "pack"], default=None,
-                    help="time one kernel only (for profiling runs)")
+    ap.add_argument("--only", choices=["gemv", "gemm", "pack", "copy"], default=None,
+                    help="time one kernel only (for profiling runs); 'copy' times a plain "
+                         "elementwise copy of the GEMV weight size, the calibration kernel "
+                         "for the HBM byte counters")
     ap.add_argument("--sweep", action="store_true",
                     help="also time the config-3/4 shapes and print a table on stderr")
     args = ap.parse_args()
@@ -247,6 +249,23 @@ def main() -> int:
         torch.cuda.empty_cache()
         log(f"pack {pack_ms * 1e3:.2f} us/call")
 
+    # ------------------------------------------------- copy (counter calibration) --
+    copy = None
+    if args.only == "copy":
+        elems = wbytes // 4
+        ccopies = max(4, -(-2 * MALL_BYTES // wbytes) + 2)
+        csrc = [torch.randn(elems, device=dev) for _ in range(ccopies)]
+        cdst = torch.empty(elems, device=dev)
+        claunch = lambda s: torch.neg(s, out=cdst)  # noqa: E731
+        copy_ms = time_graph(torch, claunch, csrc, args.steps, args.warmup)
+        del csrc
+        torch.cuda.empty_cache()
+        copy = {"workload": f"torch.neg fp32, {elems} elements: reads and writes "
+                            f"{4 * elems} bytes per launch",
+                "bytes_read": 4 * elems, "bytes_written": 4 * elems, "us": copy_ms * 1e3,
+                "GBps": 8 * elems / (copy_ms * 1e-3) / 1e9}
+        log(f"copy {copy_ms * 1e3:.2f} us/call, {copy['GBps']:.0f} GB/s read+write")
+
     # ------------------------------------------------------------ CPU baseline --
     cpu = None
     if not args.no_cpu and args.only is None:
@@ -304,6 +323,8 @@ def main() -> int:
         line["pack"] = {"workload": f"K1 quantize+pack {PR}x{PC} fp32", "us": pack_ms * 1e3,
                         "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBPS,
                                      "unit": "GB/s", "frac": gbs / HBM_PEAK_GBPS}}
+    if copy:
+        line["copy"] = copy
     if sweep:
         line["sweep"] = sweep
     print(json.dumps(line), flush=True)

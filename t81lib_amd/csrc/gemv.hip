@@ -222,199 +222,192 @@ __device__ __forceinline__ void reduce_store(floatx4 (&acc)[G], floatx4 *red, in
 }
 
 // ---------------------------------------------------------------------------------
-// gemv_persistent_kernel: one workgroup of 8 waves per CU slot, looping over 16-row
-// groups (group blockIdx.x, then + gridDim.x, ...).  The activations are the same
-// for every group, so each wave stages its K range once:
-//   1. raw loads of its activation slice (issued before anything else),
-//   2. the first RING weight sub-blocks,
-//   3. zero fill + the slice -> LDS as bf16 (fp32: hi and lo planes; int8: exact),
-//      one barrier,
-// and then streams weight limbs through the ring continuously across groups: the
-// refill for slot f + RING is issued before slot f is decoded, whichever group it
-// belongs to, so the ring never drains at a group boundary.  At the end of each
-// group the 8 partial 16x16 tiles are summed through a double-buffered LDS tile by
-// one wave (rotating with the group) while the other waves go on streaming.
-// Wave w owns limbs [w*L/8, (w+1)*L/8); all waves run nsb = ceil(max range / 4)
-// sub-blocks per group so that the per-group barriers line up.
+// gemv_group_kernel: one workgroup of W waves per 16-row group (blockIdx.x).
 //
-// Per-slot overhead is kept to a few instructions: each lane walks its weight limbs
-// with an incrementing pointer (invalid slots read the padding limb), and the B
-// operands are read unconditionally -- lanes of tokens >= M read a zero row, and
-// every staged row is zero past the wave's range.
-constexpr int kWavesP = 8;
-
+//   1. All threads load the activations (M rows, K padded with zeros to whole
+//      4-limb sub-blocks) with 16-byte loads; each wave then issues the first RING
+//      weight sub-blocks of its K range before waiting for any of them.
+//   2. The activations go to LDS as bf16 (fp32: hi and lo planes; int8: exact),
+//      plus one all-zero row that lanes of tokens >= M read; one barrier.
+//   3. Each wave streams its sub-blocks [s0, s1) through the ring: decode slot i
+//      from the LDS tables, refill slot i with the sub-block RING ahead, six MFMAs
+//      against the staged activations.
+//   4. The W partial tiles are summed through LDS, one output element per thread,
+//      always in wave order (deterministic results).
+//
+// Weights are read through a buffer resource whose base is the group's first row:
+// each lane's offset is fixed, and the hardware range check returns zeros past the
+// end of the matrix (rows >= N of the last group).  A refill past the wave's range
+// uses an offset >= 2^31, also out of range, so it reads nothing.  Lanes whose limb
+// index runs past L at the end of a row read the next row's first limbs: the
+// activations staged for those k are zero, and every byte decodes to a finite value
+// (0 or +-1), so they add exactly nothing.
 template <int XT>
-struct PersistLayout {
+struct GroupLayout {
     static constexpr int kPlanes = XT == kDtypeF32 ? 2 : 1;
     static constexpr int kElem = XT == kDtypeF32 ? 4 : (XT == kDtypeBF16 ? 2 : 1);
-    static constexpr int kChunkVals = 16 / kElem;  // activations per 16-byte load
+    static constexpr int kChunkVals = 16 / kElem;                // activations per load
+    static constexpr int kChunksPerSb = 4 * kTrits / kChunkVals;  // loads per sub-block row
 };
 
-// Dynamic LDS: red [2][8][64] floatx4 | per wave: planes x (M + 1) rows x row bytes.
-__host__ __device__ inline int persist_row_bytes(int nsb) { return nsb * 4 * kTrits * 2 + 16; }
-constexpr int kPersistRedBytes = 2 * kWavesP * 64 * 16;
-__host__ __device__ inline int persist_wave_bytes(int M, int nsb, int planes) {
-    return planes * (M + 1) * persist_row_bytes(nsb);
-}
-__host__ __device__ inline int persist_lds_bytes(int M, int nsb, int planes) {
-    return kPersistRedBytes + kWavesP * persist_wave_bytes(M, nsb, planes);
-}
+constexpr int kSbBytes = 4 * kTrits * 2;  // one staged sub-block row: 192 bf16
+constexpr int kRing = 8;
+constexpr uint32_t kOobOffset = 0x80000000u;
 
-template <int XT, int RING, int SU>
-__global__ __launch_bounds__(64 * kWavesP) void gemv_persistent_kernel(
+// Staged row pitch in bytes; the extra 16 bytes shift consecutive rows across banks.
+__host__ __device__ inline int group_pitch(int nsb) { return nsb * kSbBytes + 16; }
+__host__ __device__ inline int group_rows(int M) { return M < 16 ? M + 1 : 16; }
+
+template <int XT, int W, int SU>
+__global__ __launch_bounds__(64 * W) void gemv_group_kernel(
     const void *__restrict__ x, const uint8_t *__restrict__ w, void *__restrict__ c, int M,
-    int64_t N, int64_t K, int64_t L, int nsb, int x_aligned, float alpha, float beta,
-    const float *__restrict__ bias) {
-    using LY = PersistLayout<XT>;
+    int64_t N, int64_t K, int L, int nsb, uint32_t cpr_magic, int x_aligned, float alpha,
+    float beta, const float *__restrict__ bias) {
+    using LY = GroupLayout<XT>;
+    constexpr int T = 64 * W;
     constexpr int kElem = LY::kElem;
-    constexpr int kChunkVals = LY::kChunkVals;
+    constexpr int CV = LY::kChunkVals;
     __shared__ __attribute__((aligned(16))) uint8_t lut[kLutBytes];
-    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    floatx4 *red = reinterpret_cast<floatx4 *>(smem);
-    const int row = persist_row_bytes(nsb);
+    __shared__ __attribute__((aligned(16))) floatx4 red[W * 64];
+    extern __shared__ __attribute__((aligned(16))) uint8_t xs[];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int r = lane & 15;
     const int q = lane >> 4;
-    const int64_t groups = (N + 15) / 16;
-    const int64_t lb = (wave * L) / kWavesP;
-    const int64_t le = ((wave + 1) * L) / kWavesP;
-    const int lw = static_cast<int>(le - lb);
-    const int plane_bytes = (M + 1) * row;
-    uint8_t *xw = smem + kPersistRedBytes + wave * persist_wave_bytes(M, nsb, LY::kPlanes);
-    const int64_t my_groups =
-        groups > blockIdx.x ? (groups - blockIdx.x + gridDim.x - 1) / gridDim.x : 0;
-    const int64_t total_f = my_groups * nsb;
+    const int pitch = group_pitch(nsb);
+    const int plane_bytes = group_rows(M) * pitch;
+    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 16;
+    const int s0 = (wave * nsb) / W;
+    const int nsbw = ((wave + 1) * nsb) / W - s0;
 
-    // 1. raw activation loads: 16-byte chunks of the wave's slice, natural order
-    const int chunks_row = (lw * kTrits + kChunkVals - 1) / kChunkVals;
-    const int chunks = M * chunks_row;
-    u32x4 sraw[SU];
+    // ---- activation chunks: u = m * cpr + cc, cc over the zero-padded row ----
+    const int cpr = nsb * LY::kChunksPerSb;
+    const int chunks = M * cpr;
+    const uint8_t *xb8 = static_cast<const uint8_t *>(x);
+    const uint8_t *zero8 = reinterpret_cast<const uint8_t *>(kZeroBlock);
+    auto load_chunks = [&](int base, u32x4 (&raw)[SU]) {
 #pragma unroll
-    for (int i = 0; i < SU; ++i) {
-        const int u = lane + 64 * i;
-        const bool ok = u < chunks;
-        const int uu = ok ? u : 0;
-        const int m = chunks_row > 0 ? uu / chunks_row : 0;
-        const int cu = uu - m * chunks_row;
-        const int64_t k0 = lb * kTrits + static_cast<int64_t>(cu) * kChunkVals;
-        if (x_aligned) {  // K % kChunkVals == 0: a chunk is all inside K or all past it
-            const bool in = ok && k0 < K;
-            const uint8_t *p = in ? static_cast<const uint8_t *>(x) + (m * K + k0) * kElem
-                                  : reinterpret_cast<const uint8_t *>(kZeroBlock);
-            sraw[i] = *reinterpret_cast<const u32x4 *>(p);
-        } else {
-            uint32_t e[kChunkVals];
+        for (int i = 0; i < SU; ++i) {
+            const int u = base + tid + T * i;
+            const bool ok = u < chunks;
+            const int m = static_cast<int>(__umulhi(static_cast<uint32_t>(u), cpr_magic));
+            const int64_t k0 = static_cast<int64_t>(u - m * cpr) * CV;
+            if (x_aligned) {  // K % CV == 0: a chunk lies wholly inside K or wholly past it
+                const uint8_t *p = ok && k0 < K ? xb8 + (m * K + k0) * kElem : zero8;
+                raw[i] = *reinterpret_cast<const u32x4 *>(p);
+            } else {
+                uint32_t e[CV];
 #pragma unroll
-            for (int v = 0; v < kChunkVals; ++v) {
-                const bool in = ok && k0 + v < K;
-                const uint8_t *p = in ? static_cast<const uint8_t *>(x) + (m * K + k0 + v) * kElem
-                                      : reinterpret_cast<const uint8_t *>(kZeroBlock);
-                if constexpr (kElem == 4) e[v] = *reinterpret_cast<const uint32_t *>(p);
-                else if constexpr (kElem == 2) e[v] = *reinterpret_cast<const uint16_t *>(p);
-                else e[v] = *p;
+                for (int v = 0; v < CV; ++v) {
+                    const uint8_t *p = ok && k0 + v < K ? xb8 + (m * K + k0 + v) * kElem : zero8;
+                    if constexpr (kElem == 4) e[v] = *reinterpret_cast<const uint32_t *>(p);
+                    else if constexpr (kElem == 2) e[v] = *reinterpret_cast<const uint16_t *>(p);
+                    else e[v] = *p;
+                }
+                uint32_t wd[4];
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    if constexpr (kElem == 4) wd[d] = e[d];
+                    else if constexpr (kElem == 2) wd[d] = e[2 * d] | (e[2 * d + 1] << 16);
+                    else
+                        wd[d] = e[4 * d] | (e[4 * d + 1] << 8) | (e[4 * d + 2] << 16) |
+                                (e[4 * d + 3] << 24);
+                }
+                raw[i] = u32x4{wd[0], wd[1], wd[2], wd[3]};
             }
-            uint32_t wd[4];
-#pragma unroll
-            for (int d = 0; d < 4; ++d) {
-                if constexpr (kElem == 4) wd[d] = e[d];
-                else if constexpr (kElem == 2) wd[d] = e[2 * d] | (e[2 * d + 1] << 16);
-                else wd[d] = e[4 * d] | (e[4 * d + 1] << 8) | (e[4 * d + 2] << 16) | (e[4 * d + 3] << 24);
-            }
-            sraw[i] = u32x4{wd[0], wd[1], wd[2], wd[3]};
         }
-    }
-
-    // 2. the weight ring.  Each lane walks its limbs with a pointer: +4 limbs per
-    //    sub-block, + one group stride per group.  A slot is valid for this lane when
-    //    its limb lies in the wave's range (sb < sb_lim) and its row exists.
-    const int sb_lim = (lw - q + 3) / 4;
-    const int64_t group_step = static_cast<int64_t>(gridDim.x) * 16 * L * kTrytes;
-    const uint8_t *pad = reinterpret_cast<const uint8_t *>(kPadLimb);
-    int64_t rrow = static_cast<int64_t>(blockIdx.x) * 16 + r;  // row of the next refill
-    const uint8_t *rptr = w + (rrow * L + lb + q) * kTrytes;
-    int rsb = 0;
-    auto refill = [&]() -> u32x4 {
-        const bool ok = rsb < sb_lim && rrow < N;
-        const u32x4 v = *reinterpret_cast<const u32x4 *>(ok ? rptr : pad);
-        rptr += 4 * kTrytes;
-        if (++rsb == nsb) {
-            rsb = 0;
-            rptr += group_step - static_cast<int64_t>(nsb) * 4 * kTrytes;
-            rrow += static_cast<int64_t>(gridDim.x) * 16;
-        }
-        return v;
     };
-    u32x4 ring[RING];
+    auto stage_chunks = [&](int base, const u32x4 (&raw)[SU]) {
 #pragma unroll
-    for (int i = 0; i < RING; ++i) ring[i] = refill();
-
-    // 3. decode table, zero fill, activations -> LDS (bf16 planes); one barrier
-    lut_fill(lut, tid, 64 * kWavesP);
-    {
-        const int wave_bytes = persist_wave_bytes(M, nsb, LY::kPlanes);
-        const u32x4 z = {0u, 0u, 0u, 0u};
-        for (int b = 16 * lane; b < wave_bytes; b += 64 * 16)
-            *reinterpret_cast<u32x4 *>(xw + b) = z;
-    }
+        for (int i = 0; i < SU; ++i) {
+            const int u = base + tid + T * i;
+            if (u < chunks) {
+                const int m = static_cast<int>(__umulhi(static_cast<uint32_t>(u), cpr_magic));
+                uint8_t *dst = xs + m * pitch + (u - m * cpr) * (CV * 2);
+                if constexpr (XT == kDtypeBF16) {
+                    *reinterpret_cast<u32x4 *>(dst) = raw[i];
+                } else if constexpr (XT == kDtypeF32) {
+                    // x = hi + lo, hi = bf16(x), lo = bf16(x - hi): |x - hi - lo| <= 2^-18 |x|
+                    uint32_t h[4], l[4];
 #pragma unroll
-    for (int i = 0; i < SU; ++i) {
-        const int u = lane + 64 * i;
-        if (u < chunks) {
-            const int m = u / chunks_row;
-            const int cu = u - m * chunks_row;
-            uint8_t *dst = xw + m * row + cu * kChunkVals * 2;
-            if constexpr (XT == kDtypeBF16) {
-                *reinterpret_cast<u32x4 *>(dst) = sraw[i];
-            } else if constexpr (XT == kDtypeF32) {
-                // x = hi + lo, hi = bf16(x), lo = bf16(x - hi): |x - hi - lo| <= 2^-18 |x|
-                uint32_t h[4], l[4];
+                    for (int e = 0; e < 4; ++e) {
+                        const float f = __uint_as_float(raw[i][e]);
+                        h[e] = bf16_bits_rne(f);
+                        l[e] = bf16_bits_rne(f - bf16_bits_to_float(h[e]));
+                    }
+                    *reinterpret_cast<uint2 *>(dst) =
+                        make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+                    *reinterpret_cast<uint2 *>(dst + plane_bytes) =
+                        make_uint2(l[0] | (l[1] << 16), l[2] | (l[3] << 16));
+                } else {  // int8 -> bf16, exact
+                    uint32_t o[8];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float f = __uint_as_float(sraw[i][e]);
-                    h[e] = bf16_bits_rne(f);
-                    l[e] = bf16_bits_rne(f - bf16_bits_to_float(h[e]));
+                    for (int e = 0; e < 8; ++e) {
+                        const uint32_t wd0 = raw[i][e / 2];
+                        const int8_t b0 = static_cast<int8_t>((wd0 >> (16 * (e % 2))) & 0xFFu);
+                        const int8_t b1 =
+                            static_cast<int8_t>((wd0 >> (16 * (e % 2) + 8)) & 0xFFu);
+                        o[e] = bf16_bits_rne(static_cast<float>(b0)) |
+                               (bf16_bits_rne(static_cast<float>(b1)) << 16);
+                    }
+                    reinterpret_cast<u32x4 *>(dst)[0] = u32x4{o[0], o[1], o[2], o[3]};
+                    reinterpret_cast<u32x4 *>(dst)[1] = u32x4{o[4], o[5], o[6], o[7]};
                 }
-                *reinterpret_cast<uint2 *>(dst) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
-                *reinterpret_cast<uint2 *>(dst + plane_bytes) =
-                    make_uint2(l[0] | (l[1] << 16), l[2] | (l[3] << 16));
-            } else {  // int8 -> bf16, exact
-                uint32_t o[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const uint32_t wd0 = sraw[i][e / 2];
-                    const int8_t b0 = static_cast<int8_t>((wd0 >> (16 * (e % 2))) & 0xFFu);
-                    const int8_t b1 = static_cast<int8_t>((wd0 >> (16 * (e % 2) + 8)) & 0xFFu);
-                    o[e] = bf16_bits_rne(static_cast<float>(b0)) |
-                           (bf16_bits_rne(static_cast<float>(b1)) << 16);
-                }
-                reinterpret_cast<u32x4 *>(dst)[0] = u32x4{o[0], o[1], o[2], o[3]};
-                reinterpret_cast<u32x4 *>(dst)[1] = u32x4{o[4], o[5], o[6], o[7]};
             }
         }
+    };
+
+    // ---- weight ring: offsets relative to the group's first row ----
+    const int64_t remain = (N - n0) * L * kTrytes;
+    const int nrec = remain < 0x7FFFFFFF ? static_cast<int>(remain) : 0x7FFFFFFF;
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(w + n0 * L * kTrytes), 0, nrec, 0x00020000);
+    const uint32_t lane_base = static_cast<uint32_t>((r * L + 4 * s0 + q) * kTrytes);
+    auto fetch = [&](int f) -> u32x4 {  // sub-block s0 + f of this lane's row, or nothing
+        const uint32_t off = f < nsbw ? lane_base + static_cast<uint32_t>(64 * f) : kOobOffset;
+        return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0));
+    };
+
+    u32x4 raw[SU];
+    load_chunks(0, raw);
+    u32x4 ring[kRing];
+#pragma unroll
+    for (int i = 0; i < kRing; ++i) ring[i] = fetch(i);
+    lut_fill(lut, tid, T);
+    stage_chunks(0, raw);
+    for (int base = T * SU; base < chunks; base += T * SU) {  // large M * K only
+        load_chunks(base, raw);
+        stage_chunks(base, raw);
+    }
+    if (M < 16) {  // the zero row, in every plane
+        const u32x4 z = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int p = 0; p < LY::kPlanes; ++p)
+            for (int b = 16 * tid; b < pitch; b += 16 * T)
+                *reinterpret_cast<u32x4 *>(xs + p * plane_bytes + M * pitch + b) = z;
     }
     __syncthreads();
 
-    // 4. stream the groups.  Lane (r, q) reads its B operands at xb + sb * 4 limbs:
-    //    row r (or the zero row M), limb q of the sub-block.
-    const uint8_t *xb = xw + (r < M ? r : M) * row + q * kTrits * 2;
+    // ---- stream: lane (r, q) reads row r (the zero row for r >= M), limb q ----
+    const uint8_t *xl = xs + (r < M ? r : M) * pitch + s0 * kSbBytes + q * (kTrits * 2);
     floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-    int64_t gi = 0;
-    int sb = 0;
-    for (int64_t f0 = 0; f0 < total_f; f0 += RING) {
+    for (int f0 = 0; f0 < nsbw; f0 += kRing) {
 #pragma unroll
-        for (int i = 0; i < RING; ++i) {
+        for (int i = 0; i < kRing; ++i) {
+            const int f = f0 + i;
             // decode slot i before its refill is issued: the refill then reuses the
             // slot's registers and the ring needs no copies across iterations
             uint32_t pairs[24];
+            if (f < nsbw) {
 #pragma unroll
-            for (int d = 0; d < 4; ++d) decode_dword(lut, ring[i][d], pairs + 6 * d);
+                for (int d = 0; d < 4; ++d) decode_dword(lut, ring[i][d], pairs + 6 * d);
+            }
             __builtin_amdgcn_sched_barrier(0);
-            ring[i] = refill();  // unconditional: past the end it reads the padding limb
-            if (f0 + i < total_f) {
-                const uint8_t *src = xb + sb * (4 * kTrits * 2);
+            ring[i] = fetch(f + kRing);
+            if (f < nsbw) {
+                const uint8_t *src = xl + f * kSbBytes;
                 bf16x8 bh[6], bl[6];
 #pragma unroll
                 for (int j = 0; j < 6; ++j) {
@@ -423,23 +416,33 @@ __global__ __launch_bounds__(64 * kWavesP) void gemv_persistent_kernel(
                         bl[j] = *reinterpret_cast<const bf16x8 *>(src + plane_bytes + 16 * j);
                 }
                 acc = mfma_pairs<XT>(pairs, bh, bl, acc);
-                if (++sb == nsb) {  // group gi complete: publish, reduce, store
-                    sb = 0;
-                    floatx4 *buf = red + (gi & 1) * kWavesP * 64;
-                    buf[wave * 64 + lane] = acc;
-                    acc = floatx4{0.f, 0.f, 0.f, 0.f};
-                    __syncthreads();
-                    // the reducing wave rotates: its bias / C loads (if any) drain its own
-                    // ring, so the stall is spread over the waves
-                    if (wave == static_cast<int>(gi % kWavesP)) {
-                        floatx4 v = buf[lane];
+            }
+        }
+    }
+
+    // ---- reduce the W partial tiles, one element per thread ----
+    red[wave * 64 + lane] = acc;
+    __syncthreads();
+    const float *redf = reinterpret_cast<const float *>(red);
+    for (int e = tid; e < 256; e += T) {
+        float v = redf[e];
 #pragma unroll
-                        for (int ww = 1; ww < kWavesP; ++ww) v += buf[ww * 64 + lane];
-                        const int64_t grp = blockIdx.x + gi * gridDim.x;
-                        store_tile<XT>(v, lane, M, N, grp * 16, c, alpha, beta, bias);
-                    }
-                    ++gi;
-                }
+        for (int ww = 1; ww < W; ++ww) v += redf[ww * 256 + e];
+        const int le = e >> 2;  // lane of the tile that held element e
+        const int m = le & 15;
+        const int64_t n = n0 + 4 * (le >> 4) + (e & 3);
+        if (m < M && n < N) {
+            if constexpr (XT == kDtypeI8) {
+                int32_t *cp = static_cast<int32_t *>(c) + static_cast<int64_t>(m) * N + n;
+                int32_t y = static_cast<int32_t>(v);
+                if (beta != 0.0f) y += *cp;
+                *cp = y;
+            } else {
+                float *cp = static_cast<float *>(c) + static_cast<int64_t>(m) * N + n;
+                float y = alpha * v;
+                if (beta != 0.0f) y = y + beta * *cp;
+                if (bias != nullptr) y = y + bias[n];
+                *cp = y;
             }
         }
     }
@@ -517,77 +520,72 @@ hipError_t launch_stream(const void *x, const uint8_t *w, void *c, int m, int64_
     return hipGetLastError();
 }
 
-int cu_count() {
-    static int cus = 0;
-    if (cus == 0) {
-        int dev = 0, v = 0;
-        if (hipGetDevice(&dev) == hipSuccess &&
-            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
-            cus = v;
-        if (cus <= 0) cus = 256;
+// Dynamic LDS of the group kernel: 160 KiB per CU less its static tables.
+constexpr size_t kMaxGroupLds = 160 * 1024 - kLutBytes - 16 * 64 * 16;
+
+template <int XT, int W, int SU>
+hipError_t launch_group(const void *x, const uint8_t *w, void *c, int m, int64_t n, int64_t k,
+                        int L, int nsb, uint32_t magic, bool aligned, size_t lds, float alpha,
+                        float beta, const float *bias, hipStream_t s) {
+    auto fn = reinterpret_cast<const void *>(&gemv_group_kernel<XT, W, SU>);
+    static size_t raised = 64 * 1024;  // dynamic LDS above 64 KiB needs an opt-in
+    if (lds > raised) {
+        const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 static_cast<int>(kMaxGroupLds));
+        if (e != hipSuccess) return e;
+        raised = kMaxGroupLds;
     }
-    return cus;
-}
-
-// Resident workgroups per CU for a persistent instantiation at `lds` bytes (cached;
-// the first call also raises the dynamic-LDS limit when more than 64 KiB is asked).
-template <int XT, int RING, int SU>
-int persist_occupancy(size_t lds) {
-    static size_t cached_lds = 0;
-    static int cached = 0;
-    if (cached > 0 && cached_lds == lds) return cached;
-    auto fn = reinterpret_cast<const void *>(&gemv_persistent_kernel<XT, RING, SU>);
-    if (lds > 64 * 1024)
-        (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  static_cast<int>(lds));
-    int nb = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fn, 64 * kWavesP, lds) != hipSuccess ||
-        nb <= 0)
-        nb = 1;
-    cached_lds = lds;
-    cached = nb;
-    return nb;
-}
-
-template <int XT, int RING, int SU>
-hipError_t launch_persist(const void *x, const uint8_t *w, void *c, int m, int64_t n, int64_t k,
-                          int64_t L, int nsb, size_t lds, bool aligned, float alpha,
-                          float beta, const float *bias, hipStream_t s) {
-    const int64_t groups = (n + 15) / 16;
-    const int occ = persist_occupancy<XT, RING, SU>(lds);
-    const int64_t grid = groups < static_cast<int64_t>(cu_count()) * occ
-                             ? groups
-                             : static_cast<int64_t>(cu_count()) * occ;
-    gemv_persistent_kernel<XT, RING, SU><<<dim3(grid), dim3(64 * kWavesP), lds, s>>>(
-        x, w, c, m, n, k, L, nsb, aligned ? 1 : 0, alpha, beta, bias);
+    gemv_group_kernel<XT, W, SU><<<dim3((n + 15) / 16), dim3(64 * W), lds, s>>>(
+        x, w, c, m, n, k, L, nsb, magic, aligned ? 1 : 0, alpha, beta, bias);
     return hipGetLastError();
 }
 
-constexpr size_t kMaxPersistLds = 160 * 1024;
+template <int XT, int W>
+hipError_t launch_group_su(int su, const void *x, const uint8_t *w, void *c, int m, int64_t n,
+                           int64_t k, int L, int nsb, uint32_t magic, bool aligned, size_t lds,
+                           float alpha, float beta, const float *bias, hipStream_t s) {
+    if (su <= 2)
+        return launch_group<XT, W, 2>(x, w, c, m, n, k, L, nsb, magic, aligned, lds, alpha, beta,
+                                      bias, s);
+    if (su <= 4)
+        return launch_group<XT, W, 4>(x, w, c, m, n, k, L, nsb, magic, aligned, lds, alpha, beta,
+                                      bias, s);
+    return launch_group<XT, W, 8>(x, w, c, m, n, k, L, nsb, magic, aligned, lds, alpha, beta,
+                                  bias, s);
+}
 
 template <int XT>
 hipError_t launch_gemv_x(const void *x, const uint8_t *w, void *c, int m, int64_t n, int64_t k,
                          float alpha, float beta, const float *bias, hipStream_t s) {
-    using LY = PersistLayout<XT>;
+    using LY = GroupLayout<XT>;
     const int elem = LY::kElem;
     const int64_t L = (k + kTrits - 1) / kTrits;
-    const bool aligned = (k % LY::kChunkVals == 0) && (reinterpret_cast<uintptr_t>(x) % 16 == 0);
+    const int64_t groups = (n + 15) / 16;
     const bool aligned8 = (k % 8 == 0) && (reinterpret_cast<uintptr_t>(x) % (8 * elem) == 0);
-    if (L > 0) {
-        const int lw_max = static_cast<int>((L + kWavesP - 1) / kWavesP);
-        const int nsb = (lw_max + 3) / 4;
-        const int64_t chunks = m * ((lw_max * kTrits + LY::kChunkVals - 1) / LY::kChunkVals);
-        const int su = static_cast<int>((chunks + 63) / 64);
-        const size_t lds = static_cast<size_t>(persist_lds_bytes(m, nsb, LY::kPlanes));
-        if (su <= 4 && lds <= kMaxPersistLds) {
-            if (su <= 1)
-                return launch_persist<XT, 8, 1>(x, w, c, m, n, k, L, nsb, lds, aligned, alpha,
-                                                beta, bias, s);
-            if (su <= 2)
-                return launch_persist<XT, 8, 2>(x, w, c, m, n, k, L, nsb, lds, aligned, alpha,
-                                                beta, bias, s);
-            return launch_persist<XT, 8, 4>(x, w, c, m, n, k, L, nsb, lds, aligned, alpha, beta,
-                                            bias, s);
+    // group kernel: activations staged whole; per-group weight offsets below 2^31
+    if (L > 0 && L <= (1 << 22)) {
+        const int nsb = static_cast<int>((L + 3) / 4);
+        const size_t lds = static_cast<size_t>(LY::kPlanes) * group_rows(m) * group_pitch(nsb);
+        // waves per group: enough waves in flight (groups * W >= 2048 where possible),
+        // at least two sub-blocks per wave
+        int W = groups >= 512 ? 4 : (groups >= 256 ? 8 : 16);
+        while (W > 4 && nsb < 2 * W) W /= 2;
+        const int64_t chunks = static_cast<int64_t>(m) * nsb * LY::kChunksPerSb;
+        const int su = static_cast<int>((chunks + 64 * W - 1) / (64 * W));
+        if (lds <= kMaxGroupLds) {
+            const bool aligned =
+                (k % LY::kChunkVals == 0) && (reinterpret_cast<uintptr_t>(x) % 16 == 0);
+            const int cpr = nsb * LY::kChunksPerSb;
+            const uint32_t magic = static_cast<uint32_t>((uint64_t{1} << 32) / cpr + 1);
+            const int Li = static_cast<int>(L);
+            if (W == 4)
+                return launch_group_su<XT, 4>(su, x, w, c, m, n, k, Li, nsb, magic, aligned, lds,
+                                              alpha, beta, bias, s);
+            if (W == 8)
+                return launch_group_su<XT, 8>(su, x, w, c, m, n, k, Li, nsb, magic, aligned, lds,
+                                              alpha, beta, bias, s);
+            return launch_group_su<XT, 16>(su, x, w, c, m, n, k, Li, nsb, magic, aligned, lds,
+                                           alpha, beta, bias, s);
         }
     }
     if (aligned8) return launch_stream<XT, 2, true>(x, w, c, m, n, k, L, alpha, beta, bias, s);
