@@ -22,6 +22,8 @@
 // eight consecutive activations, one 16-byte load.  Which k an MFMA slot means
 // internally is irrelevant: A and B use the same (lane/16, slot) -> k map.
 // Output tile: lane (m, q) holds rows n = 4q + i (i < 4) of column m.
+#include <algorithm>
+
 #include "t81_device.hpp"
 #include "t81_kernels.hpp"
 
@@ -152,6 +154,21 @@ __device__ __forceinline__ floatx4 mfma_pairs(const uint32_t *pairs, const bf16x
     return acc;
 }
 
+// mfma_pairs with the six MFMAs alternating between two accumulators.
+template <int XT>
+__device__ __forceinline__ void mfma_pairs2(const uint32_t *pairs, const bf16x8 *bh,
+                                            const bf16x8 *bl, floatx4 &acc0, floatx4 &acc1) {
+#pragma unroll
+    for (int j = 0; j < 6; ++j) {
+        const u32x4 araw = {pairs[4 * j], pairs[4 * j + 1], pairs[4 * j + 2], pairs[4 * j + 3]};
+        const bf16x8 a = __builtin_bit_cast(bf16x8, araw);
+        floatx4 &acc = (j & 1) ? acc1 : acc0;
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bh[j], acc, 0, 0, 0);
+        if constexpr (XT == kDtypeF32)
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bl[j], acc, 0, 0, 0);
+    }
+}
+
 // acc += T(16 rows, one limb per lane-quarter) x B  over the six 8-trit slots of the limb.
 template <int XT>
 __device__ __forceinline__ floatx4 mfma_limb(const uint8_t *lut, u32x4 wl, const bf16x8 *bh,
@@ -222,28 +239,30 @@ __device__ __forceinline__ void reduce_store(floatx4 (&acc)[G], floatx4 *red, in
 }
 
 // ---------------------------------------------------------------------------------
-// gemv_group_kernel: one workgroup of W waves per 16-row group (blockIdx.x).
-//
-//   1. All threads load the activations (M rows, K padded with zeros to whole
-//      4-limb sub-blocks) with 16-byte loads; each wave then issues the first RING
-//      weight sub-blocks of its K range before waiting for any of them.
-//   2. The activations go to LDS as bf16 (fp32: hi and lo planes; int8: exact),
-//      plus one all-zero row that lanes of tokens >= M read; one barrier.
-//   3. Each wave streams its sub-blocks [s0, s1) through the ring: decode slot i
-//      from the LDS tables, refill slot i with the sub-block RING ahead, six MFMAs
-//      against the staged activations.
-//   4. The W partial tiles are summed through LDS, one output element per thread,
-//      always in wave order (deterministic results).
-//
-// Weights are read through a buffer resource whose base is the group's first row:
-// each lane's offset is fixed, and the hardware range check returns zeros past the
-// end of the matrix (rows >= N of the last group).  A refill past the wave's range
-// uses an offset >= 2^31, also out of range, so it reads nothing.  Lanes whose limb
-// index runs past L at the end of a row read the next row's first limbs: the
-// activations staged for those k are zero, and every byte decodes to a finite value
-// (0 or +-1), so they add exactly nothing.
+// gemv_wave_kernel: a workgroup of W waves covers G = W / Wg 16-row groups, Wg waves
+// per group, each wave a contiguous run of nsbw <= R 4-limb sub-blocks of its
+// group's K (up to 12 KB of weights).  Everything a wave needs up to the final
+// reduction is private to it, so there is no barrier before the stream:
+//   1. raw loads of the activations of its K range (M rows, zero past K), then
+//      R weight loads, one per sub-block: all of them are in flight before the
+//      first is used.  The count is a template constant, so the compiler counts
+//      outstanding loads exactly (a load issued under a condition would make every
+//      later wait a full drain); a wave with nsbw < R points the spare loads past
+//      the buffer's range, where they return zeros without touching memory;
+//   2. its own copy of the decode tables and of its activations in LDS (bf16;
+//      fp32 as hi and lo planes; int8 exactly), ordered against its own reads by a
+//      wavefront fence;
+//   3. per sub-block: decode from the tables, six MFMAs;
+//   4. partial tiles summed through LDS per group (one barrier), wave order fixed.
+// Tokens m >= M: their lanes read activation row 0.  Column m of the MFMA result
+// depends only on column m of B, and those columns are never stored.
+// Weights come through a buffer resource based at the group's first row: the
+// hardware range check returns zeros past the end of the matrix (rows >= N).
+// Limbs past L at the end of a row read the next row's first limbs; their
+// activations are staged as zero and every byte decodes to 0 or +-1, so they add
+// exactly nothing.
 template <int XT>
-struct GroupLayout {
+struct WaveLayout {
     static constexpr int kPlanes = XT == kDtypeF32 ? 2 : 1;
     static constexpr int kElem = XT == kDtypeF32 ? 4 : (XT == kDtypeBF16 ? 2 : 1);
     static constexpr int kChunkVals = 16 / kElem;                // activations per load
@@ -251,60 +270,79 @@ struct GroupLayout {
 };
 
 constexpr int kSbBytes = 4 * kTrits * 2;  // one staged sub-block row: 192 bf16
-constexpr int kRing = 8;
+constexpr int kMaxRun = 12;               // sub-blocks per wave
+#ifndef T81_GEMV_DEPTH
+#define T81_GEMV_DEPTH 4
+#endif
+constexpr int kDepth = T81_GEMV_DEPTH;    // weight loads in flight per wave
+constexpr int kMaxChunksPerLane = 8;      // activation loads per lane, all in flight at once
 constexpr uint32_t kOobOffset = 0x80000000u;
 
-// Staged row pitch in bytes; the extra 16 bytes shift consecutive rows across banks.
-__host__ __device__ inline int group_pitch(int nsb) { return nsb * kSbBytes + 16; }
-__host__ __device__ inline int group_rows(int M) { return M < 16 ? M + 1 : 16; }
+// Per-wave LDS: planes x M rows x pitch; pitch = nsbw_max sub-blocks plus 16 bytes,
+// which moves consecutive rows to other banks.
+__host__ __device__ inline int wave_pitch(int nsbw_max) { return nsbw_max * kSbBytes + 16; }
+__host__ __device__ inline int wave_lds_bytes(int M, int nsbw_max, int planes) {
+    return planes * M * wave_pitch(nsbw_max);
+}
 
-template <int XT, int W, int SU>
-__global__ __launch_bounds__(64 * W) void gemv_group_kernel(
+template <int XT, int W, int SU, int R>
+__global__ __launch_bounds__(64 * W) void gemv_wave_kernel(
     const void *__restrict__ x, const uint8_t *__restrict__ w, void *__restrict__ c, int M,
-    int64_t N, int64_t K, int L, int nsb, uint32_t cpr_magic, int x_aligned, float alpha,
-    float beta, const float *__restrict__ bias) {
-    using LY = GroupLayout<XT>;
-    constexpr int T = 64 * W;
+    int64_t N, int64_t K, int L, int nsb, int wg, int nsbw_max, uint32_t cpr_magic,
+    int x_aligned, float alpha, float beta, const float *__restrict__ bias) {
+    using LY = WaveLayout<XT>;
     constexpr int kElem = LY::kElem;
     constexpr int CV = LY::kChunkVals;
     __shared__ __attribute__((aligned(16))) uint8_t lut[kLutBytes];
     __shared__ __attribute__((aligned(16))) floatx4 red[W * 64];
-    extern __shared__ __attribute__((aligned(16))) uint8_t xs[];
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    // wave-uniform, and known to be: every quantity derived from it stays scalar and
+    // every condition on it is a scalar branch
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r = lane & 15;
     const int q = lane >> 4;
-    const int pitch = group_pitch(nsb);
-    const int plane_bytes = group_rows(M) * pitch;
-    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 16;
-    const int s0 = (wave * nsb) / W;
-    const int nsbw = ((wave + 1) * nsb) / W - s0;
+    const int G = W / wg;
+    const int g = wave / wg;
+    const int p = wave - g * wg;
+    const int64_t group = static_cast<int64_t>(blockIdx.x) * G + g;
+    const int64_t groups = (N + 15) / 16;
+    const int64_t n0 = group * 16;
+    const int s0 = (p * nsb) / wg;
+    const int nsbw = group < groups ? ((p + 1) * nsb) / wg - s0 : 0;
+    const int pitch = wave_pitch(nsbw_max);
+    const int plane_bytes = M * pitch;
+    uint8_t *xs = smem + wave * wave_lds_bytes(M, nsbw_max, LY::kPlanes);
 
-    // ---- activation chunks: u = m * cpr + cc, cc over the zero-padded row ----
-    const int cpr = nsb * LY::kChunksPerSb;
+    // ---- 1a. activation chunks of this wave: u = m * cpr + cc ----
+    const int cpr = nsbw_max * LY::kChunksPerSb;
     const int chunks = M * cpr;
+    const int cc_end = nsbw * LY::kChunksPerSb;
+    const int64_t kbase = static_cast<int64_t>(s0) * 4 * kTrits;
     const uint8_t *xb8 = static_cast<const uint8_t *>(x);
     const uint8_t *zero8 = reinterpret_cast<const uint8_t *>(kZeroBlock);
     auto load_chunks = [&](int base, u32x4 (&raw)[SU]) {
 #pragma unroll
         for (int i = 0; i < SU; ++i) {
-            const int u = base + tid + T * i;
-            const bool ok = u < chunks;
+            const int u = base + lane + 64 * i;
             const int m = static_cast<int>(__umulhi(static_cast<uint32_t>(u), cpr_magic));
-            const int64_t k0 = static_cast<int64_t>(u - m * cpr) * CV;
+            const int cc = u - m * cpr;
+            const bool ok = u < chunks && cc < cc_end;
+            const int64_t k0 = kbase + static_cast<int64_t>(cc) * CV;
             if (x_aligned) {  // K % CV == 0: a chunk lies wholly inside K or wholly past it
-                const uint8_t *p = ok && k0 < K ? xb8 + (m * K + k0) * kElem : zero8;
-                raw[i] = *reinterpret_cast<const u32x4 *>(p);
+                const uint8_t *ptr = ok && k0 < K ? xb8 + (m * K + k0) * kElem : zero8;
+                raw[i] = *reinterpret_cast<const u32x4 *>(ptr);
             } else {
                 uint32_t e[CV];
 #pragma unroll
                 for (int v = 0; v < CV; ++v) {
-                    const uint8_t *p = ok && k0 + v < K ? xb8 + (m * K + k0 + v) * kElem : zero8;
-                    if constexpr (kElem == 4) e[v] = *reinterpret_cast<const uint32_t *>(p);
-                    else if constexpr (kElem == 2) e[v] = *reinterpret_cast<const uint16_t *>(p);
-                    else e[v] = *p;
+                    const uint8_t *ptr =
+                        ok && k0 + v < K ? xb8 + (m * K + k0 + v) * kElem : zero8;
+                    if constexpr (kElem == 4) e[v] = *reinterpret_cast<const uint32_t *>(ptr);
+                    else if constexpr (kElem == 2) e[v] = *reinterpret_cast<const uint16_t *>(ptr);
+                    else e[v] = *ptr;
                 }
                 uint32_t wd[4];
 #pragma unroll
@@ -322,7 +360,7 @@ __global__ __launch_bounds__(64 * W) void gemv_group_kernel(
     auto stage_chunks = [&](int base, const u32x4 (&raw)[SU]) {
 #pragma unroll
         for (int i = 0; i < SU; ++i) {
-            const int u = base + tid + T * i;
+            const int u = base + lane + 64 * i;
             if (u < chunks) {
                 const int m = static_cast<int>(__umulhi(static_cast<uint32_t>(u), cpr_magic));
                 uint8_t *dst = xs + m * pitch + (u - m * cpr) * (CV * 2);
@@ -359,78 +397,74 @@ __global__ __launch_bounds__(64 * W) void gemv_group_kernel(
         }
     };
 
-    // ---- weight ring: offsets relative to the group's first row ----
-    const int64_t remain = (N - n0) * L * kTrytes;
+    // ---- 1b. weights: every sub-block of the run, issued before any is used ----
+    const int64_t remain = group < groups ? (N - n0) * L * kTrytes : 0;
     const int nrec = remain < 0x7FFFFFFF ? static_cast<int>(remain) : 0x7FFFFFFF;
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint8_t *>(w + n0 * L * kTrytes), 0, nrec, 0x00020000);
+        const_cast<uint8_t *>(group < groups ? w + n0 * L * kTrytes : w), 0, nrec, 0x00020000);
     const uint32_t lane_base = static_cast<uint32_t>((r * L + 4 * s0 + q) * kTrytes);
-    auto fetch = [&](int f) -> u32x4 {  // sub-block s0 + f of this lane's row, or nothing
-        const uint32_t off = f < nsbw ? lane_base + static_cast<uint32_t>(64 * f) : kOobOffset;
-        return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0));
-    };
 
     u32x4 raw[SU];
     load_chunks(0, raw);
-    u32x4 ring[kRing];
+    constexpr int D = R < kDepth ? R : kDepth;
+    u32x4 ring[D];  // sub-block f lives in ring[f % D]
+    auto fetch = [&](int f) -> u32x4 {
+        const uint32_t off = f < nsbw ? lane_base + 64u * static_cast<uint32_t>(f) : kOobOffset;
+        return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0));
+    };
 #pragma unroll
-    for (int i = 0; i < kRing; ++i) ring[i] = fetch(i);
-    lut_fill(lut, tid, T);
-    stage_chunks(0, raw);
-    for (int base = T * SU; base < chunks; base += T * SU) {  // large M * K only
-        load_chunks(base, raw);
-        stage_chunks(base, raw);
-    }
-    if (M < 16) {  // the zero row, in every plane
-        const u32x4 z = {0u, 0u, 0u, 0u};
-#pragma unroll
-        for (int p = 0; p < LY::kPlanes; ++p)
-            for (int b = 16 * tid; b < pitch; b += 16 * T)
-                *reinterpret_cast<u32x4 *>(xs + p * plane_bytes + M * pitch + b) = z;
-    }
-    __syncthreads();
+    for (int i = 0; i < D; ++i) ring[i] = fetch(i);
 
-    // ---- stream: lane (r, q) reads row r (the zero row for r >= M), limb q ----
-    const uint8_t *xl = xs + (r < M ? r : M) * pitch + s0 * kSbBytes + q * (kTrits * 2);
-    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int f0 = 0; f0 < nsbw; f0 += kRing) {
+    // ---- 2. decode tables (shared, at a fixed address: lookups need no base add),
+    //         then this wave's activations into its own LDS ----
+    lut_fill(lut, tid, 64 * W);
+    __syncthreads();
+    stage_chunks(0, raw);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // ---- 3. stream: lane (r, q) pairs row r of the group with token row r ----
+    // Two accumulators (even / odd MFMAs of a sub-block) halve the dependency chain.
+    const uint8_t *xl = xs + (r < M ? r : 0) * pitch + q * (kTrits * 2);
+    floatx4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int i = 0; i < kRing; ++i) {
-            const int f = f0 + i;
-            // decode slot i before its refill is issued: the refill then reuses the
-            // slot's registers and the ring needs no copies across iterations
-            uint32_t pairs[24];
-            if (f < nsbw) {
+    for (int f = 0; f < R; ++f) {
+        uint32_t pairs[24];
+        if (f < nsbw) {
 #pragma unroll
-                for (int d = 0; d < 4; ++d) decode_dword(lut, ring[i][d], pairs + 6 * d);
+            for (int d = 0; d < 4; ++d) decode_dword(lut, ring[f % D][d], pairs + 6 * d);
+        }
+        // the refill reuses the slot's registers once they are decoded; its count
+        // is fixed at compile time, so the loads stay counted exactly
+        __builtin_amdgcn_sched_barrier(0);
+        if (f + D < R) ring[f % D] = fetch(f + D);
+        if (f < nsbw) {
+            const uint8_t *src = xl + f * kSbBytes;
+            bf16x8 bh[6], bl[6];
+#pragma unroll
+            for (int j = 0; j < 6; ++j) {
+                bh[j] = *reinterpret_cast<const bf16x8 *>(src + 16 * j);
+                if constexpr (XT == kDtypeF32)
+                    bl[j] = *reinterpret_cast<const bf16x8 *>(src + plane_bytes + 16 * j);
             }
-            __builtin_amdgcn_sched_barrier(0);
-            ring[i] = fetch(f + kRing);
-            if (f < nsbw) {
-                const uint8_t *src = xl + f * kSbBytes;
-                bf16x8 bh[6], bl[6];
-#pragma unroll
-                for (int j = 0; j < 6; ++j) {
-                    bh[j] = *reinterpret_cast<const bf16x8 *>(src + 16 * j);
-                    if constexpr (XT == kDtypeF32)
-                        bl[j] = *reinterpret_cast<const bf16x8 *>(src + plane_bytes + 16 * j);
-                }
-                acc = mfma_pairs<XT>(pairs, bh, bl, acc);
-            }
+            mfma_pairs2<XT>(pairs, bh, bl, acc0, acc1);
         }
     }
 
-    // ---- reduce the W partial tiles, one element per thread ----
-    red[wave * 64 + lane] = acc;
+    // ---- 4. per group: sum the wg partial tiles, one element per thread ----
+    red[wave * 64 + lane] = acc0 + acc1;
     __syncthreads();
     const float *redf = reinterpret_cast<const float *>(red);
-    for (int e = tid; e < 256; e += T) {
-        float v = redf[e];
-#pragma unroll
-        for (int ww = 1; ww < W; ++ww) v += redf[ww * 256 + e];
+    for (int t = tid; t < G * 256; t += 64 * W) {
+        const int gg = t >> 8;
+        const int e = t & 255;
+        const int64_t n0g = (static_cast<int64_t>(blockIdx.x) * G + gg) * 16;
+        float v = redf[(gg * wg) * 256 + e];
+        for (int pp = 1; pp < wg; ++pp) v += redf[(gg * wg + pp) * 256 + e];
         const int le = e >> 2;  // lane of the tile that held element e
         const int m = le & 15;
-        const int64_t n = n0 + 4 * (le >> 4) + (e & 3);
+        const int64_t n = n0g + 4 * (le >> 4) + (e & 3);
         if (m < M && n < N) {
             if constexpr (XT == kDtypeI8) {
                 int32_t *cp = static_cast<int32_t *>(c) + static_cast<int64_t>(m) * N + n;
@@ -520,72 +554,111 @@ hipError_t launch_stream(const void *x, const uint8_t *w, void *c, int m, int64_
     return hipGetLastError();
 }
 
-// Dynamic LDS of the group kernel: 160 KiB per CU less its static tables.
-constexpr size_t kMaxGroupLds = 160 * 1024 - kLutBytes - 16 * 64 * 16;
+// Dynamic LDS of the wave kernel: 160 KiB per CU less its static reduction tile.
+constexpr size_t kMaxWaveLds = 160 * 1024 - 16 * 64 * 16 - kLutBytes;
 
-template <int XT, int W, int SU>
-hipError_t launch_group(const void *x, const uint8_t *w, void *c, int m, int64_t n, int64_t k,
-                        int L, int nsb, uint32_t magic, bool aligned, size_t lds, float alpha,
-                        float beta, const float *bias, hipStream_t s) {
-    auto fn = reinterpret_cast<const void *>(&gemv_group_kernel<XT, W, SU>);
+struct WaveArgs {
+    const void *x;
+    const uint8_t *w;
+    void *c;
+    int m;
+    int64_t n, k;
+    int L, nsb, wg, nsbw_max;
+    uint32_t magic;
+    bool aligned;
+    size_t lds;
+    float alpha, beta;
+    const float *bias;
+    hipStream_t s;
+};
+
+template <int XT, int W, int SU, int R>
+hipError_t launch_wave(const WaveArgs &a) {
+    auto fn = reinterpret_cast<const void *>(&gemv_wave_kernel<XT, W, SU, R>);
     static size_t raised = 64 * 1024;  // dynamic LDS above 64 KiB needs an opt-in
-    if (lds > raised) {
+    if (a.lds > raised) {
         const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 static_cast<int>(kMaxGroupLds));
+                                                 static_cast<int>(kMaxWaveLds));
         if (e != hipSuccess) return e;
-        raised = kMaxGroupLds;
+        raised = kMaxWaveLds;
     }
-    gemv_group_kernel<XT, W, SU><<<dim3((n + 15) / 16), dim3(64 * W), lds, s>>>(
-        x, w, c, m, n, k, L, nsb, magic, aligned ? 1 : 0, alpha, beta, bias);
+    const int G = W / a.wg;
+    const int64_t groups = (a.n + 15) / 16;
+    gemv_wave_kernel<XT, W, SU, R><<<dim3((groups + G - 1) / G), dim3(64 * W), a.lds, a.s>>>(
+        a.x, a.w, a.c, a.m, a.n, a.k, a.L, a.nsb, a.wg, a.nsbw_max, a.magic, a.aligned ? 1 : 0,
+        a.alpha, a.beta, a.bias);
     return hipGetLastError();
 }
 
-template <int XT, int W>
-hipError_t launch_group_su(int su, const void *x, const uint8_t *w, void *c, int m, int64_t n,
-                           int64_t k, int L, int nsb, uint32_t magic, bool aligned, size_t lds,
-                           float alpha, float beta, const float *bias, hipStream_t s) {
-    if (su <= 2)
-        return launch_group<XT, W, 2>(x, w, c, m, n, k, L, nsb, magic, aligned, lds, alpha, beta,
-                                      bias, s);
-    if (su <= 4)
-        return launch_group<XT, W, 4>(x, w, c, m, n, k, L, nsb, magic, aligned, lds, alpha, beta,
-                                      bias, s);
-    return launch_group<XT, W, 8>(x, w, c, m, n, k, L, nsb, magic, aligned, lds, alpha, beta,
-                                  bias, s);
+// Run length R: every value for bf16 activations (the decode case); 4 / 8 / 12 for
+// fp32 and int8, whose spare loads matter less next to their staging cost.
+template <int XT, int W, int SU, int R = kMaxRun>
+hipError_t launch_wave_r(int run, const WaveArgs &a) {
+    if constexpr (R <= 1) {
+        return launch_wave<XT, W, SU, 1>(a);
+    } else if constexpr (XT != kDtypeBF16 && R % 4 != 0) {
+        return launch_wave_r<XT, W, SU, R - 1>(run, a);
+    } else {
+        const int lower = XT == kDtypeBF16 ? R - 1 : R - 4;
+        if (run > lower || (XT != kDtypeBF16 && R == 4)) return launch_wave<XT, W, SU, R>(a);
+        return launch_wave_r<XT, W, SU, R - 1>(run, a);
+    }
 }
+
+template <int XT, int W>
+hipError_t launch_wave_su(int su, int run, const WaveArgs &a) {
+    if (su <= 4) return launch_wave_r<XT, W, 4>(run, a);
+    return launch_wave_r<XT, W, 8>(run, a);
+}
+
+// Waves in flight the wave kernel aims for before it splits K finer.
+constexpr int64_t kTargetWaves = 1024;
 
 template <int XT>
 hipError_t launch_gemv_x(const void *x, const uint8_t *w, void *c, int m, int64_t n, int64_t k,
                          float alpha, float beta, const float *bias, hipStream_t s) {
-    using LY = GroupLayout<XT>;
+    using LY = WaveLayout<XT>;
     const int elem = LY::kElem;
     const int64_t L = (k + kTrits - 1) / kTrits;
     const int64_t groups = (n + 15) / 16;
+    const int64_t nsb = (L + 3) / 4;
     const bool aligned8 = (k % 8 == 0) && (reinterpret_cast<uintptr_t>(x) % (8 * elem) == 0);
-    // group kernel: activations staged whole; per-group weight offsets below 2^31
-    if (L > 0 && L <= (1 << 22)) {
-        const int nsb = static_cast<int>((L + 3) / 4);
-        const size_t lds = static_cast<size_t>(LY::kPlanes) * group_rows(m) * group_pitch(nsb);
-        // waves per group: enough waves in flight (groups * W >= 2048 where possible),
-        // at least two sub-blocks per wave
-        int W = groups >= 512 ? 4 : (groups >= 256 ? 8 : 16);
-        while (W > 4 && nsb < 2 * W) W /= 2;
-        const int64_t chunks = static_cast<int64_t>(m) * nsb * LY::kChunksPerSb;
-        const int su = static_cast<int>((chunks + 64 * W - 1) / (64 * W));
-        if (lds <= kMaxGroupLds) {
-            const bool aligned =
-                (k % LY::kChunkVals == 0) && (reinterpret_cast<uintptr_t>(x) % 16 == 0);
-            const int cpr = nsb * LY::kChunksPerSb;
-            const uint32_t magic = static_cast<uint32_t>((uint64_t{1} << 32) / cpr + 1);
-            const int Li = static_cast<int>(L);
-            if (W == 4)
-                return launch_group_su<XT, 4>(su, x, w, c, m, n, k, Li, nsb, magic, aligned, lds,
-                                              alpha, beta, bias, s);
-            if (W == 8)
-                return launch_group_su<XT, 8>(su, x, w, c, m, n, k, Li, nsb, magic, aligned, lds,
-                                              alpha, beta, bias, s);
-            return launch_group_su<XT, 16>(su, x, w, c, m, n, k, Li, nsb, magic, aligned, lds,
-                                           alpha, beta, bias, s);
+    // longest run per wave: the run's loads and its activation loads all in flight
+    const int64_t max_run = std::min<int64_t>(
+        kMaxRun, (64 * kMaxChunksPerLane) / (static_cast<int64_t>(m) * LY::kChunksPerSb));
+    // waves per group: the fewest that fit the run, then more while the grid is
+    // small and every wave keeps at least two sub-blocks
+    int wg = 1;
+    while (wg <= 8 && max_run > 0 && nsb > max_run * wg) wg *= 2;
+    if (L > 0 && max_run > 0 && wg <= 8) {
+        while (wg < 8 && groups * wg < kTargetWaves && nsb >= 4 * wg) wg *= 2;
+        const int W = wg < 4 ? 4 : wg;
+        const int nsbw_max = static_cast<int>((nsb + wg - 1) / wg);
+        const size_t lds =
+            static_cast<size_t>(W) * wave_lds_bytes(m, nsbw_max, LY::kPlanes);
+        const int cpr = nsbw_max * LY::kChunksPerSb;
+        const int su = (m * cpr + 63) / 64;
+        if (lds <= kMaxWaveLds && su <= kMaxChunksPerLane) {
+            WaveArgs a;
+            a.x = x;
+            a.w = w;
+            a.c = c;
+            a.m = m;
+            a.n = n;
+            a.k = k;
+            a.L = static_cast<int>(L);
+            a.nsb = static_cast<int>(nsb);
+            a.wg = wg;
+            a.nsbw_max = nsbw_max;
+            a.magic = static_cast<uint32_t>((uint64_t{1} << 32) / cpr + 1);
+            a.aligned = (k % LY::kChunkVals == 0) && (reinterpret_cast<uintptr_t>(x) % 16 == 0);
+            a.lds = lds;
+            a.alpha = alpha;
+            a.beta = beta;
+            a.bias = bias;
+            a.s = s;
+            if (W == 4) return launch_wave_su<XT, 4>(su, nsbw_max, a);
+            return launch_wave_su<XT, 8>(su, nsbw_max, a);
         }
     }
     if (aligned8) return launch_stream<XT, 2, true>(x, w, c, m, n, k, L, alpha, beta, bias, s);
