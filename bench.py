@@ -162,6 +162,84 @@ def run_sweep(torch, ops, lib, dev) -> list:
     return rows
 
 
+# ------------------------------------------------------------------ profiles --
+# Summaries of rocprofv3 output (CSV format) for profiles/.  No GPU needed.
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_decode_llama_gate_m1_traffic.txt")
+
+
+def _read_csv(path: str) -> list:
+    import csv
+    with open(path, newline="") as f:
+        return list(csv.DictReader(f))
+
+
+def _find(d: str, suffix: str) -> str:
+    for name in sorted(os.listdir(d)):
+        if name.endswith(suffix):
+            return os.path.join(d, name)
+    raise FileNotFoundError(f"no *{suffix} in {d}")
+
+
+def summarize_trace(d: str, cmd: str, top: int = 8) -> str:
+    """Kernel table of a `rocprofv3 --kernel-trace --stats --output-format csv` run."""
+    rows = _read_csv(_find(d, "kernel_stats.csv"))
+    rows.sort(key=lambda r: -float(r["TotalDurationNs"]))
+    out = [f"command: {cmd}", "",
+           f"{'calls':>6} {'avg_us':>9} {'min_us':>9} {'max_us':>9} {'total_%':>8}  kernel"]
+    for r in rows[:top]:
+        out.append(f"{int(r['Calls']):6d} {float(r['AverageNs']) / 1e3:9.2f} "
+                   f"{float(r['MinNs']) / 1e3:9.2f} {float(r['MaxNs']) / 1e3:9.2f} "
+                   f"{float(r['Percentage']):8.2f}  {r['Name'][:110]}")
+    return "\n".join(out) + "\n"
+
+
+def _counter_median(d: str, kernel_sub: str, counter: str) -> tuple:
+    import statistics
+    vals = [float(r["Counter_Value"]) for r in _read_csv(_find(d, "counter_collection.csv"))
+            if kernel_sub in r["Kernel_Name"] and r["Counter_Name"] == counter]
+    if not vals:
+        raise ValueError(f"no {counter} rows for '{kernel_sub}' in {d}")
+    return statistics.median(vals), len(vals)
+
+
+def summarize_traffic(kernel: str, kfetch: str, kwrite: str, cfetch: str, cwrite: str,
+                      copy_bytes: int, algo_bytes: int, cmds: list) -> str:
+    """HBM bytes per launch of `kernel` from FETCH_SIZE / WRITE_SIZE runs, each scaled by
+    what the same counter reads for a plain copy (torch.neg) of `copy_bytes` each way."""
+    cf, _ = _counter_median(cfetch, "elementwise_kernel", "FETCH_SIZE")
+    cw, _ = _counter_median(cwrite, "elementwise_kernel", "WRITE_SIZE")
+    kf, nf = _counter_median(kfetch, kernel, "FETCH_SIZE")
+    kw, nw = _counter_median(kwrite, kernel, "WRITE_SIZE")
+    f_scale = copy_bytes / (cf * 1024.0)
+    w_scale = copy_bytes / (cw * 1024.0)
+    fetch = kf * 1024.0 * f_scale
+    write = kw * 1024.0 * w_scale
+    out = ["commands:"] + [f"  {c}" for c in cmds] + [
+        "",
+        f"kernel: {kernel}",
+        f"copy calibration: torch.neg over {copy_bytes} B each way; FETCH_SIZE reads "
+        f"{cf:.1f} KiB (scale {f_scale:.4f}), WRITE_SIZE reads {cw:.1f} KiB (scale {w_scale:.4f})",
+        f"kernel FETCH_SIZE median {kf:.1f} KiB over {nf} dispatches -> {fetch:.0f} B",
+        f"kernel WRITE_SIZE median {kw:.1f} KiB over {nw} dispatches -> {write:.0f} B",
+        f"algorithmic bytes per launch: {algo_bytes}",
+        f"hbm_bytes_per_launch: {int(round(fetch + write))}",
+        f"traffic / algorithmic: {(fetch + write) / algo_bytes:.4f}",
+    ]
+    return "\n".join(out) + "\n"
+
+
+def read_traffic(path: str = TRAFFIC_FILE):
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("hbm_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -187,7 +265,23 @@ def main() -> int:
                          "for the HBM byte counters")
     ap.add_argument("--sweep", action="store_true",
                     help="also time the config-3/4 shapes and print a table on stderr")
+    ap.add_argument("--summarize-trace", metavar="DIR",
+                    help="print the kernel table of a rocprofv3 csv --stats run and exit")
+    ap.add_argument("--summarize-traffic", nargs=4, metavar=("KFETCH", "KWRITE", "CFETCH", "CWRITE"),
+                    help="print calibrated HBM bytes per GEMV launch from rocprofv3 --pmc "
+                         "FETCH_SIZE / WRITE_SIZE runs of the GEMV and of the copy, and exit")
+    ap.add_argument("--cmd", action="append", default=[],
+                    help="command line(s) that produced the profile, for the summary")
     args = ap.parse_args()
+    if args.summarize_trace:
+        sys.stdout.write(summarize_trace(args.summarize_trace, " | ".join(args.cmd)))
+        return 0
+    if args.summarize_traffic:
+        K, N = 4096, 14336
+        wb = 16 * N * ((K + 47) // 48)
+        sys.stdout.write(summarize_traffic("gemv", *args.summarize_traffic, copy_bytes=wb,
+                                           algo_bytes=gemv_bytes(1, N, K), cmds=args.cmd))
+        return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the packed-ternary path is a single-GPU kernel set "
               "(multi-GPU sharding is a design note only); run with --gpus 1", file=sys.stderr)
@@ -304,7 +398,8 @@ def main() -> int:
     if gemv_ms:
         achieved = gbytes / (gemv_ms * 1e-3) / 1e9
         line["roofline"] = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS,
-                            "unit": "GB/s", "frac": achieved / HBM_PEAK_GBPS, "traffic": None}
+                            "unit": "GB/s", "frac": achieved / HBM_PEAK_GBPS,
+                            "traffic": read_traffic()}
         line["tokens_per_s_equiv"] = M / (gemv_ms * 1e-3)
     if cpu:
         line["cpu_baseline"] = cpu

@@ -119,6 +119,26 @@ int t81_hip_ternary_matmul_kernel(int which, const void *x, int x_dtype, const u
 int t81_hip_gemm_ternary_limb(const uint8_t *a, const uint8_t *b, float *c, int m, int n, int k,
                               float alpha, float beta, void *stream);
 
+/* Elementwise float32 ops of the backend contract, over n contiguous elements,
+ * bit-exact with the reference's CPU loops (each multiply and add rounded
+ * separately; a NaN condition counts as nonzero; a NaN clamp input passes
+ * through).  In-place use (out equal to an input) is allowed.
+ *   where:   out[i] = cond[i] != 0 ? x[i] : y[i]
+ *   clamp:   out[i] = in[i] < lo ? lo : (in[i] > hi ? hi : in[i])
+ *   lerp:    out[i] = start[i] + weight[i] * (end[i] - start[i])
+ *   addcmul: out[i] = in[i] + value * t1[i] * t2[i]
+ * Replace: t81::linalg::detail::rocm_where / rocm_clamp / rocm_lerp /
+ *          rocm_addcmul, include/t81/linalg/gemm_gpu.hpp:80-85, 233-249, with the
+ *          semantics of cpu_where / cpu_clamp / cpu_lerp / cpu_addcmul,
+ *          src/linalg/gemm_dispatch.cpp:145-211. */
+int t81_hip_where(const float *cond, const float *x, const float *y, float *out, int64_t n,
+                  void *stream);
+int t81_hip_clamp(const float *in, float *out, int64_t n, float lo, float hi, void *stream);
+int t81_hip_lerp(const float *start, const float *end, const float *weight, float *out,
+                 int64_t n, void *stream);
+int t81_hip_addcmul(const float *in, const float *t1, const float *t2, float value, float *out,
+                    int64_t n, void *stream);
+
 /* Host-only test hook, no device needed: writes the 16 x 27 tryte-contribution
  * table K4 uses (constant-evaluated like build_tryte_contributions,
  * include/t81/linalg/gemm.hpp:28-41), so it can be compared bit for bit. */

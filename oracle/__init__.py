@@ -38,11 +38,17 @@ _i64p = ctypes.POINTER(ctypes.c_int64)
 
 
 def build(reference: bool = True) -> None:
-    """Runs oracle/Makefile (the reference build only when its tree exists)."""
+    """Runs oracle/Makefile (the reference builds only when its tree exists; the plugin
+    check also needs libt81_hip.so, so build that first)."""
     targets = ["oracle"]
     if reference and os.path.isdir("/root/reference/src/linalg"):
         targets.append("ref")
+        if os.path.exists(os.path.join(os.path.dirname(HERE), "t81lib_amd", "libt81_hip.so")):
+            targets.append("plugin")
     subprocess.run(["make", "-s", "-C", HERE, *targets], check=True)
+
+
+PLUGIN_CHECK = os.path.join(HERE, "_ref", "plugin_check")
 
 
 def _ptr(a: np.ndarray, typ):
@@ -57,6 +63,10 @@ def _load_oracle() -> ctypes.CDLL:
     lib.orc_quantize_trit.argtypes = [ctypes.c_float, ctypes.c_float, ctypes.c_int]
     lib.orc_torch_threshold.restype = ctypes.c_float
     lib.orc_torch_threshold.argtypes = [ctypes.c_double]
+    for name in ("orc_where", "orc_lerp"):
+        getattr(lib, name).argtypes = [_f32p, _f32p, _f32p, _f32p, ctypes.c_int64]
+    lib.orc_clamp.argtypes = [_f32p, _f32p, ctypes.c_int64, ctypes.c_float, ctypes.c_float]
+    lib.orc_addcmul.argtypes = [_f32p, _f32p, _f32p, ctypes.c_float, _f32p, ctypes.c_int64]
     lib.orc_tryte_of.restype = ctypes.c_uint8
     lib.orc_tryte_of.argtypes = [ctypes.c_int] * 3
     lib.orc_trits_of.argtypes = [ctypes.c_uint8, _i8p]
@@ -272,6 +282,16 @@ class Ref:
                                                  ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                                  ctypes.c_float, ctypes.c_float]
         lib.t81ref_simd_path.restype = ctypes.c_char_p
+        for name in ("t81ref_where", "t81ref_lerp"):
+            getattr(lib, name).argtypes = [_f32p, _f32p, _f32p, _f32p, ctypes.c_longlong]
+        lib.t81ref_clamp.argtypes = [_f32p, _f32p, ctypes.c_longlong, ctypes.c_float,
+                                     ctypes.c_float]
+        lib.t81ref_addcmul.argtypes = [_f32p, _f32p, _f32p, ctypes.c_float, _f32p,
+                                       ctypes.c_longlong]
+
+    def elementwise(self, op: str, a, b=None, c=None, p0: float = 0.0, p1: float = 0.0):
+        """The reference's where / clamp / lerp / addcmul on Backend::CPU."""
+        return _elementwise(self.lib, "t81ref_", op, a, b, c, p0, p1)
 
     def tryte_table(self) -> np.ndarray:
         out = np.empty(16 * 27, np.float64)
@@ -361,3 +381,27 @@ def ref(variant: Optional[str] = None) -> Optional[Ref]:
     r = Ref(ctypes.CDLL(path), variant)
     _ref_cache[variant] = r
     return r
+
+
+def _elementwise(lib, prefix: str, op: str, a, b=None, c=None, p0: float = 0.0, p1: float = 0.0):
+    a = np.ascontiguousarray(a, np.float32)
+    n = a.size
+    out = np.empty_like(a)
+    if op == "clamp":
+        getattr(lib, prefix + "clamp")(_ptr(a, _f32p), _ptr(out, _f32p), n, p0, p1)
+        return out
+    b = np.ascontiguousarray(b, np.float32)
+    c = np.ascontiguousarray(c, np.float32)
+    if op == "addcmul":
+        getattr(lib, prefix + "addcmul")(_ptr(a, _f32p), _ptr(b, _f32p), _ptr(c, _f32p), p0,
+                                         _ptr(out, _f32p), n)
+    else:
+        getattr(lib, prefix + op)(_ptr(a, _f32p), _ptr(b, _f32p), _ptr(c, _f32p),
+                                  _ptr(out, _f32p), n)
+    return out
+
+
+def elementwise(op: str, a, b=None, c=None, p0: float = 0.0, p1: float = 0.0) -> np.ndarray:
+    """Oracle where (a=cond, b=x, c=y) / clamp (a, p0=lo, p1=hi) / lerp (a=start, b=end,
+    c=weight) / addcmul (a=input, b=t1, c=t2, p0=value) over float32 arrays."""
+    return _elementwise(lib(), "orc_", op, a, b, c, p0, p1)

@@ -17,6 +17,8 @@
 //   t81::core::detail::mul_wide_scalar            include/t81/core/detail/simd_impl.hpp:212-223
 //   t81::core::limb::from_value / from_trits      include/t81/core/limb.hpp:131-158
 //   random_limb (mt19937_64 + uniform_int(0,26))  tests/unit/test_limb_basic.cpp:58-66 (restated)
+//   t81::linalg::detail::where / clamp / lerp / addcmul on Backend::CPU
+//                                                 src/linalg/gemm_dispatch.cpp:239-322
 
 #include <array>
 #include <cstdint>
@@ -26,6 +28,8 @@
 #include <stdexcept>
 
 #include <t81/linalg/gemm.hpp>
+#include <t81/linalg/gemm_gpu.hpp>
+#include <t81/tensor_metadata.hpp>
 
 using t81::core::limb;
 
@@ -175,6 +179,32 @@ const char *t81ref_simd_path(void) {
         return "avx2";
     }
     return "scalar";
+}
+
+// Elementwise ops through the reference's public dispatch, forced to the CPU loops.
+static t81::TensorMetadata f32(const float *p, long long n) {
+    return t81::make_contiguous_metadata(static_cast<std::size_t>(n), const_cast<float *>(p));
+}
+
+void t81ref_where(const float *cond, const float *x, const float *y, float *out, long long n) {
+    auto mc = f32(cond, n), mx = f32(x, n), my = f32(y, n), mo = f32(out, n);
+    t81::linalg::detail::where(mc, mx, my, mo, t81::linalg::Backend::CPU);
+}
+
+void t81ref_clamp(const float *in, float *out, long long n, float lo, float hi) {
+    auto mi = f32(in, n), mo = f32(out, n);
+    t81::linalg::detail::clamp(mi, mo, lo, hi, t81::linalg::Backend::CPU);
+}
+
+void t81ref_lerp(const float *s, const float *e, const float *w, float *out, long long n) {
+    auto ms = f32(s, n), me = f32(e, n), mw = f32(w, n), mo = f32(out, n);
+    t81::linalg::detail::lerp(ms, me, mw, mo, t81::linalg::Backend::CPU);
+}
+
+void t81ref_addcmul(const float *in, const float *t1, const float *t2, float value, float *out,
+                    long long n) {
+    auto mi = f32(in, n), m1 = f32(t1, n), m2 = f32(t2, n), mo = f32(out, n);
+    t81::linalg::detail::addcmul(mi, m1, m2, value, mo, t81::linalg::Backend::CPU);
 }
 
 } // extern "C"

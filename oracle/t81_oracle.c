@@ -351,3 +351,28 @@ void orc_trit_matmul_i64(const int8_t *x, int64_t M, int64_t K, const uint8_t *w
         }
     }
 }
+
+/* ------------------------------------------------------------- §8(f)4 ----
+ * Elementwise float32 ops of the backend contract: the CPU loops of
+ * src/linalg/gemm_dispatch.cpp:145-211 (cpu_where :145-161, cpu_clamp :163-177,
+ * cpu_lerp :179-194, cpu_addcmul :196-211), each operation rounded separately
+ * (this file is built with -ffp-contract=off). */
+void orc_where(const float *cond, const float *x, const float *y, float *out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = cond[i] != 0.0f ? x[i] : y[i];
+}
+
+void orc_clamp(const float *in, float *out, int64_t n, float lo, float hi) {
+    for (int64_t i = 0; i < n; ++i) {
+        const float v = in[i];
+        out[i] = v < lo ? lo : (v > hi ? hi : v);
+    }
+}
+
+void orc_lerp(const float *s, const float *e, const float *w, float *out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = s[i] + w[i] * (e[i] - s[i]);
+}
+
+void orc_addcmul(const float *in, const float *t1, const float *t2, float value, float *out,
+                 int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = in[i] + value * t1[i] * t2[i];
+}

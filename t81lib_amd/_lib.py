@@ -45,6 +45,10 @@ EXPORTS = (
     "t81_hip_ternary_matmul",
     "t81_hip_ternary_matmul_kernel",
     "t81_hip_gemm_ternary_limb",
+    "t81_hip_where",
+    "t81_hip_clamp",
+    "t81_hip_lerp",
+    "t81_hip_addcmul",
     "t81_hip_limb_tryte_table",
 )
 
@@ -84,6 +88,14 @@ def _declare(lib: ctypes.CDLL) -> None:
                                                   _f, _vp, _vp]
     lib.t81_hip_gemm_ternary_limb.restype = _i
     lib.t81_hip_gemm_ternary_limb.argtypes = [_vp, _vp, _vp, _i, _i, _i, _f, _f, _vp]
+    lib.t81_hip_where.restype = _i
+    lib.t81_hip_where.argtypes = [_vp, _vp, _vp, _vp, _i64, _vp]
+    lib.t81_hip_clamp.restype = _i
+    lib.t81_hip_clamp.argtypes = [_vp, _vp, _i64, _f, _f, _vp]
+    lib.t81_hip_lerp.restype = _i
+    lib.t81_hip_lerp.argtypes = [_vp, _vp, _vp, _vp, _i64, _vp]
+    lib.t81_hip_addcmul.restype = _i
+    lib.t81_hip_addcmul.argtypes = [_vp, _vp, _vp, _f, _vp, _i64, _vp]
     lib.t81_hip_limb_tryte_table.restype = None
     lib.t81_hip_limb_tryte_table.argtypes = [_vp]
 

@@ -11,6 +11,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <initializer_list>
 #include <string>
 
 #include "../../include/t81_hip.h"
@@ -236,6 +237,54 @@ int t81_hip_gemm_ternary_limb(const uint8_t *a, const uint8_t *b, float *c, int 
     return finish(t81hip::launch_gemm_limb(a, b, c, m, n, k / 48, alpha, beta,
                                            static_cast<hipStream_t>(stream)),
                   "t81_hip_gemm_ternary_limb");
+}
+
+// src/linalg/gemm_dispatch.cpp:145-211: the CPU loops check matching lengths; here the
+// caller passes one length, so only n >= 0 and the pointers are checked.
+static int check_elementwise(int64_t n, std::initializer_list<const void *> ptrs) {
+    if (n < 0) return fail(T81_HIP_EINVAL_SHAPE, "element count must be non-negative");
+    if (n > 0)
+        for (const void *p : ptrs) {
+            if (p == nullptr)
+                return fail(T81_HIP_EINVAL_POINTER,
+                            "tensor metadata must provide a valid data pointer");
+            if (reinterpret_cast<uintptr_t>(p) % 4 != 0)
+                return fail(T81_HIP_EINVAL_POINTER, "float32 data must be 4-byte aligned");
+        }
+    return T81_HIP_OK;
+}
+
+int t81_hip_where(const float *cond, const float *x, const float *y, float *out, int64_t n,
+                  void *stream) {
+    if (int rc = check_elementwise(n, {cond, x, y, out})) return rc;
+    if (int rc = require_device("t81_hip_where")) return rc;
+    return finish(t81hip::launch_where(cond, x, y, out, n, static_cast<hipStream_t>(stream)),
+                  "t81_hip_where");
+}
+
+int t81_hip_clamp(const float *in, float *out, int64_t n, float lo, float hi, void *stream) {
+    if (int rc = check_elementwise(n, {in, out})) return rc;
+    if (int rc = require_device("t81_hip_clamp")) return rc;
+    return finish(t81hip::launch_clamp(in, out, n, lo, hi, static_cast<hipStream_t>(stream)),
+                  "t81_hip_clamp");
+}
+
+int t81_hip_lerp(const float *start, const float *end, const float *weight, float *out,
+                 int64_t n, void *stream) {
+    if (int rc = check_elementwise(n, {start, end, weight, out})) return rc;
+    if (int rc = require_device("t81_hip_lerp")) return rc;
+    return finish(
+        t81hip::launch_lerp(start, end, weight, out, n, static_cast<hipStream_t>(stream)),
+        "t81_hip_lerp");
+}
+
+int t81_hip_addcmul(const float *in, const float *t1, const float *t2, float value, float *out,
+                    int64_t n, void *stream) {
+    if (int rc = check_elementwise(n, {in, t1, t2, out})) return rc;
+    if (int rc = require_device("t81_hip_addcmul")) return rc;
+    return finish(
+        t81hip::launch_addcmul(in, t1, t2, value, out, n, static_cast<hipStream_t>(stream)),
+        "t81_hip_addcmul");
 }
 
 void t81_hip_limb_tryte_table(double *out) { t81hip::host_tryte_table(out); }

@@ -37,4 +37,14 @@ hipError_t launch_gemm(const void *x, int x_dtype, const uint8_t *w, void *c, in
 hipError_t launch_gemm_limb(const uint8_t *a, const uint8_t *b, float *c, int m, int n,
                             int k_limbs, float alpha, float beta, hipStream_t s);
 
+// elementwise.hip: the backend contract's where / clamp / lerp / addcmul (float32)
+hipError_t launch_where(const float *cond, const float *x, const float *y, float *out, int64_t n,
+                        hipStream_t s);
+hipError_t launch_clamp(const float *in, float *out, int64_t n, float lo, float hi,
+                        hipStream_t s);
+hipError_t launch_lerp(const float *start, const float *end, const float *weight, float *out,
+                       int64_t n, hipStream_t s);
+hipError_t launch_addcmul(const float *in, const float *t1, const float *t2, float value,
+                          float *out, int64_t n, hipStream_t s);
+
 }  // namespace t81hip

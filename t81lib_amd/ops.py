@@ -219,3 +219,67 @@ __all__ = [
     "quantize_pack", "quantize", "pack_cols", "unpack", "count_invalid_bytes", "ternary_matmul",
     "gemm_limb", "limb_tryte_table", "limbs_for", "torch_threshold",
 ]
+
+
+# -- elementwise float32 ops of the backend contract (gemm_gpu.hpp:80-85, 233-249) --------
+
+def _f32_operands(*tensors: torch.Tensor) -> list:
+    n = tensors[0].numel()
+    out = []
+    for i, t in enumerate(tensors):
+        _require_cuda(t, f"operand {i}")
+        if t.dtype != torch.float32:
+            raise ValueError("tensor metadata must describe float32 data")
+        if t.numel() != n:
+            raise ValueError("input shapes must match")
+        out.append(t.contiguous())
+    return out
+
+
+def _f32_out(out: Optional[torch.Tensor], like: torch.Tensor) -> torch.Tensor:
+    if out is None:
+        return torch.empty_like(like)
+    _require_cuda(out, "out")
+    if out.dtype != torch.float32 or out.numel() != like.numel() or not out.is_contiguous():
+        raise ValueError("out must be a contiguous float32 GPU tensor of the inputs' size")
+    return out
+
+
+def where(condition: torch.Tensor, x: torch.Tensor, y: torch.Tensor,
+          out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """out = condition != 0 ? x : y (cpu_where, src/linalg/gemm_dispatch.cpp:145-161)."""
+    c, a, b = _f32_operands(condition, x, y)
+    out = _f32_out(out, a)
+    _lib.check(_lib.lib().t81_hip_where(c.data_ptr(), a.data_ptr(), b.data_ptr(),
+                                        out.data_ptr(), a.numel(), _stream()))
+    return out
+
+
+def clamp(x: torch.Tensor, min_value: float, max_value: float,
+          out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """cpu_clamp, src/linalg/gemm_dispatch.cpp:163-177."""
+    (a,) = _f32_operands(x)
+    out = _f32_out(out, a)
+    _lib.check(_lib.lib().t81_hip_clamp(a.data_ptr(), out.data_ptr(), a.numel(),
+                                        float(min_value), float(max_value), _stream()))
+    return out
+
+
+def lerp(start: torch.Tensor, end: torch.Tensor, weight: torch.Tensor,
+         out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """start + weight * (end - start) (cpu_lerp, src/linalg/gemm_dispatch.cpp:179-194)."""
+    s, e, w = _f32_operands(start, end, weight)
+    out = _f32_out(out, s)
+    _lib.check(_lib.lib().t81_hip_lerp(s.data_ptr(), e.data_ptr(), w.data_ptr(), out.data_ptr(),
+                                       s.numel(), _stream()))
+    return out
+
+
+def addcmul(x: torch.Tensor, tensor1: torch.Tensor, tensor2: torch.Tensor, value: float,
+            out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """x + value * tensor1 * tensor2 (cpu_addcmul, src/linalg/gemm_dispatch.cpp:196-211)."""
+    a, t1, t2 = _f32_operands(x, tensor1, tensor2)
+    out = _f32_out(out, a)
+    _lib.check(_lib.lib().t81_hip_addcmul(a.data_ptr(), t1.data_ptr(), t2.data_ptr(),
+                                          float(value), out.data_ptr(), a.numel(), _stream()))
+    return out

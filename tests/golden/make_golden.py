@@ -15,6 +15,9 @@ source.  Vectors:
 * ``emb_*``                  gemm_ternary on one-value-per-limb embeddings: small integers
                              as limbs, which turns the limb GEMM into an exact integer GEMM
                              (the cross-check of the trit-dot oracle)
+* ``ew_*``                   where / clamp / lerp / addcmul on Backend::CPU
+                             (src/linalg/gemm_dispatch.cpp:145-211) over float32 arrays
+                             with NaN, +-inf, -0.0, denormals and zeros mixed in
 """
 
 from __future__ import annotations
@@ -114,6 +117,20 @@ def main() -> None:
     out.update(emb_T=T, emb_X=X, emb_out=emb)
 
     path = os.path.join(HERE, "ref_vectors.npz")
+    # elementwise ops of the backend contract
+    ew = np.random.default_rng(11)
+    n = 257
+    a, b, c = (ew.standard_normal(n).astype(np.float32) * 2 for _ in range(3))
+    specials = np.array([np.nan, np.inf, -np.inf, -0.0, 0.0, 1e-45, 3e38, -3e38, 1.0, -1.0],
+                        np.float32)
+    for arr, shift in ((a, 0), (b, 3), (c, 7)):
+        arr[: specials.size] = np.roll(specials, shift)
+    a[20:60:3] = 0.0
+    out.update(ew_a=a, ew_b=b, ew_c=c,
+               ew_where=ref.elementwise("where", a, b, c),
+               ew_clamp=ref.elementwise("clamp", a, p0=-0.75, p1=1.25),
+               ew_lerp=ref.elementwise("lerp", a, b, c),
+               ew_addcmul=ref.elementwise("addcmul", a, b, c, p0=0.3))
     np.savez_compressed(path, **out)
     print(f"wrote {path} ({os.path.getsize(path)} bytes, SIMD path {ref.simd_path()})")
 

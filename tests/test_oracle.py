@@ -273,3 +273,56 @@ def test_trit_matmul_against_numpy(orc):
     Xi = rng.integers(-128, 128, (M, K)).astype(np.int8)
     np.testing.assert_array_equal(orc.trit_matmul_i64(Xi, packed, K),
                                   Xi.astype(np.int64) @ T.T.astype(np.int64))
+
+
+def _same_or_both_nan(got: np.ndarray, want: np.ndarray) -> bool:
+    got = np.asarray(got, np.float32)
+    want = np.asarray(want, np.float32)
+    nan = np.isnan(want)
+    return bool(np.array_equal(np.isnan(got), nan)
+                and np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32)))
+
+
+EW_CASES = (("where", {}), ("clamp", dict(p0=-0.75, p1=1.25)), ("lerp", {}),
+            ("addcmul", dict(p0=0.3)))
+
+
+def test_elementwise_golden(orc, golden):
+    """where / clamp / lerp / addcmul equal the reference's CPU loops bit for bit
+    (src/linalg/gemm_dispatch.cpp:145-211, vectors from the compiled reference)."""
+    a, b, c = golden["ew_a"], golden["ew_b"], golden["ew_c"]
+    for op, kw in EW_CASES:
+        got = orc.elementwise(op, a, b, c, **kw)
+        assert _same_or_both_nan(got, golden["ew_" + op]), op
+
+
+def test_elementwise_closed_forms(orc):
+    nan, inf = np.float32(np.nan), np.float32(np.inf)
+    x = np.array([1.0, 2.0, 3.0, 4.0], np.float32)
+    y = np.array([-1.0, -2.0, -3.0, -4.0], np.float32)
+    cond = np.array([nan, -0.0, 0.0, 5.0], np.float32)
+    # a NaN condition is "!= 0" (takes x); -0.0 and 0.0 take y
+    np.testing.assert_array_equal(orc.elementwise("where", cond, x, y), [1.0, -2.0, -3.0, 4.0])
+    v = np.array([nan, -inf, inf, -0.75, 1.25, 0.5, -0.0], np.float32)
+    got = orc.elementwise("clamp", v, p0=-0.75, p1=1.25)
+    assert np.isnan(got[0]) and list(got[1:]) == [-0.75, 1.25, -0.75, 1.25, 0.5, 0.0]
+    s = np.array([1.5, -2.0, 1e30], np.float32)
+    e = np.array([7.0, 3.0, -1e30], np.float32)
+    np.testing.assert_array_equal(orc.elementwise("lerp", s, e, np.zeros(3, np.float32)), s)
+    # separate roundings: 0.1f * 3.0f rounds before the add (an FMA would round once)
+    t1 = np.array([0.1], np.float32)
+    t2 = np.array([3.0], np.float32)
+    want = np.float32(np.float32(np.float32(0.7) * t1[0]) * t2[0])
+    got = orc.elementwise("addcmul", np.zeros(1, np.float32), t1, t2, p0=0.7)
+    assert got[0] == want
+
+
+@pytest.mark.skipif("not __import__('oracle').ref()", reason="oracle/_ref not built here")
+def test_elementwise_matches_compiled_reference_live(orc):
+    ref = orc.ref()
+    rng = np.random.default_rng(12)
+    a, b, c = (rng.standard_normal(1001).astype(np.float32) for _ in range(3))
+    a[::5] = 0.0
+    for op, kw in EW_CASES:
+        assert _same_or_both_nan(orc.elementwise(op, a, b, c, **kw),
+                                 ref.elementwise(op, a, b, c, **kw)), op
