@@ -18,7 +18,8 @@ CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libt81_hip.so")
 ARCH = "gfx950"
 
-SOURCES = ["abi.hip", "pack.hip", "gemv.hip", "gemm.hip", "limb.hip", "elementwise.hip"]
+SOURCES = ["abi.hip", "pack.hip", "gemv.hip", "gemv_diag.hip", "gemm.hip", "limb.hip",
+           "elementwise.hip"]
 
 # -packed-fp32-ops: no v_pk_*_f32 from the compiler (they are never written by hand either).
 HIPCC_FLAGS = [
@@ -26,7 +27,6 @@ HIPCC_FLAGS = [
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     "-Wall",
     "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
@@ -42,16 +42,35 @@ def hipcc() -> str:
 
 
 def build(verbose: bool = False) -> str:
-    """Compiles the library (always; it is the build check) and returns its path."""
-    srcs = [os.path.join(CSRC, s) for s in SOURCES]
+    """Compiles the library (always; it is the build check) and returns its path.
+    Each source compiles to its own object in parallel, then one shared link."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    objdir = os.path.join(HERE, "_obj")
+    os.makedirs(objdir, exist_ok=True)
+    jobs = []
+    for src in SOURCES:
+        obj = os.path.join(objdir, os.path.splitext(src)[0] + ".o")
+        jobs.append((obj, [hipcc(), *HIPCC_FLAGS, "-c", "-o", obj, os.path.join(CSRC, src)]))
+
+    def run(cmd):
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        return subprocess.run(cmd, capture_output=True, text=True)
+
+    workers = max(1, min(len(jobs), os.cpu_count() or 1))
+    with ThreadPoolExecutor(max_workers=workers) as pool:
+        results = list(pool.map(run, [cmd for _, cmd in jobs]))
+    for (obj, _), proc in zip(jobs, results):
+        if proc.returncode != 0:
+            sys.stderr.write(proc.stdout + proc.stderr)
+            raise RuntimeError(f"hipcc failed compiling {os.path.basename(obj)}")
     tmp = LIB + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, "-o", tmp, *srcs]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    proc = subprocess.run(cmd, capture_output=True, text=True)
+    proc = run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp,
+                *[obj for obj, _ in jobs]])
     if proc.returncode != 0:
         sys.stderr.write(proc.stdout + proc.stderr)
-        raise RuntimeError("hipcc failed building libt81_hip.so")
+        raise RuntimeError("hipcc failed linking libt81_hip.so")
     os.replace(tmp, LIB)
     return LIB
 

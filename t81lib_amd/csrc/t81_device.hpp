@@ -61,46 +61,6 @@ __device__ __forceinline__ void lut_fill(uint8_t *lds, int tid, int nthreads) {
     }
 }
 
-// The same tables as a constant image, built at compile time.
-struct LutImage {
-    uint32_t words[kLutBytes / 4];
-};
-
-__host__ __device__ constexpr LutImage make_lut_image() {
-    LutImage img{};
-    for (int i = 0; i < kLutBytes / 4; ++i) {
-        const int off = 4 * i;
-        const bool in_e = off < kLutF;
-        const int rel = in_e ? off - kLutE : off - kLutF;
-        const int u = rel / 8;
-        const int part = (rel % 8) / 4;
-        uint32_t v = 0u;
-        if (rel >= 0 && u < 27 && off < kLutF + 8 * 27) {
-            const uint32_t b0 = bf16_bits_of_trit(trit_of(u, 0));
-            const uint32_t b1 = bf16_bits_of_trit(trit_of(u, 1));
-            const uint32_t b2 = bf16_bits_of_trit(trit_of(u, 2));
-            if (in_e) v = part == 0 ? (b0 | (b1 << 16)) : b2;
-            else v = part == 0 ? (b0 << 16) : (b1 | (b2 << 16));
-        }
-        img.words[i] = v;
-    }
-    return img;
-}
-
-// Global copy of the table image (ordinary global memory, read-only in practice:
-// a `const` object would live in the constant address space and be read with
-// flat loads).
-__device__ LutImage kLutImage = make_lut_image();
-
-// One wave copies the tables into its LDS: 16 bytes per lane, kLutBytes = 33 * 16.
-__device__ __forceinline__ void lut_copy(uint8_t *lds, int lane) {
-    static_assert(kLutBytes % 16 == 0 && kLutBytes / 16 <= 64, "one 16-byte piece per lane");
-    typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
-    if (lane < kLutBytes / 16)
-        reinterpret_cast<u32x4_t *>(lds)[lane] =
-            reinterpret_cast<const u32x4_t *>(kLutImage.words)[lane];
-}
-
 __device__ __forceinline__ void lut_init(uint8_t *lds, int tid, int nthreads) {
     lut_fill(lds, tid, nthreads);
     __syncthreads();
