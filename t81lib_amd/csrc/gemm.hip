@@ -10,7 +10,7 @@
 // exact while |sum| < 2^24, which the ABI enforces through K <= 131071).
 //
 // Tiling.  A workgroup of WN x WM waves computes a (32*RN*WN) x (32*CM*WM)
-// tile of C^T (weight rows x tokens).  Per k-step of kLK limbs (96 trits):
+// tile of C^T (weight rows x tokens).  Per k-step of LK limbs (48 * LK trits):
 //  * the activation tile (tokens x 96) goes global -> registers -> LDS,
 //    double-buffered, one barrier per k-step;
 //  * every wave loads its own weight rows straight into registers -- lane
@@ -30,12 +30,11 @@ namespace {
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kLK = 2;                          // limbs per k-step
-constexpr int kStepK = kLK * kTrits;            // 96 trits
-constexpr int kRowBytes = kStepK * 2 + 16;      // bf16 tile row + pad (bank spread)
-
-template <int XT, int RN, int CM, int WN, int WM>
+template <int XT, int RN, int CM, int WN, int WM, int LK>
 struct GemmCfg {
+    static constexpr int kLK = LK;                        // limbs per k-step
+    static constexpr int kStepK = kLK * kTrits;           // trits per k-step
+    static constexpr int kRowBytes = kStepK * 2 + 16;     // bf16 tile row + pad (bank spread)
     static constexpr int kThreads = 64 * WN * WM;
     static constexpr int kBN = 32 * RN * WN;  // weight rows per workgroup
     static constexpr int kBM = 32 * CM * WM;  // tokens per workgroup
@@ -104,16 +103,19 @@ __device__ __forceinline__ u32x2 load_half_limb(const uint8_t *w, int64_t row, i
                                                 int h, int64_t N, int64_t L) {
     if (row < N && limb < L) {
         const u32x2 *p = reinterpret_cast<const u32x2 *>(w + (row * L + limb) * kTrytes + 8 * h);
-        return __builtin_nontemporal_load(p);
+        return *p;
     }
     return u32x2{0x0D0D0D0Du, 0x0D0D0D0Du};  // all-zero trits
 }
 
-template <int XT, int RN, int CM, int WN, int WM, bool kAligned>
+template <int XT, int RN, int CM, int WN, int WM, int LK, bool kAligned>
 __global__ __launch_bounds__(64 * WN * WM) void gemm_kernel(
     const void *__restrict__ x, const uint8_t *__restrict__ w, void *__restrict__ c, int64_t M,
     int64_t N, int64_t K, int64_t L, float alpha, float beta, const float *__restrict__ bias) {
-    using Cfg = GemmCfg<XT, RN, CM, WN, WM>;
+    using Cfg = GemmCfg<XT, RN, CM, WN, WM, LK>;
+    constexpr int kLK = Cfg::kLK;
+    constexpr int kStepK = Cfg::kStepK;
+    constexpr int kRowBytes = Cfg::kRowBytes;
     __shared__ __attribute__((aligned(16))) uint8_t lut[kLutBytes];
     __shared__ __attribute__((aligned(16))) uint8_t xs[2][Cfg::kPlanes][Cfg::kTileBytes];
 
@@ -294,19 +296,19 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_kernel(
     }
 }
 
-template <int XT, int RN, int CM, int WN, int WM>
+template <int XT, int RN, int CM, int WN, int WM, int LK>
 hipError_t launch_gemm_t(const void *x, const uint8_t *w, void *c, int64_t m, int64_t n,
                          int64_t k, float alpha, float beta, const float *bias, hipStream_t s) {
-    using Cfg = GemmCfg<XT, RN, CM, WN, WM>;
+    using Cfg = GemmCfg<XT, RN, CM, WN, WM, LK>;
     const int64_t L = (k + kTrits - 1) / kTrits;
     const int64_t tiles = ((n + Cfg::kBN - 1) / Cfg::kBN) * ((m + Cfg::kBM - 1) / Cfg::kBM);
     const int elem = XT == kDtypeF32 ? 4 : (XT == kDtypeBF16 ? 2 : 1);
     const bool aligned = (k % 8 == 0) && (reinterpret_cast<uintptr_t>(x) % (8 * elem) == 0);
     if (aligned)
-        gemm_kernel<XT, RN, CM, WN, WM, true><<<dim3(tiles), dim3(Cfg::kThreads), 0, s>>>(
+        gemm_kernel<XT, RN, CM, WN, WM, LK, true><<<dim3(tiles), dim3(Cfg::kThreads), 0, s>>>(
             x, w, c, m, n, k, L, alpha, beta, bias);
     else
-        gemm_kernel<XT, RN, CM, WN, WM, false><<<dim3(tiles), dim3(Cfg::kThreads), 0, s>>>(
+        gemm_kernel<XT, RN, CM, WN, WM, LK, false><<<dim3(tiles), dim3(Cfg::kThreads), 0, s>>>(
             x, w, c, m, n, k, L, alpha, beta, bias);
     return hipGetLastError();
 }
@@ -314,9 +316,20 @@ hipError_t launch_gemm_t(const void *x, const uint8_t *w, void *c, int64_t m, in
 template <int XT>
 hipError_t launch_gemm_x(const void *x, const uint8_t *w, void *c, int64_t m, int64_t n,
                          int64_t k, float alpha, float beta, const float *bias, hipStream_t s) {
-    if (m <= 32) return launch_gemm_t<XT, 2, 1, 4, 1>(x, w, c, m, n, k, alpha, beta, bias, s);
-    if (m <= 64) return launch_gemm_t<XT, 2, 2, 4, 1>(x, w, c, m, n, k, alpha, beta, bias, s);
-    return launch_gemm_t<XT, 2, 4, 4, 1>(x, w, c, m, n, k, alpha, beta, bias, s);
+    constexpr int LK = 2;  // limbs per k-step
+    if (m <= 32) return launch_gemm_t<XT, 2, 1, 4, 1, LK>(x, w, c, m, n, k, alpha, beta, bias, s);
+    if (m <= 64) return launch_gemm_t<XT, 2, 2, 4, 1, LK>(x, w, c, m, n, k, alpha, beta, bias, s);
+    if constexpr (XT != kDtypeF32) {
+        // Eight waves (two per SIMD, so one wave's waits are covered by the other's
+        // MFMAs): 256 x 256 tiles while there are enough of them to spread over the
+        // GPU, 256 weight rows x 128 tokens otherwise (measured crossover ~160 tiles).
+        const int64_t tiles_big = ((n + 255) / 256) * ((m + 255) / 256);
+        if (tiles_big >= 160)
+            return launch_gemm_t<XT, 2, 4, 4, 2, LK>(x, w, c, m, n, k, alpha, beta, bias, s);
+        return launch_gemm_t<XT, 2, 2, 4, 2, LK>(x, w, c, m, n, k, alpha, beta, bias, s);
+    }
+    // fp32 activations: two LDS planes; four waves with 256 x 128 tiles
+    return launch_gemm_t<XT, 2, 4, 4, 1, LK>(x, w, c, m, n, k, alpha, beta, bias, s);
 }
 
 }  // namespace

@@ -17,7 +17,7 @@
 // leaving token m's sums in lane 16 - T + m.  Per sub-block the work is then only
 // the weight decode (16 table lookups) and eight MFMAs: no activation traffic at all.
 //
-// T = M rounded up to 1, 2 or 4, so a run holds at most 16 / T sub-blocks; R, the
+// T = M (1 or 2), so a run holds at most 16 / T sub-blocks; R, the
 // run length, is a template constant so every wave issues the same number of
 // weight loads (exact s_waitcnt counts); a wave with nsbw < R points its spare
 // loads past the buffer's range, where they return zeros without touching memory.
@@ -279,8 +279,7 @@ hipError_t launch_diag_r(int run, const DiagArgs &a) {
 template <int XT, int W>
 hipError_t launch_diag_t(int t, int run, const DiagArgs &a) {
     if (t == 1) return launch_diag_r<XT, W, 1>(run, a);
-    if (t == 2) return launch_diag_r<XT, W, 2>(run, a);
-    return launch_diag_r<XT, W, 4>(run, a);
+    return launch_diag_r<XT, W, 2>(run, a);
 }
 
 // Waves in flight the kernel aims for before it splits K finer.
@@ -294,7 +293,7 @@ hipError_t launch_diag_x(bool *handled, const void *x, const uint8_t *w, void *c
     const int64_t L = (k + kTrits - 1) / kTrits;
     // M = 3, 4 (T = 4, runs of at most 4 sub-blocks) measured slower than gemv_wave_kernel
     if (m < 1 || m > 2 || L <= 0 || L > (1 << 22)) return hipSuccess;
-    const int T = m == 1 ? 1 : (m == 2 ? 2 : 4);
+    const int T = m;  // 1 or 2
     const int64_t max_run = 16 / T;
     const int64_t groups = (n + 15) / 16;
     const int64_t nsb = (L + 3) / 4;
