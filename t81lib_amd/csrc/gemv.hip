@@ -2,6 +2,9 @@
 //
 //   C[m, n] = alpha * sum_k X[m, k] * T[n, k] + beta * C[m, n] + bias[n]
 //
+// launch_gemv sends M <= 4 to the column-strip kernel (gemv_strip.hip); the kernels
+// here take M = 5 .. 16 and the shapes the strip kernel declines.
+//
 // The packed weights (N x L x 16 bytes, the reference layout) are the only large
 // stream, so the kernel is HBM-bound: every weight byte is read exactly once,
 // with 16-byte loads, and decoded in registers.  The multiply-accumulate runs
@@ -123,10 +126,7 @@ struct WaveLayout {
 
 constexpr int kSbBytes = 4 * kTrits * 2;  // one staged sub-block row: 192 bf16
 constexpr int kMaxRun = 12;               // sub-blocks per wave
-#ifndef T81_GEMV_DEPTH
-#define T81_GEMV_DEPTH 4
-#endif
-constexpr int kDepth = T81_GEMV_DEPTH;    // weight loads in flight per wave
+constexpr int kDepth = 4;                 // weight loads in flight per wave
 constexpr int kMaxChunksPerLane = 8;      // activation loads per lane, all in flight at once
 constexpr uint32_t kOobOffset = 0x80000000u;
 
@@ -523,7 +523,7 @@ hipError_t launch_gemv(const void *x, int x_dtype, const uint8_t *w, void *c, in
                        int64_t k, float alpha, float beta, const float *bias, hipStream_t s) {
     if (m == 0 || n == 0) return hipSuccess;
     bool handled = false;
-    const hipError_t e = launch_gemv_diag(&handled, x, x_dtype, w, c, m, n, k, alpha, beta, bias, s);
+    const hipError_t e = launch_gemv_strip(&handled, x, x_dtype, w, c, m, n, k, alpha, beta, bias, s);
     if (handled || e != hipSuccess) return e;
     switch (x_dtype) {
         case kDtypeBF16: return launch_gemv_x<kDtypeBF16>(x, w, c, m, n, k, alpha, beta, bias, s);

@@ -1,5 +1,5 @@
 // t81lib_amd/csrc/gemv_common.hpp -- pieces shared by the decode-GEMV kernels
-// (gemv.hip, gemv_diag.hip): activation loads, limb loads, the MFMA step.
+// (gemv.hip, gemv_strip.hip): activation loads, limb loads, the MFMA step.
 // Everything here has internal linkage: each translation unit gets its own copy.
 #pragma once
 

@@ -1,0 +1,362 @@
+// t81lib_amd/csrc/gemv_strip.hip -- K2 for M <= 4 tokens: column strips, activations
+// fixed in registers, wide contiguous weight loads.
+//
+//   C[m, n] = alpha * sum_k X[m, k] * T[n, k] + beta * C[m, n] + bias[n]
+//
+// The limbs of a row are cut into ranges of 4*S consecutive limbs (S = 16 or 8 for one
+// token, 8 for two, 4 for up to four).  A workgroup owns H = R * RPI consecutive rows
+// (RPI = 16 / S); wave w of it streams range w of all of them (a column "strip"), so the activations
+// a lane needs never change: they are loaded once, as the B operand of
+// v_mfma_f32_16x16x32_bf16, and stay in registers.  One load instruction covers RPI
+// rows x 4*S limbs, i.e. RPI contiguous runs of 64*S bytes (1 KB, 2 x 512 B or 4 x 256 B),
+// where a 16-rows x 64 B pattern splits every load into 16 pieces.
+//
+// Lane (i, q) (i = lane % 16, q = lane / 16) of load t supplies A row i, k-slots of
+// quarter q: with a = i / S and s = i % S it holds limb l0 + q*S + s of row
+// row0 + t*RPI + a.  Lane (j, q) of B holds the activations of token j / S for limb
+// l0 + q*S + j % S.  An MFMA sums over the quarters, D[i][j] = sum_q A(i, q) . B(j, q),
+// and A(i, q) meets the activations of its own limb exactly when j % S == i % S: that
+// entry is row a's partial sum over the limbs l0 + q*S + s (q = 0..3) for token j / S.
+// The other entries mix limbs and are never read.  Each load has its own accumulator
+// (started at zero); lane (j, q) holds D[4q + e][j] for e < 4 and keeps element j % 4,
+// which for S in {4, 8, 16} is the one matched entry it holds, if any.  The MFMA count
+// per weight byte is the same for every M <= RPI; tokens past M have zero activations.
+//
+// The weights are decoded in padded order (each tryte -> bf16 t0, t1, t2, 0 through
+// one 8-byte table read), eight MFMAs per limb; the activations carry a zero in every
+// fourth slot to match.  Limbs past L read nothing (their loads point past the buffer
+// range and return zeros, which decode to finite trits) and meet zero activations;
+// rows past N read zeros and are never stored.
+//
+// At the end each wave writes its kept values to LDS and every output sums its S
+// sub-sums per range over the ranges in a fixed order: no atomics, deterministic results.
+#include <algorithm>
+
+#include "gemv_common.hpp"
+#include "t81_device.hpp"
+#include "t81_kernels.hpp"
+
+namespace t81hip {
+
+namespace {
+
+constexpr int kStripMaxWaves = 8;    // waves per workgroup (2 per SIMD: 256 registers each)
+constexpr int kStripDepth = 8;       // weight loads in flight per wave
+constexpr uint32_t kStripOob = 0x80000000u;
+
+// Padded-order decode of one dword (4 trytes) through the E table: eight dwords, each
+// pair a finished half of an MFMA operand (bf16 t0 | t1 << 16, t2 | 0 << 16).
+__device__ __forceinline__ void strip_decode(const uint8_t *lds, uint32_t w, uint32_t *out) {
+    const uint32_t w8 = w << 3;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        const uint32_t a = (w8 >> (8 * b)) & 0xFFu;
+        const uint2 e = *reinterpret_cast<const uint2 *>(lds + kLutE + a);
+        out[2 * b] = e.x;
+        out[2 * b + 1] = e.y;
+    }
+}
+
+// Natural-order bf16 activations (48 values) -> the eight padded operands:
+// operand o = (x[6o], x[6o+1], x[6o+2], 0, x[6o+3], x[6o+4], x[6o+5], 0).
+__device__ __forceinline__ void strip_pad(const bf16x8 *nat, bf16x8 *out) {
+    uint32_t d[24];
+#pragma unroll
+    for (int j = 0; j < 6; ++j) {
+        const u32x4 v = __builtin_bit_cast(u32x4, nat[j]);
+        d[4 * j] = v[0];
+        d[4 * j + 1] = v[1];
+        d[4 * j + 2] = v[2];
+        d[4 * j + 3] = v[3];
+    }
+#pragma unroll
+    for (int o = 0; o < 8; ++o) {
+        const u32x4 q = {d[3 * o], d[3 * o + 1] & 0xFFFFu,
+                         __builtin_amdgcn_alignbit(d[3 * o + 2], d[3 * o + 1], 16),
+                         d[3 * o + 2] >> 16};
+        out[o] = __builtin_bit_cast(bf16x8, q);
+    }
+}
+
+// acc += A x B over the eight padded operands of one limb (fp32: hi and lo planes).
+template <int XT>
+__device__ __forceinline__ floatx4 strip_mfma(const uint32_t *pairs, const bf16x8 *bh,
+                                              const bf16x8 *bl) {
+    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int o = 0; o < 8; ++o) {
+        const u32x4 araw = {pairs[4 * o], pairs[4 * o + 1], pairs[4 * o + 2], pairs[4 * o + 3]};
+        const bf16x8 a = __builtin_bit_cast(bf16x8, araw);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bh[o], acc, 0, 0, 0);
+        if constexpr (XT == kDtypeF32)
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bl[o], acc, 0, 0, 0);
+    }
+    return acc;
+}
+
+// Element j % 4 of a finished accumulator (lane j = lane % 16).
+__device__ __forceinline__ float strip_keep(floatx4 v, int j) {
+    const float lo = (j & 1) ? v[1] : v[0];
+    const float hi = (j & 1) ? v[3] : v[2];
+    return (j & 2) ? hi : lo;
+}
+
+// S: sub-positions per quarter (range = 4*S limbs, S in {4, 8, 16}); NW: waves, one range
+// each at a time; R: loads per range, i.e. R * (16 / S) rows per workgroup.
+template <int XT, int S, int NW, int R>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void gemv_strip_kernel(
+    const void *__restrict__ x, const uint8_t *__restrict__ w, void *__restrict__ c, int M,
+    int64_t N, int64_t K, int L, int nranges, int x_aligned, float alpha, float beta,
+    const float *__restrict__ bias) {
+    static_assert(S == 4 || S == 8 || S == 16, "one matched entry per lane needs S >= 4");
+    constexpr int RPI = 16 / S;  // rows per load (and tokens per MFMA)
+    constexpr int H = R * RPI;   // rows per workgroup
+    constexpr int D = R < kStripDepth ? R : kStripDepth;
+    __shared__ __attribute__((aligned(16))) uint8_t lut[kLutBytes];
+    __shared__ float red[NW][R][64];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int i = lane & 15;
+    const int q = lane >> 4;
+    const int64_t row0 = static_cast<int64_t>(blockIdx.x) * H;
+
+    // Weights: a buffer based at the workgroup's first row; rows past N read zeros.
+    const int64_t remain = (N - row0) * L * kTrytes;
+    const int nrec = remain < 0x7FFFFFFF ? static_cast<int>(remain) : 0x7FFFFFFF;
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(w + row0 * L * kTrytes), 0, nrec, 0x00020000);
+    const uint32_t row_bytes = static_cast<uint32_t>(L) * kTrytes;
+    const int sub = q * S + i % S;  // the lane's limb within a range, for A and for B
+
+    auto publish_lut = [&]() {
+        lut_fill(lut, tid, 64 * NW);
+        __syncthreads();
+    };
+
+    float kept[R];
+#pragma unroll
+    for (int t = 0; t < R; ++t) kept[t] = 0.0f;
+
+    bool first = true;
+    for (int rg = wave; rg < nranges; rg += NW) {
+        const int limb = rg * 4 * S + sub;
+        const bool in_row = limb < L;
+        // ---- B: activations of token i / S for the lane's limb ----
+        const int mb = i / S;
+        const bool bvalid = mb < M && in_row;
+        const int64_t xrow = static_cast<int64_t>(mb < M ? mb : 0) * K;
+        const int64_t kb = static_cast<int64_t>(limb) * kTrits;
+        XRaw xr[6];
+        if (x_aligned) {
+#pragma unroll
+            for (int j = 0; j < 6; ++j)
+                xr[j] = load_x8_raw<XT, true>(x, xrow, kb + 8 * j, K, bvalid);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 6; ++j)
+                xr[j] = load_x8_raw<XT, false>(x, xrow, kb + 8 * j, K, bvalid);
+        }
+
+        // ---- A: load t = the lane's limb of row t * RPI + i / S ----
+        const uint32_t lane_off = in_row ? static_cast<uint32_t>(i / S) * row_bytes +
+                                               static_cast<uint32_t>(limb) * kTrytes
+                                         : kStripOob;
+        auto fetch = [&](int t) -> u32x4 {
+            const uint32_t off = in_row ? lane_off + static_cast<uint32_t>(t * RPI) * row_bytes
+                                        : kStripOob;
+            return __builtin_bit_cast(u32x4,
+                                      __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0));
+        };
+        u32x4 ring[D];  // load t lives in ring[t % D]
+#pragma unroll
+        for (int t = 0; t < D; ++t) ring[t] = fetch(t);
+
+        if (first) {
+            publish_lut();
+            first = false;
+        }
+
+        bf16x8 nh[6], nl[6], bh[8], bl[8];
+#pragma unroll
+        for (int j = 0; j < 6; ++j) cvt_x8<XT>(xr[j], nh[j], nl[j]);
+        strip_pad(nh, bh);
+        if constexpr (XT == kDtypeF32) strip_pad(nl, bl);
+
+        // Software-pipelined: the table reads of load t + 1 are issued before the
+        // MFMAs of load t; a ring slot is refilled as soon as it is decoded.  The
+        // accumulator of load t is read one load later, when its MFMAs are done.
+        uint32_t cur[32], nxt[32];
+#pragma unroll
+        for (int d = 0; d < 4; ++d) strip_decode(lut, ring[0][d], cur + 8 * d);
+        __builtin_amdgcn_sched_barrier(0);
+        if (D < R) ring[0] = fetch(D);
+        floatx4 prev = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < R; ++t) {
+            if (t + 1 < R) {
+#pragma unroll
+                for (int d = 0; d < 4; ++d) strip_decode(lut, ring[(t + 1) % D][d], nxt + 8 * d);
+                __builtin_amdgcn_sched_barrier(0);
+                if (t + 1 + D < R) ring[(t + 1) % D] = fetch(t + 1 + D);
+            }
+            const floatx4 acc = strip_mfma<XT>(cur, bh, bl);
+            if (t > 0) kept[t - 1] += strip_keep(prev, i);
+            prev = acc;
+#pragma unroll
+            for (int e = 0; e < 32; ++e) cur[e] = nxt[e];
+        }
+        kept[R - 1] += strip_keep(prev, i);
+    }
+    if (first) publish_lut();  // a wave with no range still takes part in the barriers
+
+    // ---- kept values to LDS; each output sums S sub-sums per wave, waves in order ----
+#pragma unroll
+    for (int t = 0; t < R; ++t) red[wave][t][lane] = kept[t];
+    __syncthreads();
+
+    const int nw_used = nranges < NW ? nranges : NW;
+    for (int e = tid; e < H * RPI; e += 64 * NW) {
+        const int r = e / RPI;  // row within the workgroup: load r / RPI, A row group r % RPI
+        const int m = e % RPI;
+        const int t = r / RPI;
+        const int ra = r % RPI;
+        const int64_t n = row0 + r;
+        if (m >= M || n >= N) continue;
+        float val = 0.0f;
+        for (int ww = 0; ww < nw_used; ++ww) {
+#pragma unroll
+            for (int ss = 0; ss < S; ++ss) {
+                // entry D[ra*S + ss][m*S + ss] sits in lane (m*S + ss) + 16 * ((ra*S + ss) / 4)
+                val += red[ww][t][m * S + ss + 16 * ((ra * S + ss) >> 2)];
+            }
+        }
+        if constexpr (XT == kDtypeI8) {
+            int32_t *cp = static_cast<int32_t *>(c) + static_cast<int64_t>(m) * N + n;
+            int32_t y = static_cast<int32_t>(val);
+            if (beta != 0.0f) y += *cp;
+            *cp = y;
+        } else {
+            float *cp = static_cast<float *>(c) + static_cast<int64_t>(m) * N + n;
+            float y = alpha * val;
+            if (beta != 0.0f) y = y + beta * *cp;
+            if (bias != nullptr) y = y + bias[n];
+            *cp = y;
+        }
+    }
+}
+
+struct StripArgs {
+    const void *x;
+    const uint8_t *w;
+    void *c;
+    int m;
+    int64_t n, k;
+    int L, nranges;
+    bool aligned;
+    float alpha, beta;
+    const float *bias;
+    hipStream_t s;
+};
+
+template <int XT, int S, int NW, int R>
+hipError_t launch_strip(const StripArgs &a) {
+    constexpr int H = R * (16 / S);
+    const int64_t blocks = (a.n + H - 1) / H;
+    gemv_strip_kernel<XT, S, NW, R><<<dim3(static_cast<unsigned>(blocks)), dim3(64 * NW), 0,
+                                       a.s>>>(a.x, a.w, a.c, a.m, a.n, a.k, a.L, a.nranges,
+                                              a.aligned ? 1 : 0, a.alpha, a.beta, a.bias);
+    return hipGetLastError();
+}
+
+template <int XT, int S, int R>
+hipError_t launch_strip_nw(int nw, const StripArgs &a) {
+    switch (nw) {
+        case 1: return launch_strip<XT, S, 1, R>(a);
+        case 2: return launch_strip<XT, S, 2, R>(a);
+        case 3: return launch_strip<XT, S, 3, R>(a);
+        case 4: return launch_strip<XT, S, 4, R>(a);
+        case 5: return launch_strip<XT, S, 5, R>(a);
+        case 6: return launch_strip<XT, S, 6, R>(a);
+        case 7: return launch_strip<XT, S, 7, R>(a);
+        default: return launch_strip<XT, S, 8, R>(a);
+    }
+}
+
+template <int XT, int S>
+hipError_t launch_strip_nr(int nw, int r, const StripArgs &a) {
+    if (r >= 16) return launch_strip_nw<XT, S, 16>(nw, a);
+    if (r >= 8) return launch_strip_nw<XT, S, 8>(nw, a);
+    return launch_strip_nw<XT, S, 4>(nw, a);
+}
+
+// Fewer waves than this leave SIMDs idle: shorter strips are then worth their extra
+// activation reads.
+constexpr int64_t kStripMinWaves = 1200;
+
+template <int XT>
+hipError_t launch_strip_x(bool *handled, const void *x, const uint8_t *w, void *c, int m,
+                          int64_t n, int64_t k, float alpha, float beta, const float *bias,
+                          hipStream_t s) {
+    *handled = false;
+    const int64_t L = (k + kTrits - 1) / kTrits;
+    if (m < 1 || m > 4 || n <= 0 || L <= 0) return hipSuccess;
+    // S = 16 (one row x 64 limbs per load) for one token when it pads the row no more
+    // than S = 8 does; S = 8 (2 rows x 32 limbs) up to 2 tokens; S = 4 up to 4.
+    const int64_t pad16 = (L + 63) / 64 * 64;
+    const int64_t pad8 = (L + 31) / 32 * 32;
+    const int S = m == 1 && pad16 <= pad8 ? 16 : (m <= 2 ? 8 : 4);
+    // buffer offsets within a workgroup's rows must stay below 2^31
+    constexpr int64_t kElem = XT == kDtypeF32 ? 4 : (XT == kDtypeBF16 ? 2 : 1);
+    if (64 * L * kTrytes >= 0x7FFFFFFF) return hipSuccess;
+    const int64_t nranges = (L + 4 * S - 1) / (4 * S);
+    // ranges per wave, then as few waves as that allows (balanced: 10 ranges -> 5 x 2)
+    const int64_t per_wave = (nranges + kStripMaxWaves - 1) / kStripMaxWaves;
+    const int nw = static_cast<int>((nranges + per_wave - 1) / per_wave);
+    StripArgs a;
+    a.x = x;
+    a.w = w;
+    a.c = c;
+    a.m = m;
+    a.n = n;
+    a.k = k;
+    a.L = static_cast<int>(L);
+    a.nranges = static_cast<int>(nranges);
+    a.aligned = (k % 8 == 0) && (reinterpret_cast<uintptr_t>(x) % (kElem == 1 ? 8 : 16) == 0);
+    a.alpha = alpha;
+    a.beta = beta;
+    a.bias = bias;
+    a.s = s;
+    *handled = true;
+    // Loads per strip R: a wave reads 4*S*M*48 activations per range against R KB of
+    // weights, so R starts at the first of 8, 16 that keeps that ratio (bf16 bytes) at
+    // or below 0.4; then it halves, down to 4, while the launch has fewer than 1200
+    // waves (longer strips also lengthen the compute tail after the last load).
+    const double x_ratio8 = 4.0 * S * m * kTrits * 2 / (8 * 1024.0);
+    int r = x_ratio8 <= 0.4 ? 8 : 16;
+    auto waves = [&](int rr) { return (n + rr * (16 / S) - 1) / (rr * (16 / S)) * nw; };
+    while (r > 4 && waves(r) < kStripMinWaves) r /= 2;
+    switch (S) {
+        case 16: return launch_strip_nr<XT, 16>(nw, r, a);
+        case 8: return launch_strip_nr<XT, 8>(nw, r, a);
+        default: return launch_strip_nr<XT, 4>(nw, r, a);
+    }
+}
+
+}  // namespace
+
+hipError_t launch_gemv_strip(bool *handled, const void *x, int x_dtype, const uint8_t *w,
+                             void *c, int m, int64_t n, int64_t k, float alpha, float beta,
+                             const float *bias, hipStream_t s) {
+    switch (x_dtype) {
+        case kDtypeBF16:
+            return launch_strip_x<kDtypeBF16>(handled, x, w, c, m, n, k, alpha, beta, bias, s);
+        case kDtypeF32:
+            return launch_strip_x<kDtypeF32>(handled, x, w, c, m, n, k, alpha, beta, bias, s);
+        default:
+            return launch_strip_x<kDtypeI8>(handled, x, w, c, m, n, k, alpha, beta, bias, s);
+    }
+}
+
+}  // namespace t81hip

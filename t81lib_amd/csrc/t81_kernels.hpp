@@ -28,11 +28,11 @@ hipError_t launch_validate(const uint8_t *packed, int64_t count, int32_t *bad, h
 hipError_t launch_gemv(const void *x, int x_dtype, const uint8_t *w, void *c, int m, int64_t n,
                        int64_t k, float alpha, float beta, const float *bias, hipStream_t s);
 
-// gemv_diag.hip (K2, M <= 2): sets *handled = false (and launches nothing) when the
+// gemv_strip.hip (K2, M <= 4): sets *handled = false (and launches nothing) when the
 // shape is outside what it covers
-hipError_t launch_gemv_diag(bool *handled, const void *x, int x_dtype, const uint8_t *w, void *c,
-                            int m, int64_t n, int64_t k, float alpha, float beta,
-                            const float *bias, hipStream_t s);
+hipError_t launch_gemv_strip(bool *handled, const void *x, int x_dtype, const uint8_t *w,
+                             void *c, int m, int64_t n, int64_t k, float alpha, float beta,
+                             const float *bias, hipStream_t s);
 
 // gemm.hip (K3): any M
 hipError_t launch_gemm(const void *x, int x_dtype, const uint8_t *w, void *c, int64_t m,

@@ -109,6 +109,34 @@ def test_int8_activations_bit_exact(gpu, orc, M, N, K):
     np.testing.assert_array_equal(out2.cpu().numpy().astype(np.int64), want + c0.numpy())
 
 
+# M <= 4 decode shapes for the column-strip kernel: one row x 64 limbs per load (M = 1
+# when that pads the row no more), 2 x 32 (M <= 2), 4 x 16 (M <= 4); several ranges per
+# wave (K = 30000, 14336 at M = 2, 8192 at M = 3), workgroups cut off at N, partial
+# last limbs, and K % 8 != 0 (element-wise activation loads).
+STRIP = [
+    (1, 77, 3072), (1, 50, 8192), (1, 33, 14336), (1, 40, 30000), (1, 300, 4096),
+    (2, 45, 14336), (2, 129, 4096), (3, 31, 8192), (4, 70, 14336), (4, 1000, 3072),
+    (3, 9, 100), (4, 18, 4100), (1, 5, 4100),
+]
+
+
+@pytest.mark.parametrize("M,N,K", STRIP)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.int8])
+def test_decode_strip_shapes(gpu, orc, M, N, K, dtype):
+    announce(f"strip {dtype} M={M} N={N} K={K}")
+    w, x, c, bias = make_problem(M, N, K, dtype, seed=11 * M + N + K)
+    if dtype == torch.int8:
+        packed, out = run(gpu, w, x, c, bias, K, 1.0, 0.0, False, kernel=2)
+        want = orc.trit_matmul_i64(x.numpy(), packed, K)
+        np.testing.assert_array_equal(out.numpy().astype(np.int64), want)
+        return
+    for alpha, beta, use_bias in ((1.0, 0.0, False), (0.5, 1.0, True)):
+        packed, out = run(gpu, w, x, c, bias, K, alpha, beta, use_bias, kernel=2)
+        ref, scale = oracle_matmul(orc, x, packed, K, alpha, beta, c, bias if use_bias else None)
+        ok, worst, nbad = fp_tolerance_ok(out.numpy(), ref, scale, RTOL[dtype])
+        assert ok, f"alpha={alpha} beta={beta}: {nbad} outside, worst rel {worst:.3g}"
+
+
 @pytest.mark.parametrize("M", [1, 8, 16])
 def test_gemv_and_gemm_kernels_agree(gpu, orc, M):
     """M <= 16 is valid for both kernels: each must match the oracle on its own."""
