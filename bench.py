@@ -144,6 +144,45 @@ def run_sweep(torch, ops, lib, dev) -> list:
             log(f"gemv {name:14s} M={m:2d} {k:5d}->{n:5d}: {ms * 1e3:7.2f} us  {gbs:7.0f} GB/s")
         del wb
         torch.cuda.empty_cache()
+    # decode straight from GGUF TQ2_0 payloads (66 bytes per 256 weights)
+    from t81lib_amd import gguf
+    for name, k, n in [("llama.gate", 4096, 14336), ("llama.down", 14336, 4096),
+                       ("phi3.gate_up", 3072, 16384)]:
+        pbytes = n * gguf.row_bytes(k, "TQ2_0")
+        copies = max(4, -(-2 * MALL_BYTES // pbytes) + 2)
+        g = torch.Generator(dev).manual_seed(5)
+        wb = [gguf.quantize_tensor(torch.randn((n, k), generator=g, device=dev), "TQ2_0", 0.45)
+              for _ in range(copies)]
+        for m in (1, 4):
+            x = torch.randn((m, k), device=dev).to(torch.bfloat16)
+            out = torch.empty((m, n), device=dev)
+            ms = time_graph(torch, lambda w: gguf.tq2_matmul(x, w, k, c=out), wb, 512, 32)
+            nbytes = pbytes + 2 * m * k + 4 * m * n
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            rows.append({"shape": name, "format": "TQ2_0", "M": m, "K": k, "N": n,
+                         "us": ms * 1e3, "GBps": gbs, "frac_hbm": gbs / HBM_PEAK_GBPS})
+            log(f"tq2  {name:14s} M={m:2d} {k:5d}->{n:5d}: {ms * 1e3:7.2f} us  {gbs:7.0f} GB/s")
+        del wb
+        torch.cuda.empty_cache()
+    # TQ2_0 / TQ1_0 codecs over an 8192 x 3072 float32 matrix
+    src = [torch.randn((8192, 3072), device=dev) for _ in range(4)]
+    for quant in ("TQ2_0", "TQ1_0"):
+        ms = time_graph(torch, lambda w: gguf.quantize_tensor(w, quant, 0.45), src, 64, 8)
+        nbytes = 4 * 8192 * 3072 + 8192 * gguf.row_bytes(3072, quant)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        rows.append({"shape": f"{quant} quantize 8192x3072", "us": ms * 1e3, "GBps": gbs,
+                     "frac_hbm": gbs / HBM_PEAK_GBPS})
+        log(f"{quant} quantize 8192x3072: {ms * 1e3:7.2f} us  {gbs:7.0f} GB/s")
+        payloads = [gguf.quantize_tensor(w, quant, 0.45) for w in src]
+        ms = time_graph(torch, lambda p: gguf.dequantize_tensor(p, (8192, 3072), quant),
+                        payloads, 64, 8)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        rows.append({"shape": f"{quant} dequantize 8192x3072", "us": ms * 1e3, "GBps": gbs,
+                     "frac_hbm": gbs / HBM_PEAK_GBPS})
+        log(f"{quant} dequantize 8192x3072: {ms * 1e3:7.2f} us  {gbs:7.0f} GB/s")
+        del payloads
+    del src
+    torch.cuda.empty_cache()
     prefill = [("llama.qkv", 4096, 6144), ("llama.gate_up", 4096, 28672),
                ("llama.down", 14336, 4096)]
     for name, k, n in prefill:

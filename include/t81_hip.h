@@ -139,6 +139,43 @@ int t81_hip_lerp(const float *start, const float *end, const float *weight, floa
 int t81_hip_addcmul(const float *in, const float *t1, const float *t2, float value, float *out,
                     int64_t n, void *stream);
 
+/* ---- GGUF ternary block formats (llama.cpp ggml block_tq1_0 / block_tq2_0) ----
+ * 256 weights per block; a row of `cols` weights is ceil(cols / 256) blocks.
+ *   T81_TQ1_0 (ggml type 34, 54 bytes): base-3 digits packed 5 (and 4) per byte as
+ *             (v * 256 + 242) / 243, then an IEEE half scale.
+ *   T81_TQ2_0 (ggml type 35, 66 bytes): 2-bit digits, byte a*32 + c holding elements
+ *             a*128 + s*32 + c at bits 2s, then an IEEE half scale.
+ * Weight = scale * (digit - 1). */
+#define T81_TQ1_0 34
+#define T81_TQ2_0 35
+
+/* Bytes per 256-weight block of `quant` (54, 66), or T81_HIP_EINVAL_DTYPE. */
+int t81_hip_tq_block_bytes(int quant);
+
+/* Quantize rows x cols float32 (row-major) into rows x ceil(cols / 256) blocks.
+ * threshold is clipped to [0, 1]; > 0 selects |v / d| >= threshold -> sign(v),
+ * 0 rounds v / d half away from zero (d = max |v| of the block, stored as half).
+ * Replaces: _quantize_tensor + _quantize_blocks_tq1 / _quantize_blocks_tq2,
+ *           t81/gguf.py:665-690, 525-545, 601-615 (trits: _quantize_trits, :518-522). */
+int t81_hip_tq_quantize(const float *src, uint8_t *dst, int64_t rows, int64_t cols,
+                        float threshold, int quant, void *stream);
+
+/* Decode rows x ceil(cols / 256) blocks into rows x cols float32.
+ * Replaces: _decode_quant_tensor + _dequantize_blocks_tq1 / _dequantize_blocks_tq2,
+ *           t81/gguf.py:1020-1069, 618-635, 654-662. */
+int t81_hip_tq_dequantize(const uint8_t *src, float *dst, int64_t rows, int64_t cols, int quant,
+                          void *stream);
+
+/* c[m, n] = alpha * sum_k x[m, k] * W[n, k] + beta * c[m, n] + bias[n] with W given as
+ * n rows of TQ2_0 blocks (K = k weights per row), read directly (no dequantized copy).
+ * x: T81_DTYPE_BF16 / F32 / I8 (int8 values exact; the result is float32 since the
+ * block scales are).  w must be 4-byte aligned.
+ * Replaces: the dequantize-then-multiply a consumer of t81.gguf.read_gguf performs
+ *           (t81/gguf.py:1072-1121 reads, F.linear multiplies); no reference kernel. */
+int t81_hip_tq2_matmul(const void *x, int x_dtype, const uint8_t *w, float *c, int64_t m,
+                       int64_t n, int64_t k, float alpha, float beta, const float *bias,
+                       void *stream);
+
 /* Host-only test hook, no device needed: writes the 16 x 27 tryte-contribution
  * table K4 uses (constant-evaluated like build_tryte_contributions,
  * include/t81/linalg/gemm.hpp:28-41), so it can be compared bit for bit. */

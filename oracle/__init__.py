@@ -91,6 +91,19 @@ def _load_oracle() -> ctypes.CDLL:
     lib.orc_trit_matmul_abs_f64.argtypes = lib.orc_trit_matmul_f64.argtypes
     lib.orc_trit_matmul_i64.argtypes = [_i8p, ctypes.c_int64, ctypes.c_int64, _u8p,
                                         ctypes.c_int64, _i8p, _i64p]
+    lib.orc_f32_to_f16_bits.restype = ctypes.c_uint16
+    lib.orc_f32_to_f16_bits.argtypes = [ctypes.c_float]
+    lib.orc_f16_bits_to_f32.restype = ctypes.c_float
+    lib.orc_f16_bits_to_f32.argtypes = [ctypes.c_uint16]
+    lib.orc_tq_block_bytes.restype = ctypes.c_int
+    lib.orc_tq_block_bytes.argtypes = [ctypes.c_int]
+    lib.orc_tq_quantize.restype = ctypes.c_int
+    lib.orc_tq_quantize.argtypes = [_f32p, ctypes.c_int64, ctypes.c_int64, ctypes.c_float,
+                                    ctypes.c_int, _u8p]
+    lib.orc_tq_dequantize.restype = ctypes.c_int
+    lib.orc_tq_dequantize.argtypes = [_u8p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int, _f32p]
+    lib.orc_tq2_matmul_f64.argtypes = [_f64p, ctypes.c_int64, ctypes.c_int64, _u8p,
+                                       ctypes.c_int64, _f64p, _f64p]
     return lib
 
 
@@ -239,6 +252,55 @@ def trit_matmul_i64(x: np.ndarray, w_packed: np.ndarray, K: int) -> np.ndarray:
     lib().orc_trit_matmul_i64(_ptr(x, _i8p), M, K, _ptr(w_packed, _u8p), N,
                               _ptr(scratch, _i8p), _ptr(out, _i64p))
     return out
+
+
+# ------------------------------------------------------ GGUF TQ1_0 / TQ2_0 --
+TQ1_0 = 34
+TQ2_0 = 35
+TQ_BLOCK = 256
+
+
+def f32_to_f16_bits(v: float) -> int:
+    return int(lib().orc_f32_to_f16_bits(float(v)))
+
+
+def f16_bits_to_f32(h: int) -> float:
+    return float(lib().orc_f16_bits_to_f32(int(h)))
+
+
+def tq_block_bytes(quant: int) -> int:
+    return int(lib().orc_tq_block_bytes(quant))
+
+
+def tq_quantize(w: np.ndarray, threshold: float, quant: int) -> np.ndarray:
+    """(rows, cols) float32 -> (rows, blocks_per_row * block_bytes) uint8."""
+    w = np.ascontiguousarray(w, np.float32)
+    rows, cols = w.shape
+    nb = (cols + TQ_BLOCK - 1) // TQ_BLOCK
+    out = np.zeros((rows, nb * tq_block_bytes(quant)), np.uint8)
+    if lib().orc_tq_quantize(_ptr(w, _f32p), rows, cols, threshold, quant, _ptr(out, _u8p)):
+        raise ValueError("unknown quant")
+    return out
+
+
+def tq_dequantize(packed: np.ndarray, rows: int, cols: int, quant: int) -> np.ndarray:
+    packed = np.ascontiguousarray(packed, np.uint8)
+    out = np.zeros((rows, cols), np.float32)
+    if lib().orc_tq_dequantize(_ptr(packed, _u8p), rows, cols, quant, _ptr(out, _f32p)):
+        raise ValueError("unknown quant")
+    return out
+
+
+def tq2_matmul_f64(x: np.ndarray, w_tq2: np.ndarray, K: int) -> tuple[np.ndarray, np.ndarray]:
+    """(sum_k x[m,k] W[n,k], sum_k |x[m,k] W[n,k]|) in float64 over dequantized TQ2_0 rows."""
+    x = np.ascontiguousarray(x, np.float64)
+    w_tq2 = np.ascontiguousarray(w_tq2, np.uint8)
+    M, N = x.shape[0], w_tq2.shape[0]
+    out = np.empty((M, N), np.float64)
+    scale = np.empty((M, N), np.float64)
+    lib().orc_tq2_matmul_f64(_ptr(x, _f64p), M, K, _ptr(w_tq2, _u8p), N, _ptr(out, _f64p),
+                             _ptr(scale, _f64p))
+    return out, scale
 
 
 # ------------------------------------------------ the compiled reference --

@@ -49,8 +49,15 @@ EXPORTS = (
     "t81_hip_clamp",
     "t81_hip_lerp",
     "t81_hip_addcmul",
+    "t81_hip_tq_block_bytes",
+    "t81_hip_tq_quantize",
+    "t81_hip_tq_dequantize",
+    "t81_hip_tq2_matmul",
     "t81_hip_limb_tryte_table",
 )
+
+TQ1_0 = 34
+TQ2_0 = 35
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -96,6 +103,14 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.t81_hip_lerp.argtypes = [_vp, _vp, _vp, _vp, _i64, _vp]
     lib.t81_hip_addcmul.restype = _i
     lib.t81_hip_addcmul.argtypes = [_vp, _vp, _vp, _f, _vp, _i64, _vp]
+    lib.t81_hip_tq_block_bytes.restype = _i
+    lib.t81_hip_tq_block_bytes.argtypes = [_i]
+    lib.t81_hip_tq_quantize.restype = _i
+    lib.t81_hip_tq_quantize.argtypes = [_vp, _vp, _i64, _i64, _f, _i, _vp]
+    lib.t81_hip_tq_dequantize.restype = _i
+    lib.t81_hip_tq_dequantize.argtypes = [_vp, _vp, _i64, _i64, _i, _vp]
+    lib.t81_hip_tq2_matmul.restype = _i
+    lib.t81_hip_tq2_matmul.argtypes = [_vp, _i, _vp, _vp, _i64, _i64, _i64, _f, _f, _vp, _vp]
     lib.t81_hip_limb_tryte_table.restype = None
     lib.t81_hip_limb_tryte_table.argtypes = [_vp]
 

@@ -287,6 +287,70 @@ int t81_hip_addcmul(const float *in, const float *t1, const float *t2, float val
         "t81_hip_addcmul");
 }
 
+int t81_hip_tq_block_bytes(int quant) {
+    if (quant == T81_TQ1_0) return 54;
+    if (quant == T81_TQ2_0) return 66;
+    return fail(T81_HIP_EINVAL_DTYPE, "quant must be T81_TQ1_0 (34) or T81_TQ2_0 (35)");
+}
+
+int t81_hip_tq_quantize(const float *src, uint8_t *dst, int64_t rows, int64_t cols,
+                        float threshold, int quant, void *stream) {
+    if (quant != T81_TQ1_0 && quant != T81_TQ2_0)
+        return fail(T81_HIP_EINVAL_DTYPE, "quant must be T81_TQ1_0 (34) or T81_TQ2_0 (35)");
+    if (rows < 0 || cols < 0) return fail(T81_HIP_EINVAL_SHAPE, "rows and cols must be non-negative");
+    if (rows > 0 && cols > 0 && (src == nullptr || dst == nullptr))
+        return fail(T81_HIP_EINVAL_POINTER, "null data pointer");
+    if (reinterpret_cast<uintptr_t>(src) % 4 != 0)
+        return fail(T81_HIP_EINVAL_POINTER, "float32 data must be 4-byte aligned");
+    // t81/gguf.py:675-676: np.clip(threshold, 0, 1); a threshold of 0 selects rounding
+    float thr = threshold < 0.0f ? 0.0f : (threshold > 1.0f ? 1.0f : threshold);
+    if (threshold != threshold) thr = threshold;
+    const int use_thr = thr > 0.0f ? 1 : 0;
+    if (int rc = require_device("t81_hip_tq_quantize")) return rc;
+    return finish(t81hip::launch_tq_quantize(src, dst, rows, cols, thr, use_thr, quant,
+                                             static_cast<hipStream_t>(stream)),
+                  "t81_hip_tq_quantize");
+}
+
+int t81_hip_tq_dequantize(const uint8_t *src, float *dst, int64_t rows, int64_t cols, int quant,
+                          void *stream) {
+    if (quant != T81_TQ1_0 && quant != T81_TQ2_0)
+        return fail(T81_HIP_EINVAL_DTYPE, "quant must be T81_TQ1_0 (34) or T81_TQ2_0 (35)");
+    if (rows < 0 || cols < 0) return fail(T81_HIP_EINVAL_SHAPE, "rows and cols must be non-negative");
+    if (rows > 0 && cols > 0 && (src == nullptr || dst == nullptr))
+        return fail(T81_HIP_EINVAL_POINTER, "null data pointer");
+    if (reinterpret_cast<uintptr_t>(dst) % 4 != 0)
+        return fail(T81_HIP_EINVAL_POINTER, "float32 data must be 4-byte aligned");
+    if (int rc = require_device("t81_hip_tq_dequantize")) return rc;
+    return finish(t81hip::launch_tq_dequantize(src, dst, rows, cols, quant,
+                                               static_cast<hipStream_t>(stream)),
+                  "t81_hip_tq_dequantize");
+}
+
+int t81_hip_tq2_matmul(const void *x, int x_dtype, const uint8_t *w, float *c, int64_t m,
+                       int64_t n, int64_t k, float alpha, float beta, const float *bias,
+                       void *stream) {
+    if (m < 0 || n < 0 || k < 0)
+        return fail(T81_HIP_EINVAL_SHAPE, "tq2_matmul dimensions must be non-negative");
+    if (m > INT_MAX / 2 || k > (int64_t(1) << 31) || (n > 0 && !t81hip::tq2_matmul_fits(n, k)))
+        return fail(T81_HIP_EINVAL_SHAPE, "tq2_matmul dimensions too large");
+    if (x_dtype != T81_DTYPE_F32 && x_dtype != T81_DTYPE_BF16 && x_dtype != T81_DTYPE_I8)
+        return fail(T81_HIP_EINVAL_DTYPE, "activations must be float32, bfloat16 or int8");
+    if ((m > 0 && k > 0 && x == nullptr) || (n > 0 && k > 0 && w == nullptr) ||
+        (m > 0 && n > 0 && c == nullptr))
+        return fail(T81_HIP_EINVAL_POINTER, "null data pointer");
+    const uintptr_t elem = x_dtype == T81_DTYPE_F32 ? 4 : (x_dtype == T81_DTYPE_BF16 ? 2 : 1);
+    if (reinterpret_cast<uintptr_t>(w) % 4 != 0 || reinterpret_cast<uintptr_t>(x) % elem != 0 ||
+        reinterpret_cast<uintptr_t>(c) % 4 != 0 || reinterpret_cast<uintptr_t>(bias) % 4 != 0)
+        return fail(T81_HIP_EINVAL_POINTER, "misaligned weight, activation, output or bias pointer");
+    if (int rc = require_device("t81_hip_tq2_matmul")) return rc;
+    if (m == 0 || n == 0) return T81_HIP_OK;
+    // k == 0: no blocks; the kernel still writes beta * c + bias (empty sums)
+    return finish(t81hip::launch_tq2_matmul(x, x_dtype, w, c, m, n, k, alpha, beta, bias,
+                                            static_cast<hipStream_t>(stream)),
+                  "t81_hip_tq2_matmul");
+}
+
 void t81_hip_limb_tryte_table(double *out) { t81hip::host_tryte_table(out); }
 
 }  // extern "C"

@@ -34,6 +34,18 @@ hipError_t launch_gemv_strip(bool *handled, const void *x, int x_dtype, const ui
                              void *c, int m, int64_t n, int64_t k, float alpha, float beta,
                              const float *bias, hipStream_t s);
 
+// tq.hip: GGUF TQ1_0 (quant 34) / TQ2_0 (quant 35) block codecs
+hipError_t launch_tq_quantize(const float *src, uint8_t *dst, int64_t rows, int64_t cols,
+                              float thr, int use_thr, int quant, hipStream_t s);
+hipError_t launch_tq_dequantize(const uint8_t *src, float *dst, int64_t rows, int64_t cols,
+                                int quant, hipStream_t s);
+
+// gemv_tq2.hip: matmul straight from TQ2_0 weights (tokens in groups of four)
+bool tq2_matmul_fits(int64_t n, int64_t k);
+hipError_t launch_tq2_matmul(const void *x, int x_dtype, const uint8_t *w, float *c, int64_t m,
+                             int64_t n, int64_t k, float alpha, float beta, const float *bias,
+                             hipStream_t s);
+
 // gemm.hip (K3): any M
 hipError_t launch_gemm(const void *x, int x_dtype, const uint8_t *w, void *c, int64_t m,
                        int64_t n, int64_t k, float alpha, float beta, const float *bias,
