@@ -164,6 +164,28 @@ def run_sweep(torch, ops, lib, dev) -> list:
             log(f"tq2  {name:14s} M={m:2d} {k:5d}->{n:5d}: {ms * 1e3:7.2f} us  {gbs:7.0f} GB/s")
         del wb
         torch.cuda.empty_cache()
+    # backward of the Llama gate layer (14336 x 4096): T^T limbs, then dx = dy T as K3
+    k, n = 4096, 14336
+    wb = make_weights(torch, ops, lib, n, k, 4, dev, seed=6)
+    ms = time_graph(torch, lambda w: ops.transpose_packed(w, n, k), wb, 64, 8)
+    tbytes = 16 * n * ((k + 47) // 48) + 16 * k * ((n + 47) // 48)
+    gbs = tbytes / (ms * 1e-3) / 1e9
+    rows.append({"shape": "transpose_packed llama.gate 14336x4096", "us": ms * 1e3, "GBps": gbs,
+                 "frac_hbm": gbs / HBM_PEAK_GBPS})
+    log(f"transpose_packed 14336x4096: {ms * 1e3:7.2f} us  {gbs:7.0f} GB/s")
+    wt = [ops.transpose_packed(w, n, k) for w in wb[:2]]
+    del wb
+    for m in (512, 2048):
+        dy = torch.randn((m, n), device=dev).to(torch.bfloat16)
+        dx = torch.empty((m, k), device=dev)
+        ms = time_graph(torch, lambda w: ops.ternary_matmul(dy, w, n, c=dx), wt, 8, 2)
+        tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+        rows.append({"shape": "backward dx = dy T, llama.gate", "M": m, "K": n, "N": k,
+                     "us": ms * 1e3, "TFLOPs": tf, "frac_mfma": tf / BF16_PEAK_TFLOPS})
+        log(f"backward dx=dyT llama.gate M={m:5d}: {ms * 1e3:8.1f} us  {tf:7.1f} TFLOP/s")
+        del dy, dx
+    del wt
+    torch.cuda.empty_cache()
     # TQ2_0 / TQ1_0 codecs over an 8192 x 3072 float32 matrix
     src = [torch.randn((8192, 3072), device=dev) for _ in range(4)]
     for quant in ("TQ2_0", "TQ1_0"):

@@ -139,6 +139,15 @@ int t81_hip_lerp(const float *start, const float *end, const float *weight, floa
 int t81_hip_addcmul(const float *in, const float *t1, const float *t2, float value, float *out,
                     int64_t n, void *stream);
 
+/* The transposed trit matrix in the same layout: in is rows x ceil(cols / 48) x 16
+ * (row r = T[r, 0 .. cols)), out is cols x ceil(rows / 48) x 16 (row k = T[0 .. rows, k],
+ * trits past rows zero).  Both 16-byte aligned.  With it the backward of
+ * y = x T^T, dx = dy T, is t81_hip_ternary_matmul(dy, out) with K = rows.
+ * Replaces: the float unpack + matmul of _TernaryGemmFunction.backward,
+ *           t81/torch/__init__.py:291-304 (_limbs_to_trits, :100-112). */
+int t81_hip_transpose_packed(const uint8_t *packed, uint8_t *out, int64_t rows, int64_t cols,
+                             void *stream);
+
 /* ---- GGUF ternary block formats (llama.cpp ggml block_tq1_0 / block_tq2_0) ----
  * 256 weights per block; a row of `cols` weights is ceil(cols / 256) blocks.
  *   T81_TQ1_0 (ggml type 34, 54 bytes): base-3 digits packed 5 (and 4) per byte as

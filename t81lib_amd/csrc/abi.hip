@@ -287,6 +287,21 @@ int t81_hip_addcmul(const float *in, const float *t1, const float *t2, float val
         "t81_hip_addcmul");
 }
 
+int t81_hip_transpose_packed(const uint8_t *packed, uint8_t *out, int64_t rows, int64_t cols,
+                             void *stream) {
+    if (rows < 0 || cols < 0) return fail(T81_HIP_EINVAL_SHAPE, "rows and cols must be non-negative");
+    if (cols > int64_t{48} * 4 * 65535 || rows > (int64_t{1} << 36))
+        return fail(T81_HIP_EINVAL_SHAPE, "transpose_packed dimensions too large");
+    if (rows > 0 && cols > 0 && (packed == nullptr || out == nullptr))
+        return fail(T81_HIP_EINVAL_POINTER, "null data pointer");
+    if (reinterpret_cast<uintptr_t>(packed) % 16 != 0 || reinterpret_cast<uintptr_t>(out) % 16 != 0)
+        return fail(T81_HIP_EINVAL_POINTER, "packed limbs must be 16-byte aligned");
+    if (int rc = require_device("t81_hip_transpose_packed")) return rc;
+    return finish(t81hip::launch_transpose_packed(packed, out, rows, cols,
+                                                  static_cast<hipStream_t>(stream)),
+                  "t81_hip_transpose_packed");
+}
+
 int t81_hip_tq_block_bytes(int quant) {
     if (quant == T81_TQ1_0) return 54;
     if (quant == T81_TQ2_0) return 66;

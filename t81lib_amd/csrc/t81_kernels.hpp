@@ -34,6 +34,10 @@ hipError_t launch_gemv_strip(bool *handled, const void *x, int x_dtype, const ui
                              void *c, int m, int64_t n, int64_t k, float alpha, float beta,
                              const float *bias, hipStream_t s);
 
+// transpose.hip: the packed trit matrix transposed (same limb layout)
+hipError_t launch_transpose_packed(const uint8_t *in, uint8_t *out, int64_t rows, int64_t cols,
+                                   hipStream_t s);
+
 // tq.hip: GGUF TQ1_0 (quant 34) / TQ2_0 (quant 35) block codecs
 hipError_t launch_tq_quantize(const float *src, uint8_t *dst, int64_t rows, int64_t cols,
                               float thr, int use_thr, int quant, hipStream_t s);

@@ -114,6 +114,21 @@ def unpack(packed: torch.Tensor, rows: int, cols: int) -> torch.Tensor:
     return out
 
 
+def transpose_packed(packed: torch.Tensor, rows: int, cols: int) -> torch.Tensor:
+    """(rows, L, 16) limbs of T -> (cols, ceil(rows / 48), 16) limbs of T^T."""
+    _require_cuda(packed, "packed")
+    if packed.dtype != torch.uint8 or packed.ndim != 3 or packed.shape[2] != BYTES_PER_LIMB:
+        raise ValueError("packed weights must be a (N, L, 16) uint8 tensor")
+    if packed.shape[0] != rows or packed.shape[1] != limbs_for(cols):
+        raise ValueError("packed shape does not match rows / cols")
+    packed = packed.contiguous()
+    out = torch.empty((cols, limbs_for(rows), BYTES_PER_LIMB), dtype=torch.uint8,
+                      device=packed.device)
+    _lib.check(_lib.lib().t81_hip_transpose_packed(packed.data_ptr(), out.data_ptr(), rows, cols,
+                                                   _stream()))
+    return out
+
+
 def count_invalid_bytes(packed: torch.Tensor) -> int:
     """Number of bytes > 26 (non-canonical trytes); synchronises the stream."""
     _require_cuda(packed, "packed")

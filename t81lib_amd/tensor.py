@@ -73,6 +73,7 @@ class TernaryTensor(torch.Tensor):
         t._k_actual = int(k_actual)
         t._k_limbs = int(k_limbs)
         t._float_source = float_source
+        t._packed_t = None  # T^T limbs for the backward, built on first use
         t._threshold = ops.torch_threshold(threshold)
         t._semantics = semantics
         return t
@@ -116,10 +117,28 @@ class TernaryTensor(torch.Tensor):
             raise ValueError("source shape does not match the ternary tensor")
         ops.quantize_pack(src, self._threshold, _lib.THR_TORCH, out=self._packed)
         self._float_source = src
+        self._packed_t = None
 
     def trits(self) -> torch.Tensor:
         """(rows, cols) int8 trits (GPU unpack kernel)."""
         return ops.unpack(self._packed, self._rows, self._k_actual)
+
+    def transposed_packed(self) -> torch.Tensor:
+        """(cols, ceil(rows / 48), 16) limbs of T^T (GPU transpose kernel), cached until the
+        weights change."""
+        if self._packed_t is None:
+            self._packed_t = ops.transpose_packed(self._packed, self._rows, self._k_actual)
+        return self._packed_t
+
+    def grad_input(self, grad_output: torch.Tensor) -> torch.Tensor:
+        """T^T @ grad_output for grad_output (rows, tokens) -> (cols, tokens), float32: the
+        backward of the reference's _TernaryGemmFunction (t81/torch/__init__.py:291-304),
+        run as the forward GEMM over the transposed limbs."""
+        g = grad_output.to(device=self._packed.device)
+        if g.dtype not in (torch.float32, torch.bfloat16):
+            g = g.float()
+        gt = g.transpose(0, 1).contiguous()  # (tokens, rows)
+        return ops.ternary_matmul(gt, self.transposed_packed(), self._rows).transpose(0, 1)
 
     def matmul_input(self, input: torch.Tensor, bias: Optional[torch.Tensor] = None
                      ) -> torch.Tensor:
@@ -209,9 +228,7 @@ class _TernaryGemmFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_output: torch.Tensor) -> tuple[None, torch.Tensor]:
         t: TernaryTensor = ctx.ternary
-        weight = t.trits().to(torch.float32)  # (rows, cols)
-        grad = grad_output.to(device=weight.device, dtype=torch.float32)
-        grad_rhs = weight.transpose(0, 1).matmul(grad)
+        grad_rhs = t.grad_input(grad_output)
         if ctx.rhs_device.type != "cuda":
             grad_rhs = grad_rhs.to(ctx.rhs_device)
         return None, grad_rhs

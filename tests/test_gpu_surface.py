@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 import torch
 
-from t81lib_amd import nn as t8nn, t81lib
+from t81lib_amd import nn as t8nn, ops, t81lib
 from t81lib_amd.tensor import TernaryTensor, trit
 from conftest import fp_tolerance_ok
 
@@ -123,3 +123,41 @@ def test_linear_eval_vs_oracle(gpu, orc, tokens):
     assert layer.ternary_weight is not None
     layer.train()
     assert layer.ternary_weight is None
+
+
+@pytest.mark.parametrize("rows,cols", [(70, 200), (1, 1), (48, 48), (49, 97), (300, 1000),
+                                       (1000, 300), (96, 192), (5, 4097)])
+def test_transpose_packed_bit_exact(gpu, orc, rows, cols):
+    """T^T limbs equal the oracle's pack of the transposed unpacked trits (zero-padded)."""
+    announce(f"transpose_packed {rows}x{cols}")
+    g = torch.Generator("cpu").manual_seed(rows * 1000 + cols)
+    w = torch.randn(rows, cols, generator=g)
+    packed = orc.pack_rows(w.numpy(), np.float32(0.45), 0)
+    trits = orc.unpack(packed, rows, cols)
+    want = orc.pack_trits_rows(np.ascontiguousarray(trits.T))
+    got = ops.transpose_packed(torch.from_numpy(packed).to(gpu), rows, cols).cpu().numpy()
+    np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("rows,cols,tokens", [(70, 200, 5), (300, 1000, 64), (1024, 512, 512),
+                                              (4096, 1000, 33)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_grad_input_vs_oracle(gpu, orc, rows, cols, tokens, dtype):
+    """grad_rhs = T^T @ grad_output (t81/torch/__init__.py:291-304) through the transposed
+    limbs and the forward GEMM; fp32 within 1e-3, bf16 within 1e-2 of sum |t g|."""
+    announce(f"grad_input {rows}x{cols} tokens={tokens} {dtype}")
+    g = torch.Generator("cpu").manual_seed(rows + cols + tokens)
+    w = torch.randn(rows, cols, generator=g)
+    t = TernaryTensor.from_float(w.to(gpu), threshold=0.45)
+    grad = torch.randn(rows, tokens, generator=g).to(dtype)
+    got = t.grad_input(grad.to(gpu)).cpu().numpy()                       # (cols, tokens)
+    trits = t.trits().cpu().numpy().astype(np.float64)                  # (rows, cols)
+    gd = grad.to(torch.float64).numpy()
+    want = trits.T @ gd
+    scale = np.abs(trits.T) @ np.abs(gd)
+    ok, worst, nbad = fp_tolerance_ok(got, want, scale, 1e-3 if dtype == torch.float32 else 1e-2)
+    assert ok, f"{nbad} outside, worst rel {worst:.3g}"
+    # the cache follows the weights
+    t.update_from_float((-w).to(gpu))
+    np.testing.assert_array_equal(t.transposed_packed().cpu().numpy(),
+                                  ops.transpose_packed(t.packed, rows, cols).cpu().numpy())
