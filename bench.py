@@ -164,6 +164,23 @@ def run_sweep(torch, ops, lib, dev) -> list:
             log(f"tq2  {name:14s} M={m:2d} {k:5d}->{n:5d}: {ms * 1e3:7.2f} us  {gbs:7.0f} GB/s")
         del wb
         torch.cuda.empty_cache()
+    # the reference's literal matmul_input (config 1: W 1024 x 1024, X 64 x 1024): quantize
+    # 0.5 + column pack + limb GEMM fused, against pack_cols then gemm_limb
+    wr = make_weights(torch, ops, lib, 1024, 1024, 2, dev, seed=7)
+    xr = torch.randn((64, 1024), device=dev)
+    cr = torch.zeros((1024, 64), device=dev)
+    products = 1024 * 64 * ((1024 + 47) // 48)
+    ms = time_graph(torch, lambda w: ops.matmul_input_reference(w, xr, 0.5, c=cr), wr, 16, 2)
+    rows.append({"shape": "matmul_input reference_limb fused, config 1", "us": ms * 1e3,
+                 "limb_products_per_s": products / (ms * 1e-3)})
+    log(f"reference matmul_input fused (config 1): {ms * 1e3:8.1f} us  "
+        f"{products / (ms * 1e-3) / 1e9:6.2f} G limb products/s")
+    ms2 = time_graph(torch, lambda w: ops.gemm_limb(w, ops.pack_cols(xr, 0.5, lib.THR_TORCH), cr,
+                                                     1024, 64, 1024 // 48 * 48 + 48), wr, 16, 2)
+    rows.append({"shape": "matmul_input reference_limb two kernels, config 1", "us": ms2 * 1e3,
+                 "limb_products_per_s": products / (ms2 * 1e-3)})
+    log(f"reference matmul_input pack_cols + gemm_limb: {ms2 * 1e3:8.1f} us")
+    del wr, xr, cr
     # backward of the Llama gate layer (14336 x 4096): T^T limbs, then dx = dy T as K3
     k, n = 4096, 14336
     wb = make_weights(torch, ops, lib, n, k, 4, dev, seed=6)

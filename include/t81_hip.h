@@ -139,6 +139,20 @@ int t81_hip_lerp(const float *start, const float *end, const float *weight, floa
 int t81_hip_addcmul(const float *in, const float *t1, const float *t2, float value, float *out,
                     int64_t n, void *stream);
 
+/* The reference's literal matmul_input in one kernel: the activations x (tokens x k,
+ * T81_DTYPE_F32 / BF16 / F16, row-major) are quantized with the torch form of the
+ * threshold (already clamped to [0, 0.9999], T81_THR_TORCH rules) and packed
+ * column-wise inside the limb GEMM, then
+ *   c[i, j] = float(double(c[i, j]) * beta + sum_l product(w[i, l], xpacked[l, j]) * alpha)
+ * for c (rows x tokens) -- bit-identical to t81_hip_pack_cols + t81_hip_gemm_ternary_limb.
+ * w: rows x ceil(k / 48) x 16, 16-byte aligned.
+ * Replaces: TernaryTensor.matmul_input -> _pack_rhs_for_gemm -> _compute_gemm,
+ *           t81/torch/__init__.py:241-276 (quantize 0.5, _pack_columnwise :83-97,
+ *           then gemm_ternary, src/linalg/gemm_cpu.cpp:8-71). */
+int t81_hip_matmul_input_reference(const uint8_t *w, const void *x, int x_dtype, float *c,
+                                   int64_t rows, int64_t tokens, int64_t k, float threshold,
+                                   float alpha, float beta, void *stream);
+
 /* The transposed trit matrix in the same layout: in is rows x ceil(cols / 48) x 16
  * (row r = T[r, 0 .. cols)), out is cols x ceil(rows / 48) x 16 (row k = T[0 .. rows, k],
  * trits past rows zero).  Both 16-byte aligned.  With it the backward of

@@ -49,6 +49,7 @@ EXPORTS = (
     "t81_hip_clamp",
     "t81_hip_lerp",
     "t81_hip_addcmul",
+    "t81_hip_matmul_input_reference",
     "t81_hip_transpose_packed",
     "t81_hip_tq_block_bytes",
     "t81_hip_tq_quantize",
@@ -104,6 +105,9 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.t81_hip_lerp.argtypes = [_vp, _vp, _vp, _vp, _i64, _vp]
     lib.t81_hip_addcmul.restype = _i
     lib.t81_hip_addcmul.argtypes = [_vp, _vp, _vp, _f, _vp, _i64, _vp]
+    lib.t81_hip_matmul_input_reference.restype = _i
+    lib.t81_hip_matmul_input_reference.argtypes = [_vp, _vp, _i, _vp, _i64, _i64, _i64, _f, _f,
+                                                   _f, _vp]
     lib.t81_hip_transpose_packed.restype = _i
     lib.t81_hip_transpose_packed.argtypes = [_vp, _vp, _i64, _i64, _vp]
     lib.t81_hip_tq_block_bytes.restype = _i

@@ -287,6 +287,31 @@ int t81_hip_addcmul(const float *in, const float *t1, const float *t2, float val
         "t81_hip_addcmul");
 }
 
+int t81_hip_matmul_input_reference(const uint8_t *w, const void *x, int x_dtype, float *c,
+                                   int64_t rows, int64_t tokens, int64_t k, float threshold,
+                                   float alpha, float beta, void *stream) {
+    if (int rc = check_threshold(threshold, T81_THR_TORCH)) return rc;
+    if (rows < 0 || tokens < 0 || k < 0)
+        return fail(T81_HIP_EINVAL_SHAPE, "gemm_ternary dimensions must be non-negative");
+    if (rows > (int64_t{65535} * 16) || tokens > INT_MAX / 2 || k > (int64_t{1} << 31))
+        return fail(T81_HIP_EINVAL_SHAPE, "matmul_input dimensions too large");
+    if (!float_dtype(x_dtype)) return fail(T81_HIP_EINVAL_DTYPE, "input must be a float dtype");
+    if (rows == 0 || tokens == 0) {
+        g_last_error.clear();
+        return T81_HIP_OK;
+    }
+    if (c == nullptr || (k > 0 && (w == nullptr || x == nullptr)))
+        return fail(T81_HIP_EINVAL_POINTER, "null data pointer");
+    if (reinterpret_cast<uintptr_t>(w) % 16 != 0 || reinterpret_cast<uintptr_t>(c) % 4 != 0 ||
+        reinterpret_cast<uintptr_t>(x) % (x_dtype == T81_DTYPE_F32 ? 4 : 2) != 0)
+        return fail(T81_HIP_EINVAL_POINTER, "misaligned weight, activation or output pointer");
+    if (int rc = require_device("t81_hip_matmul_input_reference")) return rc;
+    return finish(t81hip::launch_gemm_limb_fused(w, x, x_dtype, c, static_cast<int>(rows),
+                                                 static_cast<int>(tokens), k, threshold, alpha,
+                                                 beta, static_cast<hipStream_t>(stream)),
+                  "t81_hip_matmul_input_reference");
+}
+
 int t81_hip_transpose_packed(const uint8_t *packed, uint8_t *out, int64_t rows, int64_t cols,
                              void *stream) {
     if (rows < 0 || cols < 0) return fail(T81_HIP_EINVAL_SHAPE, "rows and cols must be non-negative");

@@ -14,6 +14,7 @@
 // order, no FMA contraction -- are bit-identical to gemm_cpu.cpp:8-71.
 // This kernel is the parity path, not the roofline-graded one: one thread per
 // output, l ascending.
+#include "pack_common.hpp"
 #include "t81_device.hpp"
 #include "t81_kernels.hpp"
 
@@ -109,6 +110,94 @@ __global__ __launch_bounds__(256) void gemm_limb_kernel(const uint8_t *__restric
         acc = acc + scaled;
     }
     c[t] = static_cast<float>(acc);
+}
+
+// The reference's literal matmul_input in one pass (t81/torch/__init__.py:241-276):
+// the activations x (tokens x K, row-major) are quantized with the torch form of the
+// threshold and packed column-wise (_pack_columnwise, :83-97) inside the kernel, then
+// multiplied as limbs exactly as gemm_limb_kernel does.  A workgroup owns 16 weight
+// rows x 16 tokens; per chunk of limbs it packs its tokens' limbs (once, into LDS) and
+// stages its rows' limbs, and each thread then runs its output's limbs in ascending
+// order -- the same operations as pack_cols followed by gemm_limb_kernel, so the same
+// bits.  C is rows x tokens.
+constexpr int kFuseTile = 16;
+constexpr int kFuseChunk = 32;  // limbs per staged chunk
+
+template <typename T, bool kVec>
+__global__ __launch_bounds__(256) void gemm_limb_fused_kernel(
+    const uint8_t *__restrict__ a, const T *__restrict__ x, float *__restrict__ c, int M, int N,
+    int64_t K, int KL, float thr, float alpha, float beta) {
+    __shared__ uint4 xs[kFuseTile][kFuseChunk];
+    __shared__ uint4 as[kFuseTile][kFuseChunk];
+    const int tid = threadIdx.x;
+    const int ti = tid / kFuseTile;
+    const int tj = tid % kFuseTile;
+    const int64_t i0 = static_cast<int64_t>(blockIdx.y) * kFuseTile;
+    const int64_t j0 = static_cast<int64_t>(blockIdx.x) * kFuseTile;
+    const int64_t i = i0 + ti;
+    const int64_t j = j0 + tj;
+    const bool live = i < M && j < N;
+    double acc = live ? static_cast<double>(c[i * N + j]) * static_cast<double>(beta) : 0.0;
+    const uint4 *arows = reinterpret_cast<const uint4 *>(a);
+    for (int l0 = 0; l0 < KL; l0 += kFuseChunk) {
+        const int cl = KL - l0 < kFuseChunk ? KL - l0 : kFuseChunk;
+        for (int d = tid; d < kFuseTile * cl * 4; d += 256) {
+            const int tok = d / (cl * 4);
+            const int rem = d - tok * cl * 4;
+            const int l = rem >> 2;
+            const int q = rem & 3;
+            const int64_t jj = j0 + tok;
+            const uint32_t word =
+                jj < N ? pack12<T, kVec>(x + jj * K, static_cast<int64_t>(l0 + l) * kTrits + 12 * q,
+                                         K, thr, 1)
+                       : 0x0D0D0D0Du;
+            reinterpret_cast<uint32_t *>(&xs[tok][l])[q] = word;
+        }
+        for (int d = tid; d < kFuseTile * cl; d += 256) {
+            const int r = d / cl;
+            const int l = d - r * cl;
+            const int64_t ii = i0 + r;
+            as[r][l] = ii < M ? arows[ii * KL + l0 + l]
+                              : make_uint4(0x0D0D0D0Du, 0x0D0D0D0Du, 0x0D0D0D0Du, 0x0D0D0D0Du);
+        }
+        __syncthreads();
+        if (live) {
+            for (int l = 0; l < cl; ++l) {
+                const double p = multiply_to_double(as[ti][l], xs[tj][l]);
+                const double scaled = p * static_cast<double>(alpha);
+                acc = acc + scaled;
+            }
+        }
+        __syncthreads();
+    }
+    if (live) c[i * N + j] = static_cast<float>(acc);
+}
+
+template <typename T>
+hipError_t launch_fused_t(const uint8_t *a, const void *x, float *c, int m, int n, int64_t k,
+                          float thr, float alpha, float beta, hipStream_t s) {
+    const int KL = static_cast<int>((k + kTrits - 1) / kTrits);
+    const dim3 grid((n + kFuseTile - 1) / kFuseTile, (m + kFuseTile - 1) / kFuseTile);
+    // vector loads as in the column packer: K % 4 == 0 and a 16-byte aligned x
+    const bool vec = (k % 4 == 0) && (reinterpret_cast<uintptr_t>(x) % 16 == 0);
+    if (vec)
+        gemm_limb_fused_kernel<T, true><<<grid, 256, 0, s>>>(a, static_cast<const T *>(x), c, m, n,
+                                                             k, KL, thr, alpha, beta);
+    else
+        gemm_limb_fused_kernel<T, false><<<grid, 256, 0, s>>>(a, static_cast<const T *>(x), c, m, n,
+                                                              k, KL, thr, alpha, beta);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm_limb_fused(const uint8_t *a, const void *x, int x_dtype, float *c, int m,
+                                  int n, int64_t k, float thr, float alpha, float beta,
+                                  hipStream_t s) {
+    if (static_cast<int64_t>(m) * n == 0) return hipSuccess;
+    switch (x_dtype) {
+        case kDtypeF32: return launch_fused_t<float>(a, x, c, m, n, k, thr, alpha, beta, s);
+        case kDtypeBF16: return launch_fused_t<uint16_t>(a, x, c, m, n, k, thr, alpha, beta, s);
+        default: return launch_fused_t<_Float16>(a, x, c, m, n, k, thr, alpha, beta, s);
+    }
 }
 
 hipError_t launch_gemm_limb(const uint8_t *a, const uint8_t *b, float *c, int m, int n,

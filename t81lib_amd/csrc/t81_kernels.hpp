@@ -58,6 +58,10 @@ hipError_t launch_gemm(const void *x, int x_dtype, const uint8_t *w, void *c, in
 // limb.hip (K4)
 hipError_t launch_gemm_limb(const uint8_t *a, const uint8_t *b, float *c, int m, int n,
                             int k_limbs, float alpha, float beta, hipStream_t s);
+// K4 with the activations quantized (torch form) and column-packed inside the kernel
+hipError_t launch_gemm_limb_fused(const uint8_t *a, const void *x, int x_dtype, float *c, int m,
+                                  int n, int64_t k, float thr, float alpha, float beta,
+                                  hipStream_t s);
 
 // elementwise.hip: the backend contract's where / clamp / lerp / addcmul (float32)
 hipError_t launch_where(const float *cond, const float *x, const float *y, float *out, int64_t n,

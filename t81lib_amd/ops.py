@@ -114,6 +114,35 @@ def unpack(packed: torch.Tensor, rows: int, cols: int) -> torch.Tensor:
     return out
 
 
+def matmul_input_reference(w_packed: torch.Tensor, x: torch.Tensor, threshold: float = 0.5,
+                           alpha: float = 1.0, beta: float = 0.0,
+                           c: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The reference's literal matmul_input product in one kernel: x (tokens, K) quantized
+    (torch form, threshold clamped as t81/torch/__init__.py:45) and packed column-wise
+    inside the limb GEMM; returns C (rows, tokens) float32, bit-identical to
+    pack_cols + gemm_limb."""
+    _require_cuda(w_packed, "w_packed")
+    _require_cuda(x, "x")
+    if x.ndim != 2:
+        raise ValueError("t81.trit linear helpers expect 2D activations")
+    if x.dtype not in _FLOAT_CODES:
+        x = x.float()
+    x = x.contiguous()
+    tokens, k = x.shape
+    if w_packed.ndim != 3 or w_packed.shape[1] != limbs_for(k) or w_packed.dtype != torch.uint8:
+        raise ValueError("packed weight limbs do not match K")
+    w_packed = w_packed.contiguous()
+    rows = w_packed.shape[0]
+    if c is None:
+        c = torch.zeros((rows, tokens), dtype=torch.float32, device=x.device)
+    elif tuple(c.shape) != (rows, tokens) or c.dtype != torch.float32 or not c.is_contiguous():
+        raise ValueError("C tensor shape must match (rows, tokens)")
+    _lib.check(_lib.lib().t81_hip_matmul_input_reference(
+        w_packed.data_ptr(), x.data_ptr(), _FLOAT_CODES[x.dtype], c.data_ptr(), rows, tokens, k,
+        torch_threshold(threshold), alpha, beta, _stream()))
+    return c
+
+
 def transpose_packed(packed: torch.Tensor, rows: int, cols: int) -> torch.Tensor:
     """(rows, L, 16) limbs of T -> (cols, ceil(rows / 48), 16) limbs of T^T."""
     _require_cuda(packed, "packed")

@@ -183,12 +183,9 @@ class TernaryTensor(torch.Tensor):
         if self._semantics == "trit_dot":
             x = _activations(rhs.transpose(0, 1))
             return ops.ternary_matmul(x, self._packed, self._k_actual).transpose(0, 1)
-        # reference_limb: t81/torch/__init__.py:257-276
-        tokens = rhs.shape[1]
-        packed_rhs = ops.pack_cols(rhs.transpose(0, 1).float().contiguous(), 0.5, _lib.THR_TORCH)
-        out = torch.zeros((self._rows, tokens), dtype=torch.float32, device=rhs.device)
-        ops.gemm_limb(self._packed, packed_rhs, out, self._rows, tokens, self._k_limbs * 48)
-        return out
+        # reference_limb: t81/torch/__init__.py:257-276 (quantize 0.5, column pack, limb
+        # GEMM) as one kernel
+        return ops.matmul_input_reference(self._packed, rhs.transpose(0, 1).float(), 0.5)
 
 
 def _activations(x: torch.Tensor) -> torch.Tensor:

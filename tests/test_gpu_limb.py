@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 import torch
 
-from t81lib_amd import ops
+from t81lib_amd import _lib, ops
 
 pytestmark = pytest.mark.gpu
 
@@ -86,3 +86,38 @@ def test_config1_reference_path(gpu, orc):
             assert (got == 0).all()
         else:
             assert np.isinf(got).mean() > 0.9
+
+
+@pytest.mark.parametrize("tokens,k,rows", [(6, 100, 40), (1, 48, 1), (17, 4097, 33), (33, 2000, 100),
+                                           (16, 1536, 16), (5, 1, 3)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_fused_reference_matmul_input_matches_two_kernels(gpu, tokens, k, rows, dtype):
+    """matmul_input_reference (quantize 0.5 + column pack inside the limb GEMM) equals
+    pack_cols followed by gemm_limb bit for bit, for alpha / beta and ragged shapes."""
+    announce(f"fused matmul_input {dtype} tokens={tokens} k={k} rows={rows}")
+    g = torch.Generator("cpu").manual_seed(tokens * 131 + k + rows)
+    w = torch.randn(rows, k, generator=g)
+    x = (torch.randn(tokens, k, generator=g) * 0.8).to(dtype).to(gpu)
+    wp = ops.quantize_pack(w.to(gpu), ops.torch_threshold(0.45), _lib.THR_TORCH)
+    c0 = torch.randn(rows, tokens, generator=g).to(gpu)
+    for alpha, beta in ((1.0, 0.0), (0.5, 1.5), (-2.0, 0.25)):
+        want = c0.clone()
+        ops.gemm_limb(wp, ops.pack_cols(x, 0.5, _lib.THR_TORCH), want, rows, tokens,
+                      ops.limbs_for(k) * 48, alpha, beta)
+        got = ops.matmul_input_reference(wp, x, 0.5, alpha, beta, c=c0.clone())
+        np.testing.assert_array_equal(got.cpu().numpy().view(np.uint32),
+                                      want.cpu().numpy().view(np.uint32))
+
+
+def test_fused_reference_config1_vs_oracle(gpu, orc):
+    """BASELINE config 1 (effective W/0.02 variant): W 1024 x 1024 at 0.45, X 64 x 1024 at
+    0.5, alpha 1 beta 0 -- the reference CPU gemm_ternary's output, bit-exact."""
+    announce("fused matmul_input config 1")
+    g = torch.Generator("cpu").manual_seed(0)
+    w = torch.randn(1024, 1024, generator=g)
+    x = torch.randn(64, 1024, generator=g)
+    wp = orc.pack_rows(w.numpy(), np.float32(orc.torch_threshold(0.45)), 1)
+    xp = orc.pack_cols(x.numpy(), np.float32(orc.torch_threshold(0.5)), 1)
+    want = orc.gemm_limb(wp, xp, np.zeros((1024, 64), np.float32), 1024, 64, wp.shape[1] * 48)
+    got = ops.matmul_input_reference(torch.from_numpy(wp).to(gpu), x.to(gpu), 0.5).cpu().numpy()
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
