@@ -125,6 +125,40 @@ def cpu_reference_gemv(n: int, k: int, budget_s: float):
     }
 
 
+def run_spmm(torch, dev) -> list:
+    """spmm_simple on the reference example's shape (256 x 256, 3 %, N = 128) and on the
+    Llama gate shape at the same density: plan = stable row sort (timed once), apply = the
+    hot kernel (graph-timed).  Unique bytes: 12 per entry + row_ptr + B + C."""
+    from t81lib_amd import sparse
+    out = []
+    for name, srows, scols, n_feat in (("example 256x256", 256, 256, 128),
+                                       ("llama.gate 14336x4096", 14336, 4096, 128)):
+        nnz = int(srows * scols * 0.03)
+        g = torch.Generator(dev).manual_seed(8)
+        vals = torch.randint(-3, 4, (nnz,), generator=g, device=dev)
+        ri = torch.randint(0, srows, (nnz,), generator=g, device=dev, dtype=torch.int32)
+        ci = torch.randint(0, scols, (nnz,), generator=g, device=dev, dtype=torch.int32)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        A = sparse.SparseTernaryMatrix(vals, ri, ci, srows, scols)
+        plan_ms = (time.perf_counter() - t0) * 1e3
+        Bm = torch.randn((scols, n_feat), device=dev)
+        outs = [torch.empty((srows, n_feat), device=dev) for _ in range(2)]
+        ms = time_graph(torch, lambda c: A.matmul(Bm, c), outs, 256, 16)
+        nbytes = 12 * nnz + 4 * (srows + 1) + 4 * scols * n_feat + 4 * srows * n_feat
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        gather = 4.0 * nnz * n_feat / (ms * 1e-3) / 1e9
+        out.append({"shape": f"spmm_simple {name} 3% N={n_feat}", "nnz": nnz, "us": ms * 1e3,
+                    "GBps": gbs, "frac_hbm": gbs / HBM_PEAK_GBPS, "B_gather_GBps": gather,
+                    "plan_ms": plan_ms})
+        log(f"spmm {name} nnz={nnz} N={n_feat}: {ms * 1e3:7.2f} us  {gbs:6.0f} GB/s unique, "
+            f"{gather:6.0f} GB/s B gathers; plan {plan_ms:6.2f} ms")
+        A.close()
+        del A, Bm, outs, vals, ri, ci
+    torch.cuda.empty_cache()
+    return out
+
+
 def run_sweep(torch, ops, lib, dev) -> list:
     """Decode GEMV (config 3 + the Llama gate/down shapes) and prefill GEMM (config 4)."""
     rows = []
@@ -222,6 +256,7 @@ def run_sweep(torch, ops, lib, dev) -> list:
         del payloads
     del src
     torch.cuda.empty_cache()
+    rows += run_spmm(torch, dev)
     prefill = [("llama.qkv", 4096, 6144), ("llama.gate_up", 4096, 28672),
                ("llama.down", 14336, 4096)]
     for name, k, n in prefill:
@@ -337,7 +372,7 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=12.0,
                     help="seconds of single-core reference CPU work for the baseline")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["gemv", "gemm", "pack", "copy"], default=None,
+    ap.add_argument("--only", choices=["gemv", "gemm", "pack", "copy", "spmm"], default=None,
                     help="time one kernel only (for profiling runs); 'copy' times a plain "
                          "elementwise copy of the GEMV weight size, the calibration kernel "
                          "for the HBM byte counters")
@@ -454,6 +489,7 @@ def main() -> int:
         }
 
     sweep = run_sweep(torch, ops, _lib, dev) if args.sweep else None
+    spmm = run_spmm(torch, dev) if args.only == "spmm" else None
 
     gbytes = gemv_bytes(M, N, K)
     line: dict = {
@@ -500,6 +536,8 @@ def main() -> int:
         line["copy"] = copy
     if sweep:
         line["sweep"] = sweep
+    if spmm:
+        line["spmm"] = spmm
     print(json.dumps(line), flush=True)
     return 0
 

@@ -34,6 +34,7 @@ extern "C" {
 #define T81_HIP_EINVAL_POINTER (-5)   /* NULL where data is required              */
 #define T81_HIP_EHIP (-6)             /* HIP runtime error (text in last_error)   */
 #define T81_HIP_ENODEV (-7)           /* no gfx950 device                         */
+#define T81_HIP_EINVAL_INDEX (-8)     /* sparse entry index out of range          */
 
 /* element types of activations / float inputs */
 #define T81_DTYPE_F32 0
@@ -198,6 +199,45 @@ int t81_hip_tq_dequantize(const uint8_t *src, float *dst, int64_t rows, int64_t 
 int t81_hip_tq2_matmul(const void *x, int x_dtype, const uint8_t *w, float *c, int64_t m,
                        int64_t n, int64_t k, float alpha, float beta, const float *bias,
                        void *stream);
+
+/* Sparse ternary x dense (COO entries, list order significant):
+ *     C[r, :] = beta == 0 ? 0 : float(double(C[r, :]) * beta), then for each entry e in
+ *     list order: C[row_e, k] = float(double(C[row_e, k]) + double(value_e) * alpha *
+ *     double(B[col_e, k])), each multiply and add rounded in double, for k < N.
+ * B is cols x N, C rows x N, float32 row-major; values are the entries' integers (the
+ * reference's limbs built from long long).  Bit-exact with the reference.
+ * Replaces: t81::sparse::spmm_simple, include/t81/sparse/simple.hpp:37-94, as the
+ *           spmm_simple binding calls it, python/bindings.cpp:888-940. */
+typedef struct t81_hip_spmm_plan t81_hip_spmm_plan;
+
+/* Builds the device form of the matrix (entries stably sorted by row, values as double).
+ * Allocates device memory and synchronises `stream` (it reads the index check back).
+ * values / row_idx / col_idx: nnz device elements, nnz <= 2^31 - 1.  On an index
+ * outside [0, rows) x [0, cols) returns T81_HIP_EINVAL_INDEX ("Row index out of bounds"
+ * or "Column index out of bounds", the reference's messages, simple.hpp:79-84) with
+ * *first_bad = the first such entry and *plan still built from the entries before it:
+ * applying that plan leaves C as the reference leaves it when it throws.  Otherwise
+ * *first_bad = -1.  Every plan returned must be destroyed. */
+int t81_hip_spmm_plan_create(const int64_t *values, const int32_t *row_idx,
+                             const int32_t *col_idx, int64_t nnz, int rows, int cols,
+                             t81_hip_spmm_plan **plan, int64_t *first_bad, void *stream);
+
+/* C = the product above with the plan's entries; B (cols x N) and C (rows x N) device,
+ * 4-byte aligned.  Enqueues one kernel, no allocation, no synchronisation. */
+int t81_hip_spmm_plan_apply(const t81_hip_spmm_plan *plan, const float *B, float *C, int N,
+                            float alpha, float beta, void *stream);
+
+/* rows / cols / stored entries of a plan (any pointer may be NULL). */
+int t81_hip_spmm_plan_info(const t81_hip_spmm_plan *plan, int *rows, int *cols, int64_t *nnz);
+
+/* Frees the plan's device memory (after the work that uses it has completed). */
+void t81_hip_spmm_plan_destroy(t81_hip_spmm_plan *plan);
+
+/* create + apply + destroy in one call, synchronising `stream`: the binding's
+ * spmm_simple on device buffers, including the partial update of C on a bad index. */
+int t81_hip_spmm_simple(const int64_t *values, const int32_t *row_idx, const int32_t *col_idx,
+                        int64_t nnz, int rows, int cols, const float *B, float *C, int N,
+                        float alpha, float beta, void *stream);
 
 /* Host-only test hook, no device needed: writes the 16 x 27 tryte-contribution
  * table K4 uses (constant-evaluated like build_tryte_contributions,

@@ -35,6 +35,7 @@ _i8p = ctypes.POINTER(ctypes.c_int8)
 _f32p = ctypes.POINTER(ctypes.c_float)
 _f64p = ctypes.POINTER(ctypes.c_double)
 _i64p = ctypes.POINTER(ctypes.c_int64)
+_i32p = ctypes.POINTER(ctypes.c_int32)
 
 
 def build(reference: bool = True) -> None:
@@ -91,6 +92,10 @@ def _load_oracle() -> ctypes.CDLL:
     lib.orc_trit_matmul_abs_f64.argtypes = lib.orc_trit_matmul_f64.argtypes
     lib.orc_trit_matmul_i64.argtypes = [_i8p, ctypes.c_int64, ctypes.c_int64, _u8p,
                                         ctypes.c_int64, _i8p, _i64p]
+    lib.orc_spmm_simple.restype = ctypes.c_int
+    lib.orc_spmm_simple.argtypes = [_i64p, _i32p, _i32p, ctypes.c_int64, ctypes.c_int,
+                                    ctypes.c_int, _f32p, _f32p, ctypes.c_int, ctypes.c_float,
+                                    ctypes.c_float]
     lib.orc_f32_to_f16_bits.restype = ctypes.c_uint16
     lib.orc_f32_to_f16_bits.argtypes = [ctypes.c_float]
     lib.orc_f16_bits_to_f32.restype = ctypes.c_float
@@ -254,6 +259,25 @@ def trit_matmul_i64(x: np.ndarray, w_packed: np.ndarray, K: int) -> np.ndarray:
     return out
 
 
+# ----------------------------------------------------------- spmm_simple --
+def _spmm(fn, values, rows_idx, cols_idx, rows, cols, B, C, N, alpha, beta):
+    values = np.ascontiguousarray(values, np.int64)
+    rows_idx = np.ascontiguousarray(rows_idx, np.int32)
+    cols_idx = np.ascontiguousarray(cols_idx, np.int32)
+    B = np.ascontiguousarray(B, np.float32)
+    out = np.array(C, np.float32, copy=True)
+    rc = fn(_ptr(values, _i64p), _ptr(rows_idx, _i32p), _ptr(cols_idx, _i32p), values.size,
+            rows, cols, _ptr(B, _f32p), _ptr(out, _f32p), N, alpha, beta)
+    return rc, out
+
+
+def spmm_simple(values, rows_idx, cols_idx, rows: int, cols: int, B, C, N: int,
+                alpha: float = 1.0, beta: float = 0.0):
+    """(return code, C after the call): 0, -1 bad index (C partly updated), -2 bad dims."""
+    return _spmm(lib().orc_spmm_simple, values, rows_idx, cols_idx, rows, cols, B, C, N,
+                 alpha, beta)
+
+
 # ------------------------------------------------------ GGUF TQ1_0 / TQ2_0 --
 TQ1_0 = 34
 TQ2_0 = 35
@@ -350,6 +374,15 @@ class Ref:
                                      ctypes.c_float]
         lib.t81ref_addcmul.argtypes = [_f32p, _f32p, _f32p, ctypes.c_float, _f32p,
                                        ctypes.c_longlong]
+
+    def spmm_simple(self, values, rows_idx, cols_idx, rows: int, cols: int, B, C, N: int,
+                    alpha: float = 1.0, beta: float = 0.0):
+        """The reference's t81::sparse::spmm_simple: (0 or -1 if it threw, C after)."""
+        fn = self.lib.t81ref_spmm_simple
+        fn.restype = ctypes.c_int
+        fn.argtypes = [_i64p, _i32p, _i32p, ctypes.c_longlong, ctypes.c_int, ctypes.c_int,
+                       _f32p, _f32p, ctypes.c_int, ctypes.c_float, ctypes.c_float]
+        return _spmm(fn, values, rows_idx, cols_idx, rows, cols, B, C, N, alpha, beta)
 
     def elementwise(self, op: str, a, b=None, c=None, p0: float = 0.0, p1: float = 0.0):
         """The reference's where / clamp / lerp / addcmul on Backend::CPU."""

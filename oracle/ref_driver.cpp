@@ -29,6 +29,7 @@
 
 #include <t81/linalg/gemm.hpp>
 #include <t81/linalg/gemm_gpu.hpp>
+#include <t81/sparse/simple.hpp>
 #include <t81/tensor_metadata.hpp>
 
 using t81::core::limb;
@@ -205,6 +206,30 @@ void t81ref_addcmul(const float *in, const float *t1, const float *t2, float val
                     long long n) {
     auto mi = f32(in, n), m1 = f32(t1, n), m2 = f32(t2, n), mo = f32(out, n);
     t81::linalg::detail::addcmul(mi, m1, m2, value, mo, t81::linalg::Backend::CPU);
+}
+
+// t81::sparse::spmm_simple (include/t81/sparse/simple.hpp:37-94) on limbs built from
+// long long values, as the pybind11 binding does (python/bindings.cpp:910-928).
+// Returns -1 if it throws (C keeps what it held at that point).
+int t81ref_spmm_simple(const long long *values, const int *row_idx, const int *col_idx,
+                       long long nnz, int rows, int cols, const float *B, float *C, int N,
+                       float alpha, float beta) {
+    try {
+        t81::sparse::SimpleSparseTernary m;
+        m.rows = rows;
+        m.cols = cols;
+        m.row_indices.assign(row_idx, row_idx + nnz);
+        m.col_indices.assign(col_idx, col_idx + nnz);
+        m.values.reserve(static_cast<std::size_t>(nnz));
+        for (long long i = 0; i < nnz; ++i) m.values.emplace_back(values[i]);
+        const std::size_t nb = static_cast<std::size_t>(cols) * static_cast<std::size_t>(N < 0 ? 0 : N);
+        const std::size_t nc = static_cast<std::size_t>(rows) * static_cast<std::size_t>(N < 0 ? 0 : N);
+        t81::sparse::spmm_simple(m, std::span<const float>(B, nb), std::span<float>(C, nc), N,
+                                 alpha, beta);
+        return 0;
+    } catch (const std::exception &) {
+        return -1;
+    }
 }
 
 } // extern "C"

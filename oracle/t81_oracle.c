@@ -376,3 +376,35 @@ void orc_addcmul(const float *in, const float *t1, const float *t2, float value,
                  int64_t n) {
     for (int64_t i = 0; i < n; ++i) out[i] = in[i] + value * t1[i] * t2[i];
 }
+
+/* ---------------------------------------------------------- spmm_simple ----
+ * include/t81/sparse/simple.hpp:37-94: C = beta * C (each element through double,
+ * or zero when beta == 0), then for every entry in order: weight = double(value) *
+ * alpha (a limb built from a long long holds it exactly, limb_to_double sums its
+ * trits in int128 and rounds once, python/bindings.cpp:916-918), and for each k
+ * C[row, k] = float(double(C[row, k]) + weight * double(B[col, k])).  Returns -1 at
+ * the first out-of-range index (the reference throws there, after updating C for the
+ * entries before it), -2 for negative dimensions, else 0. */
+int orc_spmm_simple(const long long *values, const int32_t *row_idx, const int32_t *col_idx,
+                    int64_t nnz, int rows, int cols, const float *B, float *C, int N,
+                    float alpha, float beta) {
+    if (N < 0 || rows < 0 || cols < 0) return -2;
+    const int64_t total = (int64_t)rows * N;
+    if (beta == 0.0f) {
+        for (int64_t i = 0; i < total; ++i) C[i] = 0.0f;
+    } else {
+        const double bd = (double)beta;
+        for (int64_t i = 0; i < total; ++i) C[i] = (float)((double)C[i] * bd);
+    }
+    const double ad = (double)alpha;
+    for (int64_t e = 0; e < nnz; ++e) {
+        const int r = row_idx[e], c = col_idx[e];
+        if (r < 0 || r >= rows || c < 0 || c >= cols) return -1;
+        const double w = (double)values[e] * ad;
+        for (int k = 0; k < N; ++k) {
+            const double p = w * (double)B[(int64_t)c * N + k];
+            C[(int64_t)r * N + k] = (float)((double)C[(int64_t)r * N + k] + p);
+        }
+    }
+    return 0;
+}

@@ -24,6 +24,7 @@ EINVAL_DTYPE = -4
 EINVAL_POINTER = -5
 EHIP = -6
 ENODEV = -7
+EINVAL_INDEX = -8
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -55,6 +56,11 @@ EXPORTS = (
     "t81_hip_tq_quantize",
     "t81_hip_tq_dequantize",
     "t81_hip_tq2_matmul",
+    "t81_hip_spmm_plan_create",
+    "t81_hip_spmm_plan_apply",
+    "t81_hip_spmm_plan_info",
+    "t81_hip_spmm_plan_destroy",
+    "t81_hip_spmm_simple",
     "t81_hip_limb_tryte_table",
 )
 
@@ -118,6 +124,20 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.t81_hip_tq_dequantize.argtypes = [_vp, _vp, _i64, _i64, _i, _vp]
     lib.t81_hip_tq2_matmul.restype = _i
     lib.t81_hip_tq2_matmul.argtypes = [_vp, _i, _vp, _vp, _i64, _i64, _i64, _f, _f, _vp, _vp]
+    lib.t81_hip_spmm_plan_create.restype = _i
+    lib.t81_hip_spmm_plan_create.argtypes = [_vp, _vp, _vp, _i64, _i, _i,
+                                             ctypes.POINTER(ctypes.c_void_p),
+                                             ctypes.POINTER(ctypes.c_int64), _vp]
+    lib.t81_hip_spmm_plan_apply.restype = _i
+    lib.t81_hip_spmm_plan_apply.argtypes = [_vp, _vp, _vp, _i, _f, _f, _vp]
+    lib.t81_hip_spmm_plan_info.restype = _i
+    lib.t81_hip_spmm_plan_info.argtypes = [_vp, ctypes.POINTER(ctypes.c_int),
+                                           ctypes.POINTER(ctypes.c_int),
+                                           ctypes.POINTER(ctypes.c_int64)]
+    lib.t81_hip_spmm_plan_destroy.restype = None
+    lib.t81_hip_spmm_plan_destroy.argtypes = [_vp]
+    lib.t81_hip_spmm_simple.restype = _i
+    lib.t81_hip_spmm_simple.argtypes = [_vp, _vp, _vp, _i64, _i, _i, _vp, _vp, _i, _f, _f, _vp]
     lib.t81_hip_limb_tryte_table.restype = None
     lib.t81_hip_limb_tryte_table.argtypes = [_vp]
 
@@ -148,7 +168,8 @@ def check(rc: int) -> None:
     if rc == OK:
         return
     msg = last_error() or f"libt81_hip error {rc}"
-    if rc in (EINVAL_SHAPE, EINVAL_K48, EINVAL_THRESHOLD, EINVAL_DTYPE, EINVAL_POINTER):
+    if rc in (EINVAL_SHAPE, EINVAL_K48, EINVAL_THRESHOLD, EINVAL_DTYPE, EINVAL_POINTER,
+              EINVAL_INDEX):
         raise ValueError(msg)
     raise T81HipError(msg)
 

@@ -2,8 +2,9 @@
 //
 // Every entry point: validates on the host (the reference's checks and messages,
 // cited per function), checks that the current device is a gfx950, enqueues on
-// the caller's stream and returns.  No exceptions cross the boundary, no memory
-// is allocated, nothing is synchronised.
+// the caller's stream and returns.  No exceptions cross the boundary.  Nothing is
+// allocated or synchronised, except by the sparse plan's create / destroy (and the
+// one-shot t81_hip_spmm_simple built on them), which own device memory.
 #include <hip/hip_runtime.h>
 
 #include <atomic>
@@ -12,6 +13,7 @@
 #include <cstdio>
 #include <cstring>
 #include <initializer_list>
+#include <new>
 #include <string>
 
 #include "../../include/t81_hip.h"
@@ -389,6 +391,150 @@ int t81_hip_tq2_matmul(const void *x, int x_dtype, const uint8_t *w, float *c, i
     return finish(t81hip::launch_tq2_matmul(x, x_dtype, w, c, m, n, k, alpha, beta, bias,
                                             static_cast<hipStream_t>(stream)),
                   "t81_hip_tq2_matmul");
+}
+
+}  // extern "C"
+
+struct t81_hip_spmm_plan {
+    int rows = 0;
+    int cols = 0;
+    int64_t nnz = 0;         // entries stored (those before the first bad one)
+    int32_t *row_ptr = nullptr;  // rows + 1
+    int32_t *col = nullptr;      // nnz, sorted by row, list order within a row
+    double *val = nullptr;       // nnz
+};
+
+namespace {
+
+void spmm_free(t81_hip_spmm_plan *p) {
+    if (!p) return;
+    (void)hipFree(p->row_ptr);
+    (void)hipFree(p->col);
+    (void)hipFree(p->val);
+    delete p;
+}
+
+}  // namespace
+
+extern "C" {
+
+int t81_hip_spmm_plan_create(const int64_t *values, const int32_t *row_idx,
+                             const int32_t *col_idx, int64_t nnz, int rows, int cols,
+                             t81_hip_spmm_plan **plan, int64_t *first_bad, void *stream) {
+    const char *where = "t81_hip_spmm_plan_create";
+    if (plan == nullptr) return fail(T81_HIP_EINVAL_POINTER, "null plan pointer");
+    *plan = nullptr;
+    if (first_bad) *first_bad = -1;
+    // python/bindings.cpp:903-905, simple.hpp:46-48
+    if (rows < 0 || cols < 0) return fail(T81_HIP_EINVAL_SHAPE, "Matrix dimensions must be non-negative");
+    if (nnz < 0 || nnz > INT32_MAX)
+        return fail(T81_HIP_EINVAL_SHAPE, "entry count must be in [0, 2^31 - 1]");
+    if (nnz > 0 && (values == nullptr || row_idx == nullptr || col_idx == nullptr))
+        return fail(T81_HIP_EINVAL_POINTER, "null data pointer");
+    if (reinterpret_cast<uintptr_t>(values) % 8 != 0 || reinterpret_cast<uintptr_t>(row_idx) % 4 != 0 ||
+        reinterpret_cast<uintptr_t>(col_idx) % 4 != 0)
+        return fail(T81_HIP_EINVAL_POINTER, "misaligned entry arrays");
+    if (int rc = require_device(where)) return rc;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+
+    auto *p = new (std::nothrow) t81_hip_spmm_plan;
+    if (!p) return fail(T81_HIP_EHIP, "out of host memory");
+    p->rows = rows;
+    p->cols = cols;
+    unsigned long long *bad_dev = nullptr;
+    void *scratch = nullptr;
+    auto cleanup = [&](int rc) {
+        (void)hipFree(bad_dev);
+        (void)hipFree(scratch);
+        if (rc != T81_HIP_OK && rc != T81_HIP_EINVAL_INDEX) spmm_free(p);
+        return rc;
+    };
+    hipError_t e = hipMalloc(&bad_dev, sizeof(unsigned long long));
+    if (e != hipSuccess) return cleanup(hip_fail(e, where));
+    e = t81hip::launch_spmm_first_bad(row_idx, col_idx, nnz, rows, cols, bad_dev, s);
+    unsigned long long bad = 0;
+    if (e == hipSuccess) e = hipMemcpyAsync(&bad, bad_dev, sizeof(bad), hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return cleanup(hip_fail(e, where));
+    const int64_t n = static_cast<int64_t>(bad < static_cast<unsigned long long>(nnz) ? bad : nnz);
+    p->nnz = n;
+
+    e = hipMalloc(&p->row_ptr, (static_cast<size_t>(rows) + 1) * sizeof(int32_t));
+    if (e == hipSuccess && n > 0) e = hipMalloc(&p->col, static_cast<size_t>(n) * sizeof(int32_t));
+    if (e == hipSuccess && n > 0) e = hipMalloc(&p->val, static_cast<size_t>(n) * sizeof(double));
+    if (e == hipSuccess && n > 0) e = hipMalloc(&scratch, t81hip::spmm_sort_scratch_bytes(n));
+    if (e == hipSuccess)
+        e = t81hip::launch_spmm_build(values, row_idx, col_idx, n, rows, scratch, p->row_ptr, p->col,
+                                      p->val, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);  // scratch is freed next
+    if (e != hipSuccess) return cleanup(hip_fail(e, where));
+
+    *plan = p;
+    if (n < nnz) {
+        // simple.hpp:79-84: the row check comes first
+        int32_t r = 0;
+        e = hipMemcpy(&r, row_idx + n, sizeof(r), hipMemcpyDeviceToHost);
+        if (e != hipSuccess) {
+            *plan = nullptr;
+            return cleanup(hip_fail(e, where));  // frees p
+        }
+        if (first_bad) *first_bad = n;
+        return cleanup(fail(T81_HIP_EINVAL_INDEX, r < 0 || r >= rows ? "Row index out of bounds"
+                                                                     : "Column index out of bounds"));
+    }
+    g_last_error.clear();
+    return cleanup(T81_HIP_OK);
+}
+
+int t81_hip_spmm_plan_apply(const t81_hip_spmm_plan *plan, const float *B, float *C, int N,
+                            float alpha, float beta, void *stream) {
+    if (plan == nullptr) return fail(T81_HIP_EINVAL_POINTER, "null plan");
+    if (N < 0) return fail(T81_HIP_EINVAL_SHAPE, "Feature dimension N must be non-negative");  // bindings.cpp:906-908
+    if ((plan->rows > 0 && N > 0 && C == nullptr) || (plan->cols > 0 && N > 0 && B == nullptr))
+        return fail(T81_HIP_EINVAL_POINTER, "null data pointer");
+    if (reinterpret_cast<uintptr_t>(B) % 4 != 0 || reinterpret_cast<uintptr_t>(C) % 4 != 0)
+        return fail(T81_HIP_EINVAL_POINTER, "float32 data must be 4-byte aligned");
+    if (int rc = require_device("t81_hip_spmm_plan_apply")) return rc;
+    return finish(t81hip::launch_spmm_apply(plan->row_ptr, plan->col, plan->val, B, C, plan->rows, N,
+                                            alpha, beta, static_cast<hipStream_t>(stream)),
+                  "t81_hip_spmm_plan_apply");
+}
+
+int t81_hip_spmm_plan_info(const t81_hip_spmm_plan *plan, int *rows, int *cols, int64_t *nnz) {
+    if (plan == nullptr) return fail(T81_HIP_EINVAL_POINTER, "null plan");
+    if (rows) *rows = plan->rows;
+    if (cols) *cols = plan->cols;
+    if (nnz) *nnz = plan->nnz;
+    return T81_HIP_OK;
+}
+
+void t81_hip_spmm_plan_destroy(t81_hip_spmm_plan *plan) { spmm_free(plan); }
+
+int t81_hip_spmm_simple(const int64_t *values, const int32_t *row_idx, const int32_t *col_idx,
+                        int64_t nnz, int rows, int cols, const float *B, float *C, int N,
+                        float alpha, float beta, void *stream) {
+    if (N < 0) return fail(T81_HIP_EINVAL_SHAPE, "Feature dimension N must be non-negative");
+    if (rows < 0 || cols < 0) return fail(T81_HIP_EINVAL_SHAPE, "Matrix dimensions must be non-negative");
+    if (reinterpret_cast<uintptr_t>(B) % 4 != 0 || reinterpret_cast<uintptr_t>(C) % 4 != 0)
+        return fail(T81_HIP_EINVAL_POINTER, "float32 data must be 4-byte aligned");
+    if ((rows > 0 && N > 0 && C == nullptr) || (cols > 0 && N > 0 && B == nullptr))
+        return fail(T81_HIP_EINVAL_POINTER, "null data pointer");
+    t81_hip_spmm_plan *plan = nullptr;
+    int64_t bad = -1;
+    const int rc = t81_hip_spmm_plan_create(values, row_idx, col_idx, nnz, rows, cols, &plan, &bad,
+                                            stream);
+    if (rc != T81_HIP_OK && rc != T81_HIP_EINVAL_INDEX) return rc;
+    const std::string msg = g_last_error;
+    int rc2 = t81_hip_spmm_plan_apply(plan, B, C, N, alpha, beta, stream);
+    if (rc2 == T81_HIP_OK) {
+        const hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+        if (e != hipSuccess) rc2 = hip_fail(e, "t81_hip_spmm_simple");
+    }
+    spmm_free(plan);
+    if (rc2 != T81_HIP_OK) return rc2;
+    if (rc == T81_HIP_EINVAL_INDEX) return fail(rc, msg);
+    g_last_error.clear();
+    return T81_HIP_OK;
 }
 
 void t81_hip_limb_tryte_table(double *out) { t81hip::host_tryte_table(out); }

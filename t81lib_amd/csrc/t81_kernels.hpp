@@ -38,6 +38,17 @@ hipError_t launch_gemv_strip(bool *handled, const void *x, int x_dtype, const ui
 hipError_t launch_transpose_packed(const uint8_t *in, uint8_t *out, int64_t rows, int64_t cols,
                                    hipStream_t s);
 
+// spmm.hip: sparse ternary (COO) x dense; plan = entries stably sorted by row
+hipError_t launch_spmm_first_bad(const int32_t *row_idx, const int32_t *col_idx, int64_t nnz,
+                                 int rows, int cols, unsigned long long *first_bad, hipStream_t s);
+size_t spmm_sort_scratch_bytes(int64_t n);
+hipError_t launch_spmm_build(const int64_t *values, const int32_t *row_idx, const int32_t *col_idx,
+                             int64_t n, int rows, void *scratch, int32_t *row_ptr,
+                             int32_t *cols_out, double *vals_out, hipStream_t s);
+hipError_t launch_spmm_apply(const int32_t *row_ptr, const int32_t *cols, const double *vals,
+                             const float *B, float *C, int rows, int64_t N, float alpha, float beta,
+                             hipStream_t s);
+
 // tq.hip: GGUF TQ1_0 (quant 34) / TQ2_0 (quant 35) block codecs
 hipError_t launch_tq_quantize(const float *src, uint8_t *dst, int64_t rows, int64_t cols,
                               float thr, int use_thr, int quant, hipStream_t s);

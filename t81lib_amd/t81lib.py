@@ -2,7 +2,7 @@
 
 Same names, argument meanings, defaults and exception types as the pybind11
 module (python/bindings.cpp:759-765 constants, :769-810 ``gemm_ternary``,
-:405-517 quantize/pack, :640-686 unpack).  Arguments may be NumPy arrays /
+:405-517 quantize/pack, :640-686 unpack, :888-940 ``spmm_simple``).  Arguments may be NumPy arrays /
 buffers (copied to the GPU, results copied back -- the host-span contract of
 ``rocm_gemm_ternary``, src/linalg/gemm_rocm.cpp:335-396) or GPU torch tensors
 (used in place, no copies).  Every computation runs on the GPU; there is no
@@ -153,8 +153,65 @@ def unpack_packed_limbs(packed: Any, rows: int, cols: int):
     return _return_like(ops.unpack(t, rows, cols), host)
 
 
+def _float_span(obj: Any, count: int) -> tuple[torch.Tensor, Any]:
+    """(GPU float32 tensor, host array to write back or None), with the buffer checks and
+    messages of make_float_span (python/bindings.cpp:112-134), which the binding applies
+    to B as well as C."""
+    if isinstance(obj, torch.Tensor):
+        if obj.device.type == "cuda":
+            if obj.element_size() != 4:
+                raise ValueError("C buffer must store float32 values")
+            if not obj.is_contiguous():
+                raise ValueError("C buffer must use C-style contiguous memory")
+            if obj.numel() != count:
+                raise ValueError("C buffer byte size mismatch")
+            return obj.reshape(-1).view(torch.float32), None
+        obj = obj.numpy()  # a host tensor: its own memory
+    view = memoryview(obj)
+    if view.readonly:
+        raise ValueError("C buffer must be writable")
+    if view.itemsize != 4:
+        raise ValueError("C buffer must store float32 values")
+    if not view.c_contiguous:
+        raise ValueError("C buffer must use C-style contiguous memory")
+    if view.nbytes != count * 4:
+        raise ValueError("C buffer byte size mismatch")
+    host = np.asarray(view).reshape(-1).view(np.float32)
+    return torch.from_numpy(host.copy()).to(device=_device()), host
+
+
+def spmm_simple(values: Any, row_indices: Any, col_indices: Any, rows: int, cols: int, B: Any,
+                C: Any, N: int, alpha: float = 1.0, beta: float = 0.0) -> None:
+    """COO sparse x dense multiply over ternary weights (python/bindings.cpp:888-940):
+    C (rows x N) = alpha * A B + beta * C in place, B cols x N, entries applied in list
+    order, bit-identical to t81::sparse::spmm_simple (include/t81/sparse/simple.hpp:37-94).
+    An out-of-range index raises ValueError after updating C as the reference does
+    (beta applied, the entries before it added)."""
+    from .sparse import entry_arrays
+
+    dev = _device()
+    v, r, c = entry_arrays(values, row_indices, col_indices, dev)
+    if rows < 0 or cols < 0:
+        raise ValueError("Matrix dimensions must be non-negative")
+    if N < 0:
+        raise ValueError("Feature dimension N must be non-negative")
+    b, _ = _float_span(B, cols * N)
+    out, host = _float_span(C, rows * N)
+    L = _lib.lib()
+    rc = L.t81_hip_spmm_simple(v.data_ptr(), r.data_ptr(), c.data_ptr(), v.numel(), rows, cols,
+                               b.data_ptr(), out.data_ptr(), N, alpha, beta,
+                               torch.cuda.current_stream().cuda_stream)
+    msg = _lib.last_error() if rc != _lib.OK else ""
+    if host is not None and rc in (_lib.OK, _lib.EINVAL_INDEX):
+        host[...] = out.cpu().numpy()
+    if rc == _lib.EINVAL_INDEX:
+        raise ValueError(msg)
+    if rc != _lib.OK:
+        _lib.check(rc)
+
+
 __all__ = [
     "TRITS_PER_LIMB", "TRYTES_PER_LIMB", "BYTES_PER_LIMB", "HAS_CUDA_BACKEND",
     "HAS_METAL_BACKEND", "gemm_ternary", "quantize_to_trits", "dequantize_trits",
-    "pack_dense_matrix", "unpack_packed_limbs",
+    "pack_dense_matrix", "unpack_packed_limbs", "spmm_simple",
 ]

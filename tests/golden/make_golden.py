@@ -18,6 +18,12 @@ source.  Vectors:
 * ``ew_*``                   where / clamp / lerp / addcmul on Backend::CPU
                              (src/linalg/gemm_dispatch.cpp:145-211) over float32 arrays
                              with NaN, +-inf, -0.0, denormals and zeros mixed in
+* ``sp<i>_*``                t81::sparse::spmm_simple (include/t81/sparse/simple.hpp:37-94)
+                             on limbs built from long long as its binding does: the
+                             examples/ternary_sparse_preview.py shape, unsorted rows with
+                             repeated entries, int64 values near +-2^63, NaN / inf /
+                             denormal operands, beta == 0 over NaN, and out-of-range
+                             indices (``_rc`` -1: C as the reference leaves it on throw)
 """
 
 from __future__ import annotations
@@ -31,6 +37,58 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
 
 import oracle  # noqa: E402
+
+
+def spmm_cases():
+    """(name, values, row_idx, col_idx, rows, cols, B, C, N, alpha, beta) for spmm_simple."""
+    g = np.random.default_rng(2024)
+    f32 = np.float32
+    cases = []
+    # examples/ternary_sparse_preview.py:8-40 (256 x 256, 3 % density, values in [-3, 3]
+    # without 0), with 32 features instead of 128 to keep the fixture small
+    nnz = int(256 * 256 * 0.03)
+    v = g.integers(-3, 4, nnz).astype(np.int64)
+    v[v == 0] = 1
+    cases.append(("example", v, g.integers(0, 256, nnz).astype(np.int32),
+                  g.integers(0, 256, nnz).astype(np.int32), 256, 256,
+                  g.standard_normal((256, 32)).astype(f32), np.zeros((256, 32), f32), 32, 1.0, 0.0))
+    # unsorted rows, many entries per row, int64 values whose double rounding matters
+    rows, cols, N, nnz = 9, 7, 33, 400
+    v = g.integers(-2**62, 2**62, nnz, dtype=np.int64)
+    v[:6] = [2**63 - 1, -2**63, 2**53 + 1, -(2**53 + 1), 0, 1]
+    v[6:40] = g.integers(-5, 6, 34)
+    B = (g.standard_normal((cols, N)) * 1e-19).astype(f32)
+    B.reshape(-1)[:8] = [np.inf, -np.inf, np.nan, -0.0, 1e-45, -3e-39, 3e38, 0.0]
+    C = g.standard_normal((rows, N)).astype(f32)
+    C.reshape(-1)[:4] = [np.nan, np.inf, -1e-40, -0.0]
+    cases.append(("order_int64", v, g.integers(0, rows, nnz).astype(np.int32),
+                  g.integers(0, cols, nnz).astype(np.int32), rows, cols, B, C, N, 0.7, -1.3))
+    # beta == 0 replaces C (NaN included) by zeros before the entries
+    cases.append(("beta0_nan", g.integers(-3, 4, 12).astype(np.int64),
+                  g.integers(0, 5, 12).astype(np.int32), g.integers(0, 6, 12).astype(np.int32),
+                  5, 6, g.standard_normal((6, 3)).astype(f32), np.full((5, 3), np.nan, f32), 3,
+                  -2.5, 0.0))
+    # alpha == 0 against an infinite B: 0 * inf = NaN in the touched rows
+    Binf = np.ones((4, 2), f32)
+    Binf[1, 0] = np.inf
+    cases.append(("alpha0_inf", np.array([1, -1, 3], np.int64), np.array([0, 2, 2], np.int32),
+                  np.array([1, 0, 1], np.int32), 3, 4, Binf, np.ones((3, 2), f32), 2, 0.0, 2.0))
+    # out-of-range row at entry 7 and column at entry 0: C as left at the throw
+    ri = g.integers(0, 6, 20).astype(np.int32)
+    ci = g.integers(0, 5, 20).astype(np.int32)
+    ri[7] = 6
+    cases.append(("bad_row", g.integers(-4, 5, 20).astype(np.int64), ri, ci, 6, 5,
+                  g.standard_normal((5, 4)).astype(f32), g.standard_normal((6, 4)).astype(f32), 4,
+                  1.5, 0.5))
+    ci2 = ci.copy()
+    ci2[0] = -1
+    cases.append(("bad_col", g.integers(-4, 5, 20).astype(np.int64), ri.copy(), ci2, 7, 5,
+                  g.standard_normal((5, 4)).astype(f32), g.standard_normal((7, 4)).astype(f32), 4,
+                  1.0, -0.25))
+    cases.append(("empty", np.zeros(0, np.int64), np.zeros(0, np.int32), np.zeros(0, np.int32),
+                  4, 3, g.standard_normal((3, 5)).astype(f32), g.standard_normal((4, 5)).astype(f32),
+                  5, 1.0, 0.5))
+    return cases
 
 
 def main() -> None:
@@ -131,6 +189,14 @@ def main() -> None:
                ew_clamp=ref.elementwise("clamp", a, p0=-0.75, p1=1.25),
                ew_lerp=ref.elementwise("lerp", a, b, c),
                ew_addcmul=ref.elementwise("addcmul", a, b, c, p0=0.3))
+    for i, case in enumerate(spmm_cases()):
+        name, values, ri, ci, rows, cols, B, C, N, al, be = case
+        rc, res = ref.spmm_simple(values, ri, ci, rows, cols, B, C, N, al, be)
+        out.update({f"sp{i}_values": values, f"sp{i}_rows": ri, f"sp{i}_cols": ci,
+                    f"sp{i}_dims": np.array([rows, cols, N], np.int64),
+                    f"sp{i}_ab": np.array([al, be], np.float32), f"sp{i}_B": B, f"sp{i}_C": C,
+                    f"sp{i}_out": res, f"sp{i}_rc": np.array(rc, np.int64)})
+    out["sp_names"] = np.array([c[0] for c in spmm_cases()])
     np.savez_compressed(path, **out)
     print(f"wrote {path} ({os.path.getsize(path)} bytes, SIMD path {ref.simd_path()})")
 

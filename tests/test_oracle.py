@@ -326,3 +326,72 @@ def test_elementwise_matches_compiled_reference_live(orc):
     for op, kw in EW_CASES:
         assert _same_or_both_nan(orc.elementwise(op, a, b, c, **kw),
                                  ref.elementwise(op, a, b, c, **kw)), op
+
+
+def _spmm_case(z, i):
+    rows, cols, N = (int(d) for d in z[f"sp{i}_dims"])
+    alpha, beta = (float(a) for a in z[f"sp{i}_ab"])
+    return (z[f"sp{i}_values"], z[f"sp{i}_rows"], z[f"sp{i}_cols"], rows, cols, z[f"sp{i}_B"],
+            z[f"sp{i}_C"], N, alpha, beta)
+
+
+def test_spmm_golden(orc, golden):
+    """spmm_simple equals the compiled reference (include/t81/sparse/simple.hpp:37-94) bit
+    for bit on every fixture case, NaN payloads and the state of C on a throw included."""
+    for i, name in enumerate(golden["sp_names"]):
+        rc, out = orc.spmm_simple(*_spmm_case(golden, i))
+        assert rc == int(golden[f"sp{i}_rc"]), name
+        np.testing.assert_array_equal(out.view(np.uint32), golden[f"sp{i}_out"].view(np.uint32),
+                                      err_msg=str(name))
+
+
+def test_spmm_closed_forms(orc):
+    f32 = np.float32
+    # list order with a float rounding after every entry: 1e8 + 1 rounds back to 1e8,
+    # so the entries (1e8, 1, -1e8) give 0 while an exact or reordered sum gives 1
+    B = np.array([[1e8], [1.0]], f32)
+    rc, out = orc.spmm_simple([1, 1, -1], [0, 0, 0], [0, 1, 0], 1, 2, B, np.zeros((1, 1), f32), 1)
+    assert rc == 0 and out[0, 0] == 0.0
+    rc, out = orc.spmm_simple([1, -1, 1], [0, 0, 0], [0, 0, 1], 1, 2, B, np.zeros((1, 1), f32), 1)
+    assert out[0, 0] == 1.0
+    # the integer value becomes a double once, to nearest even: 2^53 + 1 -> 2^53
+    rc, out = orc.spmm_simple([2**53 + 1], [0], [0], 1, 1, np.ones((1, 1), f32),
+                              np.zeros((1, 1), f32), 1)
+    assert out[0, 0] == f32(2.0**53)
+    # beta == 0 zero-fills (NaN gone); beta != 0 scales through double
+    C = np.array([[np.nan, 3.0]], f32)
+    rc, out = orc.spmm_simple([], [], [], 1, 1, np.zeros((1, 2), f32), C, 2, 1.0, 0.0)
+    assert list(out[0]) == [0.0, 0.0]
+    rc, out = orc.spmm_simple([], [], [], 1, 1, np.zeros((1, 2), f32), C, 2, 1.0, 0.1)
+    assert np.isnan(out[0, 0]) and out[0, 1] == f32(np.float64(f32(3.0)) * np.float64(f32(0.1)))
+    # a dense small case equals the exact float64 product when nothing rounds
+    g = np.random.default_rng(3)
+    vals = g.integers(-3, 4, 30)
+    ri, ci = g.integers(0, 4, 30), g.integers(0, 5, 30)
+    Bi = g.integers(-8, 9, (5, 6)).astype(f32)
+    dense = np.zeros((4, 5))
+    np.add.at(dense, (ri, ci), vals)
+    rc, out = orc.spmm_simple(vals, ri, ci, 4, 5, Bi, np.zeros((4, 6), f32), 6)
+    np.testing.assert_array_equal(out, (dense @ Bi.astype(np.float64)).astype(f32))
+    # an out-of-range index stops at that entry (-1), entries before it applied
+    rc, out = orc.spmm_simple([2, 5], [0, 3], [0, 0], 1, 1, np.ones((1, 1), f32),
+                              np.zeros((1, 1), f32), 1)
+    assert rc == -1 and out[0, 0] == 2.0
+
+
+@pytest.mark.skipif("not __import__('oracle').ref()", reason="oracle/_ref not built here")
+def test_spmm_matches_compiled_reference_live(orc):
+    ref = orc.ref()
+    g = np.random.default_rng(77)
+    for rows, cols, N, nnz, alpha, beta in ((40, 30, 17, 900, 0.3, -2.0), (1, 1, 1, 50, 1.0, 0.0),
+                                            (300, 200, 8, 5000, -1.7, 1.0)):
+        vals = g.integers(-2**63, 2**63 - 1, nnz, dtype=np.int64, endpoint=True)
+        vals[::3] = g.integers(-1, 2, vals[::3].size)
+        ri = g.integers(0, rows, nnz).astype(np.int32)
+        ci = g.integers(0, cols, nnz).astype(np.int32)
+        B = (g.standard_normal((cols, N)) * 1e-17).astype(np.float32)
+        C = g.standard_normal((rows, N)).astype(np.float32)
+        got = orc.spmm_simple(vals, ri, ci, rows, cols, B, C, N, alpha, beta)
+        want = ref.spmm_simple(vals, ri, ci, rows, cols, B, C, N, alpha, beta)
+        assert got[0] == want[0]
+        np.testing.assert_array_equal(got[1].view(np.uint32), want[1].view(np.uint32))
