@@ -111,7 +111,8 @@ __device__ __forceinline__ u32x2 load_half_limb(const uint8_t *w, int64_t row, i
 template <int XT, int RN, int CM, int WN, int WM, int LK, bool kAligned>
 __global__ __launch_bounds__(64 * WN * WM) void gemm_kernel(
     const void *__restrict__ x, const uint8_t *__restrict__ w, void *__restrict__ c, int64_t M,
-    int64_t N, int64_t K, int64_t L, float alpha, float beta, const float *__restrict__ bias) {
+    int64_t N, int64_t ldc, int64_t K, int64_t L, float alpha, float beta,
+    const float *__restrict__ bias) {
     using Cfg = GemmCfg<XT, RN, CM, WN, WM, LK>;
     constexpr int kLK = Cfg::kLK;
     constexpr int kStepK = Cfg::kStepK;
@@ -261,7 +262,7 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_kernel(
             for (int a4 = 0; a4 < 4; ++a4) {
                 const int64_t nb = n0 + 32 * i + 8 * a4 + 4 * h;
                 if constexpr (XT == kDtypeI8) {
-                    int32_t *cr = static_cast<int32_t *>(c) + m * N;
+                    int32_t *cr = static_cast<int32_t *>(c) + m * ldc;
 #pragma unroll
                     for (int b = 0; b < 4; ++b) {
                         if (nb + b < N) {
@@ -271,7 +272,7 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_kernel(
                         }
                     }
                 } else {
-                    float *cr = static_cast<float *>(c) + m * N;
+                    float *cr = static_cast<float *>(c) + m * ldc;
                     float y[4];
 #pragma unroll
                     for (int b = 0; b < 4; ++b) {
@@ -296,9 +297,11 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_kernel(
     }
 }
 
+// Rows [0, n) of W and columns [0, n) of C, whose rows are ldc elements apart.
 template <int XT, int RN, int CM, int WN, int WM, int LK>
 hipError_t launch_gemm_t(const void *x, const uint8_t *w, void *c, int64_t m, int64_t n,
-                         int64_t k, float alpha, float beta, const float *bias, hipStream_t s) {
+                         int64_t ldc, int64_t k, float alpha, float beta, const float *bias,
+                         hipStream_t s) {
     using Cfg = GemmCfg<XT, RN, CM, WN, WM, LK>;
     const int64_t L = (k + kTrits - 1) / kTrits;
     const int64_t tiles = ((n + Cfg::kBN - 1) / Cfg::kBN) * ((m + Cfg::kBM - 1) / Cfg::kBM);
@@ -306,30 +309,61 @@ hipError_t launch_gemm_t(const void *x, const uint8_t *w, void *c, int64_t m, in
     const bool aligned = (k % 8 == 0) && (reinterpret_cast<uintptr_t>(x) % (8 * elem) == 0);
     if (aligned)
         gemm_kernel<XT, RN, CM, WN, WM, LK, true><<<dim3(tiles), dim3(Cfg::kThreads), 0, s>>>(
-            x, w, c, m, n, k, L, alpha, beta, bias);
+            x, w, c, m, n, ldc, k, L, alpha, beta, bias);
     else
         gemm_kernel<XT, RN, CM, WN, WM, LK, false><<<dim3(tiles), dim3(Cfg::kThreads), 0, s>>>(
-            x, w, c, m, n, k, L, alpha, beta, bias);
+            x, w, c, m, n, ldc, k, L, alpha, beta, bias);
     return hipGetLastError();
+}
+
+// Compute units of the current device (one workgroup of the big tile fits per CU).
+int cu_count() {
+    static int cached[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            cus <= 0)
+            cus = 256;
+        cached[dev] = cus;
+    }
+    return cached[dev];
 }
 
 template <int XT>
 hipError_t launch_gemm_x(const void *x, const uint8_t *w, void *c, int64_t m, int64_t n,
                          int64_t k, float alpha, float beta, const float *bias, hipStream_t s) {
     constexpr int LK = 2;  // limbs per k-step
-    if (m <= 32) return launch_gemm_t<XT, 2, 1, 4, 1, LK>(x, w, c, m, n, k, alpha, beta, bias, s);
-    if (m <= 64) return launch_gemm_t<XT, 2, 2, 4, 1, LK>(x, w, c, m, n, k, alpha, beta, bias, s);
+    if (m <= 32) return launch_gemm_t<XT, 2, 1, 4, 1, LK>(x, w, c, m, n, n, k, alpha, beta, bias, s);
+    if (m <= 64) return launch_gemm_t<XT, 2, 2, 4, 1, LK>(x, w, c, m, n, n, k, alpha, beta, bias, s);
     if constexpr (XT != kDtypeF32) {
         // Eight waves (two per SIMD, so one wave's waits are covered by the other's
         // MFMAs): 256 x 256 tiles while there are enough of them to spread over the
         // GPU, 256 weight rows x 128 tokens otherwise (measured crossover ~160 tiles).
-        const int64_t tiles_big = ((n + 255) / 256) * ((m + 255) / 256);
-        if (tiles_big >= 160)
-            return launch_gemm_t<XT, 2, 4, 4, 2, LK>(x, w, c, m, n, k, alpha, beta, bias, s);
-        return launch_gemm_t<XT, 2, 2, 4, 2, LK>(x, w, c, m, n, k, alpha, beta, bias, s);
+        const int64_t tiles_m = (m + 255) / 256;
+        const int64_t tiles_big = ((n + 255) / 256) * tiles_m;
+        if (tiles_big < 160)
+            return launch_gemm_t<XT, 2, 2, 4, 2, LK>(x, w, c, m, n, n, k, alpha, beta, bias, s);
+        // One big-tile workgroup per CU at a time: when the last round of big tiles would
+        // be at most half full, the rows of whole rounds take big tiles and the rest
+        // (fewer rows) the half-height tiles, one short round instead of a half-empty one.
+        const int64_t cus = cu_count();
+        const int64_t rem = tiles_big % cus;
+        const int64_t n1 = (tiles_big - rem) / tiles_m * 256;
+        if (tiles_big > cus && rem != 0 && 2 * rem <= cus && n1 > 0 && n1 < n) {
+            hipError_t e = launch_gemm_t<XT, 2, 4, 4, 2, LK>(x, w, c, m, n1, n, k, alpha, beta,
+                                                           bias, s);
+            if (e != hipSuccess) return e;
+            const int64_t L = (k + kTrits - 1) / kTrits;
+            return launch_gemm_t<XT, 2, 2, 4, 2, LK>(x, w + n1 * L * kTrytes,
+                                                   static_cast<uint8_t *>(c) + 4 * n1, m, n - n1,
+                                                   n, k, alpha, beta, bias ? bias + n1 : nullptr, s);
+        }
+        return launch_gemm_t<XT, 2, 4, 4, 2, LK>(x, w, c, m, n, n, k, alpha, beta, bias, s);
     }
     // fp32 activations: two LDS planes; four waves with 256 x 128 tiles
-    return launch_gemm_t<XT, 2, 4, 4, 1, LK>(x, w, c, m, n, k, alpha, beta, bias, s);
+    return launch_gemm_t<XT, 2, 4, 4, 1, LK>(x, w, c, m, n, n, k, alpha, beta, bias, s);
 }
 
 }  // namespace

@@ -235,3 +235,22 @@ def test_config4_llama_prefill_sampled(gpu, orc, layer, M):
     y2 = ops.ternary_matmul(x2, packed, K, kernel=3)
     scale = (x1.abs() + x2.abs()).sum(1, keepdim=True)
     assert bool(((y12 - y1 - y2).abs() <= 2e-3 * scale + 1e-4).all())
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.int8])
+def test_k3_row_split_full_check(gpu, orc, dtype):
+    """300 big tiles on 256 CUs: rows of whole rounds take 256 x 256 tiles and the rest
+    256 x 128 tiles in a second launch (C row stride = N, bias offset).  Every output is
+    checked, across the boundary, with ragged M and N."""
+    M, N, K = 257, 256 * 150 + 13, 100
+    announce(f"K3 row split {dtype} M={M} N={N} K={K}")
+    w, x, c, bias = make_problem(M, N, K, dtype, seed=11)
+    if dtype == torch.int8:
+        packed, out = run(gpu, w, x, c, bias, K, 1.0, 0.0, False, kernel=3)
+        want = orc.trit_matmul_i64(x.numpy(), packed, K)
+        np.testing.assert_array_equal(out.numpy().astype(np.int64), want)
+        return
+    packed, out = run(gpu, w, x, c, bias, K, 0.75, 0.5, True, kernel=3)
+    ref, scale = oracle_matmul(orc, x, packed, K, 0.75, 0.5, c, bias)
+    ok, worst, nbad = fp_tolerance_ok(out.numpy(), ref, scale, RTOL[dtype])
+    assert ok, f"{nbad} outside, worst {worst:.3g}"
