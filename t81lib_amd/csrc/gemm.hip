@@ -20,6 +20,8 @@
 //    16 contiguous bytes of the LDS tile.  The weight stream never touches LDS.
 // Output: lane (c, h) of a 32x32 block holds rows 8a + 4h + b (a, b < 4) of
 // column c, so each lane stores 4 consecutive outputs of one token.
+#include <type_traits>
+
 #include "t81_device.hpp"
 #include "t81_kernels.hpp"
 
@@ -297,6 +299,317 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_kernel(
     }
 }
 
+// ---------------------------------------------------------------------------
+// Big-tile kernel for bf16 activations: one wave per SIMD.
+//
+// A workgroup of four waves computes a 256 x 256 tile of C^T; wave (wn, wm) owns
+// 128 weight rows x 128 tokens, i.e. 4 x 4 blocks of v_mfma_f32_32x32x16_bf16
+// (256 accumulator registers).  A k-step is two limbs (96 trits):
+//  * lane (r, h) loads all 16 bytes of limb 2s + h of row 32 rb + r, so one
+//    32-trit slice of the MFMA pairs trits 8J..8J+7 of limb 2s (h = 0) with the
+//    same trits of limb 2s + 1 (h = 1), J = 0..5; B lane (c, h) reads
+//    X[c, 96s + 48h + 8J .. +8], 16 bytes of the activation tile;
+//  * the weights decode (LDS table) half a limb at a time: half p gives the
+//    A fragments of J = 3p..3p+2 for all four row blocks.  The decode of the
+//    next half runs while the MFMAs of the current one do;
+//  * the activation tile of step s + 1 goes straight from global memory into the
+//    other LDS buffer (buffer loads with the LDS bit, no registers) at the start
+//    of step s; one barrier per step.  Tile rows are 13 16-byte slots (12 chunks of
+//    8 activations + 1 pad slot), so the 16-byte B reads of 16 lanes fall on
+//    distinct banks.  Chunks past K or past M, and the pad slots, load zeros
+//    (out-of-range buffer offsets).
+constexpr int kW4Threads = 256;
+constexpr int kW4Rows = 256;                        // weight rows per workgroup
+constexpr int kW4Tokens = 256;                      // tokens per workgroup
+constexpr int kW4StepK = 2 * kTrits;                // trits per k-step
+constexpr int kW4RowSlots = kW4StepK / 8 + 1;       // 16-byte slots per tile row (+1 pad)
+constexpr int kW4RowBytes = 16 * kW4RowSlots;       // 208
+constexpr int kW4TileBytes = kW4Tokens * kW4RowBytes;
+constexpr int kW4LoadsPerWave = kW4Tokens * kW4RowSlots / (64 * 4);   // 13
+constexpr uint32_t kW4Oob = 0x80000000u;
+
+// A raw buffer descriptor over [base, base + bytes) (clamped to 2^31 - 1 bytes) whose
+// fields are forced into scalar registers: the loads then need no per-lane
+// descriptor checks.  base and bytes must be the same in every lane.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void *base, int64_t bytes) {
+    const uint64_t p = reinterpret_cast<uint64_t>(base);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(p));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(p >> 32));
+    const int n = __builtin_amdgcn_readfirstlane(bytes < 0x7FFFFFFF ? static_cast<int>(bytes)
+                                                                    : 0x7FFFFFFF);
+    return __builtin_amdgcn_make_buffer_rsrc(
+        reinterpret_cast<void *>((static_cast<uint64_t>(hi) << 32) | lo), 0, n, 0x00020000);
+}
+
+template <int XT>
+__global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
+    const void *__restrict__ x, const uint8_t *__restrict__ w, void *__restrict__ c, int64_t M,
+    int64_t N, int64_t ldc, int64_t K, int64_t L, float alpha, float beta,
+    const float *__restrict__ bias) {
+    static_assert(XT == kDtypeBF16, "the LDS tile is filled straight from bf16 activations");
+    // Two separate tile objects (not one array indexed by a run-time parity): the
+    // loads into one buffer then provably do not alias the reads of the other, and
+    // the compiler need not wait for them before every LDS read.
+    // (The table's larger alignment places it at LDS address 0, so a table address is
+    // just the byte field, with no base to add.)
+    __shared__ __attribute__((aligned(1024))) uint8_t lut[kLutBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t xs0[kW4TileBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t xs1[kW4TileBytes];
+    auto tile = [&](auto bufc) -> uint8_t * {
+        if constexpr (decltype(bufc)::value == 0) return xs0;
+        else return xs1;
+    };
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wn = wave & 1;
+    const int wm = wave >> 1;
+    const int r = lane & 31;
+    const int h = lane >> 5;
+
+    // blockIdx.x walks the weight-row tiles fastest: workgroups running together
+    // share their activation rows.  (Tile indices are uniform: readfirstlane keeps
+    // them, and the buffer descriptors built from them, in scalar registers.)
+    const int tiles_n = static_cast<int>((N + kW4Rows - 1) / kW4Rows);
+    const int bid = static_cast<int>(blockIdx.x);
+    const int tn = __builtin_amdgcn_readfirstlane(bid % tiles_n);
+    const int tm = __builtin_amdgcn_readfirstlane(bid / tiles_n);
+    const int64_t nwg = static_cast<int64_t>(tn) * kW4Rows;
+    const int64_t m0 = static_cast<int64_t>(tm) * kW4Tokens;
+    const int64_t nsteps = (L + 1) / 2;
+
+    // Weights through a buffer based at the workgroup's first row: rows past N read
+    // zeros.  A limb index past L (odd L, last step) reads the next row's first limb
+    // or zeros; either decodes to finite trits that meet zero activations.
+    const __amdgpu_buffer_rsrc_t wsrc = uniform_rsrc(w + nwg * L * kTrytes, (N - nwg) * L * kTrytes);
+    uint32_t woff[4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+        woff[rb] = (static_cast<uint32_t>(128 * wn + 32 * rb + r) * static_cast<uint32_t>(L) +
+                    static_cast<uint32_t>(h)) * kTrytes;
+    auto fetch_w = [&](int64_t step, u32x4 (&dst)[4]) {
+        const uint32_t koff = static_cast<uint32_t>(step) * (2 * kTrytes);
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb)
+            dst[rb] = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(wsrc, woff[rb] + koff, 0, 0));
+    };
+
+    // Activation tile: load i of wave w fills slots q = 64 (13 w + i) + lane, tile row
+    // q / 13, slot q % 13.  Activations through a buffer based at token m0: tokens
+    // past M read zeros.
+    const __amdgpu_buffer_rsrc_t xsrc =
+        uniform_rsrc(static_cast<const uint16_t *>(x) + m0 * K, (M - m0) * K * 2);
+    // Per-lane constants of the 13 loads: the byte offset of the chunk for k0 = 0 (or an
+    // out-of-range offset for a pad slot) and, packed four to a register, 8 * slot, the
+    // chunk's first trit within the step (past K the chunk loads zeros).
+    uint32_t tbase[kW4LoadsPerWave];
+    uint32_t tslot[(kW4LoadsPerWave + 3) / 4];
+#pragma unroll
+    for (int i = 0; i < (kW4LoadsPerWave + 3) / 4; ++i) tslot[i] = 0u;
+#pragma unroll
+    for (int i = 0; i < kW4LoadsPerWave; ++i) {
+        const uint32_t q = static_cast<uint32_t>(64 * (kW4LoadsPerWave * wave + i) + lane);
+        const uint32_t row = q / kW4RowSlots;
+        const uint32_t slot = q - row * kW4RowSlots;
+        tbase[i] = slot < kW4RowSlots - 1
+                       ? (row * static_cast<uint32_t>(K) + 8 * slot) * 2
+                       : kW4Oob;
+        tslot[i / 4] |= (8 * slot) << (8 * (i % 4));
+    }
+    // Load i of the wave's share of the tile of k-step `step` into LDS buffer buf (all
+    // zeros past the last step).
+    auto load_tile_part = [&](int64_t step, auto bufc, int i) {
+        const int64_t k0 = step * kW4StepK;
+        const uint32_t lim = k0 < K ? static_cast<uint32_t>(K - k0) : 0u;
+        const uint32_t slot8 = (tslot[i / 4] >> (8 * (i % 4))) & 0xFFu;
+        const uint32_t off = slot8 < lim ? tbase[i] + static_cast<uint32_t>(k0) * 2 : kW4Oob;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            xsrc,
+            (__attribute__((address_space(3))) void *)(
+                &tile(bufc)[16 * 64 * (kW4LoadsPerWave * wave + i)]),
+            16, off, 0, 0, 0);
+    };
+    auto load_tile = [&](int64_t step, auto bufc) {
+#pragma unroll
+        for (int i = 0; i < kW4LoadsPerWave; ++i) load_tile_part(step, bufc, i);
+    };
+
+    // Half p of the lane's limbs -> A fragments J = 3p + j of the four row blocks.
+    auto decode_half = [&](const u32x4 (&wl)[4], int p, bf16x8 (&a)[4][3]) {
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            uint32_t pairs[12];
+            decode_dword(lut, wl[rb][2 * p], pairs);
+            decode_dword(lut, wl[rb][2 * p + 1], pairs + 6);
+#pragma unroll
+            for (int j = 0; j < 3; ++j) {
+                const u32x4 raw = {pairs[4 * j], pairs[4 * j + 1], pairs[4 * j + 2],
+                                   pairs[4 * j + 3]};
+                a[rb][j] = __builtin_bit_cast(bf16x8, raw);
+            }
+        }
+    };
+
+    floatx16 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+    // B lane (c, h): token 128 wm + 32 cb + c of the tile, trits 48h + 8J.. of the step.
+    const int brow = (128 * wm + r) * kW4RowBytes + 96 * h;
+    auto read_b = [&](auto bufc, int p, int g) -> u32x4 {
+        const int j = g / 4;
+        const int cb = g % 4;
+        return *reinterpret_cast<const u32x4 *>(
+            &tile(bufc)[brow + 32 * cb * kW4RowBytes + 16 * (3 * p + j)]);
+    };
+    // decode_dword in two parts, so the table reads can be issued a chunk ahead of the
+    // merge that needs them.
+    auto table_fetch = [&](uint32_t wd, uint2 (&e)[4]) {
+        const uint32_t w8 = wd << 3;
+        e[0] = *reinterpret_cast<const uint2 *>(lut + kLutE + (w8 & 0xFFu));
+        e[1] = *reinterpret_cast<const uint2 *>(lut + kLutF + ((w8 >> 8) & 0xFFu));
+        e[2] = *reinterpret_cast<const uint2 *>(lut + kLutE + ((w8 >> 16) & 0xFFu));
+        e[3] = *reinterpret_cast<const uint2 *>(lut + kLutF + (w8 >> 24));
+    };
+    auto table_merge = [&](const uint2 (&e)[4], uint32_t *out) {
+        out[0] = e[0].x;
+        out[1] = e[0].y | e[1].x;
+        out[2] = e[1].y;
+        out[3] = e[2].x;
+        out[4] = e[2].y | e[3].x;
+        out[5] = e[3].y;
+    };
+    // The 48 MFMAs of half p (fragments a, tile buffer buf) as 12 chunks of four (one
+    // B fragment each, read a chunk ahead), fenced so that each chunk also carries a
+    // share of the decode of half q of the limbs wl into `next` (table reads in chunk
+    // g, merge in chunk g + 1) and extra(g), the chunk's share of the loads.
+    auto run_half = [&](auto bufc, int p, const bf16x8 (&a)[4][3], const u32x4 (&wl)[4], int q,
+                        bf16x8 (&next)[4][3], auto &&extra) {
+        u32x4 bq[2];
+        bq[0] = read_b(bufc, p, 0);
+        uint2 e[2][4];
+        uint32_t pairs[4][12];
+#pragma unroll
+        for (int g = 0; g < 12; ++g) {
+            if (g + 1 < 12) bq[(g + 1) & 1] = read_b(bufc, p, g + 1);
+            if (g < 8) table_fetch(wl[g / 2][2 * q + (g % 2)], e[g & 1]);
+            if (g >= 1 && g <= 8)
+                table_merge(e[(g - 1) & 1], &pairs[(g - 1) / 2][6 * ((g - 1) % 2)]);
+            extra(g);
+            const bf16x8 b = __builtin_bit_cast(bf16x8, bq[g & 1]);
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb)
+                acc[rb][g % 4] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[rb][g / 4], b,
+                                                                         acc[rb][g % 4], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+            for (int j = 0; j < 3; ++j) {
+                const u32x4 raw = {pairs[rb][4 * j], pairs[rb][4 * j + 1], pairs[rb][4 * j + 2],
+                                   pairs[rb][4 * j + 3]};
+                next[rb][j] = __builtin_bit_cast(bf16x8, raw);
+            }
+    };
+
+    lut_fill(lut, tid, kW4Threads);
+    u32x4 wcur[4], wnxt[4];
+    bf16x8 a0[4][3], a1[4][3];
+    if (nsteps > 0) {
+        fetch_w(0, wcur);
+        load_tile(0, std::integral_constant<int, 0>());
+    }
+    // vmcnt(0): the tile's LDS writes have landed before the barrier publishes them
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();
+    if (nsteps > 0) decode_half(wcur, 0, a0);
+
+    // Per step: half 0's MFMAs carry the loads for step + 1 (unconditional: past the last
+    // step they read zeros or unused weight bytes) and the decode of half 1; half 1's
+    // MFMAs carry the decode of the next step's half 0.  Steps alternate between the
+    // two tile buffers, so the loop runs two steps per iteration.
+    auto step_body = [&](int64_t step, auto bufc, auto otherc) {
+        run_half(bufc, 0, a0, wcur, 1, a1, [&](int g) {
+            if (g == 0) fetch_w(step + 1, wnxt);
+            load_tile_part(step + 1, otherc, g);
+            if (g == kW4LoadsPerWave - 2) load_tile_part(step + 1, otherc, g + 1);
+        });
+        run_half(bufc, 1, a1, wnxt, 0, a0, [&](int) {});
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) wcur[rb] = wnxt[rb];
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+        __syncthreads();
+    };
+    int64_t step = 0;
+    for (; step + 1 < nsteps; step += 2) {
+        step_body(step, std::integral_constant<int, 0>(), std::integral_constant<int, 1>());
+        step_body(step + 1, std::integral_constant<int, 1>(), std::integral_constant<int, 0>());
+    }
+    if (step < nsteps)  // odd step count: the last step, peeled (no join inside the loop)
+        step_body(step, std::integral_constant<int, 0>(), std::integral_constant<int, 1>());
+
+    // ---- epilogue: lane (c, h) of block (rb, cb) holds rows 8 a4 + 4 h + b of token c ----
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) {
+            const int64_t m = m0 + 128 * wm + 32 * cb + r;
+            if (m >= M) continue;
+            float *cr = static_cast<float *>(c) + m * ldc;
+#pragma unroll
+            for (int a4 = 0; a4 < 4; ++a4) {
+                const int64_t nb = nwg + 128 * wn + 32 * rb + 8 * a4 + 4 * h;
+                float y[4];
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    const int64_t n = nb + b;
+                    float t = alpha * acc[rb][cb][4 * a4 + b];
+                    if (n < N) {
+                        if (beta != 0.0f) t = t + beta * cr[n];
+                        if (bias != nullptr) t = t + bias[n];
+                    }
+                    y[b] = t;
+                }
+                if (nb + 3 < N && (reinterpret_cast<uintptr_t>(cr + nb) & 15u) == 0) {
+                    *reinterpret_cast<float4 *>(cr + nb) = make_float4(y[0], y[1], y[2], y[3]);
+                } else {
+#pragma unroll
+                    for (int b = 0; b < 4; ++b)
+                        if (nb + b < N) cr[nb + b] = y[b];
+                }
+            }
+        }
+    }
+}
+
+// Whether the big-tile kernel takes this shape: bf16 activations, 16-byte rows of
+// whole chunks, and 32-bit buffer offsets for a workgroup's weights and activations.
+bool gemm_w4_fits(const void *x, int64_t m, int64_t n, int64_t k) {
+    const int64_t L = (k + kTrits - 1) / kTrits;
+    return k % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+           int64_t(kW4Rows) * L * kTrytes < 0x7FFFFFFF &&
+           int64_t(kW4Tokens) * k * 2 < 0x7FFFFFFF && m > 0 && m < (int64_t(1) << 30) &&
+           n < (int64_t(1) << 30);
+}
+
+// Rows [0, n) of W and columns [0, n) of C, whose rows are ldc elements apart.
+hipError_t launch_gemm_w4(const void *x, const uint8_t *w, void *c, int64_t m, int64_t n,
+                          int64_t ldc, int64_t k, float alpha, float beta, const float *bias,
+                          hipStream_t s) {
+    const int64_t L = (k + kTrits - 1) / kTrits;
+    const int64_t tiles = ((n + kW4Rows - 1) / kW4Rows) * ((m + kW4Tokens - 1) / kW4Tokens);
+    gemm_w4_kernel<kDtypeBF16><<<dim3(tiles), dim3(kW4Threads), 0, s>>>(x, w, c, m, n, ldc, k, L,
+                                                                      alpha, beta, bias);
+    return hipGetLastError();
+}
+
 // Rows [0, n) of W and columns [0, n) of C, whose rows are ldc elements apart.
 template <int XT, int RN, int CM, int WN, int WM, int LK>
 hipError_t launch_gemm_t(const void *x, const uint8_t *w, void *c, int64_t m, int64_t n,
@@ -351,16 +664,21 @@ hipError_t launch_gemm_x(const void *x, const uint8_t *w, void *c, int64_t m, in
         const int64_t cus = cu_count();
         const int64_t rem = tiles_big % cus;
         const int64_t n1 = (tiles_big - rem) / tiles_m * 256;
+        const int64_t L = (k + kTrits - 1) / kTrits;
+        const bool w4 = XT == kDtypeBF16 && gemm_w4_fits(x, m, n, k);
+        auto big = [&](int64_t rows) {
+            return w4 ? launch_gemm_w4(x, w, c, m, rows, n, k, alpha, beta, bias, s)
+                      : launch_gemm_t<XT, 2, 4, 4, 2, LK>(x, w, c, m, rows, n, k, alpha, beta,
+                                                          bias, s);
+        };
         if (tiles_big > cus && rem != 0 && 2 * rem <= cus && n1 > 0 && n1 < n) {
-            hipError_t e = launch_gemm_t<XT, 2, 4, 4, 2, LK>(x, w, c, m, n1, n, k, alpha, beta,
-                                                           bias, s);
+            hipError_t e = big(n1);
             if (e != hipSuccess) return e;
-            const int64_t L = (k + kTrits - 1) / kTrits;
             return launch_gemm_t<XT, 2, 2, 4, 2, LK>(x, w + n1 * L * kTrytes,
                                                    static_cast<uint8_t *>(c) + 4 * n1, m, n - n1,
                                                    n, k, alpha, beta, bias ? bias + n1 : nullptr, s);
         }
-        return launch_gemm_t<XT, 2, 4, 4, 2, LK>(x, w, c, m, n, n, k, alpha, beta, bias, s);
+        return big(n);
     }
     // fp32 activations: two LDS planes; four waves with 256 x 128 tiles
     return launch_gemm_t<XT, 2, 4, 4, 1, LK>(x, w, c, m, n, n, k, alpha, beta, bias, s);

@@ -254,3 +254,23 @@ def test_k3_row_split_full_check(gpu, orc, dtype):
     ref, scale = oracle_matmul(orc, x, packed, K, 0.75, 0.5, c, bias)
     ok, worst, nbad = fp_tolerance_ok(out.numpy(), ref, scale, RTOL[dtype])
     assert ok, f"{nbad} outside, worst {worst:.3g}"
+
+
+@pytest.mark.parametrize("M,N,K", [(300, 256 * 160 + 13, 200), (512, 256 * 80, 192),
+                                   (260, 256 * 81 + 7, 480)])
+def test_k3_big_tile_full_check(gpu, orc, M, N, K):
+    """bf16 activations with K % 8 == 0 and at least 160 tiles of 256 x 256: the
+    one-wave-per-SIMD kernel (activation tile loaded straight into LDS, two k-steps per
+    loop iteration plus a peeled odd step).  Every output is checked: odd and even step
+    counts, K past the last whole step, ragged M and N, alpha/beta/bias, and (first
+    case) the row split into a second launch."""
+    announce(f"K3 big tile M={M} N={N} K={K}")
+    w, x, c, bias = make_problem(M, N, K, torch.bfloat16, seed=K)
+    packed, out = run(gpu, w, x, c, bias, K, 0.75, 0.5, True, kernel=3)
+    ref, scale = oracle_matmul(orc, x, packed, K, 0.75, 0.5, c, bias)
+    ok, worst, nbad = fp_tolerance_ok(out.numpy(), ref, scale, RTOL[torch.bfloat16])
+    assert ok, f"{nbad} outside, worst {worst:.3g}"
+    packed, out = run(gpu, w, x, c, bias, K, 1.0, 0.0, False, kernel=3)
+    ref, scale = oracle_matmul(orc, x, packed, K, 1.0, 0.0, c, None)
+    ok, worst, nbad = fp_tolerance_ok(out.numpy(), ref, scale, RTOL[torch.bfloat16])
+    assert ok, f"beta=0: {nbad} outside, worst {worst:.3g}"
