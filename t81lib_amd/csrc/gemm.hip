@@ -485,40 +485,6 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
         out[4] = e[2].y | e[3].x;
         out[5] = e[3].y;
     };
-    // The 48 MFMAs of half p (fragments a, tile buffer buf) as 12 chunks of four (one
-    // B fragment each, read a chunk ahead), fenced so that each chunk also carries a
-    // share of the decode of half q of the limbs wl into `next` (table reads in chunk
-    // g, merge in chunk g + 1) and extra(g), the chunk's share of the loads.
-    auto run_half = [&](auto bufc, int p, const bf16x8 (&a)[4][3], const u32x4 (&wl)[4], int q,
-                        bf16x8 (&next)[4][3], auto &&extra) {
-        u32x4 bq[2];
-        bq[0] = read_b(bufc, p, 0);
-        uint2 e[2][4];
-        uint32_t pairs[4][12];
-#pragma unroll
-        for (int g = 0; g < 12; ++g) {
-            if (g + 1 < 12) bq[(g + 1) & 1] = read_b(bufc, p, g + 1);
-            if (g < 8) table_fetch(wl[g / 2][2 * q + (g % 2)], e[g & 1]);
-            if (g >= 1 && g <= 8)
-                table_merge(e[(g - 1) & 1], &pairs[(g - 1) / 2][6 * ((g - 1) % 2)]);
-            extra(g);
-            const bf16x8 b = __builtin_bit_cast(bf16x8, bq[g & 1]);
-#pragma unroll
-            for (int rb = 0; rb < 4; ++rb)
-                acc[rb][g % 4] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[rb][g / 4], b,
-                                                                         acc[rb][g % 4], 0, 0, 0);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-#pragma unroll
-        for (int rb = 0; rb < 4; ++rb)
-#pragma unroll
-            for (int j = 0; j < 3; ++j) {
-                const u32x4 raw = {pairs[rb][4 * j], pairs[rb][4 * j + 1], pairs[rb][4 * j + 2],
-                                   pairs[rb][4 * j + 3]};
-                next[rb][j] = __builtin_bit_cast(bf16x8, raw);
-            }
-    };
-
     lut_fill(lut, tid, kW4Threads);
     u32x4 wcur[4], wnxt[4];
     bf16x8 a0[4][3], a1[4][3];
@@ -531,17 +497,50 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
     __syncthreads();
     if (nsteps > 0) decode_half(wcur, 0, a0);
 
-    // Per step: half 0's MFMAs carry the loads for step + 1 (unconditional: past the last
-    // step they read zeros or unused weight bytes) and the decode of half 1; half 1's
-    // MFMAs carry the decode of the next step's half 0.  Steps alternate between the
-    // two tile buffers, so the loop runs two steps per iteration.
+    // One k-step as 24 chunks of four MFMAs (chunks 0-11: half 0 with a0, 12-23: half 1
+    // with a1), one B fragment each, read two chunks ahead.  Chunks are fenced so that
+    // each also carries its share of the decode -- chunks 0-7: half 1 of wcur into a1,
+    // chunks 12-19: half 0 of wnxt (the next step) into a0; table reads in one chunk, the
+    // merge in the next -- and of the loads for the next step (chunks 0-11; unconditional:
+    // past the last step they read zeros or unused weight bytes).  Steps alternate
+    // between the two tile buffers, so the loop below runs two steps per iteration.
     auto step_body = [&](int64_t step, auto bufc, auto otherc) {
-        run_half(bufc, 0, a0, wcur, 1, a1, [&](int g) {
+        u32x4 bq[3];
+        bq[0] = read_b(bufc, 0, 0);
+        bq[1] = read_b(bufc, 0, 1);
+        uint2 e[2][4];
+        uint32_t pairs[4][12];
+#pragma unroll
+        for (int g = 0; g < 24; ++g) {
+            const int p = g / 12;
+            const int gg = g % 12;
+            if (g + 2 < 24) bq[(g + 2) % 3] = read_b(bufc, (g + 2) / 12, (g + 2) % 12);
+            if (gg < 8)
+                table_fetch((p == 0 ? wcur : wnxt)[gg / 2][2 * (1 - p) + (gg % 2)], e[gg & 1]);
+            if (gg >= 1 && gg <= 8)
+                table_merge(e[(gg - 1) & 1], &pairs[(gg - 1) / 2][6 * ((gg - 1) % 2)]);
             if (g == 0) fetch_w(step + 1, wnxt);
-            load_tile_part(step + 1, otherc, g);
-            if (g == kW4LoadsPerWave - 2) load_tile_part(step + 1, otherc, g + 1);
-        });
-        run_half(bufc, 1, a1, wnxt, 0, a0, [&](int) {});
+            if (g < 12) load_tile_part(step + 1, otherc, g);
+            if (g == 11) load_tile_part(step + 1, otherc, 12);
+            const bf16x8 b = __builtin_bit_cast(bf16x8, bq[g % 3]);
+            const bf16x8(&a)[4][3] = p == 0 ? a0 : a1;
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb)
+                acc[rb][gg % 4] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[rb][gg / 4], b,
+                                                                          acc[rb][gg % 4], 0, 0, 0);
+            if (gg == 11) {
+                bf16x8(&next)[4][3] = p == 0 ? a1 : a0;
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+                    for (int j = 0; j < 3; ++j) {
+                        const u32x4 raw = {pairs[rb][4 * j], pairs[rb][4 * j + 1],
+                                           pairs[rb][4 * j + 2], pairs[rb][4 * j + 3]};
+                        next[rb][j] = __builtin_bit_cast(bf16x8, raw);
+                    }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb) wcur[rb] = wnxt[rb];
         __builtin_amdgcn_s_waitcnt(0x0F70);
