@@ -316,6 +316,31 @@ def _counter_median(d: str, kernel_sub: str, counter: str) -> tuple:
     return statistics.median(vals), len(vals)
 
 
+def summarize_counters(d: str, kernel_sub: str, cmd: str) -> str:
+    """Median per dispatch of every counter a `rocprofv3 --pmc` run collected for the kernels
+    whose name contains `kernel_sub`.  When the MFMA busy cycles and the GPU busy cycles are
+    both there: MFMA busy per SIMD over the busy time (GRBM_GUI_ACTIVE counts the shader
+    clock of each of the 8 XCDs; 1024 SIMDs)."""
+    import statistics
+    rows = [r for r in _read_csv(_find(d, "counter_collection.csv")) if kernel_sub in r["Kernel_Name"]]
+    if not rows:
+        raise ValueError(f"no rows for '{kernel_sub}' in {d}")
+    by: dict = {}
+    for r in rows:
+        by.setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+    names = sorted({r["Kernel_Name"][:110] for r in rows})
+    out = [f"command: {cmd}", "", "kernels: " + "; ".join(names), ""]
+    med = {k: statistics.median(v) for k, v in by.items()}
+    for k in sorted(med):
+        out.append(f"{k:28s} {med[k]:18.0f}   (median of {len(by[k])} dispatches)")
+    if "SQ_VALU_MFMA_BUSY_CYCLES" in med and "GRBM_GUI_ACTIVE" in med:
+        per_xcd = med["GRBM_GUI_ACTIVE"] / 8.0
+        busy = med["SQ_VALU_MFMA_BUSY_CYCLES"] / 1024.0
+        out += ["", f"MFMA busy per SIMD: {busy:.0f} of {per_xcd:.0f} busy cycles = "
+                    f"{100.0 * busy / per_xcd:.1f} %"]
+    return "\n".join(out) + "\n"
+
+
 def summarize_traffic(kernel: str, kfetch: str, kwrite: str, cfetch: str, cwrite: str,
                       copy_bytes: int, algo_bytes: int, cmds: list) -> str:
     """HBM bytes per launch of `kernel` from FETCH_SIZE / WRITE_SIZE runs, each scaled by
@@ -372,14 +397,19 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=12.0,
                     help="seconds of single-core reference CPU work for the baseline")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["gemv", "gemm", "pack", "copy", "spmm"], default=None,
+    ap.add_argument("--only", choices=["gemv", "gemm", "pack", "copy", "spmm", "launch"],
+                    default=None,
                     help="time one kernel only (for profiling runs); 'copy' times a plain "
                          "elementwise copy of the GEMV weight size, the calibration kernel "
-                         "for the HBM byte counters")
+                         "for the HBM byte counters; 'launch' times a one-element fill, the "
+                         "per-launch floor of a graph of back-to-back kernels")
     ap.add_argument("--sweep", action="store_true",
                     help="also time the config-3/4 shapes and print a table on stderr")
     ap.add_argument("--summarize-trace", metavar="DIR",
                     help="print the kernel table of a rocprofv3 csv --stats run and exit")
+    ap.add_argument("--summarize-counters", nargs=2, metavar=("DIR", "KERNEL"),
+                    help="print the median counters of a rocprofv3 csv --pmc run for the "
+                         "kernels whose name contains KERNEL, and exit")
     ap.add_argument("--summarize-traffic", nargs=4, metavar=("KFETCH", "KWRITE", "CFETCH", "CWRITE"),
                     help="print calibrated HBM bytes per GEMV launch from rocprofv3 --pmc "
                          "FETCH_SIZE / WRITE_SIZE runs of the GEMV and of the copy, and exit")
@@ -388,6 +418,9 @@ def main() -> int:
     args = ap.parse_args()
     if args.summarize_trace:
         sys.stdout.write(summarize_trace(args.summarize_trace, " | ".join(args.cmd)))
+        return 0
+    if args.summarize_counters:
+        sys.stdout.write(summarize_counters(*args.summarize_counters, " | ".join(args.cmd)))
         return 0
     if args.summarize_traffic:
         K, N = 4096, 14336
@@ -473,6 +506,15 @@ def main() -> int:
                 "GBps": 8 * elems / (copy_ms * 1e-3) / 1e9}
         log(f"copy {copy_ms * 1e3:.2f} us/call, {copy['GBps']:.0f} GB/s read+write")
 
+    # ------------------------------------------------ launch floor (one-element fill) --
+    launch_floor = None
+    if args.only == "launch":
+        tiny = [torch.zeros(1, device=dev) for _ in range(32)]
+        lf_ms = time_graph(torch, lambda t: t.fill_(1.0), tiny, args.steps, args.warmup)
+        launch_floor = {"workload": "graph of one-element torch fill_ launches", "us": lf_ms * 1e3,
+                        "gemv_bytes_at_8TBps_us": gemv_bytes(M, N, K) / HBM_PEAK_GBPS / 1e3}
+        log(f"launch floor {lf_ms * 1e3:.2f} us/launch")
+
     # ------------------------------------------------------------ CPU baseline --
     cpu = None
     if not args.no_cpu and args.only is None:
@@ -534,6 +576,8 @@ def main() -> int:
                                      "unit": "GB/s", "frac": gbs / HBM_PEAK_GBPS}}
     if copy:
         line["copy"] = copy
+    if launch_floor:
+        line["launch_floor"] = launch_floor
     if sweep:
         line["sweep"] = sweep
     if spmm:
