@@ -108,6 +108,24 @@ int t81_hip_ternary_matmul_kernel(int which, const void *x, int x_dtype, const u
                                   void *c, int64_t m, int64_t n, int64_t k, float alpha,
                                   float beta, const float *bias, void *stream);
 
+/* Same, with a caller-owned device workspace: which = 0 (by M, as
+ * t81_hip_ternary_matmul), 2 or 3.  When K3 has few output tiles (bf16
+ * activations, K % 8 == 0) and workspace_bytes is at least
+ * t81_hip_ternary_matmul_workspace_size(...), K is split over several workgroups
+ * per tile: each writes its partial tile to the workspace and a second kernel sums
+ * the partials in split order (deterministic).  NULL / 0 bytes: no split.  The
+ * workspace must be 16-byte aligned and not used by another call at the same time.
+ * Replaces: the same reference interfaces as t81_hip_ternary_matmul; the
+ *           reference's CPU path needs no workspace, so it has no such argument. */
+int t81_hip_ternary_matmul_ws(int which, const void *x, int x_dtype, const uint8_t *w, void *c,
+                              int64_t m, int64_t n, int64_t k, float alpha, float beta,
+                              const float *bias, void *workspace, int64_t workspace_bytes,
+                              void *stream);
+
+/* Bytes of workspace t81_hip_ternary_matmul_ws uses for this shape on the current
+ * device (0: the shape does not split).  Never fails. */
+int64_t t81_hip_ternary_matmul_workspace_size(int64_t m, int64_t n, int64_t k, int x_dtype);
+
 /* K4 -- the reference's literal gemm_ternary: A (M x K/48 limbs), B (K/48 x N
  * limbs), C (M x N float32, read and written):
  *     C[i,j] = float( C[i,j]*beta + sum_l alpha * V(A[i,l]) * V(B[l,j]) )

@@ -196,27 +196,47 @@ int t81_hip_validate_packed(const uint8_t *packed, int64_t count, int32_t *bad_c
                   "t81_hip_validate_packed");
 }
 
-int t81_hip_ternary_matmul_kernel(int which, const void *x, int x_dtype, const uint8_t *w,
-                                  void *c, int64_t m, int64_t n, int64_t k, float alpha,
-                                  float beta, const float *bias, void *stream) {
+int t81_hip_ternary_matmul_ws(int which, const void *x, int x_dtype, const uint8_t *w, void *c,
+                              int64_t m, int64_t n, int64_t k, float alpha, float beta,
+                              const float *bias, void *workspace, int64_t workspace_bytes,
+                              void *stream) {
     if (int rc = check_matmul(x, x_dtype, w, c, m, n, k, alpha, beta, bias)) return rc;
+    if (which == 0) which = m <= 16 ? 2 : 3;
     if (which == 2 && m > 16) return fail(T81_HIP_EINVAL_SHAPE, "the GEMV kernel takes M <= 16");
-    if (which != 2 && which != 3) return fail(T81_HIP_EINVAL_SHAPE, "kernel must be 2 or 3");
+    if (which != 2 && which != 3) return fail(T81_HIP_EINVAL_SHAPE, "kernel must be 0, 2 or 3");
+    if (workspace_bytes < 0 || (workspace_bytes > 0 && workspace == nullptr))
+        return fail(T81_HIP_EINVAL_POINTER, "workspace pointer and size do not match");
+    if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0)
+        return fail(T81_HIP_EINVAL_POINTER, "workspace must be 16-byte aligned");
     if (int rc = require_device("t81_hip_ternary_matmul")) return rc;
     const hipStream_t s = static_cast<hipStream_t>(stream);
     hipError_t e;
     if (which == 2)
         e = t81hip::launch_gemv(x, x_dtype, w, c, static_cast<int>(m), n, k, alpha, beta, bias, s);
     else
-        e = t81hip::launch_gemm(x, x_dtype, w, c, m, n, k, alpha, beta, bias, s);
+        e = t81hip::launch_gemm(x, x_dtype, w, c, m, n, k, alpha, beta, bias, s, workspace,
+                                workspace_bytes);
     return finish(e, "t81_hip_ternary_matmul");
+}
+
+int t81_hip_ternary_matmul_kernel(int which, const void *x, int x_dtype, const uint8_t *w,
+                                  void *c, int64_t m, int64_t n, int64_t k, float alpha,
+                                  float beta, const float *bias, void *stream) {
+    if (which != 2 && which != 3) return fail(T81_HIP_EINVAL_SHAPE, "kernel must be 2 or 3");
+    return t81_hip_ternary_matmul_ws(which, x, x_dtype, w, c, m, n, k, alpha, beta, bias, nullptr,
+                                     0, stream);
 }
 
 int t81_hip_ternary_matmul(const void *x, int x_dtype, const uint8_t *w, void *c, int64_t m,
                            int64_t n, int64_t k, float alpha, float beta, const float *bias,
                            void *stream) {
-    return t81_hip_ternary_matmul_kernel(m <= 16 ? 2 : 3, x, x_dtype, w, c, m, n, k, alpha, beta,
-                                         bias, stream);
+    return t81_hip_ternary_matmul_ws(0, x, x_dtype, w, c, m, n, k, alpha, beta, bias, nullptr, 0,
+                                     stream);
+}
+
+int64_t t81_hip_ternary_matmul_workspace_size(int64_t m, int64_t n, int64_t k, int x_dtype) {
+    if (m <= 16 || m < 0 || n < 0 || k < 0) return 0;
+    return t81hip::gemm_workspace_bytes(m, n, k, x_dtype);
 }
 
 // include/t81/linalg/gemm_gpu.hpp:171-190: dimension, K % 48 and (implicitly, through

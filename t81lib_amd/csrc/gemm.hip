@@ -341,11 +341,15 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void *base,
         reinterpret_cast<void *>((static_cast<uint64_t>(hi) << 32) | lo), 0, n, 0x00020000);
 }
 
-template <int XT>
+// Split-K: with part != nullptr, workgroup (split sp, tile t) runs k-steps
+// [sp * sps, (sp + 1) * sps) and stores its raw accumulators (no alpha, beta, bias) to
+// part in the order (sp, t, wave, block, a4, lane) as float4s -- every store is 1 KB
+// contiguous; gemm_split_reduce_kernel then sums the splits in order.
+template <int XT, bool kSplit>
 __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
     const void *__restrict__ x, const uint8_t *__restrict__ w, void *__restrict__ c, int64_t M,
     int64_t N, int64_t ldc, int64_t K, int64_t L, float alpha, float beta,
-    const float *__restrict__ bias) {
+    const float *__restrict__ bias, int64_t sps, float4 *__restrict__ part) {
     static_assert(XT == kDtypeBF16, "the LDS tile is filled straight from bf16 activations");
     // Two separate tile objects (not one array indexed by a run-time parity): the
     // loads into one buffer then provably do not alias the reads of the other, and
@@ -372,12 +376,17 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
     // share their activation rows.  (Tile indices are uniform: readfirstlane keeps
     // them, and the buffer descriptors built from them, in scalar registers.)
     const int tiles_n = static_cast<int>((N + kW4Rows - 1) / kW4Rows);
+    const int tiles = tiles_n * static_cast<int>((M + kW4Tokens - 1) / kW4Tokens);
     const int bid = static_cast<int>(blockIdx.x);
-    const int tn = __builtin_amdgcn_readfirstlane(bid % tiles_n);
-    const int tm = __builtin_amdgcn_readfirstlane(bid / tiles_n);
+    const int sp = __builtin_amdgcn_readfirstlane(bid / tiles);
+    const int tt = __builtin_amdgcn_readfirstlane(bid - sp * tiles);
+    const int tn = __builtin_amdgcn_readfirstlane(tt % tiles_n);
+    const int tm = __builtin_amdgcn_readfirstlane(tt / tiles_n);
     const int64_t nwg = static_cast<int64_t>(tn) * kW4Rows;
     const int64_t m0 = static_cast<int64_t>(tm) * kW4Tokens;
-    const int64_t nsteps = (L + 1) / 2;
+    const int64_t all_steps = (L + 1) / 2;
+    const int64_t s_begin = static_cast<int64_t>(sp) * sps;
+    const int64_t s_end = s_begin + sps < all_steps ? s_begin + sps : all_steps;
 
     // Weights through a buffer based at the workgroup's first row: rows past N read
     // zeros.  A limb index past L (odd L, last step) reads the next row's first limb
@@ -488,14 +497,14 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
     lut_fill(lut, tid, kW4Threads);
     u32x4 wcur[4], wnxt[4];
     bf16x8 a0[4][3], a1[4][3];
-    if (nsteps > 0) {
-        fetch_w(0, wcur);
-        load_tile(0, std::integral_constant<int, 0>());
+    if (s_begin < s_end) {
+        fetch_w(s_begin, wcur);
+        load_tile(s_begin, std::integral_constant<int, 0>());
     }
     // vmcnt(0): the tile's LDS writes have landed before the barrier publishes them
     __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
-    if (nsteps > 0) decode_half(wcur, 0, a0);
+    if (s_begin < s_end) decode_half(wcur, 0, a0);
 
     // One k-step as 24 chunks of four MFMAs (chunks 0-11: half 0 with a0, 12-23: half 1
     // with a1), one B fragment each, read two chunks ahead.  Chunks are fenced so that
@@ -546,13 +555,28 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
         __builtin_amdgcn_s_waitcnt(0x0F70);
         __syncthreads();
     };
-    int64_t step = 0;
-    for (; step + 1 < nsteps; step += 2) {
+    int64_t step = s_begin;
+    for (; step + 1 < s_end; step += 2) {
         step_body(step, std::integral_constant<int, 0>(), std::integral_constant<int, 1>());
         step_body(step + 1, std::integral_constant<int, 1>(), std::integral_constant<int, 0>());
     }
-    if (step < nsteps)  // odd step count: the last step, peeled (no join inside the loop)
+    if (step < s_end)  // odd step count: the last step, peeled (no join inside the loop)
         step_body(step, std::integral_constant<int, 0>(), std::integral_constant<int, 1>());
+
+    if constexpr (kSplit) {
+        float4 *dst =
+            part + (((static_cast<int64_t>(sp) * tiles + tt) * 4 + wave) * 64) * 64 + lane;
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+                for (int a4 = 0; a4 < 4; ++a4)
+                    dst[((rb * 4 + cb) * 4 + a4) * 64] =
+                        make_float4(acc[rb][cb][4 * a4], acc[rb][cb][4 * a4 + 1],
+                                    acc[rb][cb][4 * a4 + 2], acc[rb][cb][4 * a4 + 3]);
+        return;
+    }
 
     // ---- epilogue: lane (c, h) of block (rb, cb) holds rows 8 a4 + 4 h + b of token c ----
 #pragma unroll
@@ -598,14 +622,105 @@ bool gemm_w4_fits(const void *x, int64_t m, int64_t n, int64_t k) {
            n < (int64_t(1) << 30);
 }
 
-// Rows [0, n) of W and columns [0, n) of C, whose rows are ldc elements apart.
+// C from the split partials: thread g owns float4 slot g of a tile's share of one
+// split (the order the big-tile kernel stores them in) and sums the nsplit partials
+// in split order, then applies alpha, beta and bias as the kernel's own epilogue does.
+__global__ __launch_bounds__(256) void gemm_split_reduce_kernel(
+    const float4 *__restrict__ part, float *__restrict__ c, int64_t M, int64_t N, int64_t ldc,
+    int tiles, int nsplit, float alpha, float beta, const float *__restrict__ bias) {
+    const int64_t per_split = static_cast<int64_t>(tiles) * 4 * 64 * 64;
+    const int tiles_n = static_cast<int>((N + kW4Rows - 1) / kW4Rows);
+    for (int64_t g = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; g < per_split;
+         g += static_cast<int64_t>(gridDim.x) * 256) {
+        const int lane = static_cast<int>(g & 63);
+        const int a4 = static_cast<int>((g >> 6) & 3);
+        const int blk = static_cast<int>((g >> 8) & 15);
+        const int wave = static_cast<int>((g >> 12) & 3);
+        const int tt = static_cast<int>(g >> 14);
+        const int rb = blk >> 2, cb = blk & 3;
+        const int wn = wave & 1, wm = wave >> 1;
+        const int r = lane & 31, h = lane >> 5;
+        const int64_t m = static_cast<int64_t>(tt / tiles_n) * kW4Tokens + 128 * wm + 32 * cb + r;
+        if (m >= M) continue;
+        float4 sum = part[g];
+        for (int sp = 1; sp < nsplit; ++sp) {
+            const float4 v = part[sp * per_split + g];
+            sum.x += v.x;
+            sum.y += v.y;
+            sum.z += v.z;
+            sum.w += v.w;
+        }
+        const float accv[4] = {sum.x, sum.y, sum.z, sum.w};
+        const int64_t nb =
+            static_cast<int64_t>(tt % tiles_n) * kW4Rows + 128 * wn + 32 * rb + 8 * a4 + 4 * h;
+        float *cr = c + m * ldc;
+        float y[4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const int64_t n = nb + b;
+            float t = alpha * accv[b];
+            if (n < N) {
+                if (beta != 0.0f) t = t + beta * cr[n];
+                if (bias != nullptr) t = t + bias[n];
+            }
+            y[b] = t;
+        }
+        if (nb + 3 < N && (reinterpret_cast<uintptr_t>(cr + nb) & 15u) == 0) {
+            *reinterpret_cast<float4 *>(cr + nb) = make_float4(y[0], y[1], y[2], y[3]);
+        } else {
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+                if (nb + b < N) cr[nb + b] = y[b];
+        }
+    }
+}
+
+// Compute units of the current device (one workgroup of the big tile fits per CU).
+int cu_count();
+
+// How the big-tile kernel splits K for a shape: with few tiles (< 160), about one
+// workgroup per CU in total, at least four k-steps per split.  nsplit == 1: no split.
+struct SplitPlan {
+    int64_t nsplit, sps, tiles;
+};
+SplitPlan gemm_split_plan(int64_t m, int64_t n, int64_t k) {
+    const int64_t L = (k + kTrits - 1) / kTrits;
+    const int64_t nsteps = (L + 1) / 2;
+    const int64_t tiles = ((n + kW4Rows - 1) / kW4Rows) * ((m + kW4Tokens - 1) / kW4Tokens);
+    SplitPlan p{1, nsteps, tiles};
+    if (m <= 64 || tiles >= 160 || tiles <= 0) return p;
+    int64_t ns = (cu_count() + tiles / 2) / tiles;
+    if (ns > nsteps / 4) ns = nsteps / 4;
+    if (ns < 2) return p;
+    p.sps = (nsteps + ns - 1) / ns;
+    p.nsplit = (nsteps + p.sps - 1) / p.sps;
+    return p;
+}
+int64_t split_workspace_bytes(const SplitPlan &p) {
+    return p.nsplit > 1 ? p.nsplit * p.tiles * kW4Rows * kW4Tokens * 4 : 0;
+}
+
+// Rows [0, n) of W and columns [0, n) of C, whose rows are ldc elements apart.  With
+// part != nullptr (room for plan.nsplit partial tiles), K is split as planned.
 hipError_t launch_gemm_w4(const void *x, const uint8_t *w, void *c, int64_t m, int64_t n,
                           int64_t ldc, int64_t k, float alpha, float beta, const float *bias,
-                          hipStream_t s) {
+                          hipStream_t s, const SplitPlan *plan = nullptr, void *part = nullptr) {
     const int64_t L = (k + kTrits - 1) / kTrits;
     const int64_t tiles = ((n + kW4Rows - 1) / kW4Rows) * ((m + kW4Tokens - 1) / kW4Tokens);
-    gemm_w4_kernel<kDtypeBF16><<<dim3(tiles), dim3(kW4Threads), 0, s>>>(x, w, c, m, n, ldc, k, L,
-                                                                      alpha, beta, bias);
+    if (plan == nullptr || plan->nsplit <= 1 || part == nullptr) {
+        gemm_w4_kernel<kDtypeBF16, false><<<dim3(tiles), dim3(kW4Threads), 0, s>>>(
+            x, w, c, m, n, ldc, k, L, alpha, beta, bias, (L + 1) / 2, nullptr);
+        return hipGetLastError();
+    }
+    gemm_w4_kernel<kDtypeBF16, true><<<dim3(tiles * plan->nsplit), dim3(kW4Threads), 0, s>>>(
+        x, w, c, m, n, ldc, k, L, alpha, beta, bias, plan->sps, static_cast<float4 *>(part));
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int64_t slots = tiles * 4 * 64 * 64;
+    const int64_t blocks = (slots + 255) / 256 < 8192 ? (slots + 255) / 256 : 8192;
+    gemm_split_reduce_kernel<<<dim3(blocks), dim3(256), 0, s>>>(
+        static_cast<const float4 *>(part), static_cast<float *>(c), m, n, ldc,
+        static_cast<int>(tiles), static_cast<int>(plan->nsplit), alpha, beta, bias);
     return hipGetLastError();
 }
 
@@ -645,10 +760,19 @@ int cu_count() {
 
 template <int XT>
 hipError_t launch_gemm_x(const void *x, const uint8_t *w, void *c, int64_t m, int64_t n,
-                         int64_t k, float alpha, float beta, const float *bias, hipStream_t s) {
+                         int64_t k, float alpha, float beta, const float *bias, hipStream_t s,
+                         void *ws, int64_t ws_bytes) {
     constexpr int LK = 2;  // limbs per k-step
     if (m <= 32) return launch_gemm_t<XT, 2, 1, 4, 1, LK>(x, w, c, m, n, n, k, alpha, beta, bias, s);
     if (m <= 64) return launch_gemm_t<XT, 2, 2, 4, 1, LK>(x, w, c, m, n, n, k, alpha, beta, bias, s);
+    if constexpr (XT == kDtypeBF16) {
+        // Few tiles and a workspace: split K over the big-tile kernel.
+        if (ws != nullptr && gemm_w4_fits(x, m, n, k)) {
+            const SplitPlan plan = gemm_split_plan(m, n, k);
+            if (plan.nsplit > 1 && ws_bytes >= split_workspace_bytes(plan))
+                return launch_gemm_w4(x, w, c, m, n, n, k, alpha, beta, bias, s, &plan, ws);
+        }
+    }
     if constexpr (XT != kDtypeF32) {
         // Eight waves (two per SIMD, so one wave's waits are covered by the other's
         // MFMAs): 256 x 256 tiles while there are enough of them to spread over the
@@ -687,13 +811,21 @@ hipError_t launch_gemm_x(const void *x, const uint8_t *w, void *c, int64_t m, in
 
 hipError_t launch_gemm(const void *x, int x_dtype, const uint8_t *w, void *c, int64_t m,
                        int64_t n, int64_t k, float alpha, float beta, const float *bias,
-                       hipStream_t s) {
+                       hipStream_t s, void *ws, int64_t ws_bytes) {
     if (m == 0 || n == 0) return hipSuccess;
     switch (x_dtype) {
-        case kDtypeBF16: return launch_gemm_x<kDtypeBF16>(x, w, c, m, n, k, alpha, beta, bias, s);
-        case kDtypeF32: return launch_gemm_x<kDtypeF32>(x, w, c, m, n, k, alpha, beta, bias, s);
-        default: return launch_gemm_x<kDtypeI8>(x, w, c, m, n, k, alpha, beta, bias, s);
+        case kDtypeBF16:
+            return launch_gemm_x<kDtypeBF16>(x, w, c, m, n, k, alpha, beta, bias, s, ws, ws_bytes);
+        case kDtypeF32:
+            return launch_gemm_x<kDtypeF32>(x, w, c, m, n, k, alpha, beta, bias, s, ws, ws_bytes);
+        default:
+            return launch_gemm_x<kDtypeI8>(x, w, c, m, n, k, alpha, beta, bias, s, ws, ws_bytes);
     }
+}
+
+int64_t gemm_workspace_bytes(int64_t m, int64_t n, int64_t k, int x_dtype) {
+    if (x_dtype != kDtypeBF16 || m <= 64 || n <= 0 || k % 8 != 0) return 0;
+    return split_workspace_bytes(gemm_split_plan(m, n, k));
 }
 
 }  // namespace t81hip

@@ -61,10 +61,12 @@ hipError_t launch_tq2_matmul(const void *x, int x_dtype, const uint8_t *w, float
                              int64_t n, int64_t k, float alpha, float beta, const float *bias,
                              hipStream_t s);
 
-// gemm.hip (K3): any M
+// gemm.hip (K3): any M.  ws (ws_bytes of device memory, may be null) lets shapes with
+// few tiles split K; gemm_workspace_bytes says how much such a shape uses (0: none).
 hipError_t launch_gemm(const void *x, int x_dtype, const uint8_t *w, void *c, int64_t m,
                        int64_t n, int64_t k, float alpha, float beta, const float *bias,
-                       hipStream_t s);
+                       hipStream_t s, void *ws = nullptr, int64_t ws_bytes = 0);
+int64_t gemm_workspace_bytes(int64_t m, int64_t n, int64_t k, int x_dtype);
 
 // limb.hip (K4)
 hipError_t launch_gemm_limb(const uint8_t *a, const uint8_t *b, float *c, int m, int n,

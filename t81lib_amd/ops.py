@@ -213,13 +213,18 @@ def ternary_matmul(x: torch.Tensor, w_packed: torch.Tensor, k: Optional[int] = N
         bias = bias.float().contiguous()
         bias_ptr = bias.data_ptr()
     lib = _lib.lib()
-    if kernel is None:
-        rc = lib.t81_hip_ternary_matmul(x.data_ptr(), _MATMUL_CODES[x.dtype], w_packed.data_ptr(),
-                                        c.data_ptr(), m, n, k, alpha, beta, bias_ptr, _stream())
-    else:
-        rc = lib.t81_hip_ternary_matmul_kernel(kernel, x.data_ptr(), _MATMUL_CODES[x.dtype],
-                                               w_packed.data_ptr(), c.data_ptr(), m, n, k, alpha,
-                                               beta, bias_ptr, _stream())
+    which = 0 if kernel is None else int(kernel)
+    if which not in (0, 2, 3):
+        raise ValueError("kernel must be 2 or 3")
+    code = _MATMUL_CODES[x.dtype]
+    # K3 with few output tiles splits K over a workspace from torch's caching allocator
+    # (safe under graph capture); its size is 0 for every other shape.
+    ws_bytes = 0 if which == 2 else int(lib.t81_hip_ternary_matmul_workspace_size(m, n, k, code))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes > 0 else None
+    rc = lib.t81_hip_ternary_matmul_ws(which, x.data_ptr(), code, w_packed.data_ptr(),
+                                       c.data_ptr(), m, n, k, alpha, beta, bias_ptr,
+                                       ws.data_ptr() if ws is not None else None, ws_bytes,
+                                       _stream())
     _lib.check(rc)
     return c
 

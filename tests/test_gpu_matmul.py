@@ -274,3 +274,53 @@ def test_k3_big_tile_full_check(gpu, orc, M, N, K):
     ref, scale = oracle_matmul(orc, x, packed, K, 1.0, 0.0, c, None)
     ok, worst, nbad = fp_tolerance_ok(out.numpy(), ref, scale, RTOL[torch.bfloat16])
     assert ok, f"beta=0: {nbad} outside, worst {worst:.3g}"
+
+
+@pytest.mark.parametrize("M,N,K", [(300, 1000, 4104), (260, 4096, 2000), (200, 700, 1536)])
+def test_k3_split_k_full_check(gpu, orc, M, N, K):
+    """Few output tiles (bf16, K % 8 == 0): K is split over several workgroups per tile,
+    partial tiles go to a workspace and a second kernel sums them in split order.  Every
+    output is checked against the oracle, with and without the workspace (the plain entry
+    point does not split), and two runs of the split path are bit-identical."""
+    announce(f"K3 split-K M={M} N={N} K={K}")
+    lib = _lib.lib()
+    ws_bytes = lib.t81_hip_ternary_matmul_workspace_size(M, N, K, _lib.DTYPE_BF16)
+    assert ws_bytes > 0, "shape expected to split"
+    w, x, c, bias = make_problem(M, N, K, torch.bfloat16, seed=M + K)
+    packed, out = run(gpu, w, x, c, bias, K, 0.75, 0.5, True, kernel=3)
+    ref, scale = oracle_matmul(orc, x, packed, K, 0.75, 0.5, c, bias)
+    ok, worst, nbad = fp_tolerance_ok(out.numpy(), ref, scale, RTOL[torch.bfloat16])
+    assert ok, f"split: {nbad} outside, worst {worst:.3g}"
+    _, out2 = run(gpu, w, x, c, bias, K, 0.75, 0.5, True, kernel=3)
+    assert torch.equal(out, out2), "split path is not deterministic"
+    pg = torch.from_numpy(packed).to(gpu)
+    xg = x.to(gpu)
+    cg = c.to(gpu).contiguous()
+    bg = bias.to(gpu)
+    rc = lib.t81_hip_ternary_matmul(xg.data_ptr(), _lib.DTYPE_BF16, pg.data_ptr(), cg.data_ptr(),
+                                    M, N, K, 0.75, 0.5, bg.data_ptr(),
+                                    torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc)
+    torch.cuda.synchronize()
+    ok, worst, nbad = fp_tolerance_ok(cg.cpu().numpy(), ref, scale, RTOL[torch.bfloat16])
+    assert ok, f"no split: {nbad} outside, worst {worst:.3g}"
+
+
+def test_k3_workspace_arguments(gpu):
+    """The workspace entry point rejects a size without a pointer and a misaligned
+    workspace, and runs without splitting when the workspace is too small."""
+    lib = _lib.lib()
+    M, N, K = 300, 1000, 4104
+    x = torch.randn((M, K), device=gpu).to(torch.bfloat16)
+    packed = ops.quantize_pack(torch.randn((N, K), device=gpu), 0.45, _lib.THR_CPP)
+    c = torch.empty((M, N), device=gpu)
+    s = torch.cuda.current_stream().cuda_stream
+    args = (3, x.data_ptr(), _lib.DTYPE_BF16, packed.data_ptr(), c.data_ptr(), M, N, K, 1.0, 0.0,
+            None)
+    assert lib.t81_hip_ternary_matmul_ws(*args, None, 64, s) == _lib.EINVAL_POINTER
+    buf = torch.empty(1 << 20, dtype=torch.uint8, device=gpu)
+    assert lib.t81_hip_ternary_matmul_ws(*args, buf.data_ptr() + 4, 64, s) == _lib.EINVAL_POINTER
+    assert lib.t81_hip_ternary_matmul_ws(*args, buf.data_ptr(), 1 << 20, s) == 0
+    want = ops.ternary_matmul(x, packed, K, kernel=3)
+    torch.cuda.synchronize()
+    assert torch.allclose(c, want, rtol=1e-5, atol=1e-3)
