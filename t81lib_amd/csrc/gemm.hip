@@ -678,6 +678,20 @@ __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(
 // Compute units of the current device (one workgroup of the big tile fits per CU).
 int cu_count();
 
+// Weight rows that run as whole rounds of 256 x 256 tiles, one workgroup per CU at a
+// time: all of them, none (fewer than 160 tiles: the GPU would be mostly idle), or,
+// when the last round would be at most half full, the rows of the whole rounds only.
+int64_t gemm_rows_whole_rounds(int64_t m, int64_t n) {
+    const int64_t tiles_m = (m + kW4Tokens - 1) / kW4Tokens;
+    const int64_t tiles_big = ((n + kW4Rows - 1) / kW4Rows) * tiles_m;
+    if (tiles_big < 160) return 0;
+    const int64_t cus = cu_count();
+    const int64_t rem = tiles_big % cus;
+    const int64_t n1 = (tiles_big - rem) / tiles_m * kW4Rows;
+    if (tiles_big > cus && rem != 0 && 2 * rem <= cus && n1 > 0 && n1 < n) return n1;
+    return n;
+}
+
 // How the big-tile kernel splits K for a shape: with few tiles (< 160), about one
 // workgroup per CU in total, at least four k-steps per split.  nsplit == 1: no split.
 struct SplitPlan {
@@ -765,43 +779,32 @@ hipError_t launch_gemm_x(const void *x, const uint8_t *w, void *c, int64_t m, in
     constexpr int LK = 2;  // limbs per k-step
     if (m <= 32) return launch_gemm_t<XT, 2, 1, 4, 1, LK>(x, w, c, m, n, n, k, alpha, beta, bias, s);
     if (m <= 64) return launch_gemm_t<XT, 2, 2, 4, 1, LK>(x, w, c, m, n, n, k, alpha, beta, bias, s);
-    if constexpr (XT == kDtypeBF16) {
-        // Few tiles and a workspace: split K over the big-tile kernel.
-        if (ws != nullptr && gemm_w4_fits(x, m, n, k)) {
-            const SplitPlan plan = gemm_split_plan(m, n, k);
-            if (plan.nsplit > 1 && ws_bytes >= split_workspace_bytes(plan))
-                return launch_gemm_w4(x, w, c, m, n, n, k, alpha, beta, bias, s, &plan, ws);
-        }
-    }
     if constexpr (XT != kDtypeF32) {
-        // Eight waves (two per SIMD, so one wave's waits are covered by the other's
-        // MFMAs): 256 x 256 tiles while there are enough of them to spread over the
-        // GPU, 256 weight rows x 128 tokens otherwise (measured crossover ~160 tiles).
-        const int64_t tiles_m = (m + 255) / 256;
-        const int64_t tiles_big = ((n + 255) / 256) * tiles_m;
-        if (tiles_big < 160)
-            return launch_gemm_t<XT, 2, 2, 4, 2, LK>(x, w, c, m, n, n, k, alpha, beta, bias, s);
-        // One big-tile workgroup per CU at a time: when the last round of big tiles would
-        // be at most half full, the rows of whole rounds take big tiles and the rest
-        // (fewer rows) the half-height tiles, one short round instead of a half-empty one.
-        const int64_t cus = cu_count();
-        const int64_t rem = tiles_big % cus;
-        const int64_t n1 = (tiles_big - rem) / tiles_m * 256;
+        // Rows [0, n1): whole rounds of 256 x 256 tiles -- the one-wave-per-SIMD kernel
+        // for bf16, else the eight-wave kernel (two waves per SIMD).  Rows [n1, n) (all
+        // of them when there are few tiles, the remainder that would leave the last round
+        // at most half full otherwise): split-K over big tiles when the caller gave a
+        // workspace, else 256 x 128 tiles of the eight-wave kernel.
+        const int64_t n1 = gemm_rows_whole_rounds(m, n);
         const int64_t L = (k + kTrits - 1) / kTrits;
         const bool w4 = XT == kDtypeBF16 && gemm_w4_fits(x, m, n, k);
-        auto big = [&](int64_t rows) {
-            return w4 ? launch_gemm_w4(x, w, c, m, rows, n, k, alpha, beta, bias, s)
-                      : launch_gemm_t<XT, 2, 4, 4, 2, LK>(x, w, c, m, rows, n, k, alpha, beta,
-                                                          bias, s);
-        };
-        if (tiles_big > cus && rem != 0 && 2 * rem <= cus && n1 > 0 && n1 < n) {
-            hipError_t e = big(n1);
-            if (e != hipSuccess) return e;
-            return launch_gemm_t<XT, 2, 2, 4, 2, LK>(x, w + n1 * L * kTrytes,
-                                                   static_cast<uint8_t *>(c) + 4 * n1, m, n - n1,
-                                                   n, k, alpha, beta, bias ? bias + n1 : nullptr, s);
+        if (n1 > 0) {
+            const hipError_t e =
+                w4 ? launch_gemm_w4(x, w, c, m, n1, n, k, alpha, beta, bias, s)
+                   : launch_gemm_t<XT, 2, 4, 4, 2, LK>(x, w, c, m, n1, n, k, alpha, beta, bias, s);
+            if (e != hipSuccess || n1 == n) return e;
         }
-        return big(n);
+        const uint8_t *w_rest = w + n1 * L * kTrytes;
+        void *c_rest = static_cast<uint8_t *>(c) + 4 * n1;
+        const float *bias_rest = bias ? bias + n1 : nullptr;
+        if (w4 && ws != nullptr) {
+            const SplitPlan plan = gemm_split_plan(m, n - n1, k);
+            if (plan.nsplit > 1 && ws_bytes >= split_workspace_bytes(plan))
+                return launch_gemm_w4(x, w_rest, c_rest, m, n - n1, n, k, alpha, beta, bias_rest,
+                                      s, &plan, ws);
+        }
+        return launch_gemm_t<XT, 2, 2, 4, 2, LK>(x, w_rest, c_rest, m, n - n1, n, k, alpha, beta,
+                                               bias_rest, s);
     }
     // fp32 activations: two LDS planes; four waves with 256 x 128 tiles
     return launch_gemm_t<XT, 2, 4, 4, 1, LK>(x, w, c, m, n, n, k, alpha, beta, bias, s);
@@ -825,7 +828,8 @@ hipError_t launch_gemm(const void *x, int x_dtype, const uint8_t *w, void *c, in
 
 int64_t gemm_workspace_bytes(int64_t m, int64_t n, int64_t k, int x_dtype) {
     if (x_dtype != kDtypeBF16 || m <= 64 || n <= 0 || k % 8 != 0) return 0;
-    return split_workspace_bytes(gemm_split_plan(m, n, k));
+    const int64_t n1 = gemm_rows_whole_rounds(m, n);
+    return n1 == n ? 0 : split_workspace_bytes(gemm_split_plan(m, n - n1, k));
 }
 
 }  // namespace t81hip

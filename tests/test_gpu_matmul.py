@@ -324,3 +324,35 @@ def test_k3_workspace_arguments(gpu):
     want = ops.ternary_matmul(x, packed, K, kernel=3)
     torch.cuda.synchronize()
     assert torch.allclose(c, want, rtol=1e-5, atol=1e-3)
+
+
+def test_k3_remainder_split_k(gpu, orc):
+    """320 big tiles on 256 CUs: whole rounds of big tiles for the first 32768 rows, and
+    the remaining 8192 rows as split-K big tiles over the workspace (C written through a
+    row stride, bias offset).  Sampled columns on both sides of the boundary against the
+    oracle, and all outputs against the path without a workspace (eight-wave remainder)."""
+    M, N, K = 300, 256 * 160, 1536
+    announce(f"K3 remainder split-K M={M} N={N} K={K}")
+    lib = _lib.lib()
+    assert lib.t81_hip_ternary_matmul_workspace_size(M, N, K, _lib.DTYPE_BF16) > 0
+    g = torch.Generator("cpu").manual_seed(21)
+    w = torch.randn((N, K), generator=g)
+    x = torch.randn((M, K), generator=g).to(torch.bfloat16)
+    c = torch.randn((M, N), generator=g)
+    bias = torch.randn((N,), generator=g)
+    packed = ops.quantize_pack(w.to(gpu), 0.45, _lib.THR_CPP)
+    xg, cg, bg = x.to(gpu), c.to(gpu), bias.to(gpu)
+    out = ops.ternary_matmul(xg, packed, K, alpha=0.75, beta=0.5, c=cg.clone(), bias=bg, kernel=3)
+    plain = cg.clone()
+    _lib.check(lib.t81_hip_ternary_matmul(xg.data_ptr(), _lib.DTYPE_BF16, packed.data_ptr(),
+                                          plain.data_ptr(), M, N, K, 0.75, 0.5, bg.data_ptr(),
+                                          torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    cols = np.sort(np.concatenate([np.random.default_rng(1).choice(32768, 64, replace=False),
+                                   32768 + np.random.default_rng(2).choice(8192, 64, replace=False)]))
+    packed_np = packed.cpu().numpy()
+    ref, scale = oracle_matmul(orc, x, packed_np, K, 0.75, 0.5, c, bias, cols=cols)
+    got = out.cpu().numpy()[:, cols]
+    ok, worst, nbad = fp_tolerance_ok(got, ref, scale, RTOL[torch.bfloat16])
+    assert ok, f"{nbad} outside, worst {worst:.3g}"
+    assert torch.allclose(out, plain, rtol=1e-5, atol=1e-3)
