@@ -356,3 +356,42 @@ def test_k3_remainder_split_k(gpu, orc):
     ok, worst, nbad = fp_tolerance_ok(got, ref, scale, RTOL[torch.bfloat16])
     assert ok, f"{nbad} outside, worst {worst:.3g}"
     assert torch.allclose(out, plain, rtol=1e-5, atol=1e-3)
+
+
+@pytest.mark.parametrize("M,N,K,dtype", [(16, 4096, 14336, torch.bfloat16),
+                                         (5, 1000, 14336, torch.float32),
+                                         (9, 3000, 9000, torch.int8),
+                                         (16, 300, 5767, torch.bfloat16),
+                                         (12, 14336, 4096, torch.bfloat16)])
+def test_k2_m5_to_16_full_check(gpu, orc, M, N, K, dtype):
+    """5 <= M <= 16 decode shapes (long and short K, ragged K, few and many row blocks):
+    every output against the oracle through the Python path and through the plain C
+    entry point; int8 bit-exact."""
+    announce(f"K2 M={M} N={N} K={K} {dtype}")
+    w, x, c, bias = make_problem(M, N, K, dtype, seed=N + M)
+    lib = _lib.lib()
+    code = {torch.bfloat16: _lib.DTYPE_BF16, torch.float32: _lib.DTYPE_F32, torch.int8: _lib.DTYPE_I8}[dtype]
+    packed = ops.quantize_pack(w.to(gpu), 0.45, _lib.THR_CPP)
+    packed_np = packed.cpu().numpy()
+    xg = x.to(gpu)
+    s = torch.cuda.current_stream().cuda_stream
+    if dtype == torch.int8:
+        want = orc.trit_matmul_i64(x.numpy(), packed_np, K)
+        out = ops.ternary_matmul(xg, packed, K)
+        plain = torch.empty((M, N), dtype=torch.int32, device=gpu)
+        _lib.check(lib.t81_hip_ternary_matmul(xg.data_ptr(), code, packed.data_ptr(),
+                                              plain.data_ptr(), M, N, K, 1.0, 0.0, None, s))
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(out.cpu().numpy().astype(np.int64), want)
+        np.testing.assert_array_equal(plain.cpu().numpy().astype(np.int64), want)
+        return
+    cg, bg = c.to(gpu), bias.to(gpu)
+    out = ops.ternary_matmul(xg, packed, K, alpha=0.75, beta=0.5, c=cg.clone(), bias=bg)
+    plain = cg.clone()
+    _lib.check(lib.t81_hip_ternary_matmul(xg.data_ptr(), code, packed.data_ptr(), plain.data_ptr(),
+                                          M, N, K, 0.75, 0.5, bg.data_ptr(), s))
+    torch.cuda.synchronize()
+    ref, scale = oracle_matmul(orc, x, packed_np, K, 0.75, 0.5, c, bias)
+    for name, got in (("workspace", out), ("plain", plain)):
+        ok, worst, nbad = fp_tolerance_ok(got.cpu().numpy(), ref, scale, RTOL[dtype])
+        assert ok, f"{name}: {nbad} outside, worst {worst:.3g}"
