@@ -110,11 +110,15 @@ __device__ __forceinline__ u32x2 load_half_limb(const uint8_t *w, int64_t row, i
     return u32x2{0x0D0D0D0Du, 0x0D0D0D0Du};  // all-zero trits
 }
 
+// Split-K: with part != nullptr, workgroup (split sp, tile t) runs k-steps
+// [sp * sps, (sp + 1) * sps) and writes its raw sums (float; int32 for int8 activations,
+// exact) to part + sp * M * N as a row-major M x N matrix; gemm_split_sum_kernel adds
+// the splits in order and applies alpha, beta and bias.
 template <int XT, int RN, int CM, int WN, int WM, int LK, bool kAligned>
 __global__ __launch_bounds__(64 * WN * WM) void gemm_kernel(
     const void *__restrict__ x, const uint8_t *__restrict__ w, void *__restrict__ c, int64_t M,
     int64_t N, int64_t ldc, int64_t K, int64_t L, float alpha, float beta,
-    const float *__restrict__ bias) {
+    const float *__restrict__ bias, int64_t sps, void *__restrict__ part) {
     using Cfg = GemmCfg<XT, RN, CM, WN, WM, LK>;
     constexpr int kLK = Cfg::kLK;
     constexpr int kStepK = Cfg::kStepK;
@@ -133,11 +137,23 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_kernel(
     // blockIdx.x walks the weight-row tiles fastest so that workgroups running
     // together share the same activation rows (they stay hot in L2).
     const int64_t tiles_n = (N + Cfg::kBN - 1) / Cfg::kBN;
-    const int64_t tn = blockIdx.x % tiles_n;
-    const int64_t tm = blockIdx.x / tiles_n;
+    const int64_t tiles = tiles_n * ((M + Cfg::kBM - 1) / Cfg::kBM);
+    const int64_t sp = blockIdx.x / tiles;
+    const int64_t tt = blockIdx.x - sp * tiles;
+    const int64_t tn = tt % tiles_n;
+    const int64_t tm = tt / tiles_n;
     const int64_t n0 = tn * Cfg::kBN + 32 * RN * wn;
     const int64_t m0 = tm * Cfg::kBM;
-    const int64_t nsteps = (L + kLK - 1) / kLK;
+    const int64_t all_steps = (L + kLK - 1) / kLK;
+    const int64_t s_begin = sp * sps;
+    const int64_t s_end = s_begin + sps < all_steps ? s_begin + sps : all_steps;
+    if (part != nullptr) {  // this split's raw sums, row-major M x N
+        c = static_cast<uint8_t *>(part) + sp * M * N * 4;
+        ldc = N;
+        alpha = 1.0f;
+        beta = 0.0f;
+        bias = nullptr;
+    }
 
     lut_init(lut, tid, Cfg::kThreads);
 
@@ -188,16 +204,16 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_kernel(
                 dst[i][l] = load_half_limb(w, n0 + 32 * i + r, step * kLK + l, h, N, L);
     };
 
-    if (nsteps > 0) {
-        fetch_tile(0);
-        fetch_w(0, wc);
+    if (s_begin < s_end) {
+        fetch_tile(s_begin);
+        fetch_w(s_begin, wc);
         store_tile(0);
     }
     __syncthreads();
 
-    for (int64_t step = 0; step < nsteps; ++step) {
-        const int buf = static_cast<int>(step & 1);
-        const bool more = step + 1 < nsteps;
+    for (int64_t step = s_begin; step < s_end; ++step) {
+        const int buf = static_cast<int>((step - s_begin) & 1);
+        const bool more = step + 1 < s_end;
         if (more) {
             fetch_tile(step + 1);
             fetch_w(step + 1, wnx);
@@ -738,22 +754,92 @@ hipError_t launch_gemm_w4(const void *x, const uint8_t *w, void *c, int64_t m, i
     return hipGetLastError();
 }
 
-// Rows [0, n) of W and columns [0, n) of C, whose rows are ldc elements apart.
+// C from the splits of the eight-wave kernel: sums part[0..nsplit) (row-major M x N
+// each) in split order -- int32 exactly for int8 activations -- then applies alpha,
+// beta and bias as the kernel's epilogue does.  C rows are ldc elements apart.
+template <int XT>
+__global__ __launch_bounds__(256) void gemm_split_sum_kernel(
+    const void *__restrict__ part, void *__restrict__ c, int64_t M, int64_t N, int64_t ldc,
+    int nsplit, float alpha, float beta, const float *__restrict__ bias) {
+    const int64_t total = M * N;
+    for (int64_t g = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; g < total;
+         g += static_cast<int64_t>(gridDim.x) * 256) {
+        const int64_t m = g / N;
+        const int64_t n = g - m * N;
+        if constexpr (XT == kDtypeI8) {
+            const int32_t *p = static_cast<const int32_t *>(part);
+            int32_t y = p[g];
+            for (int sp = 1; sp < nsplit; ++sp) y += p[sp * total + g];
+            int32_t *cp = static_cast<int32_t *>(c) + m * ldc + n;
+            if (beta != 0.0f) y += *cp;
+            *cp = y;
+        } else {
+            const float *p = static_cast<const float *>(part);
+            float v = p[g];
+            for (int sp = 1; sp < nsplit; ++sp) v += p[sp * total + g];
+            float *cp = static_cast<float *>(c) + m * ldc + n;
+            float y = alpha * v;
+            if (beta != 0.0f) y = y + beta * *cp;
+            if (bias != nullptr) y = y + bias[n];
+            *cp = y;
+        }
+    }
+}
+
+// K split for a launch of `tiles` workgroups over `nsteps` k-steps: about one workgroup
+// per CU in total, at least two k-steps per split; nsplit == 1: no split.
+SplitPlan small_split_plan(int64_t tiles, int64_t nsteps) {
+    SplitPlan p{1, nsteps, tiles};
+    if (tiles <= 0 || tiles >= 128) return p;
+    int64_t ns = (cu_count() + tiles / 2) / tiles;
+    if (ns > nsteps / 2) ns = nsteps / 2;
+    if (ns < 2) return p;
+    p.sps = (nsteps + ns - 1) / ns;
+    p.nsplit = (nsteps + p.sps - 1) / p.sps;
+    return p;
+}
+
+template <int XT, int RN, int CM, int WN, int WM, int LK>
+SplitPlan gemm_t_plan(int64_t m, int64_t n, int64_t k) {
+    using Cfg = GemmCfg<XT, RN, CM, WN, WM, LK>;
+    const int64_t L = (k + kTrits - 1) / kTrits;
+    const int64_t tiles = ((n + Cfg::kBN - 1) / Cfg::kBN) * ((m + Cfg::kBM - 1) / Cfg::kBM);
+    return small_split_plan(tiles, (L + LK - 1) / LK);
+}
+
+// Rows [0, n) of W and columns [0, n) of C, whose rows are ldc elements apart.  With a
+// workspace of at least nsplit * m * n * 4 bytes, a launch of few tiles splits K.
 template <int XT, int RN, int CM, int WN, int WM, int LK>
 hipError_t launch_gemm_t(const void *x, const uint8_t *w, void *c, int64_t m, int64_t n,
                          int64_t ldc, int64_t k, float alpha, float beta, const float *bias,
-                         hipStream_t s) {
+                         hipStream_t s, void *ws = nullptr, int64_t ws_bytes = 0) {
     using Cfg = GemmCfg<XT, RN, CM, WN, WM, LK>;
     const int64_t L = (k + kTrits - 1) / kTrits;
     const int64_t tiles = ((n + Cfg::kBN - 1) / Cfg::kBN) * ((m + Cfg::kBM - 1) / Cfg::kBM);
     const int elem = XT == kDtypeF32 ? 4 : (XT == kDtypeBF16 ? 2 : 1);
     const bool aligned = (k % 8 == 0) && (reinterpret_cast<uintptr_t>(x) % (8 * elem) == 0);
+    SplitPlan plan{1, (L + LK - 1) / LK, tiles};
+    void *part = nullptr;
+    if (ws != nullptr) {
+        const SplitPlan p = gemm_t_plan<XT, RN, CM, WN, WM, LK>(m, n, k);
+        if (p.nsplit > 1 && ws_bytes >= p.nsplit * m * n * 4) {
+            plan = p;
+            part = ws;
+        }
+    }
+    const dim3 grid(static_cast<unsigned>(tiles * plan.nsplit));
     if (aligned)
-        gemm_kernel<XT, RN, CM, WN, WM, LK, true><<<dim3(tiles), dim3(Cfg::kThreads), 0, s>>>(
-            x, w, c, m, n, ldc, k, L, alpha, beta, bias);
+        gemm_kernel<XT, RN, CM, WN, WM, LK, true><<<grid, dim3(Cfg::kThreads), 0, s>>>(
+            x, w, c, m, n, ldc, k, L, alpha, beta, bias, plan.sps, part);
     else
-        gemm_kernel<XT, RN, CM, WN, WM, LK, false><<<dim3(tiles), dim3(Cfg::kThreads), 0, s>>>(
-            x, w, c, m, n, ldc, k, L, alpha, beta, bias);
+        gemm_kernel<XT, RN, CM, WN, WM, LK, false><<<grid, dim3(Cfg::kThreads), 0, s>>>(
+            x, w, c, m, n, ldc, k, L, alpha, beta, bias, plan.sps, part);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || part == nullptr) return e;
+    const int64_t total = m * n;
+    const int64_t blocks = (total + 255) / 256 < 4096 ? (total + 255) / 256 : 4096;
+    gemm_split_sum_kernel<XT><<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s>>>(
+        part, c, m, n, ldc, static_cast<int>(plan.nsplit), alpha, beta, bias);
     return hipGetLastError();
 }
 
@@ -777,8 +863,12 @@ hipError_t launch_gemm_x(const void *x, const uint8_t *w, void *c, int64_t m, in
                          int64_t k, float alpha, float beta, const float *bias, hipStream_t s,
                          void *ws, int64_t ws_bytes) {
     constexpr int LK = 2;  // limbs per k-step
-    if (m <= 32) return launch_gemm_t<XT, 2, 1, 4, 1, LK>(x, w, c, m, n, n, k, alpha, beta, bias, s);
-    if (m <= 64) return launch_gemm_t<XT, 2, 2, 4, 1, LK>(x, w, c, m, n, n, k, alpha, beta, bias, s);
+    if (m <= 32)
+        return launch_gemm_t<XT, 2, 1, 4, 1, LK>(x, w, c, m, n, n, k, alpha, beta, bias, s, ws,
+                                                 ws_bytes);
+    if (m <= 64)
+        return launch_gemm_t<XT, 2, 2, 4, 1, LK>(x, w, c, m, n, n, k, alpha, beta, bias, s, ws,
+                                                 ws_bytes);
     if constexpr (XT != kDtypeF32) {
         // Rows [0, n1): whole rounds of 256 x 256 tiles -- the one-wave-per-SIMD kernel
         // for bf16, else the eight-wave kernel (two waves per SIMD).  Rows [n1, n) (all
@@ -804,10 +894,11 @@ hipError_t launch_gemm_x(const void *x, const uint8_t *w, void *c, int64_t m, in
                                       s, &plan, ws);
         }
         return launch_gemm_t<XT, 2, 2, 4, 2, LK>(x, w_rest, c_rest, m, n - n1, n, k, alpha, beta,
-                                               bias_rest, s);
+                                               bias_rest, s, ws, ws_bytes);
     }
     // fp32 activations: two LDS planes; four waves with 256 x 128 tiles
-    return launch_gemm_t<XT, 2, 4, 4, 1, LK>(x, w, c, m, n, n, k, alpha, beta, bias, s);
+    return launch_gemm_t<XT, 2, 4, 4, 1, LK>(x, w, c, m, n, n, k, alpha, beta, bias, s, ws,
+                                             ws_bytes);
 }
 
 }  // namespace
@@ -826,10 +917,42 @@ hipError_t launch_gemm(const void *x, int x_dtype, const uint8_t *w, void *c, in
     }
 }
 
+namespace {
+
+// Workspace of an eight-wave launch over m x n: nsplit row-major m x n partials.
+template <int XT, int RN, int CM, int WN, int WM>
+int64_t gemm_t_workspace(int64_t m, int64_t n, int64_t k) {
+    const SplitPlan p = gemm_t_plan<XT, RN, CM, WN, WM, 2>(m, n, k);
+    return p.nsplit > 1 ? p.nsplit * m * n * 4 : 0;
+}
+
+template <int XT>
+int64_t gemm_workspace_x(int64_t m, int64_t n, int64_t k) {
+    if (m <= 32) return gemm_t_workspace<XT, 2, 1, 4, 1>(m, n, k);
+    if (m <= 64) return gemm_t_workspace<XT, 2, 2, 4, 1>(m, n, k);
+    if constexpr (XT == kDtypeF32) {
+        return gemm_t_workspace<XT, 2, 4, 4, 1>(m, n, k);
+    } else {
+        // the rows after whole rounds of big tiles: split-K big tiles (bf16, aligned
+        // activations) or eight-wave 256 x 128 tiles; the larger of the two
+        const int64_t n1 = gemm_rows_whole_rounds(m, n);
+        if (n1 == n) return 0;
+        const int64_t eight = gemm_t_workspace<XT, 2, 2, 4, 2>(m, n - n1, k);
+        if constexpr (XT != kDtypeBF16) return eight;
+        const int64_t big = k % 8 == 0 ? split_workspace_bytes(gemm_split_plan(m, n - n1, k)) : 0;
+        return big > eight ? big : eight;
+    }
+}
+
+}  // namespace
+
 int64_t gemm_workspace_bytes(int64_t m, int64_t n, int64_t k, int x_dtype) {
-    if (x_dtype != kDtypeBF16 || m <= 64 || n <= 0 || k % 8 != 0) return 0;
-    const int64_t n1 = gemm_rows_whole_rounds(m, n);
-    return n1 == n ? 0 : split_workspace_bytes(gemm_split_plan(m, n - n1, k));
+    if (m <= 0 || n <= 0 || k <= 0) return 0;
+    switch (x_dtype) {
+        case kDtypeBF16: return gemm_workspace_x<kDtypeBF16>(m, n, k);
+        case kDtypeF32: return gemm_workspace_x<kDtypeF32>(m, n, k);
+        default: return gemm_workspace_x<kDtypeI8>(m, n, k);
+    }
 }
 
 }  // namespace t81hip

@@ -395,3 +395,48 @@ def test_k2_m5_to_16_full_check(gpu, orc, M, N, K, dtype):
     for name, got in (("workspace", out), ("plain", plain)):
         ok, worst, nbad = fp_tolerance_ok(got.cpu().numpy(), ref, scale, RTOL[dtype])
         assert ok, f"{name}: {nbad} outside, worst {worst:.3g}"
+
+
+@pytest.mark.parametrize("M,N,K,dtype", [(32, 4096, 14336, torch.bfloat16),
+                                         (48, 1000, 4104, torch.float32),
+                                         (20, 3000, 9000, torch.int8),
+                                         (100, 2000, 4800, torch.int8),
+                                         (64, 6144, 4096, torch.bfloat16),
+                                         (300, 1500, 3000, torch.float32)])
+def test_k3_eight_wave_split_k_full_check(gpu, orc, M, N, K, dtype):
+    """Launches of the eight-wave kernel with few tiles (17 <= M <= 64, int8 and fp32
+    activations, unaligned K) split K: each split writes its raw sums (int32 for int8,
+    exact) as a row-major M x N matrix in the workspace and a second kernel adds them in
+    split order.  Every output against the oracle, with and without the workspace; int8
+    bit-exact."""
+    announce(f"K3 eight-wave split-K M={M} N={N} K={K} {dtype}")
+    lib = _lib.lib()
+    code = {torch.bfloat16: _lib.DTYPE_BF16, torch.float32: _lib.DTYPE_F32, torch.int8: _lib.DTYPE_I8}[dtype]
+    assert lib.t81_hip_ternary_matmul_workspace_size(M, N, K, code) > 0, "shape expected to split"
+    w, x, c, bias = make_problem(M, N, K, dtype, seed=M * 7 + K)
+    packed = ops.quantize_pack(w.to(gpu), 0.45, _lib.THR_CPP)
+    packed_np = packed.cpu().numpy()
+    xg = x.to(gpu)
+    s = torch.cuda.current_stream().cuda_stream
+    if dtype == torch.int8:
+        want = orc.trit_matmul_i64(x.numpy(), packed_np, K)
+        cg = c.round().to(torch.int32).to(gpu)
+        out = ops.ternary_matmul(xg, packed, K, beta=1.0, c=cg.clone())
+        plain = cg.clone()
+        _lib.check(lib.t81_hip_ternary_matmul(xg.data_ptr(), code, packed.data_ptr(),
+                                              plain.data_ptr(), M, N, K, 1.0, 1.0, None, s))
+        torch.cuda.synchronize()
+        want = want + cg.cpu().numpy().astype(np.int64)
+        np.testing.assert_array_equal(out.cpu().numpy().astype(np.int64), want)
+        np.testing.assert_array_equal(plain.cpu().numpy().astype(np.int64), want)
+        return
+    cg, bg = c.to(gpu), bias.to(gpu)
+    out = ops.ternary_matmul(xg, packed, K, alpha=0.75, beta=0.5, c=cg.clone(), bias=bg)
+    plain = cg.clone()
+    _lib.check(lib.t81_hip_ternary_matmul(xg.data_ptr(), code, packed.data_ptr(), plain.data_ptr(),
+                                          M, N, K, 0.75, 0.5, bg.data_ptr(), s))
+    torch.cuda.synchronize()
+    ref, scale = oracle_matmul(orc, x, packed_np, K, 0.75, 0.5, c, bias)
+    for name, got in (("workspace", out), ("plain", plain)):
+        ok, worst, nbad = fp_tolerance_ok(got.cpu().numpy(), ref, scale, RTOL[dtype])
+        assert ok, f"{name}: {nbad} outside, worst {worst:.3g}"
