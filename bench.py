@@ -125,6 +125,156 @@ def cpu_reference_gemv(n: int, k: int, budget_s: float):
     }
 
 
+# ------------------------------------------------------- config 5: decoder stack --
+# A Llama-3-8B-shaped decoder whose four projections per layer are t8.nn.Linear
+# (t81lib_amd.nn.Linear, eval mode: packed once, then K2 / K3 per call); RMSNorm,
+# RoPE, attention and the lm_head stay dense torch code, as the config leaves them.
+# Attention runs in float32 on a float32 KV cache (keys stored transposed), so every
+# batched product has contiguous or sliced -- never transposed -- operands.
+
+LLAMA3_8B = dict(layers=32, hidden=4096, heads=32, kv_heads=8, ffn=14336, vocab=128256)
+
+
+class DecoderStack:
+    """Random-init ternary decoder: weights ~ N(0, 1) (the effective W / 0.02, so the
+    0.45 threshold leaves ~1/3 zero trits; literal N(0, 0.02) weights would all be zero),
+    embedding and lm_head ~ N(0, 0.02) in bf16.  ``reference=True`` replaces each packed
+    linear by F.linear in float32 with the same trits (the test oracle of the stack)."""
+
+    def __init__(self, torch, dev, layers, hidden, heads, kv_heads, ffn, vocab, max_batch,
+                 max_tokens, seed=0, reference=False):
+        from t81lib_amd import nn as t8nn
+        from t81lib_amd import ops
+
+        self.t = torch
+        self.F = torch.nn.functional
+        self.hidden, self.heads, self.kv_heads, self.ffn = hidden, heads, kv_heads, ffn
+        self.hd = hidden // heads
+        self.group = heads // kv_heads
+        self.reference = reference
+        g = torch.Generator(dev).manual_seed(seed)
+        shapes = {"qkv": (hidden, hidden + 2 * kv_heads * self.hd), "o": (hidden, hidden),
+                  "gate_up": (hidden, 2 * ffn), "down": (ffn, hidden)}
+        self.blocks = []
+        for _ in range(layers):
+            blk = {}
+            for name, (fin, fout) in shapes.items():
+                lin = t8nn.Linear(fin, fout, bias=False, device=dev)
+                with torch.no_grad():
+                    lin.weight.copy_(torch.randn((fout, fin), generator=g, device=dev))
+                lin.eval()
+                with torch.no_grad():   # pack now (K1), outside any timed region
+                    lin(torch.zeros((1, fin), dtype=torch.bfloat16, device=dev))
+                if reference:
+                    tw = lin.ternary_weight
+                    blk[name] = ops.unpack(tw.packed, fout, fin).float()
+                else:
+                    blk[name] = lin
+            blk["n1"] = torch.ones(hidden, dtype=torch.bfloat16, device=dev)
+            blk["n2"] = torch.ones(hidden, dtype=torch.bfloat16, device=dev)
+            self.blocks.append(blk)
+        self.norm = torch.ones(hidden, dtype=torch.bfloat16, device=dev)
+        self.embed = (torch.randn((vocab, hidden), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        self.lm_head_t = (torch.randn((hidden, vocab), generator=g, device=dev) * 0.02).to(
+            torch.bfloat16)
+        # float32 KV cache: keys as (B, kv_heads, hd, T), values as (B, kv_heads, T, hd)
+        self.kt = [torch.zeros((max_batch, kv_heads, self.hd, max_tokens), device=dev)
+                   for _ in range(layers)]
+        self.v = [torch.zeros((max_batch, kv_heads, max_tokens, self.hd), device=dev)
+                  for _ in range(layers)]
+        inv = 1.0 / (500000.0 ** (torch.arange(0, self.hd, 2, device=dev).float() / self.hd))
+        ang = torch.arange(max_tokens, device=dev).float()[:, None] * inv[None, :]
+        self.cos, self.sin = ang.cos(), ang.sin()            # (T, hd / 2)
+
+    def _linear(self, blk, name, x2d):
+        if self.reference:
+            return self.F.linear(x2d.float(), blk[name])
+        return blk[name](x2d)
+
+    def _rmsnorm(self, x, w):
+        xf = x.float()
+        return (xf * self.t.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-5)).to(x.dtype) * w
+
+    def _rope(self, x, pos0):           # x (B, S, nh, hd) float32
+        s = x.shape[1]
+        c = self.cos[pos0:pos0 + s][None, :, None, :]
+        sn = self.sin[pos0:pos0 + s][None, :, None, :]
+        x1, x2 = x[..., : self.hd // 2], x[..., self.hd // 2:]
+        return self.t.cat([x1 * c - x2 * sn, x2 * c + x1 * sn], dim=-1)
+
+    def forward(self, tokens, pos0: int):
+        """tokens (B, S) -> float32 logits of the last position (B, vocab)."""
+        t = self.t
+        B, S = tokens.shape
+        H, KV, hd, G = self.hidden, self.kv_heads, self.hd, self.group
+        x = self.embed[tokens]                                    # (B, S, H) bf16
+        T = pos0 + S
+        for li, blk in enumerate(self.blocks):
+            h = self._rmsnorm(x, blk["n1"]).reshape(B * S, H)
+            qkv = self._linear(blk, "qkv", h)                     # float32
+            q = self._rope(qkv[:, :H].reshape(B, S, self.heads, hd), pos0)
+            k = self._rope(qkv[:, H:H + KV * hd].reshape(B, S, KV, hd), pos0)
+            v = qkv[:, H + KV * hd:].reshape(B, S, KV, hd)
+            self.kt[li][:B, :, :, pos0:T] = k.permute(0, 2, 3, 1)
+            self.v[li][:B, :, pos0:T, :] = v.permute(0, 2, 1, 3)
+            qg = q.reshape(B, S, KV, G, hd).permute(0, 2, 3, 1, 4).reshape(B, KV, G * S, hd)
+            scores = t.matmul(qg, self.kt[li][:B, :, :, :T]) * (1.0 / hd ** 0.5)
+            if S > 1:
+                qpos = pos0 + t.arange(G * S, device=x.device) % S
+                mask = t.arange(T, device=x.device)[None, :] > qpos[:, None]
+                scores = scores.masked_fill(mask, float("-inf"))
+            att = t.matmul(t.softmax(scores, dim=-1), self.v[li][:B, :, :T, :])
+            att = att.reshape(B, KV, G, S, hd).permute(0, 3, 1, 2, 4).reshape(B * S, H)
+            x = x + self._linear(blk, "o", att.to(t.bfloat16)).reshape(B, S, H).to(t.bfloat16)
+            h2 = self._rmsnorm(x, blk["n2"]).reshape(B * S, H)
+            gu = self._linear(blk, "gate_up", h2)
+            act = (self.F.silu(gu[:, : self.ffn]) * gu[:, self.ffn:]).to(t.bfloat16)
+            x = x + self._linear(blk, "down", act).reshape(B, S, H).to(t.bfloat16)
+        xl = self._rmsnorm(x[:, -1], self.norm)                   # (B, H) bf16
+        return t.matmul(xl, self.lm_head_t).float()
+
+
+def run_stack(torch, dev, prompt=1024, steps=256, batches=(1, 32)) -> dict:
+    """Config 5: prompt of 1024 random token ids per sequence, then 256 greedy decode
+    steps, at batch 1 and 32; tokens/s of prefill and of decode (eager launches)."""
+    cfg = LLAMA3_8B
+    t0 = time.perf_counter()
+    st = DecoderStack(torch, dev, cfg["layers"], cfg["hidden"], cfg["heads"], cfg["kv_heads"],
+                      cfg["ffn"], cfg["vocab"], max(batches), prompt + steps, seed=9)
+    torch.cuda.synchronize()
+    log(f"stack built ({cfg['layers']} layers, weights packed) in {time.perf_counter() - t0:.1f} s")
+    out = {"workload": "config 5: Llama-3-8B-shaped 32-layer decoder, t8.nn.Linear projections "
+                       "(K1 pack, K2 / K3 matmul), dense bf16 embedding / lm_head / RMSNorm, "
+                       "float32 attention and KV cache, random token ids, greedy",
+           "prompt": prompt, "decode_steps": steps, "results": []}
+    g = torch.Generator(dev).manual_seed(10)
+    with torch.no_grad():
+        st.forward(torch.randint(0, cfg["vocab"], (1, 16), generator=g, device=dev), 0)  # warm-up
+        for b in batches:
+            tokens = torch.randint(0, cfg["vocab"], (b, prompt), generator=g, device=dev)
+            torch.cuda.synchronize()
+            t1 = time.perf_counter()
+            logits = st.forward(tokens, 0)
+            torch.cuda.synchronize()
+            t_pre = time.perf_counter() - t1
+            nxt = logits.argmax(-1, keepdim=True)
+            t2 = time.perf_counter()
+            for i in range(steps):
+                logits = st.forward(nxt, prompt + i)
+                nxt = logits.argmax(-1, keepdim=True)
+            torch.cuda.synchronize()
+            t_dec = time.perf_counter() - t2
+            r = {"batch": b, "prefill_s": t_pre, "prefill_tokens_per_s": b * prompt / t_pre,
+                 "decode_s": t_dec, "decode_tokens_per_s": b * steps / t_dec}
+            out["results"].append(r)
+            log(f"stack batch {b}: prefill {b * prompt} tokens in {t_pre * 1e3:.1f} ms "
+                f"({r['prefill_tokens_per_s']:.0f} tok/s), decode {steps} steps in "
+                f"{t_dec:.2f} s ({r['decode_tokens_per_s']:.0f} tok/s)")
+    del st
+    torch.cuda.empty_cache()
+    return out
+
+
 def run_spmm(torch, dev) -> list:
     """spmm_simple on the reference example's shape (256 x 256, 3 %, N = 128) and on the
     Llama gate shape at the same density: plan = stable row sort (timed once), apply = the
@@ -397,12 +547,13 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=12.0,
                     help="seconds of single-core reference CPU work for the baseline")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["gemv", "gemm", "pack", "copy", "spmm", "launch"],
+    ap.add_argument("--only", choices=["gemv", "gemm", "pack", "copy", "spmm", "launch", "stack"],
                     default=None,
                     help="time one kernel only (for profiling runs); 'copy' times a plain "
                          "elementwise copy of the GEMV weight size, the calibration kernel "
                          "for the HBM byte counters; 'launch' times a one-element fill, the "
-                         "per-launch floor of a graph of back-to-back kernels")
+                         "per-launch floor of a graph of back-to-back kernels; 'stack' runs "
+                         "config 5, the 32-layer decoder, prefill + greedy decode tokens/s")
     ap.add_argument("--sweep", action="store_true",
                     help="also time the config-3/4 shapes and print a table on stderr")
     ap.add_argument("--summarize-trace", metavar="DIR",
@@ -532,6 +683,7 @@ def main() -> int:
 
     sweep = run_sweep(torch, ops, _lib, dev) if args.sweep else None
     spmm = run_spmm(torch, dev) if args.only == "spmm" else None
+    stack = run_stack(torch, dev) if args.only == "stack" else None
 
     gbytes = gemv_bytes(M, N, K)
     line: dict = {
@@ -582,6 +734,8 @@ def main() -> int:
         line["sweep"] = sweep
     if spmm:
         line["spmm"] = spmm
+    if stack:
+        line["stack"] = stack
     print(json.dumps(line), flush=True)
     return 0
 
