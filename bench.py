@@ -233,10 +233,70 @@ class DecoderStack:
         xl = self._rmsnorm(x[:, -1], self.norm)                   # (B, H) bf16
         return t.matmul(xl, self.lm_head_t).float()
 
+    def decode_static(self, tok, pos):
+        """One decode step with shapes that do not depend on the position, so it can be
+        captured in a graph: tok (B, 1) token ids, pos a one-element device tensor.  The
+        step attends over the whole cache with the slots past pos masked out."""
+        t = self.t
+        B = tok.shape[0]
+        H, KV, hd, G = self.hidden, self.kv_heads, self.hd, self.group
+        tmax = self.kt[0].shape[3]
+        x = self.embed[tok]                                       # (B, 1, H)
+        c = self.cos.index_select(0, pos)[None, :, None, :]
+        sn = self.sin.index_select(0, pos)[None, :, None, :]
+
+        def rope(v):
+            v1, v2 = v[..., : hd // 2], v[..., hd // 2:]
+            return t.cat([v1 * c - v2 * sn, v2 * c + v1 * sn], dim=-1)
+
+        mask = t.arange(tmax, device=tok.device)[None, :] > pos[:, None]      # (1, tmax)
+        for li, blk in enumerate(self.blocks):
+            h = self._rmsnorm(x, blk["n1"]).reshape(B, H)
+            qkv = self._linear(blk, "qkv", h)
+            q = rope(qkv[:, :H].reshape(B, 1, self.heads, hd))
+            k = rope(qkv[:, H:H + KV * hd].reshape(B, 1, KV, hd))
+            v = qkv[:, H + KV * hd:].reshape(B, 1, KV, hd)
+            kt, vc = self.kt[li][:B], self.v[li][:B]
+            kt.index_copy_(3, pos, k.permute(0, 2, 3, 1).contiguous())
+            vc.index_copy_(2, pos, v.permute(0, 2, 1, 3).contiguous())
+            qg = q.reshape(B, KV, G, hd)
+            scores = (t.matmul(qg, kt) * (1.0 / hd ** 0.5)).masked_fill(mask, float("-inf"))
+            att = t.matmul(t.softmax(scores, dim=-1), vc).reshape(B, H)
+            x = x + self._linear(blk, "o", att.to(t.bfloat16)).reshape(B, 1, H).to(t.bfloat16)
+            h2 = self._rmsnorm(x, blk["n2"]).reshape(B, H)
+            gu = self._linear(blk, "gate_up", h2)
+            act = (self.F.silu(gu[:, : self.ffn]) * gu[:, self.ffn:]).to(t.bfloat16)
+            x = x + self._linear(blk, "down", act).reshape(B, 1, H).to(t.bfloat16)
+        xl = self._rmsnorm(x[:, -1], self.norm)
+        return t.matmul(xl, self.lm_head_t).float()
+
+    def decode_graph(self, batch):
+        """A captured greedy decode step for `batch` sequences: returns (graph, token
+        buffer, position tensor, logits).  Set the token buffer to the last tokens and the
+        position to theirs; each replay writes the step's logits, puts the argmax in the
+        token buffer and advances the position."""
+        t = self.t
+        dev = self.embed.device
+        tok = t.zeros((batch, 1), dtype=t.long, device=dev)
+        pos = t.zeros((1,), dtype=t.long, device=dev)
+        side = t.cuda.Stream()
+        side.wait_stream(t.cuda.current_stream())
+        with t.cuda.stream(side):
+            self.decode_static(tok, pos)                          # warm-up outside capture
+        t.cuda.current_stream().wait_stream(side)
+        t.cuda.synchronize()
+        graph = t.cuda.CUDAGraph()
+        with t.cuda.graph(graph):
+            logits = self.decode_static(tok, pos)
+            tok.copy_(logits.argmax(-1, keepdim=True))
+            pos.add_(1)
+        return graph, tok, pos, logits
+
 
 def run_stack(torch, dev, prompt=1024, steps=256, batches=(1, 32)) -> dict:
     """Config 5: prompt of 1024 random token ids per sequence, then 256 greedy decode
-    steps, at batch 1 and 32; tokens/s of prefill and of decode (eager launches)."""
+    steps, at batch 1 and 32; tokens/s of prefill (eager) and of decode (each step one
+    replay of a captured graph)."""
     cfg = LLAMA3_8B
     t0 = time.perf_counter()
     st = DecoderStack(torch, dev, cfg["layers"], cfg["hidden"], cfg["heads"], cfg["kv_heads"],
@@ -245,31 +305,37 @@ def run_stack(torch, dev, prompt=1024, steps=256, batches=(1, 32)) -> dict:
     log(f"stack built ({cfg['layers']} layers, weights packed) in {time.perf_counter() - t0:.1f} s")
     out = {"workload": "config 5: Llama-3-8B-shaped 32-layer decoder, t8.nn.Linear projections "
                        "(K1 pack, K2 / K3 matmul), dense bf16 embedding / lm_head / RMSNorm, "
-                       "float32 attention and KV cache, random token ids, greedy",
+                       "float32 attention and KV cache, random token ids, greedy; prefill eager, "
+                       "decode steps replayed from a captured graph",
            "prompt": prompt, "decode_steps": steps, "results": []}
     g = torch.Generator(dev).manual_seed(10)
     with torch.no_grad():
         st.forward(torch.randint(0, cfg["vocab"], (1, 16), generator=g, device=dev), 0)  # warm-up
         for b in batches:
+            graph, tok, pos, _ = st.decode_graph(b)   # before the prompt fills the cache
             tokens = torch.randint(0, cfg["vocab"], (b, prompt), generator=g, device=dev)
             torch.cuda.synchronize()
             t1 = time.perf_counter()
             logits = st.forward(tokens, 0)
             torch.cuda.synchronize()
             t_pre = time.perf_counter() - t1
-            nxt = logits.argmax(-1, keepdim=True)
+            tok.copy_(logits.argmax(-1, keepdim=True))
+            pos.fill_(prompt)
+            torch.cuda.synchronize()
             t2 = time.perf_counter()
-            for i in range(steps):
-                logits = st.forward(nxt, prompt + i)
-                nxt = logits.argmax(-1, keepdim=True)
+            for _ in range(steps):
+                graph.replay()
             torch.cuda.synchronize()
             t_dec = time.perf_counter() - t2
             r = {"batch": b, "prefill_s": t_pre, "prefill_tokens_per_s": b * prompt / t_pre,
-                 "decode_s": t_dec, "decode_tokens_per_s": b * steps / t_dec}
+                 "decode_s": t_dec, "decode_tokens_per_s": b * steps / t_dec,
+                 "decode_ms_per_step": t_dec / steps * 1e3}
             out["results"].append(r)
             log(f"stack batch {b}: prefill {b * prompt} tokens in {t_pre * 1e3:.1f} ms "
                 f"({r['prefill_tokens_per_s']:.0f} tok/s), decode {steps} steps in "
-                f"{t_dec:.2f} s ({r['decode_tokens_per_s']:.0f} tok/s)")
+                f"{t_dec:.2f} s ({r['decode_tokens_per_s']:.0f} tok/s, "
+                f"{r['decode_ms_per_step']:.2f} ms/step)")
+            del graph
     del st
     torch.cuda.empty_cache()
     return out

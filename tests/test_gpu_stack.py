@@ -1,13 +1,16 @@
 """Config 5 in miniature: a decoder stack whose projections are t8.nn.Linear
 (t81lib_amd.nn.Linear in eval mode: K1 pack, then K2 for decode steps and K3 for the
-prompt) against the same stack with F.linear in float32 over the same trits.
+prompt) against the same stack with F.linear in float32 over the same trits, and the
+captured-graph decode step against the eager one.
 
-The two differ only in the projections' summation order (both take the same bf16
-activations and the same trits), so the logits agree to float32 rounding carried
+The two stacks differ only in the projections' summation order (both take the same
+bf16 activations and the same trits), so the logits agree to float32 rounding carried
 through two layers and the bf16 residual stream; greedy tokens agree.
 """
 
 from __future__ import annotations
+
+import sys
 
 import pytest
 import torch
@@ -19,10 +22,13 @@ pytestmark = pytest.mark.gpu
 TINY = dict(layers=2, hidden=256, heads=4, kv_heads=2, ffn=512, vocab=512)
 
 
+def _announce(case):
+    sys.__stderr__.write(f"[gpu case] {case}\n")
+    sys.__stderr__.flush()
+
+
 def test_decoder_stack_matches_float_reference(gpu):
-    sys_stderr = __import__("sys").__stderr__
-    sys_stderr.write("[gpu case] decoder stack tiny\n")
-    sys_stderr.flush()
+    _announce("decoder stack tiny vs float32 reference")
     prompt, steps, batch = 40, 6, 3
     kw = dict(max_batch=batch, max_tokens=prompt + steps, seed=5)
     ours = bench.DecoderStack(torch, gpu, **TINY, **kw)
@@ -39,3 +45,34 @@ def test_decoder_stack_matches_float_reference(gpu):
             agree += int((no == nr).sum())
             lo, lr = ours.forward(nr, prompt + i), ref.forward(nr, prompt + i)
     assert agree >= 0.9 * steps * batch
+
+
+@pytest.mark.parametrize("batch", [1, 4])
+def test_decode_graph_replays_match_eager(gpu, batch):
+    """Each replay of the captured step (K2 inside the graph, masked full-cache attention)
+    against the eager step on a second stack with the same weights and the same prompt,
+    fed the same tokens; every replay checked, with eager work between replays."""
+    _announce(f"decode graph replays batch={batch}")
+    prompt, steps = 24, 5
+    kw = dict(max_batch=batch, max_tokens=prompt + steps, seed=8)
+    a = bench.DecoderStack(torch, gpu, **TINY, **kw)
+    b = bench.DecoderStack(torch, gpu, **TINY, **kw)
+    g = torch.Generator(gpu).manual_seed(9)
+    tokens = torch.randint(0, TINY["vocab"], (batch, prompt), generator=g, device=gpu)
+    with torch.no_grad():
+        graph, tok, pos, logits = a.decode_graph(batch)
+        la = a.forward(tokens, 0)
+        lb = b.forward(tokens, 0)
+        torch.testing.assert_close(la, lb, rtol=0, atol=0)
+        tok.copy_(la.argmax(-1, keepdim=True))
+        pos.fill_(prompt)
+        nxt = lb.argmax(-1, keepdim=True)
+        for i in range(steps):
+            graph.replay()
+            torch.cuda.synchronize()
+            le = b.forward(nxt, prompt + i)
+            scale = le.abs().max().item()
+            assert (logits - le).abs().max().item() <= 1e-3 * scale + 1e-4, f"replay {i}"
+            assert int(pos.item()) == prompt + i + 1
+            nxt = tok.clone()
+            assert torch.equal(nxt, le.argmax(-1, keepdim=True)), f"replay {i} tokens"
