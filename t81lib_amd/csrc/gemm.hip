@@ -27,6 +27,21 @@
 
 namespace t81hip {
 
+// Compute units of the current device, cached per device.
+int cu_count() {
+    static int cached[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            cus <= 0)
+            cus = 256;
+        cached[dev] = cus;
+    }
+    return cached[dev];
+}
+
 namespace {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
@@ -691,9 +706,6 @@ __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(
     }
 }
 
-// Compute units of the current device (one workgroup of the big tile fits per CU).
-int cu_count();
-
 // Weight rows that run as whole rounds of 256 x 256 tiles, one workgroup per CU at a
 // time: all of them, none (fewer than 160 tiles: the GPU would be mostly idle), or,
 // when the last round would be at most half full, the rows of the whole rounds only.
@@ -841,21 +853,6 @@ hipError_t launch_gemm_t(const void *x, const uint8_t *w, void *c, int64_t m, in
     gemm_split_sum_kernel<XT><<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s>>>(
         part, c, m, n, ldc, static_cast<int>(plan.nsplit), alpha, beta, bias);
     return hipGetLastError();
-}
-
-// Compute units of the current device (one workgroup of the big tile fits per CU).
-int cu_count() {
-    static int cached[64] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cached[dev] == 0) {
-        int cus = 0;
-        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            cus <= 0)
-            cus = 256;
-        cached[dev] = cus;
-    }
-    return cached[dev];
 }
 
 template <int XT>

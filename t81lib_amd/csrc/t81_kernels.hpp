@@ -68,6 +68,9 @@ hipError_t launch_gemm(const void *x, int x_dtype, const uint8_t *w, void *c, in
                        hipStream_t s, void *ws = nullptr, int64_t ws_bytes = 0);
 int64_t gemm_workspace_bytes(int64_t m, int64_t n, int64_t k, int x_dtype);
 
+// Compute units of the current device (256 on MI355X), cached per device.
+int cu_count();
+
 // limb.hip (K4)
 hipError_t launch_gemm_limb(const uint8_t *a, const uint8_t *b, float *c, int m, int n,
                             int k_limbs, float alpha, float beta, hipStream_t s);

@@ -137,6 +137,19 @@ def test_decode_strip_shapes(gpu, orc, M, N, K, dtype):
         assert ok, f"alpha={alpha} beta={beta}: {nbad} outside, worst rel {worst:.3g}"
 
 
+@pytest.mark.parametrize("M,N,K", [(1, 14336, 4096), (1, 14336, 6144), (2, 14336, 4096)])
+def test_decode_strip_balanced_full_check(gpu, orc, M, N, K):
+    """bf16 strip launches whose strip length is shortened by one load to even out the
+    workgroups per CU (7 loads for 1 x 4096 x 14336, 14 for the other two): every
+    output against the oracle, with alpha, beta and bias."""
+    announce(f"strip balanced M={M} N={N} K={K}")
+    w, x, c, bias = make_problem(M, N, K, torch.bfloat16, seed=3 * M + N + K)
+    packed, out = run(gpu, w, x, c, bias, K, 0.75, 0.5, True, kernel=2)
+    ref, scale = oracle_matmul(orc, x, packed, K, 0.75, 0.5, c, bias)
+    ok, worst, nbad = fp_tolerance_ok(out.numpy(), ref, scale, RTOL[torch.bfloat16])
+    assert ok, f"{nbad} outside, worst rel {worst:.3g}"
+
+
 @pytest.mark.parametrize("M", [1, 8, 16])
 def test_gemv_and_gemm_kernels_agree(gpu, orc, M):
     """M <= 16 is valid for both kernels: each must match the oracle on its own."""
