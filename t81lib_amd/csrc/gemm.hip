@@ -358,6 +358,7 @@ constexpr int kW4RowBytes = 16 * kW4RowSlots;       // 208
 constexpr int kW4TileBytes = kW4Tokens * kW4RowBytes;
 constexpr int kW4LoadsPerWave = kW4Tokens * kW4RowSlots / (64 * 4);   // 13
 constexpr uint32_t kW4Oob = 0x80000000u;
+constexpr int kW4StageStride = 68;   // floats per staged output row: 64 columns + 4 pad
 
 // A raw buffer descriptor over [base, base + bytes) (clamped to 2^31 - 1 bytes) whose
 // fields are forced into scalar registers: the loads then need no per-lane
@@ -372,15 +373,20 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void *base,
         reinterpret_cast<void *>((static_cast<uint64_t>(hi) << 32) | lo), 0, n, 0x00020000);
 }
 
-// Split-K: with part != nullptr, workgroup (split sp, tile t) runs k-steps
-// [sp * sps, (sp + 1) * sps) and stores its raw accumulators (no alpha, beta, bias) to
-// part in the order (sp, t, wave, block, a4, lane) as float4s -- every store is 1 KB
-// contiguous; gemm_split_reduce_kernel then sums the splits in order.
-template <int XT, bool kSplit>
+// Work items.  Weight rows [0, n1) run as whole 256 x 256 tiles (all k-steps, result
+// to C); rows [n1, N), with nsplit > 0, as split-K items: item (split sp, tile t of that
+// region) runs k-steps [sp * sps, (sp + 1) * sps) and stores its raw accumulators (no
+// alpha, beta, bias) to part in the order (sp, t, wave, block, a4, lane) as float4s --
+// every store is 1 KB contiguous; gemm_split_reduce_kernel then sums the splits in
+// order.  Half of
+// the split items come first and half last in the item order, so the workgroups that
+// start with a (shorter) split item finish their whole tiles half a tile out of step
+// with the others, and the C stores of the two halves do not all land at once.
+template <int XT>
 __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
-    const void *__restrict__ x, const uint8_t *__restrict__ w, void *__restrict__ c, int64_t M,
-    int64_t N, int64_t ldc, int64_t K, int64_t L, float alpha, float beta,
-    const float *__restrict__ bias, int64_t sps, float4 *__restrict__ part) {
+    const void *__restrict__ x, const uint8_t *__restrict__ w, void *__restrict__ c, int M, int N,
+    int ldc, int K, int L, float alpha, float beta, const float *__restrict__ bias, int n1,
+    int sps, float4 *__restrict__ part, int nsplit) {
     static_assert(XT == kDtypeBF16, "the LDS tile is filled straight from bf16 activations");
     // Two separate tile objects (not one array indexed by a run-time parity): the
     // loads into one buffer then provably do not alias the reads of the other, and
@@ -390,45 +396,65 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
     __shared__ __attribute__((aligned(1024))) uint8_t lut[kLutBytes];
     __shared__ __attribute__((aligned(16))) uint8_t xs0[kW4TileBytes];
     __shared__ __attribute__((aligned(16))) uint8_t xs1[kW4TileBytes];
+    // Epilogue staging, one region per wave: 32 tokens x 64 weight rows of results.
+    __shared__ __attribute__((aligned(16))) float cst[4][32 * kW4StageStride];
     auto tile = [&](auto bufc) -> uint8_t * {
         if constexpr (decltype(bufc)::value == 0) return xs0;
         else return xs1;
     };
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wn = wave & 1;
     const int wm = wave >> 1;
+
+    // Items walk the weight-row tiles fastest: items running together share their
+    // activation rows.  (Tile indices are uniform: readfirstlane keeps them, and the
+    // buffer descriptors built from them, in scalar registers.)  The grid is
+    // persistent, one workgroup per CU taking items blockIdx.x, + gridDim.x, ...: a
+    // new workgroup per tile started only after the C stores of the whole previous
+    // round had drained (~15 us a round at M = 2048).
+    const int tiles_m = (M + kW4Tokens - 1) / kW4Tokens;
+    const int tn1 = (n1 + kW4Rows - 1) / kW4Rows;        // row tiles of whole tiles
+    const int tn2 = (N - n1 + kW4Rows - 1) / kW4Rows;    // row tiles of split items
+    const int full_items = tn1 * tiles_m;
+    const int tiles2 = tn2 * tiles_m;
+    const int split_items = nsplit > 0 ? tiles2 * nsplit : 0;
+    const int head = split_items / 2;                    // split items placed first
+    const int total = full_items + split_items;
+    const int all_steps = (L + 1) / 2;
+    lut_fill(lut, tid, kW4Threads);  // published by the first item's barrier
+    for (int q = static_cast<int>(blockIdx.x); q < total; q += static_cast<int>(gridDim.x)) {
+    // The lane index passes through an empty asm once per item, so the per-lane offsets
+    // derived from it are recomputed per item instead of being hoisted out of the loop
+    // and kept live across the epilogue (where they would spill).
+    int lane = tid & 63;
+    asm volatile("" : "+v"(lane));
     const int r = lane & 31;
     const int h = lane >> 5;
-
-    // blockIdx.x walks the weight-row tiles fastest: workgroups running together
-    // share their activation rows.  (Tile indices are uniform: readfirstlane keeps
-    // them, and the buffer descriptors built from them, in scalar registers.)
-    const int tiles_n = static_cast<int>((N + kW4Rows - 1) / kW4Rows);
-    const int tiles = tiles_n * static_cast<int>((M + kW4Tokens - 1) / kW4Tokens);
-    const int bid = static_cast<int>(blockIdx.x);
-    const int sp = __builtin_amdgcn_readfirstlane(bid / tiles);
-    const int tt = __builtin_amdgcn_readfirstlane(bid - sp * tiles);
+    const bool split = q < head || q >= head + full_items;
+    const int item = __builtin_amdgcn_readfirstlane(q < head ? q : (split ? q - full_items : q - head));
+    const int sp = split ? item / tiles2 : 0;
+    const int tt = split ? item - sp * tiles2 : item;          // tile within its region
+    const int tiles_n = split ? tn2 : tn1;
     const int tn = __builtin_amdgcn_readfirstlane(tt % tiles_n);
     const int tm = __builtin_amdgcn_readfirstlane(tt / tiles_n);
-    const int64_t nwg = static_cast<int64_t>(tn) * kW4Rows;
-    const int64_t m0 = static_cast<int64_t>(tm) * kW4Tokens;
-    const int64_t all_steps = (L + 1) / 2;
-    const int64_t s_begin = static_cast<int64_t>(sp) * sps;
-    const int64_t s_end = s_begin + sps < all_steps ? s_begin + sps : all_steps;
+    const int nwg = (split ? n1 : 0) + tn * kW4Rows;
+    const int m0 = tm * kW4Tokens;
+    const int s_begin = split ? sp * sps : 0;
+    const int s_end = split && s_begin + sps < all_steps ? s_begin + sps : all_steps;
 
     // Weights through a buffer based at the workgroup's first row: rows past N read
     // zeros.  A limb index past L (odd L, last step) reads the next row's first limb
     // or zeros; either decodes to finite trits that meet zero activations.
-    const __amdgpu_buffer_rsrc_t wsrc = uniform_rsrc(w + nwg * L * kTrytes, (N - nwg) * L * kTrytes);
+    const __amdgpu_buffer_rsrc_t wsrc = uniform_rsrc(w + static_cast<int64_t>(nwg) * L * kTrytes,
+                                                   static_cast<int64_t>(N - nwg) * L * kTrytes);
     uint32_t woff[4];
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb)
         woff[rb] = (static_cast<uint32_t>(128 * wn + 32 * rb + r) * static_cast<uint32_t>(L) +
                     static_cast<uint32_t>(h)) * kTrytes;
-    auto fetch_w = [&](int64_t step, u32x4 (&dst)[4]) {
+    auto fetch_w = [&](int step, u32x4 (&dst)[4]) {
         const uint32_t koff = static_cast<uint32_t>(step) * (2 * kTrytes);
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb)
@@ -440,7 +466,8 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
     // q / 13, slot q % 13.  Activations through a buffer based at token m0: tokens
     // past M read zeros.
     const __amdgpu_buffer_rsrc_t xsrc =
-        uniform_rsrc(static_cast<const uint16_t *>(x) + m0 * K, (M - m0) * K * 2);
+        uniform_rsrc(static_cast<const uint16_t *>(x) + static_cast<int64_t>(m0) * K,
+                     static_cast<int64_t>(M - m0) * K * 2);
     // Per-lane constants of the 13 loads: the byte offset of the chunk for k0 = 0 (or an
     // out-of-range offset for a pad slot) and, packed four to a register, 8 * slot, the
     // chunk's first trit within the step (past K the chunk loads zeros).
@@ -460,8 +487,8 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
     }
     // Load i of the wave's share of the tile of k-step `step` into LDS buffer buf (all
     // zeros past the last step).
-    auto load_tile_part = [&](int64_t step, auto bufc, int i) {
-        const int64_t k0 = step * kW4StepK;
+    auto load_tile_part = [&](int step, auto bufc, int i) {
+        const int k0 = step * kW4StepK;
         const uint32_t lim = k0 < K ? static_cast<uint32_t>(K - k0) : 0u;
         const uint32_t slot8 = (tslot[i / 4] >> (8 * (i % 4))) & 0xFFu;
         const uint32_t off = slot8 < lim ? tbase[i] + static_cast<uint32_t>(k0) * 2 : kW4Oob;
@@ -471,7 +498,7 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
                 &tile(bufc)[16 * 64 * (kW4LoadsPerWave * wave + i)]),
             16, off, 0, 0, 0);
     };
-    auto load_tile = [&](int64_t step, auto bufc) {
+    auto load_tile = [&](int step, auto bufc) {
 #pragma unroll
         for (int i = 0; i < kW4LoadsPerWave; ++i) load_tile_part(step, bufc, i);
     };
@@ -525,7 +552,6 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
         out[4] = e[2].y | e[3].x;
         out[5] = e[3].y;
     };
-    lut_fill(lut, tid, kW4Threads);
     u32x4 wcur[4], wnxt[4];
     bf16x8 a0[4][3], a1[4][3];
     if (s_begin < s_end) {
@@ -544,7 +570,7 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
     // merge in the next -- and of the loads for the next step (chunks 0-11; unconditional:
     // past the last step they read zeros or unused weight bytes).  Steps alternate
     // between the two tile buffers, so the loop below runs two steps per iteration.
-    auto step_body = [&](int64_t step, auto bufc, auto otherc) {
+    auto step_body = [&](int step, auto bufc, auto otherc) {
         u32x4 bq[3];
         bq[0] = read_b(bufc, 0, 0);
         bq[1] = read_b(bufc, 0, 1);
@@ -586,7 +612,7 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
         __builtin_amdgcn_s_waitcnt(0x0F70);
         __syncthreads();
     };
-    int64_t step = s_begin;
+    int step = s_begin;
     for (; step + 1 < s_end; step += 2) {
         step_body(step, std::integral_constant<int, 0>(), std::integral_constant<int, 1>());
         step_body(step + 1, std::integral_constant<int, 1>(), std::integral_constant<int, 0>());
@@ -594,9 +620,9 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
     if (step < s_end)  // odd step count: the last step, peeled (no join inside the loop)
         step_body(step, std::integral_constant<int, 0>(), std::integral_constant<int, 1>());
 
-    if constexpr (kSplit) {
+    if (split) {
         float4 *dst =
-            part + (((static_cast<int64_t>(sp) * tiles + tt) * 4 + wave) * 64) * 64 + lane;
+            part + (((static_cast<int64_t>(sp) * tiles2 + tt) * 4 + wave) * 64) * 64 + lane;
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
@@ -606,41 +632,79 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
                     dst[((rb * 4 + cb) * 4 + a4) * 64] =
                         make_float4(acc[rb][cb][4 * a4], acc[rb][cb][4 * a4 + 1],
                                     acc[rb][cb][4 * a4 + 2], acc[rb][cb][4 * a4 + 3]);
-        return;
+        continue;
     }
 
     // ---- epilogue: lane (c, h) of block (rb, cb) holds rows 8 a4 + 4 h + b of token c ----
+    // The results go out 32 tokens x 64 weight rows at a time
+    // through the wave's LDS region: written there in the MFMA layout, read back as four
+    // tokens x 64 consecutive rows per instruction, so each global store (and each C read
+    // for beta) covers four 256-byte runs instead of 32 runs of 32 bytes.  A wave's LDS
+    // operations complete in order, so the region needs no barrier.
+    float *cdst = static_cast<float *>(c);
+    const int col0 = nwg;
+    const int ldv = ldc;
+    const int nv = N;
+    const float al = alpha;
+    const float be = beta;
+    const float *bi = bias;
+    const bool vec4 = ldv % 4 == 0 && (reinterpret_cast<uintptr_t>(cdst) & 15u) == 0;
+    float *st = cst[wave];
+    const int tq = lane >> 4;          // token within a group of four
+    const int tc = 4 * (lane & 15);    // first of the lane's four rows within the 64
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
+    for (int cb = 0; cb < 4; ++cb) {
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb) {
-            const int64_t m = m0 + 128 * wm + 32 * cb + r;
-            if (m >= M) continue;
-            float *cr = static_cast<float *>(c) + m * ldc;
+        for (int rp = 0; rp < 2; ++rp) {
 #pragma unroll
-            for (int a4 = 0; a4 < 4; ++a4) {
-                const int64_t nb = nwg + 128 * wn + 32 * rb + 8 * a4 + 4 * h;
-                float y[4];
+            for (int j = 0; j < 2; ++j)
 #pragma unroll
-                for (int b = 0; b < 4; ++b) {
-                    const int64_t n = nb + b;
-                    float t = alpha * acc[rb][cb][4 * a4 + b];
-                    if (n < N) {
-                        if (beta != 0.0f) t = t + beta * cr[n];
-                        if (bias != nullptr) t = t + bias[n];
+                for (int a4 = 0; a4 < 4; ++a4)
+                    *reinterpret_cast<float4 *>(&st[r * kW4StageStride + 32 * j + 8 * a4 + 4 * h]) =
+                        make_float4(acc[2 * rp + j][cb][4 * a4], acc[2 * rp + j][cb][4 * a4 + 1],
+                                    acc[2 * rp + j][cb][4 * a4 + 2], acc[2 * rp + j][cb][4 * a4 + 3]);
+            const int nb = col0 + 128 * wn + 64 * rp + tc;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int tok = 4 * i + tq;
+                const float4 v = *reinterpret_cast<const float4 *>(&st[tok * kW4StageStride + tc]);
+                const int m = m0 + 128 * wm + 32 * cb + tok;
+                if (m >= M) continue;
+                float *cr = cdst + static_cast<int64_t>(m) * ldv;
+                float y[4] = {al * v.x, al * v.y, al * v.z, al * v.w};
+                if (vec4 && nb + 3 < nv) {
+                    if (be != 0.0f) {
+                        const float4 cv = *reinterpret_cast<const float4 *>(cr + nb);
+                        y[0] += be * cv.x;
+                        y[1] += be * cv.y;
+                        y[2] += be * cv.z;
+                        y[3] += be * cv.w;
                     }
-                    y[b] = t;
-                }
-                if (nb + 3 < N && (reinterpret_cast<uintptr_t>(cr + nb) & 15u) == 0) {
+                    if (bi != nullptr) {
+                        const float4 bv = *reinterpret_cast<const float4 *>(bi + nb);
+                        y[0] += bv.x;
+                        y[1] += bv.y;
+                        y[2] += bv.z;
+                        y[3] += bv.w;
+                    }
                     *reinterpret_cast<float4 *>(cr + nb) = make_float4(y[0], y[1], y[2], y[3]);
                 } else {
 #pragma unroll
-                    for (int b = 0; b < 4; ++b)
-                        if (nb + b < N) cr[nb + b] = y[b];
+                    for (int b = 0; b < 4; ++b) {
+                        const int n = nb + b;
+                        if (n < nv) {
+                            float t = y[b];
+                            if (be != 0.0f) t = t + be * cr[n];
+                            if (bi != nullptr) t = t + bi[n];
+                            cr[n] = t;
+                        }
+                    }
                 }
             }
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
+    }  // work items
 }
 
 // Whether the big-tile kernel takes this shape: bf16 activations, 16-byte rows of
@@ -742,27 +806,35 @@ int64_t split_workspace_bytes(const SplitPlan &p) {
     return p.nsplit > 1 ? p.nsplit * p.tiles * kW4Rows * kW4Tokens * 4 : 0;
 }
 
-// Rows [0, n) of W and columns [0, n) of C, whose rows are ldc elements apart.  With
-// part != nullptr (room for plan.nsplit partial tiles), K is split as planned.
+// Rows [0, n1) of W as whole big tiles and, with plan != nullptr (nsplit > 1) and part
+// (room for the plan's partial tiles), rows [n1, n) as split-K items, in one launch;
+// then the split partials are summed into C.  C rows are ldc elements apart.
 hipError_t launch_gemm_w4(const void *x, const uint8_t *w, void *c, int64_t m, int64_t n,
-                          int64_t ldc, int64_t k, float alpha, float beta, const float *bias,
-                          hipStream_t s, const SplitPlan *plan = nullptr, void *part = nullptr) {
+                          int64_t n1, int64_t ldc, int64_t k, float alpha, float beta,
+                          const float *bias, hipStream_t s, const SplitPlan *plan = nullptr,
+                          void *part = nullptr) {
     const int64_t L = (k + kTrits - 1) / kTrits;
-    const int64_t tiles = ((n + kW4Rows - 1) / kW4Rows) * ((m + kW4Tokens - 1) / kW4Tokens);
-    if (plan == nullptr || plan->nsplit <= 1 || part == nullptr) {
-        gemm_w4_kernel<kDtypeBF16, false><<<dim3(tiles), dim3(kW4Threads), 0, s>>>(
-            x, w, c, m, n, ldc, k, L, alpha, beta, bias, (L + 1) / 2, nullptr);
-        return hipGetLastError();
-    }
-    gemm_w4_kernel<kDtypeBF16, true><<<dim3(tiles * plan->nsplit), dim3(kW4Threads), 0, s>>>(
-        x, w, c, m, n, ldc, k, L, alpha, beta, bias, plan->sps, static_cast<float4 *>(part));
-    hipError_t e = hipGetLastError();
+    const int64_t tiles_m = (m + kW4Tokens - 1) / kW4Tokens;
+    const bool split = plan != nullptr && plan->nsplit > 1 && part != nullptr && n1 < n;
+    const int64_t items = ((n1 + kW4Rows - 1) / kW4Rows) * tiles_m +
+                          (split ? plan->nsplit * plan->tiles : 0);
+    if (items <= 0) return hipSuccess;
+    const int64_t cus = cu_count();
+    gemm_w4_kernel<kDtypeBF16><<<dim3(items < cus ? items : cus), dim3(kW4Threads), 0, s>>>(
+        x, w, c, static_cast<int>(m), static_cast<int>(split ? n : n1), static_cast<int>(ldc),
+        static_cast<int>(k), static_cast<int>(L), alpha, beta, bias, static_cast<int>(n1),
+        split ? static_cast<int>(plan->sps) : 0, static_cast<float4 *>(part),
+        split ? static_cast<int>(plan->nsplit) : 0);
+    if (!split) return hipGetLastError();
+    const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    const int64_t tiles = plan->tiles;
     const int64_t slots = tiles * 4 * 64 * 64;
     const int64_t blocks = (slots + 255) / 256 < 8192 ? (slots + 255) / 256 : 8192;
     gemm_split_reduce_kernel<<<dim3(blocks), dim3(256), 0, s>>>(
-        static_cast<const float4 *>(part), static_cast<float *>(c), m, n, ldc,
-        static_cast<int>(tiles), static_cast<int>(plan->nsplit), alpha, beta, bias);
+        static_cast<const float4 *>(part), static_cast<float *>(c) + n1, m, n - n1, ldc,
+        static_cast<int>(tiles), static_cast<int>(plan->nsplit), alpha, beta,
+        bias ? bias + n1 : nullptr);
     return hipGetLastError();
 }
 
@@ -875,21 +947,21 @@ hipError_t launch_gemm_x(const void *x, const uint8_t *w, void *c, int64_t m, in
         const int64_t n1 = gemm_rows_whole_rounds(m, n);
         const int64_t L = (k + kTrits - 1) / kTrits;
         const bool w4 = XT == kDtypeBF16 && gemm_w4_fits(x, m, n, k);
+        if (w4 && ws != nullptr && n1 < n) {
+            // one launch: whole tiles for rows [0, n1), split-K items for the rest
+            const SplitPlan plan = gemm_split_plan(m, n - n1, k);
+            if (plan.nsplit > 1 && ws_bytes >= split_workspace_bytes(plan))
+                return launch_gemm_w4(x, w, c, m, n, n1, n, k, alpha, beta, bias, s, &plan, ws);
+        }
         if (n1 > 0) {
             const hipError_t e =
-                w4 ? launch_gemm_w4(x, w, c, m, n1, n, k, alpha, beta, bias, s)
+                w4 ? launch_gemm_w4(x, w, c, m, n1, n1, n, k, alpha, beta, bias, s)
                    : launch_gemm_t<XT, 2, 4, 4, 2, LK>(x, w, c, m, n1, n, k, alpha, beta, bias, s);
             if (e != hipSuccess || n1 == n) return e;
         }
         const uint8_t *w_rest = w + n1 * L * kTrytes;
         void *c_rest = static_cast<uint8_t *>(c) + 4 * n1;
         const float *bias_rest = bias ? bias + n1 : nullptr;
-        if (w4 && ws != nullptr) {
-            const SplitPlan plan = gemm_split_plan(m, n - n1, k);
-            if (plan.nsplit > 1 && ws_bytes >= split_workspace_bytes(plan))
-                return launch_gemm_w4(x, w_rest, c_rest, m, n - n1, n, k, alpha, beta, bias_rest,
-                                      s, &plan, ws);
-        }
         return launch_gemm_t<XT, 2, 2, 4, 2, LK>(x, w_rest, c_rest, m, n - n1, n, k, alpha, beta,
                                                bias_rest, s, ws, ws_bytes);
     }
