@@ -337,15 +337,15 @@ __global__ __launch_bounds__(64 * W) void gemv_wave_kernel(
 // ---------------------------------------------------------------------------------
 // gemv_stream_kernel: for M * K too large to stage, activations come straight from
 // global memory, fetched one sub-block ahead and issued before the weight prefetch
-// (so waiting for them never drains the weight loads).  Waves split K round-robin.
-template <int XT, int G, bool kAligned>
-__global__ __launch_bounds__(256) void gemv_stream_kernel(const void *__restrict__ x,
+// (so waiting for them never drains the weight loads).  The KS waves of a workgroup
+// split K round-robin; each activation fragment serves its G 16-row groups.
+template <int XT, int G, bool kAligned, int KS>
+__global__ __launch_bounds__(64 * KS) void gemv_stream_kernel(const void *__restrict__ x,
                                                           const uint8_t *__restrict__ w,
                                                           void *__restrict__ c, int M, int64_t N,
                                                           int64_t K, int64_t L, float alpha,
                                                           float beta,
                                                           const float *__restrict__ bias) {
-    constexpr int KS = 4;
     __shared__ __attribute__((aligned(16))) uint8_t lut[kLutBytes];
     __shared__ __attribute__((aligned(16))) floatx4 red[KS * G * 64];
 
@@ -368,7 +368,7 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(const void *__restrict
     u32x4 wcur[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) wcur[g] = load_limb(w, n0 + 16 * g + r, 4 * s + q, N, L, L);
-    lut_init(lut, tid, 256);
+    lut_init(lut, tid, 64 * KS);
 
     floatx4 acc[G];
 #pragma unroll
@@ -397,13 +397,30 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(const void *__restrict
     reduce_store<XT, G, KS>(acc, red, wave, lane, M, N, n0, c, alpha, beta, bias);
 }
 
-template <int XT, int G, bool kAligned>
+template <int XT, int G, bool kAligned, int KS>
 hipError_t launch_stream(const void *x, const uint8_t *w, void *c, int m, int64_t n, int64_t k,
                          int64_t L, float alpha, float beta, const float *bias, hipStream_t s) {
     const int64_t blocks = (n + 16 * G - 1) / (16 * G);
-    gemv_stream_kernel<XT, G, kAligned><<<dim3(blocks), dim3(256), 0, s>>>(x, w, c, m, n, k, L,
-                                                                          alpha, beta, bias);
+    gemv_stream_kernel<XT, G, kAligned, KS><<<dim3(blocks), dim3(64 * KS), 0, s>>>(
+        x, w, c, m, n, k, L, alpha, beta, bias);
     return hipGetLastError();
+}
+
+// Rows per workgroup and waves splitting K for the stream kernel (timed on config-3/4
+// decode shapes): 9..16 tokens over >= 9216 rows share each activation fragment
+// between four row groups (llama.gate M = 16 14.4 -> 13.0 us); up to 8 tokens over a
+// long K (>= 40 sub-blocks) split it over eight waves (llama.down M = 8 21.2 ->
+// 15.6 us); else two row groups, four waves.
+template <int XT, bool kAligned>
+hipError_t launch_stream_shape(const void *x, const uint8_t *w, void *c, int m, int64_t n,
+                               int64_t k, int64_t L, float alpha, float beta, const float *bias,
+                               hipStream_t s) {
+    const int64_t nsb = (L + 3) / 4;
+    if (m > 8 && n >= 9216)
+        return launch_stream<XT, 4, kAligned, 4>(x, w, c, m, n, k, L, alpha, beta, bias, s);
+    if (m <= 8 && nsb >= 40)
+        return launch_stream<XT, 2, kAligned, 8>(x, w, c, m, n, k, L, alpha, beta, bias, s);
+    return launch_stream<XT, 2, kAligned, 4>(x, w, c, m, n, k, L, alpha, beta, bias, s);
 }
 
 // Dynamic LDS of the wave kernel: 160 KiB per CU less its static reduction tile.
@@ -513,8 +530,8 @@ hipError_t launch_gemv_x(const void *x, const uint8_t *w, void *c, int m, int64_
             return launch_wave_su<XT, 8>(su, nsbw_max, a);
         }
     }
-    if (aligned8) return launch_stream<XT, 2, true>(x, w, c, m, n, k, L, alpha, beta, bias, s);
-    return launch_stream<XT, 2, false>(x, w, c, m, n, k, L, alpha, beta, bias, s);
+    if (aligned8) return launch_stream_shape<XT, true>(x, w, c, m, n, k, L, alpha, beta, bias, s);
+    return launch_stream_shape<XT, false>(x, w, c, m, n, k, L, alpha, beta, bias, s);
 }
 
 }  // namespace
