@@ -415,7 +415,9 @@ def test_k2_m5_to_16_full_check(gpu, orc, M, N, K, dtype):
                                          (20, 3000, 9000, torch.int8),
                                          (100, 2000, 4800, torch.int8),
                                          (64, 6144, 4096, torch.bfloat16),
-                                         (300, 1500, 3000, torch.float32)])
+                                         (300, 1500, 3000, torch.float32),
+                                         (32, 16384, 3072, torch.bfloat16),
+                                         (20, 20000, 2000, torch.int8)])
 def test_k3_eight_wave_split_k_full_check(gpu, orc, M, N, K, dtype):
     """Launches of the eight-wave kernel with few tiles (17 <= M <= 64, int8 and fp32
     activations, unaligned K) split K: each split writes its raw sums (int32 for int8,
