@@ -39,7 +39,7 @@ namespace {
 
 constexpr int kTq2Bytes = 66;
 constexpr int kTq2MaxWaves = 8;
-constexpr int kTq2Depth = 8;
+constexpr int kTq2Depth = 4;   // loads in flight per wave, refilled as each is decoded
 constexpr uint32_t kTq2Oob = 0x80000000u;
 constexpr int kTq2LutWords = 512;  // 256 entries x 8 bytes
 
@@ -284,9 +284,8 @@ struct Tq2Args {
     hipStream_t s;
 };
 
-template <int XT, int S, int NW>
+template <int XT, int S, int NW, int R>
 hipError_t launch_tq2(const Tq2Args &a) {
-    constexpr int R = 8;
     constexpr int H = R * (16 / S);
     const int64_t blocks = (a.n + H - 1) / H;
     gemv_tq2_kernel<XT, S, NW, R><<<dim3(static_cast<unsigned>(blocks)), dim3(64 * NW), 0, a.s>>>(
@@ -294,18 +293,31 @@ hipError_t launch_tq2(const Tq2Args &a) {
     return hipGetLastError();
 }
 
-template <int XT, int S>
+template <int XT, int S, int R>
 hipError_t launch_tq2_nw(int nw, const Tq2Args &a) {
     switch (nw) {
-        case 1: return launch_tq2<XT, S, 1>(a);
-        case 2: return launch_tq2<XT, S, 2>(a);
-        case 3: return launch_tq2<XT, S, 3>(a);
-        case 4: return launch_tq2<XT, S, 4>(a);
-        case 5: return launch_tq2<XT, S, 5>(a);
-        case 6: return launch_tq2<XT, S, 6>(a);
-        case 7: return launch_tq2<XT, S, 7>(a);
-        default: return launch_tq2<XT, S, 8>(a);
+        case 1: return launch_tq2<XT, S, 1, R>(a);
+        case 2: return launch_tq2<XT, S, 2, R>(a);
+        case 3: return launch_tq2<XT, S, 3, R>(a);
+        case 4: return launch_tq2<XT, S, 4, R>(a);
+        case 5: return launch_tq2<XT, S, 5, R>(a);
+        case 6: return launch_tq2<XT, S, 6, R>(a);
+        case 7: return launch_tq2<XT, S, 7, R>(a);
+        default: return launch_tq2<XT, S, 8, R>(a);
     }
+}
+
+// Eight block loads per strip, or seven when that lowers the busiest CU's share of
+// the workgroups (4096 -> 14336: 896 workgroups, 3.5 per CU, become 1024, 4 per CU).
+template <int XT, int S>
+hipError_t launch_tq2_r(int nw, const Tq2Args &a) {
+    const int64_t cus = cu_count();
+    auto busiest = [&](int64_t r) {
+        const int64_t blocks = (a.n + r * (16 / S) - 1) / (r * (16 / S));
+        return (blocks + cus - 1) / cus * r;
+    };
+    if (busiest(7) < busiest(8)) return launch_tq2_nw<XT, S, 7>(nw, a);
+    return launch_tq2_nw<XT, S, 8>(nw, a);
 }
 
 // One launch for up to four tokens.
@@ -332,8 +344,8 @@ hipError_t launch_tq2_group(const void *x, const uint8_t *w, float *c, int m, in
     a.beta = beta;
     a.bias = bias;
     a.s = s;
-    if (S == 8) return launch_tq2_nw<XT, 8>(nw, a);
-    return launch_tq2_nw<XT, 4>(nw, a);
+    if (S == 8) return launch_tq2_r<XT, 8>(nw, a);
+    return launch_tq2_r<XT, 4>(nw, a);
 }
 
 template <int XT>
