@@ -10,10 +10,11 @@
 // instead of materialising T as floats (t81/torch/__init__.py:291-304 unpacks it to
 // float32 and multiplies on the host).
 //
-// A workgroup takes 48 input rows (one output limb column) x 192 input columns (four
-// input limbs): 192 lanes read one 16-byte limb each (rows of 64 contiguous bytes), decode
-// it to int8 trits in LDS, and after one barrier 192 lanes each assemble one 16-byte output
-// limb from a column of the tile.  Every byte in and out is touched once: HBM-bound.
+// A workgroup takes 192 input rows (four output limb columns) x 192 input columns (four
+// input limbs): each input limb is read once (rows of 64 contiguous bytes) and decoded to
+// int8 trits in LDS; after one barrier each output limb is assembled from a column of the
+// tile, four consecutive threads writing the four consecutive limbs (64 contiguous bytes)
+// of one output row.  Every byte in and out is touched once: HBM-bound.
 #include "t81_device.hpp"
 #include "t81_kernels.hpp"
 
@@ -21,23 +22,25 @@ namespace t81hip {
 
 namespace {
 
-constexpr int kTileLimbs = 4;                  // input limbs per tile row
+constexpr int kTileLimbs = 4;                   // input limbs per tile row
+constexpr int kOutLimbs = 4;                    // output limbs per tile column
 constexpr int kTileCols = kTileLimbs * kTrits;  // 192 input columns = output rows
+constexpr int kTileRows = kOutLimbs * kTrits;   // 192 input rows
 constexpr int kPitch = kTileCols + 4;           // LDS row pitch (bytes), spreads banks
 
 __global__ __launch_bounds__(256) void transpose_packed_kernel(const uint8_t *__restrict__ in,
                                                                uint8_t *__restrict__ out,
                                                                int64_t rows, int64_t cols,
                                                                int64_t L, int64_t Lt) {
-    __shared__ __attribute__((aligned(16))) int8_t tile[kTrits * kPitch];
+    __shared__ __attribute__((aligned(16))) int8_t tile[kTileRows * kPitch];
     const int tid = threadIdx.x;
-    const int64_t lt = blockIdx.x;                                  // output limb index
+    const int64_t lt0 = static_cast<int64_t>(blockIdx.x) * kOutLimbs;  // first output limb
     const int64_t c0 = static_cast<int64_t>(blockIdx.y) * kTileLimbs;  // first input limb
 
-    if (tid < kTrits * kTileLimbs) {
-        const int r = tid / kTileLimbs;
-        const int l = tid % kTileLimbs;
-        const int64_t row = lt * kTrits + r;
+    for (int i = tid; i < kTileRows * kTileLimbs; i += 256) {
+        const int r = i / kTileLimbs;
+        const int l = i % kTileLimbs;
+        const int64_t row = lt0 * kTrits + r;
         const int64_t limb = c0 + l;
         uint32_t w[4] = {0x0D0D0D0Du, 0x0D0D0D0Du, 0x0D0D0D0Du, 0x0D0D0D0Du};  // zero trits
         if (row < rows && limb < L) {
@@ -55,25 +58,28 @@ __global__ __launch_bounds__(256) void transpose_packed_kernel(const uint8_t *__
     }
     __syncthreads();
 
-    if (tid < kTileCols) {
-        const int64_t k = c0 * kTrits + tid;  // output row
-        if (k < cols) {
-            uint32_t o[4];
+    for (int i = tid; i < kTileCols * kOutLimbs; i += 256) {
+        const int kk = i / kOutLimbs;     // output row within the tile
+        const int ol = i % kOutLimbs;     // output limb within the tile
+        const int64_t k = c0 * kTrits + kk;
+        const int64_t lt = lt0 + ol;
+        if (k >= cols || lt >= Lt) continue;
+        const int8_t *src = tile + ol * kTrits * kPitch + kk;
+        uint32_t o[4];
 #pragma unroll
-            for (int d = 0; d < 4; ++d) {
-                uint32_t word = 0;
+        for (int d = 0; d < 4; ++d) {
+            uint32_t word = 0;
 #pragma unroll
-                for (int b = 0; b < 4; ++b) {
-                    const int j = 4 * d + b;  // output tryte
-                    const int t0 = tile[(3 * j) * kPitch + tid];
-                    const int t1 = tile[(3 * j + 1) * kPitch + tid];
-                    const int t2 = tile[(3 * j + 2) * kPitch + tid];
-                    word |= static_cast<uint32_t>(13 + t0 + 3 * t1 + 9 * t2) << (8 * b);
-                }
-                o[d] = word;
+            for (int b = 0; b < 4; ++b) {
+                const int j = 4 * d + b;  // output tryte
+                const int t0 = src[(3 * j) * kPitch];
+                const int t1 = src[(3 * j + 1) * kPitch];
+                const int t2 = src[(3 * j + 2) * kPitch];
+                word |= static_cast<uint32_t>(13 + t0 + 3 * t1 + 9 * t2) << (8 * b);
             }
-            *reinterpret_cast<uint4 *>(out + (k * Lt + lt) * kTrytes) = make_uint4(o[0], o[1], o[2], o[3]);
+            o[d] = word;
         }
+        *reinterpret_cast<uint4 *>(out + (k * Lt + lt) * kTrytes) = make_uint4(o[0], o[1], o[2], o[3]);
     }
 }
 
@@ -84,7 +90,8 @@ hipError_t launch_transpose_packed(const uint8_t *in, uint8_t *out, int64_t rows
     if (rows == 0 || cols == 0) return hipSuccess;
     const int64_t L = (cols + kTrits - 1) / kTrits;
     const int64_t Lt = (rows + kTrits - 1) / kTrits;
-    const dim3 grid(static_cast<unsigned>(Lt), static_cast<unsigned>((L + kTileLimbs - 1) / kTileLimbs));
+    const dim3 grid(static_cast<unsigned>((Lt + kOutLimbs - 1) / kOutLimbs),
+                    static_cast<unsigned>((L + kTileLimbs - 1) / kTileLimbs));
     transpose_packed_kernel<<<grid, 256, 0, s>>>(in, out, rows, cols, L, Lt);
     return hipGetLastError();
 }
