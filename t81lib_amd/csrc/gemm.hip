@@ -717,37 +717,52 @@ bool gemm_w4_fits(const void *x, int64_t m, int64_t n, int64_t k) {
            n < (int64_t(1) << 30);
 }
 
-// C from the split partials: thread g owns float4 slot g of a tile's share of one
-// split (the order the big-tile kernel stores them in) and sums the nsplit partials
-// in split order, then applies alpha, beta and bias as the kernel's own epilogue does.
+// C from the split partials.  Workgroup (tile, wave, token block cb) sums that
+// block's 1024 float4 slots over the splits in split order (coalesced: 1 KB runs in the
+// order the big-tile kernel stored them), stages its 32 tokens x 128 weight rows in LDS,
+// then writes them as 512-byte runs of C rows, applying alpha, beta and bias as the
+// kernel's own epilogue does.
+constexpr int kReducePitch = 132;   // floats per staged token row: 128 + 4 pad
+
 __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(
     const float4 *__restrict__ part, float *__restrict__ c, int64_t M, int64_t N, int64_t ldc,
     int tiles, int nsplit, float alpha, float beta, const float *__restrict__ bias) {
-    const int64_t per_split = static_cast<int64_t>(tiles) * 4 * 64 * 64;
+    __shared__ __attribute__((aligned(16))) float st[32 * kReducePitch];
+    const int tt = static_cast<int>(blockIdx.x >> 4);
+    const int wave = static_cast<int>((blockIdx.x >> 2) & 3);
+    const int cb = static_cast<int>(blockIdx.x & 3);
+    const int wn = wave & 1, wm = wave >> 1;
     const int tiles_n = static_cast<int>((N + kW4Rows - 1) / kW4Rows);
-    for (int64_t g = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; g < per_split;
-         g += static_cast<int64_t>(gridDim.x) * 256) {
-        const int lane = static_cast<int>(g & 63);
-        const int a4 = static_cast<int>((g >> 6) & 3);
-        const int blk = static_cast<int>((g >> 8) & 15);
-        const int wave = static_cast<int>((g >> 12) & 3);
-        const int tt = static_cast<int>(g >> 14);
-        const int rb = blk >> 2, cb = blk & 3;
-        const int wn = wave & 1, wm = wave >> 1;
-        const int r = lane & 31, h = lane >> 5;
-        const int64_t m = static_cast<int64_t>(tt / tiles_n) * kW4Tokens + 128 * wm + 32 * cb + r;
-        if (m >= M) continue;
-        float4 sum = part[g];
+    const int64_t m0 = static_cast<int64_t>(tt / tiles_n) * kW4Tokens + 128 * wm + 32 * cb;
+    if (m0 >= M) return;
+    const int64_t per_split = static_cast<int64_t>(tiles) * 4 * 64 * 64;
+    const float4 *src = part + (static_cast<int64_t>(tt) * 4 + wave) * 4096;
+    for (int i = threadIdx.x; i < 1024; i += 256) {
+        // slot ((rb * 4 + cb) * 4 + a4) * 64 + lane, lane (r, h): token 32 cb + r, weight
+        // rows 32 rb + 8 a4 + 4 h + (0..3)
+        const int lane = i & 63, a4 = (i >> 6) & 3, rb = i >> 8;
+        const int slot = ((rb * 4 + cb) * 4 + a4) * 64 + lane;
+        float4 v = src[slot];
         for (int sp = 1; sp < nsplit; ++sp) {
-            const float4 v = part[sp * per_split + g];
-            sum.x += v.x;
-            sum.y += v.y;
-            sum.z += v.z;
-            sum.w += v.w;
+            const float4 t = src[sp * per_split + slot];
+            v.x += t.x;
+            v.y += t.y;
+            v.z += t.z;
+            v.w += t.w;
         }
-        const float accv[4] = {sum.x, sum.y, sum.z, sum.w};
-        const int64_t nb =
-            static_cast<int64_t>(tt % tiles_n) * kW4Rows + 128 * wn + 32 * rb + 8 * a4 + 4 * h;
+        const int r = lane & 31, h = lane >> 5;
+        *reinterpret_cast<float4 *>(&st[r * kReducePitch + 32 * rb + 8 * a4 + 4 * h]) = v;
+    }
+    __syncthreads();
+    const int64_t n0 = static_cast<int64_t>(tt % tiles_n) * kW4Rows + 128 * wn;
+    const bool vec4 = ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(c) & 15u) == 0;
+    for (int i = threadIdx.x; i < 32 * 32; i += 256) {
+        const int tok = i >> 5, c4 = i & 31;
+        const int64_t m = m0 + tok;
+        if (m >= M) continue;
+        const float4 v = *reinterpret_cast<const float4 *>(&st[tok * kReducePitch + 4 * c4]);
+        const float accv[4] = {v.x, v.y, v.z, v.w};
+        const int64_t nb = n0 + 4 * c4;
         float *cr = c + m * ldc;
         float y[4];
 #pragma unroll
@@ -760,7 +775,7 @@ __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(
             }
             y[b] = t;
         }
-        if (nb + 3 < N && (reinterpret_cast<uintptr_t>(cr + nb) & 15u) == 0) {
+        if (vec4 && nb + 3 < N) {
             *reinterpret_cast<float4 *>(cr + nb) = make_float4(y[0], y[1], y[2], y[3]);
         } else {
 #pragma unroll
@@ -829,9 +844,7 @@ hipError_t launch_gemm_w4(const void *x, const uint8_t *w, void *c, int64_t m, i
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int64_t tiles = plan->tiles;
-    const int64_t slots = tiles * 4 * 64 * 64;
-    const int64_t blocks = (slots + 255) / 256 < 8192 ? (slots + 255) / 256 : 8192;
-    gemm_split_reduce_kernel<<<dim3(blocks), dim3(256), 0, s>>>(
+    gemm_split_reduce_kernel<<<dim3(static_cast<unsigned>(tiles * 16)), dim3(256), 0, s>>>(
         static_cast<const float4 *>(part), static_cast<float *>(c) + n1, m, n - n1, ldc,
         static_cast<int>(tiles), static_cast<int>(plan->nsplit), alpha, beta,
         bias ? bias + n1 : nullptr);
