@@ -708,13 +708,16 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
 }
 
 // Whether the big-tile kernel takes this shape: bf16 activations, 16-byte rows of
-// whole chunks, and 32-bit buffer offsets for a workgroup's weights and activations.
+// whole chunks, 32-bit buffer offsets for a workgroup's weights and activations, and
+// tile counts (< 2^26) whose work items fit the kernel's int indices (split plans only
+// arise below 160 tiles).
 bool gemm_w4_fits(const void *x, int64_t m, int64_t n, int64_t k) {
     const int64_t L = (k + kTrits - 1) / kTrits;
     return k % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
            int64_t(kW4Rows) * L * kTrytes < 0x7FFFFFFF &&
            int64_t(kW4Tokens) * k * 2 < 0x7FFFFFFF && m > 0 && m < (int64_t(1) << 30) &&
-           n < (int64_t(1) << 30);
+           n < (int64_t(1) << 30) &&
+           ((m + kW4Tokens - 1) / kW4Tokens) * ((n + kW4Rows - 1) / kW4Rows) < (int64_t(1) << 26);
 }
 
 // C from the split partials.  Workgroup (tile, wave, token block cb) sums that
