@@ -1,11 +1,15 @@
 """``Linear``: the reference's ``t8.nn.Linear`` (t81/nn/linear.py:18-125) on the GPU path.
 
 Eval mode packs the weight once (K1, threshold 0.45 by default, cached until
-``train()`` or ``load_state_dict``) and runs the packed matmul with the bias
-fused into the epilogue (K2 for <= 16 tokens, K3 above).  Train mode keeps the
-reference's quantization-aware forward, ``F.linear(x, ternary(w / s) * s, b)``
-with ``s`` an EMA(0.99) of max |w| and a straight-through gradient
-(t81/nn/linear.py:72-99, t81/qat.py:49-57); it is plain torch code.
+``train()`` or ``load_state_dict``) and runs the packed matmul (K2 for <= 16
+tokens, K3 above), with the bias fused into the kernel's epilogue when no
+gradient is needed and added by autograd otherwise (so ``bias.grad`` is filled,
+as in the reference).  Train mode keeps the reference's quantization-aware
+forward, ``F.linear(x, ternary(w / s) * s, b)`` with ``s`` an EMA(0.99) of max |w|
+(t81/nn/linear.py:72-99): the weight gradient flows through the dorso_round
+surrogate of :func:`t81lib_amd.qat.ternary`, and ``configure_qat`` switches on
+stochastic ternarization (t81/nn/linear.py:124-125, t81/qat.py:12-25).  Training
+is plain torch code.
 """
 
 from __future__ import annotations
@@ -17,17 +21,10 @@ import torch
 from torch import nn
 from torch.nn import functional as F
 
+from .qat import ternary
 from .tensor import TernaryTensor
 
 _DEFAULT_THRESHOLD = 0.45
-
-
-def _quantize_ste(x: torch.Tensor, threshold: float) -> torch.Tensor:
-    """ternary(x) with a straight-through gradient (t81/qat.py:12-57, deterministic)."""
-    thr = float(max(0.0, min(threshold, 1.0)))
-    c = x.detach().clamp(-1.0, 1.0)
-    q = torch.where(c.abs() >= thr, torch.sign(c), torch.zeros_like(c))
-    return x + (q - x).detach()
 
 
 class Linear(nn.Linear):
@@ -41,6 +38,7 @@ class Linear(nn.Linear):
         self.semantics = semantics
         self.ternary_weight: Optional[TernaryTensor] = None
         self.register_buffer("training_scale", None)
+        self._stochastic_rounding = False
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if self.training:
@@ -57,14 +55,18 @@ class Linear(nn.Linear):
             return self._packed_linear(x.reshape(batch * seq, features)).reshape(batch, seq, -1)
         if x.ndim != 2:
             raise ValueError("t81.nn.Linear expects 2D or 3D inputs")
-        bias = self.bias.detach() if self.bias is not None else None
-        if torch.is_grad_enabled() and x.requires_grad:
-            return self.ternary_weight.matmul_input(x, bias=bias)
-        return self.ternary_weight.linear(x, bias=bias)
+        bias = self.bias
+        if torch.is_grad_enabled() and (x.requires_grad or (bias is not None and bias.requires_grad)):
+            # autograd: dx through the transposed limbs, dbias through the addition
+            out = self.ternary_weight.matmul_input(x)
+            return out + bias if bias is not None else out
+        return self.ternary_weight.linear(x, bias=bias.detach() if bias is not None else None)
 
     def _quantize_training_weight(self) -> torch.Tensor:
         scale = self._update_training_scale()
-        return _quantize_ste(self.weight / scale, self.ternary_threshold) * scale
+        quantized = ternary(self.weight / scale, threshold=self.ternary_threshold,
+                            stochastic=self._stochastic_rounding)
+        return quantized * scale
 
     def _update_training_scale(self) -> torch.Tensor:
         candidate = self.weight.detach().abs().amax().clamp(min=1e-6).to(torch.float32)
@@ -98,6 +100,10 @@ class Linear(nn.Linear):
         self.ternary_weight = None
         self.training_scale = None
         return result
+
+    def configure_qat(self, *, stochastic_rounding: bool) -> None:
+        """t81/nn/linear.py:124-125: stochastic ternarization of the training weights."""
+        self._stochastic_rounding = stochastic_rounding
 
 
 __all__ = ["Linear"]

@@ -14,14 +14,30 @@ host.  Two readings of ``matmul_input`` are available:
   (t81/torch/__init__.py:241-276): activations quantized at 0.5, packed
   column-wise, multiplied as limb integers by K4; bit-exact with the
   reference CPU ``gemm_ternary``, including its +-inf outputs.
+
+Importing this module also installs the reference's two global patches
+(t81/torch/__init__.py:307-335): ``nn.Module.to(dtype=trit)`` converts every 2-D
+parameter of a network into a cached ``TernaryTensor`` with a forward pre-hook
+that keeps it in step with the float weights, and ``nn.Linear.forward`` runs the
+packed matmul for layers that carry such a cache.  Differences, each a fix of a
+reference defect: the reference forwards ``dtype=trit`` to torch's own
+``Module.to``, which rejects a non-``torch.dtype`` with a TypeError before any
+conversion happens, so here the trit marker is taken out of the arguments
+first; the reference re-packs every cached weight twice per forward (the hook
+and the patched forward both call ``update_from_float``), here a weight is
+re-packed only when its parameter changed (its version counter or storage), so
+weights written through ``.data`` need ``refresh_ternary_weights(module)``; and
+inputs with more than two dimensions are flattened to (rows, features), where
+the reference's ``matmul_input`` raises.
 """
 
 from __future__ import annotations
 
 import warnings
-from typing import Callable, Optional
+from typing import Any, Callable, Dict, Mapping, Optional, Sequence
 
 import torch
+from torch import nn
 
 from . import _lib, ops
 
@@ -231,4 +247,111 @@ class _TernaryGemmFunction(torch.autograd.Function):
         return None, grad_rhs
 
 
-__all__ = ["trit", "TritDtype", "TernaryTensor", "SEMANTICS"]
+# ------------------------------------------------- whole-network conversion --
+# Semantics given to the TernaryTensors that model.to(dtype=trit) creates.
+conversion_semantics = "trit_dot"
+
+
+def _extract_dtype_arg(args: Sequence[Any], kwargs: Mapping[str, Any]) -> Any:
+    """t81/torch/__init__.py:127-134, also accepting the trit marker positionally."""
+    if kwargs.get("dtype") is not None:
+        return kwargs["dtype"]
+    for arg in args:
+        if arg is trit or isinstance(arg, torch.dtype):
+            return arg
+    return None
+
+
+def _param_key(param: torch.Tensor) -> tuple:
+    return (param.data_ptr(), param._version, tuple(param.shape))
+
+
+def _sync_ternary_weights(module: nn.Module, _inputs: Sequence[Any] = ()) -> None:
+    """Forward pre-hook (t81/torch/__init__.py:136-141): re-pack each cached weight whose
+    parameter changed since it was packed (version counter, storage or shape)."""
+    cache: Dict[str, TernaryTensor] = getattr(module, "_t81_ternary_cache", {})
+    keys: Dict[str, tuple] = module.__dict__.setdefault("_t81_ternary_keys", {})
+    for name, ternary in cache.items():
+        param = getattr(module, name)
+        key = _param_key(param)
+        if keys.get(name) != key:
+            ternary.update_from_float(param.detach())
+            keys[name] = key
+
+
+def refresh_ternary_weights(module: nn.Module) -> None:
+    """Re-packs every cached weight of ``module`` and its children unconditionally (for
+    weights written through ``.data``, which leaves the version counter unchanged)."""
+    for sub in module.modules():
+        sub.__dict__.pop("_t81_ternary_keys", None)
+        _sync_ternary_weights(sub)
+
+
+def _apply_ternary_conversion(module: nn.Module) -> None:
+    """t81/torch/__init__.py:144-164: every submodule with 2-D parameters gets a cache of
+    TernaryTensors (threshold: ``ternary_threshold``, else ``threshold``, else 0.5) and
+    the forward pre-hook."""
+    for sub in module.modules():
+        if hasattr(sub, "_t81_ternary_cache"):
+            continue
+        cache: Dict[str, TernaryTensor] = {}
+        keys: Dict[str, tuple] = {}
+        for name, param in sub.named_parameters(recurse=False):
+            if param.ndim != 2:
+                continue
+            threshold = getattr(sub, "ternary_threshold", getattr(sub, "threshold", 0.5))
+            cache[name] = TernaryTensor.from_float(param.detach(), threshold=threshold,
+                                                   semantics=conversion_semantics)
+            keys[name] = _param_key(param)
+        if cache:
+            sub._t81_ternary_cache = cache
+            sub.__dict__["_t81_ternary_keys"] = keys
+            if not hasattr(sub, "_t81_hook_handle"):
+                sub._t81_hook_handle = sub.register_forward_pre_hook(_sync_ternary_weights)
+
+
+_original_module_to = nn.Module.to
+
+
+def _ternary_module_to(self: nn.Module, *args, **kwargs) -> nn.Module:
+    """nn.Module.to (t81/torch/__init__.py:310-318): ``dtype=trit`` converts the network
+    after the rest of the call (device moves, ...) has been applied."""
+    if _extract_dtype_arg(args, kwargs) is not trit:
+        return _original_module_to(self, *args, **kwargs)
+    args = tuple(a for a in args if a is not trit)
+    kwargs = {k: v for k, v in kwargs.items() if not (k == "dtype" and v is trit)}
+    module = _original_module_to(self, *args, **kwargs) if (args or kwargs) else self
+    _apply_ternary_conversion(module)
+    return module
+
+
+_original_linear_forward = nn.Linear.forward
+
+
+def _ternary_linear_forward(self: nn.Linear, input: torch.Tensor) -> torch.Tensor:
+    """nn.Linear.forward (t81/torch/__init__.py:323-333): layers with a cached ternary
+    weight run the packed matmul; the bias is added in float32 (fused into the kernel
+    when no gradient is needed)."""
+    cache: Dict[str, TernaryTensor] = getattr(self, "_t81_ternary_cache", {})
+    ternary = cache.get("weight")
+    if ternary is None:
+        return _original_linear_forward(self, input)
+    _sync_ternary_weights(self)
+    lead = input.shape[:-1]
+    x = input.reshape(-1, input.shape[-1]) if input.ndim != 2 else input
+    bias = self.bias
+    grad = torch.is_grad_enabled() and (
+        input.requires_grad or (bias is not None and bias.requires_grad))
+    if grad or x.device.type != "cuda" or ternary._semantics != "trit_dot":
+        out = ternary.matmul_input(x)
+        if bias is not None:
+            out = out + bias
+    else:
+        out = ternary.linear(x, bias=bias.detach() if bias is not None else None)
+    return out.reshape(*lead, out.shape[-1]) if input.ndim != 2 else out
+
+
+nn.Module.to = _ternary_module_to
+nn.Linear.forward = _ternary_linear_forward
+
+__all__ = ["trit", "TritDtype", "TernaryTensor", "SEMANTICS", "refresh_ternary_weights"]

@@ -55,6 +55,35 @@ def gpu():
     return torch.device("cuda", 0)
 
 
+U32 = 2.0 ** -24          # unit roundoff of float32
+NORTH_STAR_RTOL = {"f32": 1e-3, "bf16": 1e-2}
+
+
+def _dtype_name(dtype) -> str:
+    s = str(dtype)
+    if s in ("f32", "torch.float32"):
+        return "f32"
+    if s in ("bf16", "torch.bfloat16"):
+        return "bf16"
+    raise ValueError(f"no float tolerance for {dtype}")
+
+
+def accum_rtol(k: int, dtype) -> float:
+    """Tolerance of the trit-dot kernels, relative to sum_k |alpha x_k t_k| + |beta c| +
+    |bias|.  A trit times a bf16 value is exact in float32, so the only error of a bf16
+    product is float32 summation: n additions in any order lose at most (n - 1) u of the
+    summed magnitudes (u = 2^-24); u is doubled for the matrix cores' internal rounding,
+    and 16 more additions cover the split-K partial sums and the alpha / beta / bias
+    epilogue.  float32 activations run as a hi + lo bf16 pair: twice the terms and a
+    representation error |x - hi - lo| <= 2^-16 |x|.  The result is capped by the
+    north-star elementwise tolerance (1e-2 bf16, 1e-3 float32), which only binds for
+    float32 at very long K."""
+    name = _dtype_name(dtype)
+    terms = k if name == "bf16" else 2 * k
+    bound = 2.0 * (terms + 16) * U32 + (0.0 if name == "bf16" else 2.0 ** -16)
+    return min(bound, NORTH_STAR_RTOL[name])
+
+
 def fp_tolerance_ok(got, ref, scale, rtol, atol=1e-6):
     """|got - ref| <= rtol * scale + atol elementwise, scale = sum_k |alpha x_k t_k| + |beta c| + |bias|
     (a relative tolerance on the terms that were summed, so cancellation in a sum does not

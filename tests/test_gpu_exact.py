@@ -1,0 +1,224 @@
+"""Bit-exact pins of the bfloat16 hot-path kernels (K2 decode GEMV, K3 prefill GEMM).
+
+The activations are integers with |x| <= 127, which bfloat16 holds exactly.  Every
+product x * t (t a trit) is then an integer, every partial sum stays below 2^24 in
+magnitude, and float32 adds such integers without rounding in any order: the
+kernel's float32 output must equal the int64 oracle bit for bit.  alpha = 0.5,
+integer C and integer bias keep the epilogue exact too (alpha * acc has one
+fractional bit).  A kernel that drops or repeats any limb, any trit, any split or
+any tile fails these tests on essentially every output it touches.
+
+Paths covered (shapes taken from the configs):
+* K2 column-strip kernel, natural trit order: one token, 4096 -> 14336 (two 32-limb
+  rows per load, seven loads per strip) and the 3072-wide Phi-3 shapes (one row x
+  64 limbs per load);
+* K2 column-strip kernel, padded order: one token at K = 8192 / 14336; 2 tokens
+  (S = 8) and 3-4 tokens (S = 4);
+* K2 gemv.hip: 8, 12 and 16 tokens (activations staged in LDS, or streamed with
+  two or four row groups per fragment);
+* K3 big-tile kernel (one wave per SIMD): config 4 at M = 2048 (gate_up: whole
+  256 x 256 tiles for the first 24576 rows, split-K items for the remaining 4096
+  in the same launch, an odd step count with the peeled last step), M = 512
+  (every tile split over the workspace) and M = 8192, plus small shapes with odd
+  and even step counts, ragged M and N and K past the last whole step.
+
+Full-size K3 outputs are checked twice: a seeded sample of tokens x rows, drawn
+from every region of the launch, against the C oracle on the packed bytes, and
+every output against a float64 product of the unpacked trits on the GPU (exact:
+integer sums far below 2^53).
+"""
+
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from t81lib_amd import _lib, ops
+
+pytestmark = pytest.mark.gpu
+
+
+def announce(case: str) -> None:
+    sys.__stderr__.write(f"[gpu case] {case}\n")
+    sys.__stderr__.flush()
+
+
+def int_problem(M, N, K, seed):
+    g = torch.Generator("cpu").manual_seed(seed)
+    w = torch.randn((N, K), generator=g)                        # ~1/3 zero trits at 0.45
+    x = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int32)
+    x[:, ::97] = 0                                              # a few exact zeros
+    c = torch.randint(-1000, 1001, (M, N), generator=g).float()
+    bias = torch.randint(-1000, 1001, (N,), generator=g).float()
+    return w, x, c, bias
+
+
+def expected(acc: np.ndarray, alpha: float, beta: float, c: np.ndarray, bias) -> np.ndarray:
+    """alpha * acc + beta * c + bias, exact in float64, then float32 (exact: < 2^24)."""
+    y = alpha * acc.astype(np.float64)
+    if beta != 0.0:
+        y = y + beta * c.astype(np.float64)
+    if bias is not None:
+        y = y + bias.astype(np.float64)
+    assert np.abs(y).max(initial=0.0) < 2 ** 23, "test values must stay exact in float32"
+    return y.astype(np.float32)
+
+
+def assert_bits(got: np.ndarray, want: np.ndarray, what: str) -> None:
+    got = np.ascontiguousarray(got, np.float32)
+    bad = got.view(np.uint32) != want.view(np.uint32)
+    if bad.any():
+        i = np.argwhere(bad)[0]
+        raise AssertionError(f"{what}: {int(bad.sum())} of {bad.size} outputs differ; first at "
+                             f"{tuple(int(v) for v in i)}: got {got[tuple(i)]!r}, "
+                             f"want {want[tuple(i)]!r}")
+
+
+# --------------------------------------------------------------------- K2 --
+PHI3 = {"qkv": (3072, 9216), "o": (3072, 3072), "gate_up": (3072, 16384), "down": (8192, 3072)}
+LLAMA = {"qkv": (4096, 6144), "gate": (4096, 14336), "down": (14336, 4096)}
+
+K2_CASES = (
+    [("phi3." + name, M, K, N) for name, (K, N) in PHI3.items() for M in (1, 4, 16)]
+    + [("llama.gate", M, 4096, 14336) for M in (1, 2, 3, 8, 12, 16)]
+    + [("llama.down", M, 14336, 4096) for M in (1, 2, 4, 8, 16)]
+    + [("llama.qkv", 1, 4096, 6144), ("ragged", 1, 4100, 77), ("ragged", 3, 1000, 333),
+       ("ragged", 13, 5767, 300)]
+)
+
+
+@pytest.mark.parametrize("name,M,K,N", K2_CASES)
+def test_k2_integer_bf16_bit_exact(gpu, orc, name, M, K, N):
+    announce(f"exact K2 {name} M={M} K={K} N={N}")
+    w, x, c, bias = int_problem(M, N, K, seed=M * 7919 + K + N)
+    packed = ops.quantize_pack(w.to(gpu), 0.45, _lib.THR_CPP)
+    packed_np = packed.cpu().numpy()
+    acc = orc.trit_matmul_i64(x.to(torch.int8).numpy(), packed_np, K) if K <= 131071 else None
+    xg = x.to(torch.bfloat16).to(gpu)
+    assert torch.equal(xg.float().cpu(), x.float()), "integers must be exact in bfloat16"
+    cg = c.to(gpu)
+    for alpha, beta, use_bias in ((1.0, 0.0, False), (0.5, 1.0, True), (-2.0, 0.5, True)):
+        out = ops.ternary_matmul(xg, packed, K, alpha=alpha, beta=beta,
+                                 c=cg.clone() if beta else None,
+                                 bias=bias.to(gpu) if use_bias else None, kernel=2)
+        want = expected(acc, alpha, beta, c.numpy(), bias.numpy() if use_bias else None)
+        assert_bits(out.cpu().numpy(), want, f"alpha={alpha} beta={beta} bias={use_bias}")
+
+
+# --------------------------------------------------------------------- K3 --
+def _sample(M, N, n1, seed, tokens=48, rows=96):
+    """Tokens from every 256-token tile; rows from both the whole-tile region [0, n1)
+    and the split region [n1, N), including each region's first and last row."""
+    rng = np.random.default_rng(seed)
+    toks = set(rng.choice(M, min(tokens, M), replace=False).tolist())
+    toks.update({0, M - 1, min(M - 1, 255), min(M - 1, 256)})
+    picks = {0, N - 1}
+    if 0 < n1 < N:
+        picks.update({n1 - 1, n1})
+        picks.update(rng.choice(n1, rows // 2, replace=False).tolist())
+        picks.update((n1 + rng.choice(N - n1, rows // 2, replace=False)).tolist())
+    else:
+        picks.update(rng.choice(N, min(rows, N), replace=False).tolist())
+    return np.array(sorted(toks)), np.array(sorted(picks))
+
+
+def whole_round_rows(M: int, N: int) -> int:
+    """Weight rows the K3 launcher runs as whole 256 x 256 tiles (the rest, if any, as
+    split-K items): whole rounds of one tile per CU when the last round would be at most
+    half full, else all rows (the launcher's rule)."""
+    tiles_m = -(-M // 256)
+    tiles = -(-N // 256) * tiles_m
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    rem = tiles % cus
+    n1 = (tiles - rem) // tiles_m * 256
+    if tiles >= 160 and tiles > cus and rem != 0 and 2 * rem <= cus and 0 < n1 < N:
+        return n1
+    return N
+
+
+def _gpu_exact_product(xg_f64: torch.Tensor, packed: torch.Tensor, N: int, K: int) -> torch.Tensor:
+    """x @ T^T in float64 on the GPU from the unpacked trits (exact for these integers)."""
+    tt = ops.unpack(packed, N, K).to(torch.float64).t().contiguous()   # (K, N)
+    return torch.matmul(xg_f64, tt)
+
+
+K3_FULL = [
+    # name, M, K, N
+    ("llama.gate_up", 2048, 4096, 28672),   # whole tiles + split items, odd step count
+    ("llama.qkv", 2048, 4096, 6144),
+    ("llama.down", 2048, 14336, 4096),
+    ("llama.qkv", 512, 4096, 6144),         # every tile split over the workspace
+    ("llama.down", 512, 14336, 4096),
+    ("llama.qkv", 8192, 4096, 6144),
+]
+
+
+@pytest.mark.parametrize("name,M,K,N", K3_FULL)
+def test_k3_config4_integer_bf16_bit_exact(gpu, orc, name, M, K, N):
+    announce(f"exact K3 {name} M={M} K={K} N={N}")
+    g = torch.Generator("cpu").manual_seed(M + N + K)
+    w = torch.randn((N, K), generator=g)
+    x = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int32)
+    packed = ops.quantize_pack(w.to(gpu), 0.45, _lib.THR_CPP)
+    del w
+    xg = x.to(torch.bfloat16).to(gpu)
+    gg = torch.Generator(gpu).manual_seed(M * 3 + N)
+    cg = torch.randint(-1000, 1001, (M, N), generator=gg, device=gpu).float()
+    bias = torch.randint(-1000, 1001, (N,), generator=gg, device=gpu).float()
+    exact = _gpu_exact_product(x.to(torch.float64).to(gpu), packed, N, K)
+    toks, rows = _sample(M, N, whole_round_rows(M, N), seed=M + K)
+    packed_np = packed.cpu().numpy()
+    acc_s = orc.trit_matmul_i64(x[torch.from_numpy(toks)].to(torch.int8).numpy(),
+                                packed_np[rows], K)
+    np.testing.assert_array_equal(
+        exact[torch.from_numpy(toks).to(gpu)][:, torch.from_numpy(rows).to(gpu)]
+        .cpu().numpy().astype(np.int64), acc_s, err_msg="float64 GPU product vs oracle")
+    for alpha, beta, use_bias in ((1.0, 0.0, False), (0.5, 1.0, True)):
+        out = ops.ternary_matmul(xg, packed, K, alpha=alpha, beta=beta,
+                                 c=cg.clone() if beta else None,
+                                 bias=bias if use_bias else None, kernel=3)
+        want_full = alpha * exact
+        if beta:
+            want_full = want_full + beta * cg.double()
+        if use_bias:
+            want_full = want_full + bias.double()
+        assert float(want_full.abs().max()) < 2 ** 23
+        bad = int((out.double() != want_full).sum())
+        assert bad == 0, f"alpha={alpha} beta={beta}: {bad} of {M * N} outputs differ"
+        tsel = torch.from_numpy(toks).to(gpu)
+        rsel = torch.from_numpy(rows).to(gpu)
+        got_s = out[tsel][:, rsel].cpu().numpy()
+        c_s = cg[tsel][:, rsel].cpu().numpy()
+        want_s = expected(acc_s, alpha, beta, c_s, bias[rsel].cpu().numpy() if use_bias else None)
+        assert_bits(got_s, want_s, f"sampled vs oracle alpha={alpha} beta={beta}")
+        del out, want_full
+    del exact
+    torch.cuda.empty_cache()
+
+
+K3_SMALL = [
+    # M, N, K: >= 160 big tiles (whole-tile kernel), odd and even step counts, K past
+    # the last whole step, ragged M / N, more tiles than CUs; then few tiles (split-K)
+    (300, 256 * 160 + 13, 200), (512, 256 * 80, 192), (260, 256 * 81 + 7, 480),
+    (512, 256 * 200 - 5, 96), (300, 1000, 4104), (260, 4096, 2000), (200, 700, 1536),
+    (300, 256 * 160, 1536),
+]
+
+
+@pytest.mark.parametrize("M,N,K", K3_SMALL)
+def test_k3_big_tile_integer_bf16_bit_exact(gpu, orc, M, N, K):
+    announce(f"exact K3 big tile M={M} N={N} K={K}")
+    w, x, c, bias = int_problem(M, N, K, seed=M + N + K)
+    packed = ops.quantize_pack(w.to(gpu), 0.45, _lib.THR_CPP)
+    acc = orc.trit_matmul_i64(x.to(torch.int8).numpy(), packed.cpu().numpy(), K)
+    xg = x.to(torch.bfloat16).to(gpu)
+    cg = c.to(gpu)
+    for alpha, beta, use_bias in ((1.0, 0.0, False), (0.5, 1.0, True)):
+        out = ops.ternary_matmul(xg, packed, K, alpha=alpha, beta=beta,
+                                 c=cg.clone() if beta else None,
+                                 bias=bias.to(gpu) if use_bias else None, kernel=3)
+        want = expected(acc, alpha, beta, c.numpy(), bias.numpy() if use_bias else None)
+        assert_bits(out.cpu().numpy(), want, f"alpha={alpha} beta={beta}")

@@ -13,7 +13,7 @@ import torch
 
 from t81lib_amd import nn as t8nn, ops, t81lib
 from t81lib_amd.tensor import TernaryTensor, trit
-from conftest import fp_tolerance_ok
+from conftest import accum_rtol, fp_tolerance_ok
 
 pytestmark = pytest.mark.gpu
 
@@ -118,7 +118,8 @@ def test_linear_eval_vs_oracle(gpu, orc, tokens):
     b = layer.bias.detach().double().cpu().numpy()
     ref = orc.trit_matmul_f64(xf, wp, 300) + b
     scale = orc.trit_matmul_abs_f64(xf, wp, 300) + np.abs(b)
-    ok, worst, nbad = fp_tolerance_ok(y.reshape(-1, 130).float().cpu().numpy(), ref, scale, 1e-2)
+    ok, worst, nbad = fp_tolerance_ok(y.reshape(-1, 130).float().cpu().numpy(), ref, scale,
+                                      accum_rtol(300, torch.bfloat16))
     assert ok, f"{nbad} outside, worst {worst:.3g}"
     assert layer.ternary_weight is not None
     layer.train()
@@ -144,7 +145,7 @@ def test_transpose_packed_bit_exact(gpu, orc, rows, cols):
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_grad_input_vs_oracle(gpu, orc, rows, cols, tokens, dtype):
     """grad_rhs = T^T @ grad_output (t81/torch/__init__.py:291-304) through the transposed
-    limbs and the forward GEMM; fp32 within 1e-3, bf16 within 1e-2 of sum |t g|."""
+    limbs and the forward GEMM, within the float32 summation bound of sum |t g| (K = rows)."""
     announce(f"grad_input {rows}x{cols} tokens={tokens} {dtype}")
     g = torch.Generator("cpu").manual_seed(rows + cols + tokens)
     w = torch.randn(rows, cols, generator=g)
@@ -155,7 +156,7 @@ def test_grad_input_vs_oracle(gpu, orc, rows, cols, tokens, dtype):
     gd = grad.to(torch.float64).numpy()
     want = trits.T @ gd
     scale = np.abs(trits.T) @ np.abs(gd)
-    ok, worst, nbad = fp_tolerance_ok(got, want, scale, 1e-3 if dtype == torch.float32 else 1e-2)
+    ok, worst, nbad = fp_tolerance_ok(got, want, scale, accum_rtol(rows, dtype))
     assert ok, f"{nbad} outside, worst rel {worst:.3g}"
     # the cache follows the weights
     t.update_from_float((-w).to(gpu))

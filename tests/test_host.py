@@ -71,3 +71,23 @@ def test_linear_train_mode_is_quantization_aware():
     assert layer.ternary_weight is None
     layer.eval()
     assert layer.ternary_weight is None  # packed lazily on the first eval forward
+
+
+def test_module_to_trit_argument_handling():
+    """model.to(dtype=trit) takes the trit marker out before torch's own Module.to (which
+    would raise TypeError on it), converts only then, and needs the GPU (no CPU fallback);
+    other .to calls pass through."""
+    from t81lib_amd import tensor as tt
+
+    assert tt._extract_dtype_arg((), {"dtype": trit}) is trit
+    assert tt._extract_dtype_arg((trit,), {}) is trit
+    assert tt._extract_dtype_arg(("cpu", torch.float16), {}) is torch.float16
+    assert tt._extract_dtype_arg(("cpu",), {}) is None
+    layer = torch.nn.Linear(4, 3)
+    assert layer.to(torch.float64) is layer and layer.weight.dtype == torch.float64
+    if not torch.cuda.is_available():
+        with pytest.raises((_lib.T81HipError, RuntimeError)):
+            layer.to(dtype=trit)
+    # without a cache the patched forward is the original
+    x = torch.randn(2, 4, dtype=torch.float64)
+    torch.testing.assert_close(layer(x), torch.nn.functional.linear(x, layer.weight, layer.bias))
