@@ -126,6 +126,20 @@ int t81_hip_ternary_matmul_ws(int which, const void *x, int x_dtype, const uint8
  * device (0: the shape does not split).  Never fails. */
 int64_t t81_hip_ternary_matmul_workspace_size(int64_t m, int64_t n, int64_t k, int x_dtype);
 
+/* Same as t81_hip_ternary_matmul_ws(which, ...) given a workspace of exactly
+ * t81_hip_ternary_matmul_workspace_size(m, n, k, x_dtype) bytes -- identical kernels,
+ * split plan and results, bit for bit -- but allocating nothing: the workspace is a
+ * static 64 MiB device array in the library, one copy per device, reserved when the
+ * library's code object is loaded on that device and held until the process ends.
+ * Shapes whose split needs more than 64 MiB are rejected (T81_HIP_EINVAL_SHAPE, nothing
+ * launched).  Every call on a device shares that array: calls that may overlap on one
+ * device (other streams or threads) race and must be serialised by the caller.
+ * No counterpart in the reference: it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, serving loops that forbid hipMalloc). */
+int t81_hip_ternary_matmul_noalloc(int which, const void *x, int x_dtype, const uint8_t *w,
+                                   void *c, int64_t m, int64_t n, int64_t k, float alpha,
+                                   float beta, const float *bias, void *stream);
+
 /* K4 -- the reference's literal gemm_ternary: A (M x K/48 limbs), B (K/48 x N
  * limbs), C (M x N float32, read and written):
  *     C[i,j] = float( C[i,j]*beta + sum_l alpha * V(A[i,l]) * V(B[l,j]) )

@@ -47,6 +47,7 @@ EXPORTS = (
     "t81_hip_ternary_matmul_kernel",
     "t81_hip_ternary_matmul_ws",
     "t81_hip_ternary_matmul_workspace_size",
+    "t81_hip_ternary_matmul_noalloc",
     "t81_hip_gemm_ternary_limb",
     "t81_hip_where",
     "t81_hip_clamp",
@@ -108,6 +109,9 @@ def _declare(lib: ctypes.CDLL) -> None:
                                               _vp, _vp, _i64, _vp]
     lib.t81_hip_ternary_matmul_workspace_size.restype = _i64
     lib.t81_hip_ternary_matmul_workspace_size.argtypes = [_i64, _i64, _i64, _i]
+    lib.t81_hip_ternary_matmul_noalloc.restype = _i
+    lib.t81_hip_ternary_matmul_noalloc.argtypes = [_i, _vp, _i, _vp, _vp, _i64, _i64, _i64, _f,
+                                                   _f, _vp, _vp]
     lib.t81_hip_gemm_ternary_limb.restype = _i
     lib.t81_hip_gemm_ternary_limb.argtypes = [_vp, _vp, _vp, _i, _i, _i, _f, _f, _vp]
     lib.t81_hip_where.restype = _i

@@ -20,7 +20,7 @@ ARCH = "gfx950"
 
 SOURCES = ["abi.hip", "pack.hip", "gemv.hip", "gemv_strip.hip", "gemm.hip",
            "limb.hip", "elementwise.hip", "tq.hip", "gemv_tq2.hip", "transpose.hip",
-           "spmm.hip"]
+           "spmm.hip", "noalloc.hip"]
 
 # -packed-fp32-ops: no v_pk_*_f32 from the compiler (they are never written by hand either).
 HIPCC_FLAGS = [

@@ -112,6 +112,8 @@ int check_matmul(const void *x, int x_dtype, const uint8_t *w, void *c, int64_t 
 
 }  // namespace
 
+int t81hip::report_error(int code, const char *msg) { return fail(code, msg); }
+
 extern "C" {
 
 int t81_hip_available(void) {

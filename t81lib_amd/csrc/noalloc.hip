@@ -1,0 +1,78 @@
+// t81lib_amd/csrc/noalloc.hip -- t81_hip_ternary_matmul_noalloc: the trit-dot matmul with
+// the K3 split-K workspace taken from a static device array, for callers that cannot
+// allocate device memory (code under HIP graph capture, serving loops that forbid it).
+//
+// `scratch` is a file-scope device array, reserved when the code object is loaded on a
+// device and held until the process ends, one copy per device at its own address.  In
+// host code its name is only a registration handle, so each device's address is looked
+// up once with hipGetSymbolAddress (that device current) and that pointer is what the
+// kernels receive.  Every call on a device shares the array: calls that overlap on one
+// device (different streams, or threads) race and must be serialised by the caller.
+// Nothing in it needs to start at zero -- a split launch writes every partial it later
+// reads -- so the last call's contents are simply overwritten.
+#include <hip/hip_runtime.h>
+
+#include <mutex>
+#include <string>
+
+#include "../../include/t81_hip.h"
+#include "t81_kernels.hpp"
+
+namespace {
+
+constexpr int64_t kScratchBytes = int64_t{64} << 20;   // 64 MiB
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::once_flag g_once[kMaxDevices];
+void *g_scratch[kMaxDevices];
+hipError_t g_lookup[kMaxDevices];
+
+// The current device's address of `scratch` (looked up on the first call per device).
+int scratch_address(void **out) {
+    int dev = 0;
+    const hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess)
+        return t81hip::report_error(T81_HIP_EHIP, (std::string("t81_hip_ternary_matmul_noalloc: ") +
+                                                   hipGetErrorString(e)).c_str());
+    if (dev < 0 || dev >= kMaxDevices)
+        return t81hip::report_error(T81_HIP_ENODEV, "device index out of range");
+    std::call_once(g_once[dev], [dev] {
+        g_lookup[dev] = hipGetSymbolAddress(&g_scratch[dev], HIP_SYMBOL(scratch));
+    });
+    if (g_lookup[dev] != hipSuccess)
+        return t81hip::report_error(
+            T81_HIP_EHIP, (std::string("t81_hip_ternary_matmul_noalloc: scratch lookup: ") +
+                           hipGetErrorString(g_lookup[dev])).c_str());
+    *out = g_scratch[dev];
+    return T81_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int t81_hip_ternary_matmul_noalloc(int which, const void *x, int x_dtype, const uint8_t *w,
+                                   void *c, int64_t m, int64_t n, int64_t k, float alpha,
+                                   float beta, const float *bias, void *stream) {
+    // Same workspace as t81_hip_ternary_matmul_ws is given by its callers (exactly
+    // t81_hip_ternary_matmul_workspace_size bytes), so the split plan -- and with it the
+    // order of every sum -- is the same, and so are the results, bit for bit.
+    const bool gemv = which == 2 || (which == 0 && m <= 16);
+    const int64_t need = gemv ? 0 : t81_hip_ternary_matmul_workspace_size(m, n, k, x_dtype);
+    if (need > kScratchBytes)
+        return t81hip::report_error(
+            T81_HIP_EINVAL_SHAPE,
+            ("t81_hip_ternary_matmul_noalloc: this shape splits K over " + std::to_string(need) +
+             " bytes of workspace, more than the " + std::to_string(kScratchBytes) +
+             "-byte static scratch; use t81_hip_ternary_matmul_ws")
+                .c_str());
+    void *ws = nullptr;
+    if (need > 0) {
+        if (int rc = scratch_address(&ws)) return rc;
+    }
+    return t81_hip_ternary_matmul_ws(which, x, x_dtype, w, c, m, n, k, alpha, beta, bias, ws,
+                                     need, stream);
+}
+
+}  // extern "C"

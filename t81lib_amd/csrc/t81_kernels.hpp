@@ -13,6 +13,9 @@ constexpr int kDtypeBF16 = 1;
 constexpr int kDtypeI8 = 2;
 constexpr int kDtypeF16 = 3;
 
+// abi.hip: records msg as the calling thread's last error and returns code
+int report_error(int code, const char *msg);
+
 // pack.hip
 hipError_t launch_quantize_pack_rows(const void *w, int dtype, uint8_t *out, int64_t rows,
                                      int64_t cols, float thr, int torch_form, hipStream_t s);

@@ -1,0 +1,102 @@
+"""t81_hip_ternary_matmul_noalloc: the trit-dot matmul with its split-K workspace in the
+library's static device scratch, called through the C ABI and compared with
+t81_hip_ternary_matmul_ws given a workspace of exactly the size it asks for -- same
+kernels and split plan, so the outputs must agree bit for bit -- on two calls in a row,
+the second on a smaller input, for each activation type that splits."""
+
+from __future__ import annotations
+
+import sys
+
+import pytest
+import torch
+
+from t81lib_amd import _lib, ops
+
+pytestmark = pytest.mark.gpu
+
+SCRATCH = 64 << 20
+
+
+def announce(case: str) -> None:
+    sys.__stderr__.write(f"[gpu case] {case}\n")
+    sys.__stderr__.flush()
+
+
+def _problem(gpu, M, N, K, dtype, seed):
+    g = torch.Generator("cpu").manual_seed(seed)
+    packed = ops.quantize_pack(torch.randn((N, K), generator=g).to(gpu), 0.45, _lib.THR_CPP)
+    if dtype == torch.int8:
+        x = torch.randint(-128, 128, (M, K), generator=g, dtype=torch.int8)
+        c = torch.randint(-1000, 1000, (M, N), generator=g, dtype=torch.int32)
+        bias, alpha, beta = None, 1.0, 1.0
+    else:
+        x = torch.randn((M, K), generator=g).to(dtype)
+        c = torch.randn((M, N), generator=g)
+        bias, alpha, beta = torch.randn((N,), generator=g).to(gpu), 0.75, 0.5
+    return x.to(gpu), packed, c.to(gpu), bias, alpha, beta
+
+
+def _code(dtype):
+    return {torch.bfloat16: _lib.DTYPE_BF16, torch.float32: _lib.DTYPE_F32,
+            torch.int8: _lib.DTYPE_I8}[dtype]
+
+
+def _run_pair(gpu, M, N, K, dtype, seed):
+    """(noalloc output, _ws output, workspace bytes) for one problem."""
+    lib = _lib.lib()
+    x, packed, c, bias, alpha, beta = _problem(gpu, M, N, K, dtype, seed)
+    code = _code(dtype)
+    need = lib.t81_hip_ternary_matmul_workspace_size(M, N, K, code)
+    s = torch.cuda.current_stream().cuda_stream
+    bptr = bias.data_ptr() if bias is not None else None
+    c_ws = c.clone()
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device=gpu)
+    _lib.check(lib.t81_hip_ternary_matmul_ws(0, x.data_ptr(), code, packed.data_ptr(),
+                                             c_ws.data_ptr(), M, N, K, alpha, beta, bptr,
+                                             ws.data_ptr() if need > 0 else None, need, s))
+    c_na = c.clone()
+    _lib.check(lib.t81_hip_ternary_matmul_noalloc(0, x.data_ptr(), code, packed.data_ptr(),
+                                                  c_na.data_ptr(), M, N, K, alpha, beta, bptr, s))
+    torch.cuda.synchronize()
+    return c_na, c_ws, need
+
+
+@pytest.mark.parametrize("dtype,shapes", [
+    # bf16: whole big tiles + split-K items in one launch (Llama gate_up at M = 2048, the
+    # full 64 MiB), then every tile split (qkv at M = 512), then a smaller split shape
+    (torch.bfloat16, [(2048, 28672, 4096), (512, 6144, 4096), (300, 1000, 4104)]),
+    # int8 and float32: eight-wave splits of few tiles (int32 partials exact for int8)
+    (torch.int8, [(20, 3000, 9000), (20, 1200, 4000)]),
+    (torch.float32, [(48, 1000, 4104), (40, 700, 2000)]),
+])
+def test_noalloc_matches_workspace_entry_point(gpu, dtype, shapes):
+    for i, (M, N, K) in enumerate(shapes):
+        announce(f"noalloc {dtype} call {i + 1} M={M} N={N} K={K}")
+        c_na, c_ws, need = _run_pair(gpu, M, N, K, dtype, seed=M + N + K)
+        assert 0 < need <= SCRATCH, f"shape expected to split within the scratch ({need} B)"
+        assert torch.equal(c_na.view(torch.int32), c_ws.view(torch.int32)), \
+            f"call {i + 1}: {int((c_na != c_ws).sum())} outputs differ"
+
+
+def test_noalloc_without_split_and_rejection(gpu):
+    lib = _lib.lib()
+    announce("noalloc K2 and unsplit K3")
+    for M, N, K in ((4, 300, 4096), (2048, 8192, 1024)):
+        c_na, c_ws, need = _run_pair(gpu, M, N, K, torch.bfloat16, seed=M)
+        assert need == 0
+        assert torch.equal(c_na, c_ws)
+    # a shape whose split needs more than the scratch is refused before any launch
+    announce("noalloc rejection")
+    M, K = 512, 4096
+    N = next(n for n in range(6144, 256 * 160, 256)
+             if lib.t81_hip_ternary_matmul_workspace_size(M, n, K, _lib.DTYPE_BF16) > SCRATCH)
+    x, packed, c, bias, alpha, beta = _problem(gpu, M, N, K, torch.bfloat16, seed=5)
+    before = c.clone()
+    rc = lib.t81_hip_ternary_matmul_noalloc(0, x.data_ptr(), _lib.DTYPE_BF16, packed.data_ptr(),
+                                            c.data_ptr(), M, N, K, alpha, beta, bias.data_ptr(),
+                                            torch.cuda.current_stream().cuda_stream)
+    assert rc == _lib.EINVAL_SHAPE
+    assert "static scratch" in _lib.last_error()
+    torch.cuda.synchronize()
+    assert torch.equal(c, before)
