@@ -55,74 +55,226 @@ def make_weights(torch, ops, lib, n: int, k: int, copies: int, dev, seed: int):
     return out
 
 
-def time_graph(torch, launch, buffers, steps: int, warmup: int) -> float:
-    """Captures one launch per buffer into a graph, replays it; returns ms per launch."""
+def _capture(torch, launch, items, stream):
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for b in items:
+            launch(b)
+    return graph
+
+
+def time_graph(torch, launch, buffers, steps: int, warmup: int, dist: bool = False,
+               min_launches: int = 100, min_ms: float = 50.0):
+    """Times exactly `steps` launches of `launch`, rotating through `buffers`, captured in
+    HIP graphs so the GPU runs them back to back on one stream: a graph of one launch per
+    buffer (replayed steps // len(buffers) times) plus one of the remaining launches.
+    `warmup` untimed launches (whole rotations) run first, then a synchronisation, then one
+    more untimed rotation ahead of the start event; the timed region ends with a
+    synchronisation and is timed with HIP events on the launch stream.  Returns ms per
+    launch; with dist=True a dict that adds the spread: each replay of the rotation graph
+    timed on its own, over at least `min_launches` launches and `min_ms` of GPU time
+    (median / p10 / p90 of the per-launch time)."""
+    import numpy as np
+
+    steps = max(1, int(steps))
+    n = len(buffers)
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):
-        for i in range(min(warmup, len(buffers)) or 1):
-            launch(buffers[i % len(buffers)])
+        for i in range(min(max(warmup, 1), n)):   # eager warm-up outside any capture
+            launch(buffers[i])
     torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=stream):
-        for b in buffers:
-            launch(b)
+    full = _capture(torch, launch, buffers, stream)
+    rest = _capture(torch, launch, buffers[: steps % n], stream) if steps % n else None
     torch.cuda.synchronize()
-    reps = max(1, -(-steps // len(buffers)))
-    for _ in range(max(1, warmup // len(buffers))):
-        graph.replay()
+    for _ in range(-(-warmup // n)):
+        full.replay()
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(stream):
+        # one untimed rotation ahead of the start event keeps the GPU busy while the host
+        # submits the timed graphs, so the region holds the K launches back to back and
+        # not the host's graph-launch latency
+        full.replay()
         start.record(stream)
-        for _ in range(reps):
-            graph.replay()
+        for _ in range(steps // n):
+            full.replay()
+        if rest is not None:
+            rest.replay()
         end.record(stream)
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / (reps * len(buffers))
+    ms = start.elapsed_time(end) / steps
+    if not dist:
+        return ms
+    reps = max(3, -(-min_launches // n), int(np.ceil(min_ms / max(ms * n, 1e-6))))
+    events = []
+    with torch.cuda.stream(stream):
+        for _ in range(reps):
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            full.replay()
+            b.record(stream)
+            events.append((a, b))
+    torch.cuda.synchronize()
+    per = np.array([a.elapsed_time(b) / n for a, b in events])
+    return {"ms": ms, "timed_launches": steps, "mean_ms": float(per.mean()),
+            "median_ms": float(np.median(per)), "p10_ms": float(np.percentile(per, 10)),
+            "p90_ms": float(np.percentile(per, 90)), "samples": reps,
+            "launches_per_sample": n}
 
 
-def cpu_reference_gemv(n: int, k: int, budget_s: float):
-    """Reference gemm_ternary (the compiled reference CPU path) on the same GEMV workload:
-    W (n x L limbs) times one packed activation column, timed over row blocks until
-    `budget_s` has elapsed or all rows are done.  Returns (GB/s of packed weights, detail)."""
+def spread_us(d: dict) -> dict:
+    """The spread of a time_graph(dist=True) result, in microseconds."""
+    return {"median_us": d["median_ms"] * 1e3, "p10_us": d["p10_ms"] * 1e3,
+            "p90_us": d["p90_ms"] * 1e3, "mean_us": d["mean_ms"] * 1e3,
+            "samples": d["samples"], "launches_per_sample": d["launches_per_sample"]}
+
+
+def sha256_tensors(torch, *tensors) -> str:
+    """SHA-256 over the bytes of the given (device or host) tensors, in order."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for t in tensors:
+        h.update(t.detach().contiguous().view(-1).view(torch.uint8).cpu().numpy().tobytes())
+    return h.hexdigest()
+
+
+def cpu_threads() -> int:
+    """Host threads for the all-core CPU baselines: the cores this process may use, at most
+    16 (a GPU box's CPU share per GPU)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def _reference_lib():
+    """(library, kind): the reference's own compiled CPU path (oracle/_ref), else the
+    oracle's C restatement."""
+    import oracle
+
+    ref = oracle.ref()
+    if ref is None:
+        ref = oracle.ref("generic")
+    return (ref, "reference") if ref is not None else (None, "port")
+
+
+def cpu_limb_gemm(wp, xp, n_tok: int, k: int, budget_s: float, threads: int = 1) -> dict:
+    """The reference CPU gemm_ternary (oracle/_ref: gemm_ternary_cpu_impl compiled from the
+    reference's sources; the oracle's C restatement where that is not built) over weight
+    rows wp (rows x L x 16) times the packed activation columns xp (L x n_tok x 16), in
+    blocks of 16 rows spread over `threads` host threads (ctypes releases the GIL, so the
+    blocks run in parallel), until every row is done or `budget_s` has passed.  Returns
+    rows done, seconds and limb products per second."""
+    import threading
+
     import numpy as np
 
     import oracle
 
-    ref = oracle.ref()
-    kind = "reference"
-    if ref is None:
-        ref = oracle.ref("generic")
-    if ref is None:
-        kind = "port"
-    rng = np.random.default_rng(0)
-    limbs = (k + 47) // 48
-    w = rng.standard_normal((n, k)).astype(np.float32)
-    wp = oracle.pack_rows(w, 0.45, 0)                                   # (n, L, 16)
-    x = rng.standard_normal((1, k)).astype(np.float32)
-    xp = oracle.pack_cols(x, np.float32(oracle.torch_threshold(0.5)), 1)  # (L, 1, 16)
-    c = np.zeros((n, 1), np.float32)
-    block = 256
-    rows_done = 0
+    ref, kind = _reference_lib()
+    rows = wp.shape[0]
+    limbs = wp.shape[1]
+    c = np.zeros((rows, n_tok), np.float32)
+    block = 16
+    nxt = [0]
+    done = [0]
+    lock = threading.Lock()
     t0 = time.perf_counter()
-    while rows_done < n and time.perf_counter() - t0 < budget_s:
-        r1 = min(n, rows_done + block)
-        if kind == "reference":
-            ref.gemm_ternary_rows(wp, xp, c, n, 1, limbs * 48, rows_done, r1)
-        else:
-            c[rows_done:r1] = oracle.gemm_limb(wp[rows_done:r1], xp, c[rows_done:r1],
-                                               r1 - rows_done, 1, limbs * 48)
-        rows_done = r1
+
+    def worker():
+        while True:
+            with lock:
+                if nxt[0] >= rows or time.perf_counter() - t0 >= budget_s:
+                    return
+                r0 = nxt[0]
+                nxt[0] = min(rows, r0 + block)
+            r1 = min(rows, r0 + block)
+            if kind == "reference":
+                ref.gemm_ternary_rows(wp, xp, c, rows, n_tok, limbs * 48, r0, r1)
+            else:
+                c[r0:r1] = oracle.gemm_limb(wp[r0:r1], xp, c[r0:r1], r1 - r0, n_tok, limbs * 48)
+            with lock:
+                done[0] += r1 - r0
+
+    pool = [threading.Thread(target=worker) for _ in range(threads)]
+    for t in pool:
+        t.start()
+    for t in pool:
+        t.join()
     dt = time.perf_counter() - t0
-    nbytes = 16 * rows_done * limbs
-    variant = ref.variant if kind == "reference" else "oracle C restatement"
-    simd = ref.simd_path() if kind == "reference" else "scalar"
-    return nbytes / dt / 1e9, {
-        "kind": kind, "rows": rows_done, "seconds": dt, "limb_products": rows_done * limbs,
-        "variant": variant, "simd": simd,
-    }
+    products = done[0] * limbs * n_tok
+    return {"kind": kind, "rows": done[0], "seconds": dt, "limb_products": products,
+            "limb_products_per_s": products / dt, "threads": threads,
+            "variant": ref.variant if kind == "reference" else "oracle C restatement",
+            "simd": ref.simd_path() if kind == "reference" else "scalar"}
+
+
+def _gemv_inputs(n: int, k: int, n_tok: int, seed: int):
+    import numpy as np
+
+    import oracle
+
+    rng = np.random.default_rng(seed)
+    w = rng.standard_normal((n, k)).astype(np.float32)
+    wp = oracle.pack_rows(w, 0.45, 0)                                       # (n, L, 16)
+    x = rng.standard_normal((n_tok, k)).astype(np.float32)
+    xp = oracle.pack_cols(x, np.float32(oracle.torch_threshold(0.5)), 1)    # (L, n_tok, 16)
+    return wp, xp
+
+
+def cpu_reference_gemv(n: int, k: int, budget_s: float, threads: int = 1):
+    """The GEMV workload (W n x L limbs times one packed activation column) on the
+    reference CPU path.  Returns (GB/s of packed weights streamed, detail)."""
+    wp, xp = _gemv_inputs(n, k, 1, seed=0)
+    d = cpu_limb_gemm(wp, xp, 1, k, budget_s, threads)
+    limbs = wp.shape[1]
+    return 16 * d["rows"] * limbs / d["seconds"] / 1e9, d
+
+
+def cpu_reference_gemm(m: int, n: int, k: int, rows: int, tokens: int, budget_s: float,
+                       threads: int = 1):
+    """The prefill GEMM workload sampled: `rows` weight rows x `tokens` activation columns
+    of the m x n x k problem on the reference CPU path, extrapolated linearly in
+    m * n * L limb products.  Returns (TFLOP/s-equivalent of the full GEMM, detail)."""
+    wp, xp = _gemv_inputs(rows, k, tokens, seed=1)
+    d = cpu_limb_gemm(wp, xp, tokens, k, budget_s, threads)
+    limbs = wp.shape[1]
+    full_s = m * n * limbs / d["limb_products_per_s"]
+    d["extrapolated_full_s"] = full_s
+    return 2.0 * m * n * k / full_s / 1e12, d
+
+
+def cpu_pack(rows: int, cols: int, threads: int = 1, reps: int = 3):
+    """K1's workload on the CPU: the oracle's single-thread restatement of
+    pack_dense_matrix (python/bindings.cpp:497-515) over a rows x cols float32 matrix,
+    split into row blocks over `threads` threads; median of `reps` runs.  Returns
+    (GB/s of algorithmic bytes, seconds)."""
+    import threading
+
+    import numpy as np
+
+    import oracle
+
+    w = (np.random.default_rng(2).standard_normal((rows, cols)) * 0.02).astype(np.float32)
+    bounds = np.linspace(0, rows, threads + 1).astype(int)
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        pool = [threading.Thread(target=oracle.pack_rows, args=(w[a:b], 0.45, 0))
+                for a, b in zip(bounds[:-1], bounds[1:])]
+        for t in pool:
+            t.start()
+        for t in pool:
+            t.join()
+        times.append(time.perf_counter() - t0)
+    sec = float(np.median(times))
+    nbytes = 4 * rows * cols + 16 * rows * ((cols + 47) // 48)
+    return nbytes / sec / 1e9, sec
 
 
 # ------------------------------------------------------- config 5: decoder stack --
@@ -613,13 +765,17 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=12.0,
                     help="seconds of single-core reference CPU work for the baseline")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["gemv", "gemm", "pack", "copy", "spmm", "launch", "stack"],
+    ap.add_argument("--only", choices=["gemv", "gemm", "pack", "copy", "read", "spmm", "launch",
+                                       "stack"],
                     default=None,
                     help="time one kernel only (for profiling runs); 'copy' times a plain "
                          "elementwise copy of the GEMV weight size, the calibration kernel "
-                         "for the HBM byte counters; 'launch' times a one-element fill, the "
+                         "for the HBM byte counters; 'read' a plain reduction over the GEMV "
+                         "weight copies (the read floor); 'launch' a one-element fill, the "
                          "per-launch floor of a graph of back-to-back kernels; 'stack' runs "
                          "config 5, the 32-layer decoder, prefill + greedy decode tokens/s")
+    ap.add_argument("--no-stack", action="store_true",
+                    help="skip config 5 (the decoder stack) in the default run")
     ap.add_argument("--sweep", action="store_true",
                     help="also time the config-3/4 shapes and print a table on stderr")
     ap.add_argument("--summarize-trace", metavar="DIR",
@@ -659,98 +815,163 @@ def main() -> int:
         return 1
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    result: dict = {}
+    only = args.only
+    threads = cpu_threads()
 
     # ---------------------------------------------------------- K2 decode GEMV --
     M, K, N = 1, 4096, 14336
     wbytes = 16 * N * ((K + 47) // 48)
     copies = max(8, -(-2 * MALL_BYTES // wbytes) + 4)
-    gemv_ms = None
-    if args.only in (None, "gemv"):
+    gemv = None
+    floors: dict = {}
+    if only in (None, "gemv", "read", "copy", "launch"):
         log(f"GEMV {K}->{N} M={M}: {copies} weight copies of {wbytes / 1e6:.1f} MB")
         wbufs = make_weights(torch, ops, _lib, N, K, copies, dev, seed=1)
         x = torch.randn((M, K), device=dev).to(torch.bfloat16)
-        out = torch.empty((M, N), device=dev)
-        launch = lambda wb: ops.ternary_matmul(x, wb, K, c=out, kernel=2)  # noqa: E731
-        gemv_ms = time_graph(torch, launch, wbufs, args.steps, args.warmup)
+        if only in (None, "gemv"):
+            out = torch.empty((M, N), device=dev)
+            launch = lambda wb: ops.ternary_matmul(x, wb, K, c=out, kernel=2)  # noqa: E731
+            gemv = time_graph(torch, launch, wbufs, args.steps, args.warmup, dist=True)
+            gemv["sha256"] = sha256_tensors(torch, wbufs[0], x)
+            log(f"GEMV {gemv['ms'] * 1e3:.2f} us/call over {args.steps} calls "
+                f"(median {gemv['median_ms'] * 1e3:.2f}, p10 {gemv['p10_ms'] * 1e3:.2f}, "
+                f"p90 {gemv['p90_ms'] * 1e3:.2f})")
+        if only in (None, "read"):
+            # the read floor: a plain coalesced streaming read of the same weight copies
+            # (csrc/floors.hip), best of four grid sizes
+            import ctypes
+
+            flib = ctypes.CDLL(os.path.join(ROOT, "t81lib_amd", "libt81_floors.so"))
+            flib.t81_floor_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+                                            ctypes.c_int, ctypes.c_void_p]
+            sink = torch.empty(8192, dtype=torch.int32, device=dev)
+            best = None
+            for blocks in (256, 512, 1024, 2048, 4096):
+                def rd(wb, blocks=blocks):
+                    rc = flib.t81_floor_read(wb.data_ptr(), wbytes, sink.data_ptr(), blocks,
+                                             torch.cuda.current_stream().cuda_stream)
+                    if rc != 0:
+                        raise RuntimeError(f"t81_floor_read failed ({rc})")
+                r = time_graph(torch, rd, wbufs, max(args.steps, 256), 32, dist=True)
+                if best is None or r["median_ms"] < best[1]["median_ms"]:
+                    best = (blocks, r)
+            blocks, r = best
+            floors["read"] = {"workload": f"plain coalesced read of one {wbytes}-byte weight "
+                                          f"copy (16-byte loads, {blocks} workgroups of 256, "
+                                          f"best of 256-4096), {copies} rotating copies",
+                              "us": r["median_ms"] * 1e3,
+                              "GBps": wbytes / (r["median_ms"] * 1e-3) / 1e9, **spread_us(r)}
+            log(f"read floor {floors['read']['us']:.2f} us/launch, "
+                f"{floors['read']['GBps']:.0f} GB/s ({blocks} workgroups)")
+        if only in (None, "copy"):
+            # counter calibration and the measured copy bandwidth (read + write)
+            elems = wbytes // 4
+            ccopies = max(4, -(-2 * MALL_BYTES // wbytes) + 2)
+            csrc = [torch.randn(elems, device=dev) for _ in range(ccopies)]
+            cdst = torch.empty(elems, device=dev)
+            cp = time_graph(torch, lambda t: torch.neg(t, out=cdst), csrc,  # noqa: E731
+                            max(args.steps, 256), 32, dist=True)
+            floors["copy"] = {"workload": f"torch.neg fp32, {elems} elements: reads and writes "
+                                          f"{4 * elems} bytes per launch",
+                              "bytes_read": 4 * elems, "bytes_written": 4 * elems,
+                              "us": cp["median_ms"] * 1e3,
+                              "GBps": 8 * elems / (cp["median_ms"] * 1e-3) / 1e9,
+                              **spread_us(cp)}
+            del csrc, cdst
+            log(f"copy {floors['copy']['us']:.2f} us/launch, {floors['copy']['GBps']:.0f} GB/s")
+        if only in (None, "launch"):
+            tiny = [torch.zeros(1, device=dev) for _ in range(32)]
+            lf = time_graph(torch, lambda t: t.fill_(1.0), tiny, max(args.steps, 256), 32,  # noqa
+                            dist=True)
+            floors["launch"] = {"workload": "graph of one-element torch fill_ launches",
+                                "us": lf["median_ms"] * 1e3, **spread_us(lf)}
+            log(f"launch floor {floors['launch']['us']:.2f} us/launch")
         del wbufs
         torch.cuda.empty_cache()
-        log(f"GEMV {gemv_ms * 1e3:.2f} us/call")
 
     # --------------------------------------------------------- K3 prefill GEMM --
     GM, GK, GN = 2048, 4096, 28672
-    gemm_ms = None
-    if args.only in (None, "gemm"):
+    gemm = None
+    if only in (None, "gemm"):
         log(f"GEMM M={GM} {GK}->{GN}")
         gw = make_weights(torch, ops, _lib, GN, GK, 2, dev, seed=2)
         gx = torch.randn((GM, GK), device=dev).to(torch.bfloat16)
         gout = torch.empty((GM, GN), device=dev)
         glaunch = lambda wb: ops.ternary_matmul(gx, wb, GK, c=gout, kernel=3)  # noqa: E731
-        gsteps = max(4, min(64, args.steps // 32))
-        gemm_ms = time_graph(torch, glaunch, gw, gsteps, 4)
+        # exactly 100 timed launches (and >= 50 ms of spread samples) whatever --steps is,
+        # after 20 untimed ones that bring the clocks to their loaded state
+        gemm = time_graph(torch, glaunch, gw, 100, 20, dist=True)
+        gemm["sha256"] = sha256_tensors(torch, gw[0], gx)
         del gw, gx, gout
         torch.cuda.empty_cache()
-        log(f"GEMM {gemm_ms:.3f} ms/call")
+        log(f"GEMM {gemm['ms']:.3f} ms/call over 100 calls (median {gemm['median_ms']:.3f})")
 
     # ------------------------------------------------------------- K1 pack --
     PR, PC = 8192, 3072
-    pack_ms = None
-    if args.only in (None, "pack"):
+    pack = None
+    if only in (None, "pack"):
         pbytes = 4 * PR * PC + 16 * PR * ((PC + 47) // 48)
         pcopies = max(4, -(-2 * MALL_BYTES // pbytes) + 2)
         srcs = [torch.randn((PR, PC), device=dev) * 0.02 for _ in range(pcopies)]
         pout = torch.empty((PR, (PC + 47) // 48, 16), dtype=torch.uint8, device=dev)
         plaunch = lambda s: ops.quantize_pack(s, 0.45, _lib.THR_CPP, out=pout)  # noqa: E731
-        pack_ms = time_graph(torch, plaunch, srcs, max(64, args.steps // 8), 8)
+        pack = time_graph(torch, plaunch, srcs, max(128, args.steps // 8), 8, dist=True)
+        pack["sha256"] = sha256_tensors(torch, srcs[0])
         del srcs
         torch.cuda.empty_cache()
-        log(f"pack {pack_ms * 1e3:.2f} us/call")
+        log(f"pack {pack['ms'] * 1e3:.2f} us/call")
 
-    # ------------------------------------------------- copy (counter calibration) --
-    copy = None
-    if args.only == "copy":
-        elems = wbytes // 4
-        ccopies = max(4, -(-2 * MALL_BYTES // wbytes) + 2)
-        csrc = [torch.randn(elems, device=dev) for _ in range(ccopies)]
-        cdst = torch.empty(elems, device=dev)
-        claunch = lambda s: torch.neg(s, out=cdst)  # noqa: E731
-        copy_ms = time_graph(torch, claunch, csrc, args.steps, args.warmup)
-        del csrc
-        torch.cuda.empty_cache()
-        copy = {"workload": f"torch.neg fp32, {elems} elements: reads and writes "
-                            f"{4 * elems} bytes per launch",
-                "bytes_read": 4 * elems, "bytes_written": 4 * elems, "us": copy_ms * 1e3,
-                "GBps": 8 * elems / (copy_ms * 1e-3) / 1e9}
-        log(f"copy {copy_ms * 1e3:.2f} us/call, {copy['GBps']:.0f} GB/s read+write")
-
-    # ------------------------------------------------ launch floor (one-element fill) --
-    launch_floor = None
-    if args.only == "launch":
-        tiny = [torch.zeros(1, device=dev) for _ in range(32)]
-        lf_ms = time_graph(torch, lambda t: t.fill_(1.0), tiny, args.steps, args.warmup)
-        launch_floor = {"workload": "graph of one-element torch fill_ launches", "us": lf_ms * 1e3,
-                        "gemv_bytes_at_8TBps_us": gemv_bytes(M, N, K) / HBM_PEAK_GBPS / 1e3}
-        log(f"launch floor {lf_ms * 1e3:.2f} us/launch")
-
-    # ------------------------------------------------------------ CPU baseline --
+    # ------------------------------------------------------------ CPU baselines --
     cpu = None
-    if not args.no_cpu and args.only is None:
-        log("reference CPU gemm_ternary on the GEMV workload (1 core)")
-        gbps, detail = cpu_reference_gemv(N, K, args.cpu_budget)
+    if not args.no_cpu and only is None:
+        budget = args.cpu_budget
+        log(f"CPU baselines: reference gemm_ternary and pack, 1 and {threads} threads")
+        g1, d1 = cpu_reference_gemv(N, K, 0.35 * budget, 1)
+        ga, da = cpu_reference_gemv(N, K, 0.1 * budget, threads)
+        host = f"host {cpu_model()}, nproc {os.cpu_count()}"
         cpu = {
-            "value": gbps, "unit": "GB/s", "cores": 1, "kind": detail["kind"],
-            "sample": (f"reference gemm_ternary_cpu_impl ({detail['variant']}, SIMD "
-                       f"{detail['simd']}) on {detail['rows']} of {N} weight rows x "
-                       f"{(K + 47) // 48} limbs x 1 packed activation column = "
-                       f"{detail['limb_products']} limb products in {detail['seconds']:.2f} s; "
-                       f"GB/s of packed weights streamed; host {cpu_model()}, "
-                       f"nproc {os.cpu_count()}"),
+            "value": g1, "unit": "GB/s", "cores": 1, "kind": d1["kind"],
+            "sample": (f"reference gemm_ternary_cpu_impl ({d1['variant']}, SIMD {d1['simd']}) "
+                       f"on {d1['rows']} of {N} weight rows x {(K + 47) // 48} limbs x 1 packed "
+                       f"activation column = {d1['limb_products']} limb products in "
+                       f"{d1['seconds']:.2f} s; GB/s of packed weights streamed; {host}"),
+            "all_cores": {"value": ga, "unit": "GB/s", "cores": threads, "kind": da["kind"],
+                          "sample": f"same kernel over {da['rows']} rows in 16-row blocks on "
+                                    f"{threads} threads, {da['seconds']:.2f} s"},
         }
+        if gemm is not None:
+            t1, e1 = cpu_reference_gemm(GM, GN, GK, 256, 64, 0.3 * budget, 1)
+            ta, ea = cpu_reference_gemm(GM, GN, GK, 1024, 64, 0.1 * budget, threads)
+            gemm["cpu_baseline"] = {
+                "value": t1, "unit": "TFLOP/s-equivalent", "cores": 1, "kind": e1["kind"],
+                "sample": (f"reference gemm_ternary_cpu_impl on {e1['rows']} weight rows x 64 "
+                           f"packed activation columns x {(GK + 47) // 48} limbs "
+                           f"({e1['limb_products']} limb products, {e1['seconds']:.2f} s), "
+                           f"extrapolated linearly in M*N*L to {GM}x{GN}x{GK}: "
+                           f"{e1['extrapolated_full_s']:.0f} s; 2*M*N*K flops"),
+                "all_cores": {"value": ta, "unit": "TFLOP/s-equivalent", "cores": threads,
+                              "kind": ea["kind"],
+                              "sample": f"{ea['rows']} rows x 64 columns on {threads} threads, "
+                                        f"extrapolated: {ea['extrapolated_full_s']:.0f} s"},
+            }
+        if pack is not None:
+            p1, s1 = cpu_pack(PR, PC, 1)
+            pa, sa = cpu_pack(PR, PC, threads)
+            pack["cpu_baseline"] = {
+                "value": p1, "unit": "GB/s", "cores": 1, "kind": "port",
+                "sample": (f"the oracle's C restatement of pack_dense_matrix "
+                           f"(python/bindings.cpp:497-515) on the full {PR}x{PC} float32 matrix, "
+                           f"median of 3: {s1 * 1e3:.1f} ms"),
+                "all_cores": {"value": pa, "unit": "GB/s", "cores": threads, "kind": "port",
+                              "sample": f"row blocks on {threads} threads, {sa * 1e3:.1f} ms"},
+            }
 
     sweep = run_sweep(torch, ops, _lib, dev) if args.sweep else None
-    spmm = run_spmm(torch, dev) if args.only == "spmm" else None
-    stack = run_stack(torch, dev) if args.only == "stack" else None
+    spmm = run_spmm(torch, dev) if only == "spmm" else None
+    stack = run_stack(torch, dev) if only == "stack" or (only is None and not args.no_stack) \
+        else None
 
+    gemv_ms = gemv["ms"] if gemv else None
     gbytes = gemv_bytes(M, N, K)
     line: dict = {
         "metric": METRIC,
@@ -774,28 +995,39 @@ def main() -> int:
         line["roofline"] = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS,
                             "unit": "GB/s", "frac": achieved / HBM_PEAK_GBPS,
                             "traffic": read_traffic()}
+        if "copy" in floors:
+            line["roofline"]["measured_copy_GBps"] = floors["copy"]["GBps"]
+            line["roofline"]["frac_of_measured_copy"] = achieved / floors["copy"]["GBps"]
+        line["timing"] = {**spread_us(gemv), "timed_launches": gemv["timed_launches"]}
         line["tokens_per_s_equiv"] = M / (gemv_ms * 1e-3)
+        line["inputs_sha256"] = gemv["sha256"]
     if cpu:
         line["cpu_baseline"] = cpu
-    if gemm_ms:
+    if gemm:
         flops = 2.0 * GM * GN * GK
-        tflops = flops / (gemm_ms * 1e-3) / 1e12
+        tflops = flops / (gemm["ms"] * 1e-3) / 1e12
         line["gemm"] = {
             "workload": f"prefill GEMM K3, M={GM}, {GK}->{GN} (Llama-3-8B gate_up), bf16 x",
-            "ms": gemm_ms, "tflops": tflops, "tokens_per_s_equiv": GM / (gemm_ms * 1e-3),
+            "ms": gemm["ms"], "timed_launches": gemm["timed_launches"], "tflops": tflops,
+            "tokens_per_s_equiv": GM / (gemm["ms"] * 1e-3),
             "roofline": {"bound": "mfma", "achieved": tflops, "peak": BF16_PEAK_TFLOPS,
                          "unit": "TFLOP/s", "frac": tflops / BF16_PEAK_TFLOPS},
+            "timing": spread_us(gemm), "inputs_sha256": gemm["sha256"],
         }
-    if pack_ms:
+        if "cpu_baseline" in gemm:
+            line["gemm"]["cpu_baseline"] = gemm["cpu_baseline"]
+    if pack:
         pbytes = 4 * PR * PC + 16 * PR * ((PC + 47) // 48)
-        gbs = pbytes / (pack_ms * 1e-3) / 1e9
-        line["pack"] = {"workload": f"K1 quantize+pack {PR}x{PC} fp32", "us": pack_ms * 1e3,
+        gbs = pbytes / (pack["ms"] * 1e-3) / 1e9
+        line["pack"] = {"workload": f"K1 quantize+pack {PR}x{PC} fp32", "us": pack["ms"] * 1e3,
+                        "timed_launches": pack["timed_launches"],
                         "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBPS,
-                                     "unit": "GB/s", "frac": gbs / HBM_PEAK_GBPS}}
-    if copy:
-        line["copy"] = copy
-    if launch_floor:
-        line["launch_floor"] = launch_floor
+                                     "unit": "GB/s", "frac": gbs / HBM_PEAK_GBPS},
+                        "timing": spread_us(pack), "inputs_sha256": pack["sha256"]}
+        if "cpu_baseline" in pack:
+            line["pack"]["cpu_baseline"] = pack["cpu_baseline"]
+    if floors:
+        line["floors"] = floors
     if sweep:
         line["sweep"] = sweep
     if spmm:

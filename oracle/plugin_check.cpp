@@ -9,8 +9,11 @@
 // now routes to Backend::ROCm, i.e. the plugin), detail::gemm_ternary on
 // TensorMetadata (gemm_dispatch.cpp:325-344) and detail::where / clamp / lerp /
 // addcmul (gemm_dispatch.cpp:239-322) -- and compares every result bit for bit
-// with the same call forced to Backend::CPU.  Prints one line per check; exit
-// status 0 only if all match.
+// with the same call forced to Backend::CPU.  It also checks the plugin's trit-dot
+// overload of gemm_ternary (t81lib_amd/plugin/t81_rocm_trit.hpp), which the reference
+// lacks, against a trit-by-trit sum over limb::to_trits of the same packed weights:
+// integer-valued activations make every sum exact, so those results must be exact too.
+// Prints one line per check; exit status 0 only if all match.
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -20,9 +23,16 @@
 #include <span>
 #include <vector>
 
+#include <hip/hip_runtime_api.h>
+
+#include <stdexcept>
+#include <string>
+
 #include <t81/linalg/gemm.hpp>
 #include <t81/linalg/gemm_gpu.hpp>
 #include <t81/tensor_metadata.hpp>
+
+#include "../t81lib_amd/plugin/t81_rocm_trit.hpp"
 
 using t81::core::limb;
 namespace ld = t81::linalg::detail;
@@ -85,6 +95,126 @@ void check_gemm(std::mt19937_64 &rng, int M, int N, int K_limbs, int nz, float a
     report(what, same_bits(c_rocm, c_cpu));
 }
 
+// ---- trit-dot overload ----
+std::uint16_t bf16_of_int(int v) {
+    const float f = static_cast<float>(v);
+    std::uint32_t u;
+    std::memcpy(&u, &f, 4);
+    return static_cast<std::uint16_t>(u >> 16);  // exact for |v| <= 256
+}
+
+struct TritProblem {
+    int M, N, K;
+    std::vector<limb> W;                   // N x L
+    std::vector<int> xi;                   // M x K integer activations
+    std::vector<double> want;              // M x N, alpha/beta/bias applied
+};
+
+TritProblem trit_problem(std::mt19937_64 &rng, int M, int N, int K, float alpha, float beta,
+                         const std::vector<float> &c0, const std::vector<float> &bias) {
+    TritProblem p{M, N, K, {}, {}, {}};
+    const int L = (K + limb::TRITS - 1) / limb::TRITS;
+    std::uniform_int_distribution<int> trit(-1, 1), xv(-127, 127);
+    std::vector<std::int8_t> T(static_cast<std::size_t>(N) * K);
+    for (auto &t : T) t = static_cast<std::int8_t>(trit(rng));
+    p.W.resize(static_cast<std::size_t>(N) * L);
+    for (int n = 0; n < N; ++n)
+        for (int l = 0; l < L; ++l) {
+            std::array<std::int8_t, limb::TRITS> tr{};
+            for (int j = 0; j < limb::TRITS && l * limb::TRITS + j < K; ++j)
+                tr[j] = T[static_cast<std::size_t>(n) * K + l * limb::TRITS + j];
+            p.W[static_cast<std::size_t>(n) * L + l] = limb::from_trits(tr);
+        }
+    p.xi.resize(static_cast<std::size_t>(M) * K);
+    for (auto &v : p.xi) v = xv(rng);
+    p.want.assign(static_cast<std::size_t>(M) * N, 0.0);
+    for (int n = 0; n < N; ++n) {
+        // the trits as the packed limbs hold them
+        std::vector<int> tn(K);
+        for (int l = 0; l < L; ++l) {
+            const auto tr = p.W[static_cast<std::size_t>(n) * L + l].to_trits();
+            for (int j = 0; j < limb::TRITS && l * limb::TRITS + j < K; ++j) tn[l * limb::TRITS + j] = tr[j];
+        }
+        for (int m = 0; m < M; ++m) {
+            long long acc = 0;
+            for (int k = 0; k < K; ++k) acc += static_cast<long long>(p.xi[static_cast<std::size_t>(m) * K + k]) * tn[k];
+            double y = static_cast<double>(alpha) * static_cast<double>(acc);
+            if (beta != 0.0f) y += static_cast<double>(beta) * c0[static_cast<std::size_t>(m) * N + n];
+            if (!bias.empty()) y += bias[n];
+            p.want[static_cast<std::size_t>(m) * N + n] = y;
+        }
+    }
+    return p;
+}
+
+bool exact(const std::vector<float> &got, const std::vector<double> &want) {
+    for (std::size_t i = 0; i < got.size(); ++i)
+        if (static_cast<double>(got[i]) != want[i]) return false;
+    return got.size() == want.size();
+}
+
+void check_trit(std::mt19937_64 &rng, int M, int N, int K, t81::linalg::TritActivation xt,
+                float alpha, float beta, bool with_bias, bool device) {
+    using t81::linalg::TritActivation;
+    std::uniform_int_distribution<int> cv(-1000, 1000);
+    std::vector<float> c0(static_cast<std::size_t>(M) * N), bias;
+    for (auto &v : c0) v = static_cast<float>(cv(rng));
+    if (with_bias) {
+        bias.resize(N);
+        for (auto &v : bias) v = static_cast<float>(cv(rng));
+    }
+    const TritProblem p = trit_problem(rng, M, N, K, alpha, beta, c0, bias);
+    std::vector<std::uint16_t> xb;
+    std::vector<float> xf;
+    std::vector<std::int8_t> x8;
+    const void *xhost = nullptr;
+    std::size_t xbytes = 0;
+    if (xt == TritActivation::BFloat16) {
+        for (int v : p.xi) xb.push_back(bf16_of_int(v));
+        xhost = xb.data(), xbytes = xb.size() * 2;
+    } else if (xt == TritActivation::Float32) {
+        for (int v : p.xi) xf.push_back(static_cast<float>(v));
+        xhost = xf.data(), xbytes = xf.size() * 4;
+    } else {
+        for (int v : p.xi) x8.push_back(static_cast<std::int8_t>(v));
+        xhost = x8.data(), xbytes = x8.size();
+    }
+    std::vector<float> c = c0;
+    std::vector<std::int32_t> ci(c0.begin(), c0.end());
+    void *cptr = xt == TritActivation::Int8 ? static_cast<void *>(ci.data()) : c.data();
+    if (!device) {
+        t81::linalg::gemm_ternary(xhost, xt, p.W, cptr, M, N, K, alpha, beta,
+                                  with_bias ? bias.data() : nullptr);
+    } else {  // device-resident buffers on a stream of the caller's
+        void *dx, *dw, *dc, *db = nullptr;
+        hipStream_t s;
+        (void)hipStreamCreate(&s);
+        (void)hipMalloc(&dx, xbytes);
+        (void)hipMalloc(&dw, p.W.size() * sizeof(limb));
+        (void)hipMalloc(&dc, c.size() * 4);
+        (void)hipMemcpy(dx, xhost, xbytes, hipMemcpyHostToDevice);
+        (void)hipMemcpy(dw, p.W.data(), p.W.size() * sizeof(limb), hipMemcpyHostToDevice);
+        (void)hipMemcpy(dc, cptr, c.size() * 4, hipMemcpyHostToDevice);
+        if (with_bias) {
+            (void)hipMalloc(&db, bias.size() * 4);
+            (void)hipMemcpy(db, bias.data(), bias.size() * 4, hipMemcpyHostToDevice);
+        }
+        t81::linalg::gemm_ternary(dx, xt, std::span<const limb>(static_cast<const limb *>(dw), p.W.size()),
+                                  dc, M, N, K, alpha, beta, static_cast<const float *>(db), s);
+        (void)hipStreamSynchronize(s);
+        (void)hipMemcpy(cptr, dc, c.size() * 4, hipMemcpyDeviceToHost);
+        (void)hipFree(dx), (void)hipFree(dw), (void)hipFree(dc);
+        if (db) (void)hipFree(db);
+        (void)hipStreamDestroy(s);
+    }
+    if (xt == TritActivation::Int8) c.assign(ci.begin(), ci.end());
+    char what[128];
+    std::snprintf(what, sizeof what, "trit gemm_ternary %s M=%d N=%d K=%d a=%g b=%g%s%s",
+                  xt == TritActivation::BFloat16 ? "bf16" : (xt == TritActivation::Float32 ? "f32" : "i8"),
+                  M, N, K, alpha, beta, with_bias ? " bias" : "", device ? " device" : " host");
+    report(what, exact(c, p.want));
+}
+
 }  // namespace
 
 int main() {
@@ -141,6 +271,56 @@ int main() {
     ld::addcmul(ma, mb, mc, 0.3f, mr, Backend::ROCm);
     ld::addcmul(ma, mb, mc, 0.3f, mq, Backend::CPU);
     report("addcmul", same_bits(r, q));
+
+    {  // trit-dot overload: K2 (M <= 16) and K3 shapes, host and device buffers
+        using t81::linalg::TritActivation;
+        check_trit(rng, 1, 300, 4096, TritActivation::BFloat16, 1.0f, 0.0f, false, false);
+        check_trit(rng, 4, 257, 1000, TritActivation::BFloat16, 0.5f, 1.0f, true, true);
+        check_trit(rng, 16, 96, 3072, TritActivation::Float32, 1.0f, 0.0f, true, false);
+        check_trit(rng, 300, 512, 4104, TritActivation::BFloat16, 0.5f, 1.0f, true, true);
+        check_trit(rng, 100, 200, 2000, TritActivation::Float32, -2.0f, 0.5f, false, true);
+        check_trit(rng, 9, 70, 500, TritActivation::Int8, 1.0f, 1.0f, false, false);
+        check_trit(rng, 200, 300, 1536, TritActivation::Int8, 1.0f, 0.0f, false, true);
+        // TensorMetadata route: bf16 X, limbs W, float C and bias, host memory
+        std::mt19937_64 r2(7);
+        const int M = 33, N = 65, K = 500;
+        std::vector<float> c0(static_cast<std::size_t>(M) * N, 0.0f), bias(N, 0.0f);
+        const TritProblem p = trit_problem(r2, M, N, K, 1.0f, 0.0f, c0, {});
+        std::vector<std::uint16_t> xb;
+        for (int v : p.xi) xb.push_back(bf16_of_int(v));
+        std::vector<float> c(c0.size(), -1.0f);
+        auto mk = [](void *ptr, std::int64_t r, std::int64_t cc, t81::ScalarType t) {
+            t81::TensorMetadata m;
+            m.data_ptr = ptr;
+            m.sizes = {r, cc};
+            m.strides = {cc, 1};
+            m.dtype = t;
+            return m;
+        };
+        auto mx = mk(xb.data(), M, K, t81::ScalarType::BFloat16);
+        auto mw = mk(const_cast<limb *>(p.W.data()), N, (K + 47) / 48, t81::ScalarType::TernaryLimb);
+        auto mc = mk(c.data(), M, N, t81::ScalarType::Float);
+        auto mb = t81::make_contiguous_metadata(bias.size(), bias.data());
+        ld::gemm_ternary_trit(mx, mw, mc, 1.0f, 0.0f, &mb);
+        report("detail::gemm_ternary_trit(TensorMetadata)", exact(c, p.want));
+        // argument errors come back as std::invalid_argument with the reference's wording
+        bool threw = false;
+        try {
+            t81::linalg::gemm_ternary(xb.data(), TritActivation::BFloat16,
+                                      std::span<const limb>(p.W.data(), p.W.size() - 1), c.data(),
+                                      M, N, K);
+        } catch (const std::invalid_argument &e) {
+            threw = std::string(e.what()) == "W span size does not match (N, ceil(K / 48))";
+        }
+        report("trit gemm_ternary rejects a short W span", threw);
+        threw = false;
+        try {
+            t81::linalg::gemm_ternary(xb.data(), TritActivation::BFloat16, p.W, c.data(), -1, N, K);
+        } catch (const std::invalid_argument &e) {
+            threw = std::string(e.what()) == "gemm_ternary dimensions must be non-negative";
+        }
+        report("trit gemm_ternary rejects negative dimensions", threw);
+    }
 
     std::printf("plugin_check: %s\n", failures == 0 ? "all bit-exact" : "FAILED");
     return failures == 0 ? 0 : 1;

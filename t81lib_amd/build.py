@@ -1,7 +1,9 @@
 """Builds libt81_hip.so in-tree with hipcc for gfx950.
 
-``python -m t81lib_amd.build`` (or ``__graft_entry__.build()``) compiles every
-``csrc/*.hip`` into ``t81lib_amd/libt81_hip.so``.  The library travels with the
+``python -m t81lib_amd.build`` (or ``__graft_entry__.build()``) compiles the
+library sources of ``csrc/`` into ``t81lib_amd/libt81_hip.so``, and the
+measurement kernels bench.py uses (``csrc/floors.hip``, not part of the t81lib
+path) into ``t81lib_amd/libt81_floors.so``.  The libraries travel with the
 source tree; nothing is installed.
 """
 
@@ -16,6 +18,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libt81_hip.so")
+FLOORS_LIB = os.path.join(HERE, "libt81_floors.so")
 ARCH = "gfx950"
 
 SOURCES = ["abi.hip", "pack.hip", "gemv.hip", "gemv_strip.hip", "gemm.hip",
@@ -43,14 +46,15 @@ def hipcc() -> str:
 
 
 def build(verbose: bool = False) -> str:
-    """Compiles the library (always; it is the build check) and returns its path.
-    Each source compiles to its own object in parallel, then one shared link."""
+    """Compiles the libraries (always; it is the build check) and returns the path of
+    libt81_hip.so.  Each source compiles to its own object in parallel, then one shared
+    link per library."""
     from concurrent.futures import ThreadPoolExecutor
 
     objdir = os.path.join(HERE, "_obj")
     os.makedirs(objdir, exist_ok=True)
     jobs = []
-    for src in SOURCES:
+    for src in SOURCES + ["floors.hip"]:
         obj = os.path.join(objdir, os.path.splitext(src)[0] + ".o")
         jobs.append((obj, [hipcc(), *HIPCC_FLAGS, "-c", "-o", obj, os.path.join(CSRC, src)]))
 
@@ -66,13 +70,15 @@ def build(verbose: bool = False) -> str:
         if proc.returncode != 0:
             sys.stderr.write(proc.stdout + proc.stderr)
             raise RuntimeError(f"hipcc failed compiling {os.path.basename(obj)}")
-    tmp = LIB + ".tmp"
-    proc = run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp,
-                *[obj for obj, _ in jobs]])
-    if proc.returncode != 0:
-        sys.stderr.write(proc.stdout + proc.stderr)
-        raise RuntimeError("hipcc failed linking libt81_hip.so")
-    os.replace(tmp, LIB)
+    objs = {os.path.basename(obj): obj for obj, _ in jobs}
+    floors_obj = objs.pop("floors.o")
+    for lib, members in ((LIB, list(objs.values())), (FLOORS_LIB, [floors_obj])):
+        tmp = lib + ".tmp"
+        proc = run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *members])
+        if proc.returncode != 0:
+            sys.stderr.write(proc.stdout + proc.stderr)
+            raise RuntimeError(f"hipcc failed linking {os.path.basename(lib)}")
+        os.replace(tmp, lib)
     return LIB
 
 

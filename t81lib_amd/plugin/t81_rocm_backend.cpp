@@ -19,6 +19,10 @@
 //    std::runtime_error (HIP / device codes), as in src/linalg/gemm_rocm.cpp:22-27.
 // Difference: buffers already in device memory (hipPointerGetAttributes says so)
 // are used in place; host buffers are staged through temporary device copies.
+//
+// It also defines the trit-dot overload of gemm_ternary declared in t81_rocm_trit.hpp
+// (X times the packed trit matrix, on the decode GEMV / prefill GEMM kernels), which the
+// reference has no counterpart for: its C++ gemm_ternary multiplies limb integers only.
 #include <hip/hip_runtime_api.h>
 
 #include <cstddef>
@@ -31,6 +35,7 @@
 #include <t81/tensor_metadata.hpp>
 
 #include "t81_hip.h"
+#include "t81_rocm_trit.hpp"
 
 namespace t81::linalg::detail {
 
@@ -78,6 +83,7 @@ class DeviceView {
         if (owned_) (void)hipFree(dev_);
     }
     void *get() const { return dev_; }
+    bool staged() const { return owned_; }
     void write_back() {
         check_hip(hipDeviceSynchronize(), "hipDeviceSynchronize");
         if (owned_) check_hip(hipMemcpy(host_, dev_, bytes_, hipMemcpyDeviceToHost), "hipMemcpy D2H");
@@ -175,4 +181,119 @@ void rocm_addcmul(const TensorMetadata &input, const TensorMetadata &tensor1,
     dout.write_back();
 }
 
+// ---------------------------------------------------------------- trit-dot --
+namespace {
+
+int dtype_code(TritActivation t) {
+    switch (t) {
+        case TritActivation::Float32: return T81_DTYPE_F32;
+        case TritActivation::BFloat16: return T81_DTYPE_BF16;
+        case TritActivation::Int8: return T81_DTYPE_I8;
+    }
+    throw std::invalid_argument("unknown activation type");
+}
+
+std::size_t dtype_bytes(TritActivation t) {
+    return t == TritActivation::Float32 ? 4 : (t == TritActivation::BFloat16 ? 2 : 1);
+}
+
+// rank-2 contiguous metadata -> (rows, cols, first element)
+struct Matrix2 {
+    std::int64_t rows, cols;
+    std::uint8_t *data;
+};
+
+Matrix2 matrix2(const TensorMetadata &m, std::size_t elem, const char *name) {
+    if (m.sizes.size() != 2)
+        throw std::invalid_argument(std::string(name) + " must be a rank-2 tensor");
+    if (m.data_ptr == nullptr && m.numel() > 0)
+        throw std::invalid_argument("tensor metadata must provide a valid data pointer");
+    if (!m.is_contiguous())
+        throw std::invalid_argument("tensor metadata must describe contiguous storage");
+    if (m.sizes[0] < 0 || m.sizes[1] < 0)
+        throw std::invalid_argument("gemm_ternary dimensions must be non-negative");
+    const std::int64_t offset = m.storage_offset > 0 ? m.storage_offset : 0;
+    return {m.sizes[0], m.sizes[1],
+            static_cast<std::uint8_t *>(m.data_ptr) + static_cast<std::size_t>(offset) * elem};
+}
+
+}  // namespace
+
 }  // namespace t81::linalg::detail
+
+namespace t81::linalg {
+
+void gemm_ternary(const void *X, TritActivation x_type, std::span<const core::limb> W, void *C,
+                  int M, int N, int K, float alpha, float beta, const float *bias,
+                  void *stream) {
+    if (M < 0 || N < 0 || K < 0)
+        throw std::invalid_argument("gemm_ternary dimensions must be non-negative");
+    const std::size_t L = (static_cast<std::size_t>(K) + core::limb::TRITS - 1) / core::limb::TRITS;
+    if (static_cast<std::size_t>(N) * L != W.size())
+        throw std::invalid_argument("W span size does not match (N, ceil(K / 48))");
+    const int code = detail::dtype_code(x_type);
+    if (M == 0 || N == 0) return;
+    if (!detail::rocm_available())
+        throw std::runtime_error("the trit-dot gemm_ternary needs a gfx950 device");
+    const std::size_t xb = static_cast<std::size_t>(M) * static_cast<std::size_t>(K) *
+                           detail::dtype_bytes(x_type);
+    const std::size_t cb = static_cast<std::size_t>(M) * static_cast<std::size_t>(N) * 4;
+    detail::DeviceView x(X, xb, true), w(W.data(), W.size_bytes(), true);
+    detail::DeviceView c(C, cb, beta != 0.0f), b(bias, bias ? static_cast<std::size_t>(N) * 4 : 0, true);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    // K3's split-K workspace for shapes with few output tiles, stream-ordered
+    const std::int64_t wsb = t81_hip_ternary_matmul_workspace_size(M, N, K, code);
+    void *ws = nullptr;
+    if (wsb > 0) detail::check_hip(hipMallocAsync(&ws, static_cast<std::size_t>(wsb), s), "hipMallocAsync");
+    const int rc = t81_hip_ternary_matmul_ws(0, x.get(), code,
+                                             static_cast<const std::uint8_t *>(w.get()), c.get(),
+                                             M, N, K, alpha, beta,
+                                             static_cast<const float *>(b.get()), ws, wsb, s);
+    if (ws != nullptr) (void)hipFreeAsync(ws, s);
+    detail::check_rc(rc);
+    if (stream == nullptr || x.staged() || w.staged() || c.staged() || b.staged()) c.write_back();
+}
+
+namespace detail {
+
+void gemm_ternary_trit(const TensorMetadata &X, const TensorMetadata &W, TensorMetadata &C,
+                       float alpha, float beta, const TensorMetadata *bias) {
+    TritActivation xt;
+    switch (X.dtype) {
+        case ScalarType::Float: xt = TritActivation::Float32; break;
+        case ScalarType::BFloat16: xt = TritActivation::BFloat16; break;
+        case ScalarType::Char: xt = TritActivation::Int8; break;
+        default: throw std::invalid_argument("activations must be float32, bfloat16 or int8");
+    }
+    if (!W.dtype_is_ternary_limb())
+        throw std::invalid_argument("packed weights must be TernaryLimb metadata");
+    const ScalarType c_type = xt == TritActivation::Int8 ? ScalarType::Int : ScalarType::Float;
+    if (C.dtype != c_type)
+        throw std::invalid_argument(xt == TritActivation::Int8
+                                        ? "C must be int32 for int8 activations"
+                                        : "tensor metadata must describe float32 data");
+    const Matrix2 x = matrix2(X, dtype_bytes(xt), "X");
+    const Matrix2 w = matrix2(W, sizeof(core::limb), "W");
+    const Matrix2 c = matrix2(C, 4, "C");
+    const std::int64_t L = (x.cols + core::limb::TRITS - 1) / core::limb::TRITS;
+    if (w.cols != L)
+        throw std::invalid_argument("W shape must match the ceil(K / 48) dimension of X");
+    if (c.rows != x.rows || c.cols != w.rows)
+        throw std::invalid_argument("C shape must match the output dimensions");
+    const float *bp = nullptr;
+    if (bias != nullptr) {
+        if (!bias->dtype_is_float32() || bias->numel() != static_cast<std::size_t>(w.rows))
+            throw std::invalid_argument("bias must hold N float32 values");
+        bp = float_data(*bias);
+    }
+    if (x.rows > INT32_MAX || w.rows > INT32_MAX || x.cols > INT32_MAX)
+        throw std::invalid_argument("gemm_ternary dimensions too large");
+    gemm_ternary(x.data, xt,
+                 std::span<const core::limb>(reinterpret_cast<const core::limb *>(w.data),
+                                             static_cast<std::size_t>(w.rows * w.cols)),
+                 c.data, static_cast<int>(x.rows), static_cast<int>(w.rows),
+                 static_cast<int>(x.cols), alpha, beta, bp, nullptr);
+}
+
+}  // namespace detail
+}  // namespace t81::linalg

@@ -76,3 +76,35 @@ def test_decode_graph_replays_match_eager(gpu, batch):
             assert int(pos.item()) == prompt + i + 1
             nxt = tok.clone()
             assert torch.equal(nxt, le.argmax(-1, keepdim=True)), f"replay {i} tokens"
+
+
+FULL = dict(layers=2, hidden=4096, heads=32, kv_heads=8, ffn=14336, vocab=128256)
+
+
+@pytest.mark.parametrize("batch", [1, 32])
+def test_full_size_layers_prefill_and_decode(gpu, batch):
+    """Config 5 at its real shapes: two Llama-3-8B layers (hidden 4096, ffn 14336, 32 query
+    / 8 key-value heads, vocab 128256), a 1024-token prompt per sequence (K3 over 1024 *
+    batch tokens) and greedy decode steps (K2 at batch 1, K3 at batch 32), against the same
+    stack with F.linear in float32 over the same trits."""
+    _announce(f"decoder stack full-size layers batch={batch}")
+    prompt, steps = 1024, 4
+    kw = dict(max_batch=batch, max_tokens=prompt + steps, seed=11)
+    ours = bench.DecoderStack(torch, gpu, **FULL, **kw)
+    ref = bench.DecoderStack(torch, gpu, **FULL, reference=True, **kw)
+    g = torch.Generator(gpu).manual_seed(12)
+    tokens = torch.randint(0, FULL["vocab"], (batch, prompt), generator=g, device=gpu)
+    agree = 0
+    with torch.no_grad():
+        lo, lr = ours.forward(tokens, 0), ref.forward(tokens, 0)
+        for i in range(steps + 1):
+            scale = lr.abs().max().item()
+            err = (lo - lr).abs().max().item()
+            assert err <= 2e-2 * scale + 1e-3, f"step {i}: max |diff| {err:.4g}, scale {scale:.4g}"
+            no, nr = lo.argmax(-1, keepdim=True), lr.argmax(-1, keepdim=True)
+            agree += int((no == nr).sum())
+            if i < steps:
+                lo, lr = ours.forward(nr, prompt + i), ref.forward(nr, prompt + i)
+    assert agree >= 0.9 * (steps + 1) * batch, f"greedy tokens agree {agree} of {(steps + 1) * batch}"
+    del ours, ref
+    torch.cuda.empty_cache()
