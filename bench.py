@@ -28,6 +28,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBPS = 8000.0          # MI355X HBM3E
 BF16_PEAK_TFLOPS = 2500.0       # dense bf16 MFMA
+INT8_PEAK_TOPS = 5000.0         # dense int8 MFMA
 MALL_BYTES = 256 << 20
 
 METRIC = ("ternary GEMV HBM GB/s (% of peak) + prefill GEMM TFLOP/s (% MFMA peak), 1 GPU")
@@ -906,6 +907,21 @@ def main() -> int:
         torch.cuda.empty_cache()
         log(f"GEMM {gemm['ms']:.3f} ms/call over 100 calls (median {gemm['median_ms']:.3f})")
 
+    # ----------------------------------------- K3 prefill GEMM, int8 activations --
+    gemm_i8 = None
+    if only in (None, "gemm"):
+        log(f"GEMM int8 M={GM} {GK}->{GN}")
+        gw = make_weights(torch, ops, _lib, GN, GK, 2, dev, seed=2)
+        gx8 = torch.randint(-128, 128, (GM, GK), device=dev, dtype=torch.int8)
+        gout8 = torch.empty((GM, GN), device=dev, dtype=torch.int32)
+        glaunch8 = lambda wb: ops.ternary_matmul(gx8, wb, GK, c=gout8, kernel=3)  # noqa: E731
+        gemm_i8 = time_graph(torch, glaunch8, gw, 100, 20, dist=True)
+        gemm_i8["sha256"] = sha256_tensors(torch, gw[0], gx8)
+        del gw, gx8, gout8
+        torch.cuda.empty_cache()
+        log(f"GEMM int8 {gemm_i8['ms']:.3f} ms/call over 100 calls "
+            f"(median {gemm_i8['median_ms']:.3f})")
+
     # ------------------------------------------------------------- K1 pack --
     PR, PC = 8192, 3072
     pack = None
@@ -1016,6 +1032,16 @@ def main() -> int:
         }
         if "cpu_baseline" in gemm:
             line["gemm"]["cpu_baseline"] = gemm["cpu_baseline"]
+    if gemm_i8:
+        tops = 2.0 * GM * GN * GK / (gemm_i8["ms"] * 1e-3) / 1e12
+        line["gemm_int8"] = {
+            "workload": f"prefill GEMM K3, M={GM}, {GK}->{GN} (Llama-3-8B gate_up), int8 x, "
+                        f"exact int32 out (integer matrix cores)",
+            "ms": gemm_i8["ms"], "timed_launches": gemm_i8["timed_launches"], "tops": tops,
+            "roofline": {"bound": "mfma", "achieved": tops, "peak": INT8_PEAK_TOPS,
+                         "unit": "TOP/s", "frac": tops / INT8_PEAK_TOPS},
+            "timing": spread_us(gemm_i8), "inputs_sha256": gemm_i8["sha256"],
+        }
     if pack:
         pbytes = 4 * PR * PC + 16 * PR * ((PC + 47) // 48)
         gbs = pbytes / (pack["ms"] * 1e-3) / 1e9

@@ -21,7 +21,7 @@ LIB = os.path.join(HERE, "libt81_hip.so")
 FLOORS_LIB = os.path.join(HERE, "libt81_floors.so")
 ARCH = "gfx950"
 
-SOURCES = ["abi.hip", "pack.hip", "gemv.hip", "gemv_strip.hip", "gemm.hip",
+SOURCES = ["abi.hip", "pack.hip", "gemv.hip", "gemv_strip.hip", "gemm.hip", "gemm_i8.hip",
            "limb.hip", "elementwise.hip", "tq.hip", "gemv_tq2.hip", "transpose.hip",
            "spmm.hip", "noalloc.hip"]
 

@@ -956,6 +956,12 @@ hipError_t launch_gemm_x(const void *x, const uint8_t *w, void *c, int64_t m, in
     if (m <= 64)
         return launch_gemm_t<XT, 2, 2, 4, 1, LK>(x, w, c, m, n, n, k, alpha, beta, bias, s, ws,
                                                  ws_bytes);
+    if constexpr (XT == kDtypeI8) {
+        // int8 activations on the integer matrix cores (gemm_i8.hip) when the shape allows
+        if (gemm_i8_fits(x, m, n, k))
+            return launch_gemm_i8(x, w, static_cast<int32_t *>(c), m, n, k, beta != 0.0f, s, ws,
+                                  ws_bytes);
+    }
     if constexpr (XT != kDtypeF32) {
         // Rows [0, n1): whole rounds of 256 x 256 tiles -- the one-wave-per-SIMD kernel
         // for bf16, else the eight-wave kernel (two waves per SIMD).  Rows [n1, n) (all
@@ -1022,9 +1028,16 @@ int64_t gemm_workspace_x(int64_t m, int64_t n, int64_t k) {
     } else {
         // the rows after whole rounds of big tiles: split-K big tiles (bf16, aligned
         // activations) or eight-wave 256 x 128 tiles; the larger of the two
+        int64_t i8 = 0;
+        if constexpr (XT == kDtypeI8) {
+            // the integer big-tile kernel's split-K plan (K % 16 == 0), or the eight-wave
+            // kernel's when the activations turn out misaligned; the larger of the two
+            if (k % 16 == 0) i8 = gemm_i8_workspace_bytes(m, n, k);
+        }
         const int64_t n1 = gemm_rows_whole_rounds(m, n);
-        if (n1 == n) return 0;
+        if (n1 == n) return i8;
         const int64_t eight = gemm_t_workspace<XT, 2, 2, 4, 2>(m, n - n1, k);
+        if constexpr (XT == kDtypeI8) return eight > i8 ? eight : i8;
         if constexpr (XT != kDtypeBF16) return eight;
         const int64_t big = k % 8 == 0 ? split_workspace_bytes(gemm_split_plan(m, n - n1, k)) : 0;
         return big > eight ? big : eight;

@@ -1,0 +1,490 @@
+// t81lib_amd/csrc/gemm_i8.hip -- K3 for int8 activations on the integer matrix cores.
+//
+//   C[m, n] = sum_k X[m, k] * T[n, k] (+ C[m, n] when beta == 1), int32, exact
+//
+// The bf16 big-tile kernel (gemm.hip) with the integer MFMA v_mfma_i32_32x32x32_i8 in
+// place of v_mfma_f32_32x32x16_bf16: trits decode to int8 (-1, 0, +1), the activations
+// go to the matrix cores as they are, and the sums are int32 -- exact for any K the
+// int32 result can hold (|sum| <= 128 K), at twice the bf16 rate (5 POP/s dense).
+//
+// Tiling (as the bf16 kernel): a workgroup of four waves, one per SIMD, computes a
+// 256 x 256 tile of C^T; wave (wn, wm) owns 128 weight rows x 128 tokens, 4 x 4 blocks
+// of 32 x 32 int32 accumulators (all 256 AGPRs).  A k-step is two limbs (96 trits):
+//  * lane (r, h) loads the 16 bytes of limb 2s + h of row 32 rb + r and decodes it into
+//    three 16-trit operands (J = 0, 1, 2: trits 16J .. 16J + 15 of the limb, one int8
+//    each); B lane (c, h) reads X[c, 96 s + 48 h + 16 J .. + 16], 16 bytes of the
+//    activation tile.  A lane's element e and the B lane's element e are the same k, so
+//    every MFMA pairs each trit with its own activation;
+//  * decode: a 32-entry LDS table maps a tryte u to the int8 word (t0, t1, t2, 0) (entries
+//    past 26 are zero); v_perm_b32 packs the words of four trytes into the three
+//    natural-order dwords of their twelve trits;
+//  * the activation tile of step s + 1 (256 tokens x 96 int8, rows of 7 16-byte slots,
+//    one a pad slot so that the 16-byte B reads of 16 lanes fall on distinct banks) goes
+//    straight from global memory into the other LDS buffer with buffer loads carrying
+//    the LDS bit, issued during step s; one barrier per step.  Chunks past K or past M,
+//    and the pad slots, load zeros (out-of-range buffer offsets), so K must be a multiple
+//    of 16 (a chunk never straddles the end of a row).
+// Work items, rounds, split-K items for the rows after whole rounds, and the LDS-staged
+// epilogue follow the bf16 kernel; split partials are int32 and sum exactly.
+#include "t81_device.hpp"
+#include "t81_kernels.hpp"
+
+namespace t81hip {
+
+namespace {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kI8Threads = 256;
+constexpr int kI8Rows = 256;                      // weight rows per workgroup
+constexpr int kI8Tokens = 256;                    // tokens per workgroup
+constexpr int kI8StepK = 2 * kTrits;              // trits per k-step
+constexpr int kI8RowSlots = kI8StepK / 16 + 1;    // 16-byte slots per tile row (+1 pad)
+constexpr int kI8RowBytes = 16 * kI8RowSlots;     // 112
+constexpr int kI8TileBytes = kI8Tokens * kI8RowBytes;
+constexpr int kI8LoadsPerWave = kI8Tokens * kI8RowSlots / (64 * 4);   // 7
+constexpr uint32_t kI8Oob = 0x80000000u;
+constexpr int kI8StageStride = 68;                // int32 per staged output row (64 + 4 pad)
+constexpr int kI8LutBytes = 32 * 4 + 16;          // 32 words + slack for invalid bytes
+
+static_assert(kI8Tokens * kI8RowSlots % (64 * 4) == 0, "tile loads must split evenly");
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t i8_rsrc(const void *base, int64_t bytes) {
+    const uint64_t p = reinterpret_cast<uint64_t>(base);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(p));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(p >> 32));
+    const int n = __builtin_amdgcn_readfirstlane(bytes < 0x7FFFFFFF ? static_cast<int>(bytes)
+                                                                    : 0x7FFFFFFF);
+    return __builtin_amdgcn_make_buffer_rsrc(
+        reinterpret_cast<void *>((static_cast<uint64_t>(hi) << 32) | lo), 0, n, 0x00020000);
+}
+
+// word u = int8 bytes (t0, t1, t2, 0) of tryte u (u = 13 + t0 + 3 t1 + 9 t2), zero past 26
+__device__ __forceinline__ void i8_lut_fill(uint8_t *lds, int tid, int nthreads) {
+    uint32_t *words = reinterpret_cast<uint32_t *>(lds);
+    for (int i = tid; i < kI8LutBytes / 4; i += nthreads) {
+        uint32_t v = 0u;
+        if (i < 27) {
+            v = static_cast<uint32_t>(static_cast<uint8_t>(static_cast<int8_t>(trit_of(i, 0)))) |
+                static_cast<uint32_t>(static_cast<uint8_t>(static_cast<int8_t>(trit_of(i, 1)))) << 8 |
+                static_cast<uint32_t>(static_cast<uint8_t>(static_cast<int8_t>(trit_of(i, 2)))) << 16;
+        }
+        words[i] = v;
+    }
+}
+
+// Split-K: rows [0, n1) run as whole 256 x 256 tiles, rows [n1, N) (nsplit > 0) as split-K
+// items storing raw int32 partials to part in (split, tile, wave, block, a4, lane) order,
+// summed by gemm_split_reduce_i8_kernel.  Half of the split items come first in the item
+// order and half last (see the bf16 kernel).
+__global__ __launch_bounds__(kI8Threads) void gemm_w4_i8_kernel(
+    const int8_t *__restrict__ x, const uint8_t *__restrict__ w, int32_t *__restrict__ c, int M,
+    int N, int ldc, int K, int L, int accumulate, int n1, int sps, i32x4 *__restrict__ part,
+    int nsplit) {
+    // the table first: its larger alignment puts it at LDS address 0, so a table address is
+    // just the byte field
+    __shared__ __attribute__((aligned(1024))) uint8_t lut[kI8LutBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t xs0[kI8TileBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t xs1[kI8TileBytes];
+    __shared__ __attribute__((aligned(16))) int32_t cst[4][32 * kI8StageStride];
+    auto tile = [&](auto bufc) -> uint8_t * {
+        if constexpr (decltype(bufc)::value == 0) return xs0;
+        else return xs1;
+    };
+
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wn = wave & 1;
+    const int wm = wave >> 1;
+
+    const int tiles_m = (M + kI8Tokens - 1) / kI8Tokens;
+    const int tn1 = (n1 + kI8Rows - 1) / kI8Rows;
+    const int tn2 = (N - n1 + kI8Rows - 1) / kI8Rows;
+    const int full_items = tn1 * tiles_m;
+    const int tiles2 = tn2 * tiles_m;
+    const int split_items = nsplit > 0 ? tiles2 * nsplit : 0;
+    const int head = split_items / 2;
+    const int total = full_items + split_items;
+    const int all_steps = (L + 1) / 2;
+    i8_lut_fill(lut, tid, kI8Threads);  // published by the first item's barrier
+    for (int q = static_cast<int>(blockIdx.x); q < total; q += static_cast<int>(gridDim.x)) {
+    int lane = tid & 63;
+    asm volatile("" : "+v"(lane));
+    const int r = lane & 31;
+    const int h = lane >> 5;
+    const bool split = q < head || q >= head + full_items;
+    const int item = __builtin_amdgcn_readfirstlane(q < head ? q : (split ? q - full_items : q - head));
+    const int sp = split ? item / tiles2 : 0;
+    const int tt = split ? item - sp * tiles2 : item;
+    const int tiles_n = split ? tn2 : tn1;
+    const int tn = __builtin_amdgcn_readfirstlane(tt % tiles_n);
+    const int tm = __builtin_amdgcn_readfirstlane(tt / tiles_n);
+    const int nwg = (split ? n1 : 0) + tn * kI8Rows;
+    const int m0 = tm * kI8Tokens;
+    const int s_begin = split ? sp * sps : 0;
+    const int s_end = split && s_begin + sps < all_steps ? s_begin + sps : all_steps;
+
+    // weights: rows past N read zeros; a limb past L (odd L, last step) reads the next
+    // row's first limb or zeros -- finite trits that meet zero activations
+    const __amdgpu_buffer_rsrc_t wsrc = i8_rsrc(w + static_cast<int64_t>(nwg) * L * kTrytes,
+                                                static_cast<int64_t>(N - nwg) * L * kTrytes);
+    uint32_t woff[4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+        woff[rb] = (static_cast<uint32_t>(128 * wn + 32 * rb + r) * static_cast<uint32_t>(L) +
+                    static_cast<uint32_t>(h)) * kTrytes;
+    auto fetch_w = [&](int step, u32x4 (&dst)[4]) {
+        const uint32_t koff = static_cast<uint32_t>(step) * (2 * kTrytes);
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb)
+            dst[rb] = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(wsrc, woff[rb] + koff, 0, 0));
+    };
+
+    // activation tile: load i of wave w fills slots q = 64 (7 w + i) + lane, tile row q / 7,
+    // slot q % 7; tokens past M read zeros (buffer based at token m0)
+    const __amdgpu_buffer_rsrc_t xsrc = i8_rsrc(x + static_cast<int64_t>(m0) * K,
+                                                static_cast<int64_t>(M - m0) * K);
+    uint32_t tbase[kI8LoadsPerWave];
+    uint32_t tslot[(kI8LoadsPerWave + 3) / 4];
+#pragma unroll
+    for (int i = 0; i < (kI8LoadsPerWave + 3) / 4; ++i) tslot[i] = 0u;
+#pragma unroll
+    for (int i = 0; i < kI8LoadsPerWave; ++i) {
+        const uint32_t qq = static_cast<uint32_t>(64 * (kI8LoadsPerWave * wave + i) + lane);
+        const uint32_t row = qq / kI8RowSlots;
+        const uint32_t slot = qq - row * kI8RowSlots;
+        tbase[i] = slot < kI8RowSlots - 1 ? row * static_cast<uint32_t>(K) + 16 * slot : kI8Oob;
+        tslot[i / 4] |= (16 * slot) << (8 * (i % 4));
+    }
+    auto load_tile_part = [&](int step, auto bufc, int i) {
+        const int k0 = step * kI8StepK;
+        const uint32_t lim = k0 < K ? static_cast<uint32_t>(K - k0) : 0u;
+        const uint32_t slot16 = (tslot[i / 4] >> (8 * (i % 4))) & 0xFFu;
+        const uint32_t off = slot16 < lim ? tbase[i] + static_cast<uint32_t>(k0) : kI8Oob;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            xsrc,
+            (__attribute__((address_space(3))) void *)(
+                &tile(bufc)[16 * 64 * (kI8LoadsPerWave * wave + i)]),
+            16, off, 0, 0, 0);
+    };
+    auto load_tile = [&](int step, auto bufc) {
+#pragma unroll
+        for (int i = 0; i < kI8LoadsPerWave; ++i) load_tile_part(step, bufc, i);
+    };
+
+    // decode: table words of the four trytes of weight dword `wd`
+    auto table_fetch = [&](uint32_t wd, uint32_t (&t)[4]) {
+        const uint32_t w4 = wd << 2;
+        t[0] = *reinterpret_cast<const uint32_t *>(lut + (w4 & 0x7Fu));
+        t[1] = *reinterpret_cast<const uint32_t *>(lut + ((w4 >> 8) & 0x7Fu));
+        t[2] = *reinterpret_cast<const uint32_t *>(lut + ((w4 >> 16) & 0x7Fu));
+        t[3] = *reinterpret_cast<const uint32_t *>(lut + ((w4 >> 24) & 0x7Fu));
+    };
+    // the twelve trits of those four words as three dwords, natural order
+    auto table_merge = [&](const uint32_t (&t)[4], uint32_t *out) {
+        out[0] = __builtin_amdgcn_perm(t[1], t[0], 0x04020100u);
+        out[1] = __builtin_amdgcn_perm(t[2], t[1], 0x05040201u);
+        out[2] = __builtin_amdgcn_perm(t[3], t[2], 0x06050402u);
+    };
+
+    i32x16 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
+
+    // B lane (c, h): token 128 wm + 32 cb + c of the tile, bytes 48 h + 16 J of the step
+    const int brow = (128 * wm + r) * kI8RowBytes + 48 * h;
+    auto read_b = [&](auto bufc, int g) -> i32x4 {
+        const int j = g / 4;
+        const int cb = g % 4;
+        return *reinterpret_cast<const i32x4 *>(
+            &tile(bufc)[brow + 32 * cb * kI8RowBytes + 16 * j]);
+    };
+
+    // Weights run two steps ahead: wcur holds step s, wnxt step s + 1 (loaded during step
+    // s - 1), and step s + 2 is loaded into wn2 at the start of step s.
+    u32x4 wcur[4], wnxt[4], wn2[4];
+    i32x4 a[2][4][3];   // operands of the step with parity P / of the other one
+    // merge the table words of weight dword dw of row block rb into operand dwords
+    // 3 dw .. 3 dw + 2 (operand d / 4, component d % 4)
+    auto merge_into = [&](const uint32_t (&t)[4], i32x4 (&ops)[4][3], int rb, int dw) {
+        uint32_t o[3];
+        table_merge(t, o);
+#pragma unroll
+        for (int e = 0; e < 3; ++e) {
+            const int d = 3 * dw + e;
+            ops[rb][d / 4][d % 4] = static_cast<int>(o[e]);
+        }
+    };
+
+    if (s_begin < s_end) {
+        fetch_w(s_begin, wcur);
+        fetch_w(s_begin + 1, wnxt);
+        load_tile(s_begin, std::integral_constant<int, 0>());
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): the tile has landed before the barrier
+    __syncthreads();
+    if (s_begin < s_end) {
+        // the first step's J = 0 operands and dwords 4, 5 of its J = 1 operands
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+            for (int dw = 0; dw < 2; ++dw) {
+                uint32_t t[4];
+                table_fetch(wcur[rb][dw], t);
+                merge_into(t, a[0], rb, dw);
+            }
+    }
+
+    // One k-step as 12 chunks of four MFMAs (chunk g: J = g / 4, token block cb = g % 4,
+    // row blocks 0..3), one B fragment each, read two chunks ahead.  Each of chunks 0-7 also
+    // issues the table reads of two weight dwords, merged in the next chunk: chunks 0-3
+    // weight dwords 2 and 3 of this step (the rest of its J = 1 and J = 2 operands), chunks
+    // 4-7 dwords 0 and 1 of the next step (its J = 0 operands and the start of its J = 1).
+    // Chunks 0-6 issue the next step's tile loads, chunk 0 the weights of the step after
+    // next (past the last step they read zeros or unused weight bytes).
+    auto step_body = [&](int step, auto bufc, auto otherc) {
+        constexpr int P = decltype(bufc)::value;
+        i32x4 bq[3];
+        bq[0] = read_b(bufc, 0);
+        bq[1] = read_b(bufc, 1);
+        uint32_t t[2][2][4];
+#pragma unroll
+        for (int g = 0; g < 12; ++g) {
+            if (g + 2 < 12) bq[(g + 2) % 3] = read_b(bufc, g + 2);
+            if (g == 0) fetch_w(step + 2, wn2);
+            if (g < kI8LoadsPerWave) load_tile_part(step + 1, otherc, g);
+            if (g >= 1 && g <= 8) {   // merge the reads of chunk g - 1
+                const int gp = g - 1;
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const int rb = 2 * (gp % 2) + e;
+                    const int dw = gp < 4 ? 2 + gp / 2 : (gp - 4) / 2;
+                    if (gp < 4) merge_into(t[gp & 1][e], a[P], rb, dw);
+                    else merge_into(t[gp & 1][e], a[P ^ 1], rb, dw);
+                }
+            }
+            if (g < 8) {
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const int rb = 2 * (g % 2) + e;
+                    const int dw = g < 4 ? 2 + g / 2 : (g - 4) / 2;
+                    table_fetch((g < 4 ? wcur : wnxt)[rb][dw], t[g & 1][e]);
+                }
+            }
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb)
+                acc[rb][g % 4] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[P][rb][g / 4], bq[g % 3],
+                                                                       acc[rb][g % 4], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            wcur[rb] = wnxt[rb];
+            wnxt[rb] = wn2[rb];
+        }
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+        __syncthreads();
+    };
+    int step = s_begin;
+    for (; step + 1 < s_end; step += 2) {
+        step_body(step, std::integral_constant<int, 0>(), std::integral_constant<int, 1>());
+        step_body(step + 1, std::integral_constant<int, 1>(), std::integral_constant<int, 0>());
+    }
+    if (step < s_end)  // odd step count: the last step, peeled
+        step_body(step, std::integral_constant<int, 0>(), std::integral_constant<int, 1>());
+
+    if (split) {
+        i32x4 *dst = part + (((static_cast<int64_t>(sp) * tiles2 + tt) * 4 + wave) * 64) * 64 + lane;
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+                for (int a4 = 0; a4 < 4; ++a4)
+                    dst[((rb * 4 + cb) * 4 + a4) * 64] =
+                        i32x4{acc[rb][cb][4 * a4], acc[rb][cb][4 * a4 + 1],
+                              acc[rb][cb][4 * a4 + 2], acc[rb][cb][4 * a4 + 3]};
+        continue;
+    }
+
+    // epilogue through the wave's LDS region, as in the bf16 kernel
+    const int col0 = nwg;
+    const bool vec4 = ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(c) & 15u) == 0;
+    int32_t *st = cst[wave];
+    const int tq = lane >> 4;
+    const int tc = 4 * (lane & 15);
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) {
+#pragma unroll
+        for (int rp = 0; rp < 2; ++rp) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int a4 = 0; a4 < 4; ++a4)
+                    *reinterpret_cast<i32x4 *>(&st[r * kI8StageStride + 32 * j + 8 * a4 + 4 * h]) =
+                        i32x4{acc[2 * rp + j][cb][4 * a4], acc[2 * rp + j][cb][4 * a4 + 1],
+                              acc[2 * rp + j][cb][4 * a4 + 2], acc[2 * rp + j][cb][4 * a4 + 3]};
+            const int nb = col0 + 128 * wn + 64 * rp + tc;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int tok = 4 * i + tq;
+                const i32x4 v = *reinterpret_cast<const i32x4 *>(&st[tok * kI8StageStride + tc]);
+                const int m = m0 + 128 * wm + 32 * cb + tok;
+                if (m >= M) continue;
+                int32_t *cr = c + static_cast<int64_t>(m) * ldc;
+                int32_t y[4] = {v[0], v[1], v[2], v[3]};
+                if (vec4 && nb + 3 < N) {
+                    if (accumulate) {
+                        const i32x4 cv = *reinterpret_cast<const i32x4 *>(cr + nb);
+                        y[0] += cv[0];
+                        y[1] += cv[1];
+                        y[2] += cv[2];
+                        y[3] += cv[3];
+                    }
+                    *reinterpret_cast<i32x4 *>(cr + nb) = i32x4{y[0], y[1], y[2], y[3]};
+                } else {
+#pragma unroll
+                    for (int b = 0; b < 4; ++b) {
+                        const int n = nb + b;
+                        if (n < N) cr[n] = accumulate ? y[b] + cr[n] : y[b];
+                    }
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    }  // work items
+}
+
+constexpr int kI8ReducePitch = 132;
+
+// C from the int32 split partials: workgroup (tile, wave, token block cb) sums that block's
+// 1024 slots over the splits in split order, stages 32 tokens x 128 rows in LDS and writes
+// them as runs of C rows (adding C when accumulating).
+__global__ __launch_bounds__(256) void gemm_split_reduce_i8_kernel(
+    const i32x4 *__restrict__ part, int32_t *__restrict__ c, int64_t M, int64_t N, int64_t ldc,
+    int tiles, int nsplit, int accumulate) {
+    __shared__ __attribute__((aligned(16))) int32_t st[32 * kI8ReducePitch];
+    const int tt = static_cast<int>(blockIdx.x >> 4);
+    const int wave = static_cast<int>((blockIdx.x >> 2) & 3);
+    const int cb = static_cast<int>(blockIdx.x & 3);
+    const int wn = wave & 1, wm = wave >> 1;
+    const int tiles_n = static_cast<int>((N + kI8Rows - 1) / kI8Rows);
+    const int64_t m0 = static_cast<int64_t>(tt / tiles_n) * kI8Tokens + 128 * wm + 32 * cb;
+    if (m0 >= M) return;
+    const int64_t per_split = static_cast<int64_t>(tiles) * 4 * 64 * 64;
+    const i32x4 *src = part + (static_cast<int64_t>(tt) * 4 + wave) * 4096;
+    for (int i = threadIdx.x; i < 1024; i += 256) {
+        const int lane = i & 63, a4 = (i >> 6) & 3, rb = i >> 8;
+        const int slot = ((rb * 4 + cb) * 4 + a4) * 64 + lane;
+        i32x4 v = src[slot];
+        for (int s = 1; s < nsplit; ++s) v += src[s * per_split + slot];
+        const int r = lane & 31, h = lane >> 5;
+        *reinterpret_cast<i32x4 *>(&st[r * kI8ReducePitch + 32 * rb + 8 * a4 + 4 * h]) = v;
+    }
+    __syncthreads();
+    const int64_t n0 = static_cast<int64_t>(tt % tiles_n) * kI8Rows + 128 * wn;
+    for (int i = threadIdx.x; i < 32 * 32; i += 256) {
+        const int tok = i >> 5, c4 = i & 31;
+        const int64_t m = m0 + tok;
+        if (m >= M) continue;
+        const i32x4 v = *reinterpret_cast<const i32x4 *>(&st[tok * kI8ReducePitch + 4 * c4]);
+        int32_t *cr = c + m * ldc;
+        const int64_t nb = n0 + 4 * c4;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const int64_t n = nb + b;
+            if (n < N) cr[n] = accumulate ? v[b] + cr[n] : v[b];
+        }
+    }
+}
+
+// Weight rows run as whole rounds of 256 x 256 tiles (the bf16 kernel's rule).
+int64_t i8_rows_whole_rounds(int64_t m, int64_t n) {
+    const int64_t tiles_m = (m + kI8Tokens - 1) / kI8Tokens;
+    const int64_t tiles_big = ((n + kI8Rows - 1) / kI8Rows) * tiles_m;
+    if (tiles_big < 160) return 0;
+    const int64_t cus = cu_count();
+    const int64_t rem = tiles_big % cus;
+    const int64_t n1 = (tiles_big - rem) / tiles_m * kI8Rows;
+    if (tiles_big > cus && rem != 0 && 2 * rem <= cus && n1 > 0 && n1 < n) return n1;
+    return n;
+}
+
+struct I8Plan {
+    int64_t n1;                       // rows [0, n1) as whole tiles
+    int64_t nsplit, sps, tiles;       // rows [n1, n): split-K items (nsplit > 1)
+};
+
+// About one workgroup per CU for the rows that do not fill whole rounds, at least four
+// k-steps per split.
+I8Plan i8_plan(int64_t m, int64_t n, int64_t k) {
+    const int64_t L = (k + kTrits - 1) / kTrits;
+    const int64_t nsteps = (L + 1) / 2;
+    I8Plan p{i8_rows_whole_rounds(m, n), 1, nsteps, 0};
+    if (p.n1 == n) return p;
+    p.tiles = ((n - p.n1 + kI8Rows - 1) / kI8Rows) * ((m + kI8Tokens - 1) / kI8Tokens);
+    int64_t ns = (cu_count() + p.tiles / 2) / p.tiles;
+    if (ns > nsteps / 4) ns = nsteps / 4;
+    if (ns < 2) {
+        ns = 1;
+    } else {
+        p.sps = (nsteps + ns - 1) / ns;
+        ns = (nsteps + p.sps - 1) / p.sps;
+    }
+    p.nsplit = ns;
+    return p;
+}
+
+}  // namespace
+
+// Whether the integer big-tile kernel takes this shape: more than 64 tokens, K a multiple
+// of 16 (whole 16-byte activation chunks), 16-byte aligned activations, 32-bit buffer
+// offsets and int indices.
+bool gemm_i8_fits(const void *x, int64_t m, int64_t n, int64_t k) {
+    const int64_t L = (k + kTrits - 1) / kTrits;
+    return m > 64 && k > 0 && k % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+           int64_t(kI8Rows) * L * kTrytes < 0x7FFFFFFF && int64_t(kI8Tokens) * k < 0x7FFFFFFF &&
+           m < (int64_t(1) << 30) && n < (int64_t(1) << 30) &&
+           ((m + kI8Tokens - 1) / kI8Tokens) * ((n + kI8Rows - 1) / kI8Rows) < (int64_t(1) << 26);
+}
+
+int64_t gemm_i8_workspace_bytes(int64_t m, int64_t n, int64_t k) {
+    const I8Plan p = i8_plan(m, n, k);
+    return p.nsplit > 1 ? p.nsplit * p.tiles * kI8Rows * kI8Tokens * 4 : 0;
+}
+
+// Rows [0, n1) as whole tiles and the rest as split-K items over ws when it is large
+// enough (else rows [n1, n) run as whole tiles too, in the same launch).
+hipError_t launch_gemm_i8(const void *x, const uint8_t *w, int32_t *c, int64_t m, int64_t n,
+                          int64_t k, bool accumulate, hipStream_t s, void *ws, int64_t ws_bytes) {
+    const int64_t L = (k + kTrits - 1) / kTrits;
+    I8Plan p = i8_plan(m, n, k);
+    const bool split = p.nsplit > 1 && ws != nullptr &&
+                       ws_bytes >= p.nsplit * p.tiles * kI8Rows * kI8Tokens * 4;
+    if (!split) p.n1 = n;
+    const int64_t tiles_m = (m + kI8Tokens - 1) / kI8Tokens;
+    const int64_t items = ((p.n1 + kI8Rows - 1) / kI8Rows) * tiles_m + (split ? p.nsplit * p.tiles : 0);
+    if (items <= 0) return hipSuccess;
+    const int64_t cus = cu_count();
+    gemm_w4_i8_kernel<<<dim3(static_cast<unsigned>(items < cus ? items : cus)), dim3(kI8Threads), 0, s>>>(
+        static_cast<const int8_t *>(x), w, c, static_cast<int>(m), static_cast<int>(n),
+        static_cast<int>(n), static_cast<int>(k), static_cast<int>(L), accumulate ? 1 : 0,
+        static_cast<int>(p.n1), split ? static_cast<int>(p.sps) : 0, static_cast<i32x4 *>(ws),
+        split ? static_cast<int>(p.nsplit) : 0);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || !split) return e;
+    gemm_split_reduce_i8_kernel<<<dim3(static_cast<unsigned>(p.tiles * 16)), dim3(256), 0, s>>>(
+        static_cast<const i32x4 *>(ws), c + p.n1, m, n - p.n1, n, static_cast<int>(p.tiles),
+        static_cast<int>(p.nsplit), accumulate ? 1 : 0);
+    return hipGetLastError();
+}
+
+}  // namespace t81hip

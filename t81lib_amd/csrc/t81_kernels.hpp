@@ -71,6 +71,13 @@ hipError_t launch_gemm(const void *x, int x_dtype, const uint8_t *w, void *c, in
                        hipStream_t s, void *ws = nullptr, int64_t ws_bytes = 0);
 int64_t gemm_workspace_bytes(int64_t m, int64_t n, int64_t k, int x_dtype);
 
+// gemm_i8.hip (K3, int8 activations, integer matrix cores): whether a shape takes it, the
+// workspace its split-K plan uses, and the launch (C int32; accumulate: C += product)
+bool gemm_i8_fits(const void *x, int64_t m, int64_t n, int64_t k);
+int64_t gemm_i8_workspace_bytes(int64_t m, int64_t n, int64_t k);
+hipError_t launch_gemm_i8(const void *x, const uint8_t *w, int32_t *c, int64_t m, int64_t n,
+                          int64_t k, bool accumulate, hipStream_t s, void *ws, int64_t ws_bytes);
+
 // Compute units of the current device (256 on MI355X), cached per device.
 int cu_count();
 

@@ -222,3 +222,76 @@ def test_k3_big_tile_integer_bf16_bit_exact(gpu, orc, M, N, K):
                                  bias=bias.to(gpu) if use_bias else None, kernel=3)
         want = expected(acc, alpha, beta, c.numpy(), bias.numpy() if use_bias else None)
         assert_bits(out.cpu().numpy(), want, f"alpha={alpha} beta={beta}")
+
+
+# ------------------------------------------------------------ K3, int8 activations --
+I8_FULL = [
+    # name, M, K, N: whole tiles + split-K items (gate_up), all split (M = 512), odd step
+    # counts (K = 4096: 43 steps), long K (down), M = 8192
+    ("llama.gate_up", 2048, 4096, 28672),
+    ("llama.down", 2048, 14336, 4096),
+    ("llama.qkv", 512, 4096, 6144),
+    ("llama.qkv", 8192, 4096, 6144),
+]
+I8_SMALL = [
+    # M > 64 and K % 16 == 0 take the integer big-tile kernel: ragged M / N, K past the last
+    # whole step, even and odd step counts, more tiles than CUs, few tiles (split-K)
+    (300, 256 * 160 + 13, 208), (260, 256 * 81 + 7, 480), (512, 256 * 200 - 5, 96),
+    (65, 1000, 4096), (300, 1000, 4112), (100, 2000, 4800), (257, 700, 16),
+]
+
+
+def _int8_problem(M, N, K, seed):
+    g = torch.Generator("cpu").manual_seed(seed)
+    w = torch.randn((N, K), generator=g)
+    x = torch.randint(-128, 128, (M, K), generator=g, dtype=torch.int8)
+    c = torch.randint(-(1 << 20), 1 << 20, (M, N), generator=g, dtype=torch.int32)
+    return w, x, c
+
+
+@pytest.mark.parametrize("M,N,K", I8_SMALL)
+def test_k3_int8_big_tile_bit_exact(gpu, orc, M, N, K):
+    """int32 results of the integer-MFMA kernel equal the int64 oracle, with beta = 0 and
+    beta = 1 (C accumulated exactly)."""
+    announce(f"exact K3 int8 M={M} N={N} K={K}")
+    w, x, c = _int8_problem(M, N, K, seed=M * 3 + N + K)
+    packed = ops.quantize_pack(w.to(gpu), 0.45, _lib.THR_CPP)
+    want = orc.trit_matmul_i64(x.numpy(), packed.cpu().numpy(), K)
+    xg = x.to(gpu)
+    out = ops.ternary_matmul(xg, packed, K, kernel=3)
+    assert out.dtype == torch.int32
+    np.testing.assert_array_equal(out.cpu().numpy().astype(np.int64), want)
+    out = ops.ternary_matmul(xg, packed, K, beta=1.0, c=c.to(gpu), kernel=3)
+    np.testing.assert_array_equal(out.cpu().numpy().astype(np.int64), want + c.numpy())
+
+
+@pytest.mark.parametrize("name,M,K,N", I8_FULL)
+def test_k3_int8_config4_bit_exact(gpu, orc, name, M, K, N):
+    """Config-4 shapes with int8 activations: every output against a float64 product of the
+    unpacked trits on the GPU (exact), and a sample from every region against the oracle."""
+    announce(f"exact K3 int8 {name} M={M} K={K} N={N}")
+    g = torch.Generator("cpu").manual_seed(M + N + K + 1)
+    w = torch.randn((N, K), generator=g)
+    x = torch.randint(-128, 128, (M, K), generator=g, dtype=torch.int8)
+    packed = ops.quantize_pack(w.to(gpu), 0.45, _lib.THR_CPP)
+    del w
+    xg = x.to(gpu)
+    exact = _gpu_exact_product(xg.to(torch.float64), packed, N, K)
+    gg = torch.Generator(gpu).manual_seed(M * 5 + N)
+    cg = torch.randint(-(1 << 20), 1 << 20, (M, N), generator=gg, device=gpu, dtype=torch.int32)
+    toks, rows = _sample(M, N, whole_round_rows(M, N), seed=M + K + 1)
+    acc_s = orc.trit_matmul_i64(x[torch.from_numpy(toks)].numpy(), packed.cpu().numpy()[rows], K)
+    tsel = torch.from_numpy(toks).to(gpu)
+    rsel = torch.from_numpy(rows).to(gpu)
+    for beta in (0.0, 1.0):
+        out = ops.ternary_matmul(xg, packed, K, beta=beta, c=cg.clone() if beta else None,
+                                 kernel=3)
+        want = exact + (cg.double() if beta else 0)
+        bad = int((out.double() != want).sum())
+        assert bad == 0, f"beta={beta}: {bad} of {M * N} outputs differ"
+        got_s = out[tsel][:, rsel].cpu().numpy().astype(np.int64)
+        want_s = acc_s + (cg[tsel][:, rsel].cpu().numpy().astype(np.int64) if beta else 0)
+        np.testing.assert_array_equal(got_s, want_s)
+        del out, want
+    del exact
+    torch.cuda.empty_cache()
