@@ -24,7 +24,9 @@ from typing import Optional
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-_ORACLE_SO = os.path.join(HERE, "liboracle.so")
+# T81_ORACLE_LIB selects another build of the same sources (tests/sanitize builds one
+# with AddressSanitizer + UndefinedBehaviorSanitizer and runs the oracle tests on it).
+_ORACLE_SO = os.environ.get("T81_ORACLE_LIB") or os.path.join(HERE, "liboracle.so")
 REF_DIR = os.path.join(HERE, "_ref")
 
 TRITS = 48

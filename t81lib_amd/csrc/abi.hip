@@ -65,6 +65,13 @@ int finish(hipError_t e, const char *where) {
 
 bool float_dtype(int d) { return d == T81_DTYPE_F32 || d == T81_DTYPE_BF16 || d == T81_DTYPE_F16; }
 
+// a * b elements (a, b >= 0) beyond any device buffer (2^40, far above 288 GB of
+// elements of any type): rejected before a launch forms the product, which could overflow.
+bool too_many(int64_t a, int64_t b) {
+    constexpr int64_t kLimit = int64_t{1} << 40;
+    return a > kLimit || b > kLimit || (a > 0 && b > kLimit / a);
+}
+
 // python/bindings.cpp:419-421 / 463-465 (C++ form); t81/torch/__init__.py:45 (torch form,
 // clamped by the caller -- here only range-checked).
 int check_threshold(float thr, int mode) {
@@ -128,6 +135,7 @@ int t81_hip_quantize_pack(const void *w, int w_dtype, uint8_t *out, int64_t rows
                           float threshold, int thr_mode, void *stream) {
     if (int rc = check_threshold(threshold, thr_mode)) return rc;
     if (rows < 0 || cols < 0) return fail(T81_HIP_EINVAL_SHAPE, "rows and cols must be non-negative");
+    if (too_many(rows, cols)) return fail(T81_HIP_EINVAL_SHAPE, "rows x cols too large");
     if (!float_dtype(w_dtype)) return fail(T81_HIP_EINVAL_DTYPE, "weights must be a float dtype");
     if (rows > 0 && cols > 0 && (w == nullptr || out == nullptr))
         return fail(T81_HIP_EINVAL_POINTER, "null data pointer");
@@ -145,6 +153,7 @@ int t81_hip_quantize(const void *src, int dtype, int8_t *out, int64_t count, flo
                      int thr_mode, void *stream) {
     if (int rc = check_threshold(threshold, thr_mode)) return rc;
     if (count < 0) return fail(T81_HIP_EINVAL_SHAPE, "count must be non-negative");
+    if (too_many(count, 1)) return fail(T81_HIP_EINVAL_SHAPE, "count too large");
     if (!float_dtype(dtype)) return fail(T81_HIP_EINVAL_DTYPE, "input must be a float dtype");
     if (count > 0 && (src == nullptr || out == nullptr))
         return fail(T81_HIP_EINVAL_POINTER, "null data pointer");
@@ -159,6 +168,7 @@ int t81_hip_pack_cols(const void *x, int x_dtype, uint8_t *out, int64_t tokens, 
                       float threshold, int thr_mode, void *stream) {
     if (int rc = check_threshold(threshold, thr_mode)) return rc;
     if (tokens < 0 || k < 0) return fail(T81_HIP_EINVAL_SHAPE, "dimensions must be non-negative");
+    if (too_many(tokens, k)) return fail(T81_HIP_EINVAL_SHAPE, "tokens x k too large");
     if (!float_dtype(x_dtype)) return fail(T81_HIP_EINVAL_DTYPE, "input must be a float dtype");
     if (tokens > 0 && k > 0 && (x == nullptr || out == nullptr))
         return fail(T81_HIP_EINVAL_POINTER, "null data pointer");
@@ -177,8 +187,11 @@ int t81_hip_unpack(const uint8_t *packed, int8_t *out, int64_t rows, int64_t lim
                    int64_t cols, void *stream) {
     if (rows < 0 || cols < 0 || limbs_per_row < 0)
         return fail(T81_HIP_EINVAL_SHAPE, "rows and cols must be non-negative");
-    if (cols > limbs_per_row * 48)
+    // limbs needed for cols trits, compared without forming limbs_per_row * 48 (overflow)
+    if (cols / 48 + (cols % 48 != 0 ? 1 : 0) > limbs_per_row)
         return fail(T81_HIP_EINVAL_SHAPE, "cols exceeds packed trit capacity");
+    if (too_many(rows, cols) || too_many(rows, limbs_per_row))
+        return fail(T81_HIP_EINVAL_SHAPE, "unpack dimensions too large");
     if (rows > 0 && cols > 0 && (packed == nullptr || out == nullptr))
         return fail(T81_HIP_EINVAL_POINTER, "null data pointer");
     if (int rc = require_device("t81_hip_unpack")) return rc;
@@ -190,6 +203,7 @@ int t81_hip_unpack(const uint8_t *packed, int8_t *out, int64_t rows, int64_t lim
 int t81_hip_validate_packed(const uint8_t *packed, int64_t count, int32_t *bad_count,
                             void *stream) {
     if (count < 0) return fail(T81_HIP_EINVAL_SHAPE, "count must be non-negative");
+    if (too_many(count, 1)) return fail(T81_HIP_EINVAL_SHAPE, "count too large");
     if (bad_count == nullptr || (count > 0 && packed == nullptr))
         return fail(T81_HIP_EINVAL_POINTER, "null data pointer");
     if (int rc = require_device("t81_hip_validate_packed")) return rc;
@@ -362,6 +376,7 @@ int t81_hip_tq_quantize(const float *src, uint8_t *dst, int64_t rows, int64_t co
     if (quant != T81_TQ1_0 && quant != T81_TQ2_0)
         return fail(T81_HIP_EINVAL_DTYPE, "quant must be T81_TQ1_0 (34) or T81_TQ2_0 (35)");
     if (rows < 0 || cols < 0) return fail(T81_HIP_EINVAL_SHAPE, "rows and cols must be non-negative");
+    if (too_many(rows, cols)) return fail(T81_HIP_EINVAL_SHAPE, "rows x cols too large");
     if (rows > 0 && cols > 0 && (src == nullptr || dst == nullptr))
         return fail(T81_HIP_EINVAL_POINTER, "null data pointer");
     if (reinterpret_cast<uintptr_t>(src) % 4 != 0)
@@ -381,6 +396,7 @@ int t81_hip_tq_dequantize(const uint8_t *src, float *dst, int64_t rows, int64_t 
     if (quant != T81_TQ1_0 && quant != T81_TQ2_0)
         return fail(T81_HIP_EINVAL_DTYPE, "quant must be T81_TQ1_0 (34) or T81_TQ2_0 (35)");
     if (rows < 0 || cols < 0) return fail(T81_HIP_EINVAL_SHAPE, "rows and cols must be non-negative");
+    if (too_many(rows, cols)) return fail(T81_HIP_EINVAL_SHAPE, "rows x cols too large");
     if (rows > 0 && cols > 0 && (src == nullptr || dst == nullptr))
         return fail(T81_HIP_EINVAL_POINTER, "null data pointer");
     if (reinterpret_cast<uintptr_t>(dst) % 4 != 0)
