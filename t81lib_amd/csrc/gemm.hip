@@ -342,7 +342,8 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_kernel(
 //    X[c, 96s + 48h + 8J .. +8], 16 bytes of the activation tile;
 //  * the weights decode (LDS table) half a limb at a time: half p gives the
 //    A fragments of J = 3p..3p+2 for all four row blocks.  The decode of the
-//    next half runs while the MFMAs of the current one do;
+//    next half runs while the MFMAs of the current one do; the weights of a step
+//    are loaded two steps ahead;
 //  * the activation tile of step s + 1 goes straight from global memory into the
 //    other LDS buffer (buffer loads with the LDS bit, no registers) at the start
 //    of step s; one barrier per step.  Tile rows are 13 16-byte slots (12 chunks of
@@ -552,43 +553,48 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
         out[4] = e[2].y | e[3].x;
         out[5] = e[3].y;
     };
-    u32x4 wcur[4], wnxt[4];
+    u32x4 wcur[4], wnxt[4], wnn[4];
     bf16x8 a0[4][3], a1[4][3];
     if (s_begin < s_end) {
         fetch_w(s_begin, wcur);
         load_tile(s_begin, std::integral_constant<int, 0>());
     }
-    // vmcnt(0): the tile's LDS writes have landed before the barrier publishes them
-    __builtin_amdgcn_s_waitcnt(0x0F70);
+    fetch_w(s_begin + 1, wnxt);   // stays in flight across the barrier
+    // vmcnt(4): the tile's LDS writes have landed before the barrier publishes them
+    __builtin_amdgcn_s_waitcnt(0x0F74);
     __syncthreads();
     if (s_begin < s_end) decode_half(wcur, 0, a0);
 
     // One k-step as 24 chunks of four MFMAs (chunks 0-11: half 0 with a0, 12-23: half 1
-    // with a1), one B fragment each, read two chunks ahead.  Chunks are fenced so that
+    // with a1), one B fragment each, read three chunks ahead.  Chunks are fenced so that
     // each also carries its share of the decode -- chunks 0-7: half 1 of wcur into a1,
-    // chunks 12-19: half 0 of wnxt (the next step) into a0; table reads in one chunk, the
-    // merge in the next -- and of the loads for the next step (chunks 0-11; unconditional:
-    // past the last step they read zeros or unused weight bytes).  Steps alternate
+    // chunks 12-19: half 0 of wnxt (the next step) into a0; table reads two chunks ahead
+    // of their merge -- and of the loads: the tile of the next step (chunks 0-11), then
+    // the weights of the step after it (chunk 12).  Issued after the tile loads, the
+    // weight loads can stay in flight across the end-of-step wait (vmcnt(4)), so they
+    // have a step and a half to land, not half a step.  (All loads are unconditional:
+    // past the last step they read zeros or unused weight bytes.)  Steps alternate
     // between the two tile buffers, so the loop below runs two steps per iteration.
     auto step_body = [&](int step, auto bufc, auto otherc) {
-        u32x4 bq[3];
+        u32x4 bq[4];
         bq[0] = read_b(bufc, 0, 0);
         bq[1] = read_b(bufc, 0, 1);
-        uint2 e[2][4];
+        bq[2] = read_b(bufc, 0, 2);
+        uint2 e[3][4];
         uint32_t pairs[4][12];
 #pragma unroll
         for (int g = 0; g < 24; ++g) {
             const int p = g / 12;
             const int gg = g % 12;
-            if (g + 2 < 24) bq[(g + 2) % 3] = read_b(bufc, (g + 2) / 12, (g + 2) % 12);
+            if (g + 3 < 24) bq[(g + 3) % 4] = read_b(bufc, (g + 3) / 12, (g + 3) % 12);
             if (gg < 8)
-                table_fetch((p == 0 ? wcur : wnxt)[gg / 2][2 * (1 - p) + (gg % 2)], e[gg & 1]);
-            if (gg >= 1 && gg <= 8)
-                table_merge(e[(gg - 1) & 1], &pairs[(gg - 1) / 2][6 * ((gg - 1) % 2)]);
-            if (g == 0) fetch_w(step + 1, wnxt);
+                table_fetch((p == 0 ? wcur : wnxt)[gg / 2][2 * (1 - p) + (gg % 2)], e[gg % 3]);
+            if (gg >= 2 && gg <= 9)
+                table_merge(e[(gg - 2) % 3], &pairs[(gg - 2) / 2][6 * ((gg - 2) % 2)]);
             if (g < 12) load_tile_part(step + 1, otherc, g);
             if (g == 11) load_tile_part(step + 1, otherc, 12);
-            const bf16x8 b = __builtin_bit_cast(bf16x8, bq[g % 3]);
+            if (g == 12) fetch_w(step + 2, wnn);
+            const bf16x8 b = __builtin_bit_cast(bf16x8, bq[g % 4]);
             const bf16x8(&a)[4][3] = p == 0 ? a0 : a1;
 #pragma unroll
             for (int rb = 0; rb < 4; ++rb)
@@ -608,8 +614,12 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
             __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb) wcur[rb] = wnxt[rb];
-        __builtin_amdgcn_s_waitcnt(0x0F70);
+        for (int rb = 0; rb < 4; ++rb) {
+            wcur[rb] = wnxt[rb];
+            wnxt[rb] = wnn[rb];
+        }
+        // vmcnt(4): the tile loads are older than the four weight loads of step + 2
+        __builtin_amdgcn_s_waitcnt(0x0F74);
         __syncthreads();
     };
     int step = s_begin;
