@@ -110,7 +110,7 @@ int t81_hip_ternary_matmul_kernel(int which, const void *x, int x_dtype, const u
 
 /* Same, with a caller-owned device workspace: which = 0 (by M, as
  * t81_hip_ternary_matmul), 2 or 3.  When K3 has few output tiles (bf16
- * activations, K % 8 == 0) and workspace_bytes is at least
+ * activations, K % 8 == 0), or K2 runs 5..16 tokens, and workspace_bytes is at least
  * t81_hip_ternary_matmul_workspace_size(...), K is split over several workgroups
  * per tile: each writes its partial tile to the workspace and a second kernel sums
  * the partials in split order (deterministic).  NULL / 0 bytes: no split.  The

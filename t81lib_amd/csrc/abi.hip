@@ -228,7 +228,8 @@ int t81_hip_ternary_matmul_ws(int which, const void *x, int x_dtype, const uint8
     const hipStream_t s = static_cast<hipStream_t>(stream);
     hipError_t e;
     if (which == 2)
-        e = t81hip::launch_gemv(x, x_dtype, w, c, static_cast<int>(m), n, k, alpha, beta, bias, s);
+        e = t81hip::launch_gemv(x, x_dtype, w, c, static_cast<int>(m), n, k, alpha, beta, bias, s,
+                                workspace, workspace_bytes);
     else
         e = t81hip::launch_gemm(x, x_dtype, w, c, m, n, k, alpha, beta, bias, s, workspace,
                                 workspace_bytes);
@@ -251,7 +252,10 @@ int t81_hip_ternary_matmul(const void *x, int x_dtype, const uint8_t *w, void *c
 }
 
 int64_t t81_hip_ternary_matmul_workspace_size(int64_t m, int64_t n, int64_t k, int x_dtype) {
-    if (m <= 16 || m < 0 || n < 0 || k < 0) return 0;
+    if (m < 0 || n < 0 || k < 0 || m > INT_MAX / 2 || n > (int64_t(1) << 40) ||
+        k > (int64_t(1) << 31))
+        return 0;
+    if (m <= 16) return t81hip::gemv_workspace_bytes(m, n, k, x_dtype);
     return t81hip::gemm_workspace_bytes(m, n, k, x_dtype);
 }
 

@@ -397,6 +397,290 @@ __global__ __launch_bounds__(64 * KS) void gemv_stream_kernel(const void *__rest
     reduce_store<XT, G, KS>(acc, red, wave, lane, M, N, n0, c, alpha, beta, bias);
 }
 
+// ---------------------------------------------------------------------------------
+// gemv_tile_kernel: 5..16 tokens fill the 16 columns of every MFMA tile, so one load of
+// 16 rows x 4 limbs (16 bytes per lane) yields a whole 16 x 16 block of partial sums,
+// and the activations it meets -- 16 tokens x 192 trits, six 16-byte fragments per
+// lane -- are the same for every 16-row group.  So a wave owns one 4-limb sub-block of
+// K for its whole life: that sub-block's activations are loaded once, stay in
+// registers as the B operand, and R row groups stream through them (6 KB of activation
+// reads per wave against R KB of weights, where the stream kernel above reads them
+// again for every one or two row groups).
+//
+// Workgroup (row block b, split p): R row groups (16R rows) x NW consecutive
+// sub-blocks, wave w taking sub-block p * NW + w.  Each load is a new row group, so it
+// gets its own accumulator; the loads run four in flight, each slot refilled as soon
+// as it is decoded, the table reads of load t + 1 issued before the MFMAs of load t
+// (the column-strip kernel's pipeline).  At the end the NW partial tiles of each row
+// group are summed through LDS in wave order.  With one split the workgroup applies
+// alpha, beta and bias and stores C; with P > 1 splits it stores its raw sums to the
+// caller's workspace (one M x N row-major matrix per split) and gemv_split_sum_kernel
+// adds the splits in split order.  Every sum has a fixed order.
+//
+// Lane (r, q): A = limb 4 * sb + q of row 16 t + r of the block (load t); B = the
+// activations of token r for the same limb (zeros for r >= M or past K).  A limb past L
+// reads zeros (outside the buffer range), which decode to finite trits and meet zero
+// activations; rows past N read zeros and are not stored.  Waves whose sub-block is
+// past the last one (the last split of a K that is not a multiple of NW sub-blocks)
+// load nothing and contribute zero tiles.
+template <int XT, int NW, int R>
+__global__ __launch_bounds__(64 * NW) void gemv_tile_kernel(
+    const void *__restrict__ x, const uint8_t *__restrict__ w, void *__restrict__ c, int M,
+    int64_t N, int64_t K, int L, int nsb, int nb, int x_aligned, float alpha, float beta,
+    const float *__restrict__ bias, float *__restrict__ part) {
+    constexpr int D = R < kDepth ? R : kDepth;
+    __shared__ __attribute__((aligned(16))) uint8_t lut[kLutBytes];
+    __shared__ __attribute__((aligned(16))) floatx4 red[NW * R * 64];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r = lane & 15;
+    const int q = lane >> 4;
+    const int b = static_cast<int>(blockIdx.x % static_cast<unsigned>(nb));
+    const int p = static_cast<int>(blockIdx.x / static_cast<unsigned>(nb));
+    const int64_t row0 = static_cast<int64_t>(b) * 16 * R;
+    const int sb = p * NW + wave;  // wave-uniform
+    const bool active = sb < nsb;
+    const int limb = 4 * sb + q;
+    const bool in_row = active && limb < L;
+
+    floatx4 acc[R];
+#pragma unroll
+    for (int t = 0; t < R; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    // Weights through a buffer based at the block's first row: rows past N read zeros.
+    const int64_t remain = (N - row0) * L * kTrytes;
+    const int nrec = remain < 0x7FFFFFFF ? static_cast<int>(remain) : 0x7FFFFFFF;
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(w + row0 * L * kTrytes), 0, nrec, 0x00020000);
+    const uint32_t row_bytes = static_cast<uint32_t>(L) * kTrytes;
+    const uint32_t lane_off =
+        static_cast<uint32_t>(r) * row_bytes + static_cast<uint32_t>(limb) * kTrytes;
+    auto fetch = [&](int t) -> u32x4 {
+        const uint32_t off =
+            in_row ? lane_off + 16u * static_cast<uint32_t>(t) * row_bytes : kOobOffset;
+        return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0));
+    };
+
+    XRaw xr[6];
+    u32x4 ring[D];  // load t lives in ring[t % D]
+    if (active) {
+        // B: the activations of token r for the lane's limb, issued before the weights
+        const bool bvalid = r < M && in_row;
+        const int64_t xrow = static_cast<int64_t>(r < M ? r : 0) * K;
+        const int64_t kb = static_cast<int64_t>(limb) * kTrits;
+        if (x_aligned) {
+#pragma unroll
+            for (int j = 0; j < 6; ++j) xr[j] = load_x8_raw<XT, true>(x, xrow, kb + 8 * j, K, bvalid);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 6; ++j) xr[j] = load_x8_raw<XT, false>(x, xrow, kb + 8 * j, K, bvalid);
+        }
+#pragma unroll
+        for (int t = 0; t < D; ++t) ring[t] = fetch(t);
+    }
+    lut_fill(lut, tid, 64 * NW);
+    __syncthreads();
+
+    if (active) {
+        bf16x8 bh[6], bl[6];
+#pragma unroll
+        for (int j = 0; j < 6; ++j) cvt_x8<XT>(xr[j], bh[j], bl[j]);
+        uint32_t cur[24], nxt[24];
+#pragma unroll
+        for (int d = 0; d < 4; ++d) decode_dword(lut, ring[0][d], cur + 6 * d);
+        __builtin_amdgcn_sched_barrier(0);
+        if (D < R) ring[0] = fetch(D);
+#pragma unroll
+        for (int t = 0; t < R; ++t) {
+            if (t + 1 < R) {
+#pragma unroll
+                for (int d = 0; d < 4; ++d) decode_dword(lut, ring[(t + 1) % D][d], nxt + 6 * d);
+                __builtin_amdgcn_sched_barrier(0);
+                if (t + 1 + D < R) ring[(t + 1) % D] = fetch(t + 1 + D);
+            }
+            acc[t] = mfma_pairs<XT>(cur, bh, bl, acc[t]);
+#pragma unroll
+            for (int e = 0; e < 24; ++e) cur[e] = nxt[e];
+        }
+    }
+
+    // ---- per row group: the NW partial tiles summed in wave order ----
+#pragma unroll
+    for (int t = 0; t < R; ++t) red[(wave * R + t) * 64 + lane] = acc[t];
+    __syncthreads();
+    for (int e = tid; e < R * 64; e += 64 * NW) {
+        const int t = e >> 6;
+        const int l = e & 63;
+        floatx4 v = red[t * 64 + l];
+#pragma unroll
+        for (int ww = 1; ww < NW; ++ww) v += red[(ww * R + t) * 64 + l];
+        const int64_t n0 = row0 + 16 * t;
+        if (part == nullptr) {
+            store_tile<XT>(v, l, M, N, n0, c, alpha, beta, bias);
+        } else {
+            // lane l of the tile holds rows n0 + 4 (l / 16) + i of token l % 16
+            const int m = l & 15;
+            if (m >= M) continue;
+            const int64_t nb4 = n0 + 4 * (l >> 4);
+            float *dst = part + (static_cast<int64_t>(p) * M + m) * N + nb4;
+            if (nb4 + 3 < N && (reinterpret_cast<uintptr_t>(dst) & 15u) == 0) {
+                *reinterpret_cast<float4 *>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (nb4 + i < N) dst[i] = v[i];
+            }
+        }
+    }
+}
+
+// C from the P split partials of gemv_tile_kernel (M x N row-major each, raw sums):
+// summed in split order, then alpha, beta and bias as store_tile applies them.  For
+// int8 activations every partial and every sum is an integer below 2^24 in magnitude
+// (K <= 131071), so the float sums are exact and convert to int32 exactly.
+template <int XT>
+__global__ __launch_bounds__(256) void gemv_split_sum_kernel(
+    const float *__restrict__ part, void *__restrict__ c, int M, int64_t N, int P, float alpha,
+    float beta, const float *__restrict__ bias) {
+    const int64_t total = static_cast<int64_t>(M) * N;
+    const int64_t quads = (N + 3) / 4;   // four consecutive outputs of one row per thread
+    const bool vec = N % 4 == 0;         // then every quad is 16-byte aligned (part, C)
+    for (int64_t g = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; g < M * quads;
+         g += static_cast<int64_t>(gridDim.x) * 256) {
+        const int64_t m = g / quads;
+        const int64_t n0 = (g - m * quads) * 4;
+        const int64_t base = m * N + n0;
+        const int cnt = N - n0 < 4 ? static_cast<int>(N - n0) : 4;
+        float v[4];
+        if (vec) {
+            float4 a = *reinterpret_cast<const float4 *>(part + base);
+            for (int sp = 1; sp < P; ++sp) {
+                const float4 b = *reinterpret_cast<const float4 *>(part + sp * total + base);
+                a.x += b.x;
+                a.y += b.y;
+                a.z += b.z;
+                a.w += b.w;
+            }
+            v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        } else {
+            for (int i = 0; i < cnt; ++i) {
+                float t = part[base + i];
+                for (int sp = 1; sp < P; ++sp) t += part[sp * total + base + i];
+                v[i] = t;
+            }
+        }
+        for (int i = 0; i < cnt; ++i) {
+            if constexpr (XT == kDtypeI8) {
+                int32_t *cp = static_cast<int32_t *>(c) + base + i;
+                int32_t y = static_cast<int32_t>(v[i]);
+                if (beta != 0.0f) y += *cp;
+                *cp = y;
+            } else {
+                float *cp = static_cast<float *>(c) + base + i;
+                float y = alpha * v[i];
+                if (beta != 0.0f) y = y + beta * *cp;
+                if (bias != nullptr) y = y + bias[n0 + i];
+                *cp = y;
+            }
+        }
+    }
+}
+
+// The tile kernel's plan for a shape: NW waves (sub-blocks) per workgroup, P splits of K,
+// R row groups per workgroup -- four, fewer where the grid would not give every CU a
+// workgroup (a plan sweep on the config-3/4 shapes at 16 tokens: eight waves and four
+// row groups were best or within 5 % of best on each).  P depends on K alone, so the
+// order of every sum is a function of the shape.
+struct TilePlan {
+    int nw, r, p;
+    int64_t nb;
+};
+TilePlan gemv_tile_plan(int64_t n, int64_t k) {
+    const int64_t L = (k + kTrits - 1) / kTrits;
+    const int64_t nsb = (L + 3) / 4;
+    TilePlan t;
+    t.nw = nsb <= 4 ? 4 : 8;
+    t.p = static_cast<int>((nsb + t.nw - 1) / t.nw);
+    const int64_t groups = (n + 15) / 16;
+    const int64_t cus = cu_count();
+    t.r = 4;
+    while (t.r > 1 && (groups + t.r - 1) / t.r * t.p < cus) t.r /= 2;
+    t.nb = (groups + t.r - 1) / t.r;
+    return t;
+}
+
+// Whether the tile kernel takes this call, and the workspace its splits need.  Its time
+// hardly depends on M, and its K splits end in a second launch (about 3 us on top of the
+// main kernel at 16 tokens); measured against the stream / wave kernels it is faster
+// for 9..16 tokens over a long K (>= 32 sub-blocks) and at most 8192 rows -- 14336 ->
+// 4096 at 16 tokens 22.5 -> 17.6 us, 8192 -> 3072 13.7 -> 10.1 us -- and slower on
+// the wide and short-K config-3/4 shapes, which keep those kernels.
+bool gemv_tile_fits(int m, int64_t n, int64_t k) {
+    const int64_t L = (k + kTrits - 1) / kTrits;
+    const int64_t nsb = (L + 3) / 4;
+    // buffer offsets within a block (16 R rows, R <= 4) stay below 2^31; grid and
+    // split indices fit the kernel's ints
+    return m >= 9 && m <= 16 && n > 0 && n <= 8192 && nsb >= 32 &&
+           int64_t{64} * L * kTrytes < 0x7FFFFFFF && (n + 15) / 16 * nsb < (int64_t{1} << 30);
+}
+
+int64_t gemv_tile_workspace_bytes(int m, int64_t n, int64_t k) {
+    if (!gemv_tile_fits(m, n, k)) return 0;
+    const TilePlan t = gemv_tile_plan(n, k);
+    return t.p > 1 ? int64_t{4} * t.p * m * n : 0;
+}
+
+template <int XT, int NW, int R>
+hipError_t launch_tile_r(const TilePlan &t, const void *x, const uint8_t *w, void *c, int m,
+                         int64_t n, int64_t k, bool aligned, float alpha, float beta,
+                         const float *bias, float *part, hipStream_t s) {
+    const int L = static_cast<int>((k + kTrits - 1) / kTrits);
+    const int nsb = (L + 3) / 4;
+    gemv_tile_kernel<XT, NW, R><<<dim3(static_cast<unsigned>(t.nb * t.p)), dim3(64 * NW), 0, s>>>(
+        x, w, c, m, n, k, L, nsb, static_cast<int>(t.nb), aligned ? 1 : 0, alpha, beta, bias,
+        t.p > 1 ? part : nullptr);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || t.p == 1) return e;
+    const int64_t quads = static_cast<int64_t>(m) * ((n + 3) / 4);
+    const int64_t blocks = std::min<int64_t>((quads + 255) / 256, 4 * cu_count());
+    gemv_split_sum_kernel<XT><<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s>>>(
+        part, c, m, n, t.p, alpha, beta, bias);
+    return hipGetLastError();
+}
+
+template <int XT, int NW>
+hipError_t launch_tile_nw(const TilePlan &t, const void *x, const uint8_t *w, void *c, int m,
+                          int64_t n, int64_t k, bool aligned, float alpha, float beta,
+                          const float *bias, float *part, hipStream_t s) {
+    switch (t.r) {
+        case 4: return launch_tile_r<XT, NW, 4>(t, x, w, c, m, n, k, aligned, alpha, beta, bias, part, s);
+        case 2: return launch_tile_r<XT, NW, 2>(t, x, w, c, m, n, k, aligned, alpha, beta, bias, part, s);
+        default: return launch_tile_r<XT, NW, 1>(t, x, w, c, m, n, k, aligned, alpha, beta, bias, part, s);
+    }
+}
+
+// Runs the tile kernel when the shape fits and the workspace holds its splits;
+// *handled is false otherwise (the caller then takes the wave / stream kernels).
+template <int XT>
+hipError_t launch_gemv_tile(bool *handled, const void *x, const uint8_t *w, void *c, int m,
+                            int64_t n, int64_t k, float alpha, float beta, const float *bias,
+                            void *ws, int64_t ws_bytes, hipStream_t s) {
+    *handled = false;
+    if (!gemv_tile_fits(m, n, k)) return hipSuccess;
+    const TilePlan t = gemv_tile_plan(n, k);
+    if (t.p > 1 && (ws == nullptr || ws_bytes < int64_t{4} * t.p * m * n)) return hipSuccess;
+    constexpr int64_t kElem = XT == kDtypeF32 ? 4 : (XT == kDtypeBF16 ? 2 : 1);
+    const bool aligned =
+        (k % 8 == 0) && (reinterpret_cast<uintptr_t>(x) % (kElem == 1 ? 8 : 16) == 0);
+    *handled = true;
+    float *part = static_cast<float *>(ws);
+    if (t.nw == 4)
+        return launch_tile_nw<XT, 4>(t, x, w, c, m, n, k, aligned, alpha, beta, bias, part, s);
+    return launch_tile_nw<XT, 8>(t, x, w, c, m, n, k, aligned, alpha, beta, bias, part, s);
+}
+
 template <int XT, int G, bool kAligned, int KS>
 hipError_t launch_stream(const void *x, const uint8_t *w, void *c, int m, int64_t n, int64_t k,
                          int64_t L, float alpha, float beta, const float *bias, hipStream_t s) {
@@ -536,11 +820,33 @@ hipError_t launch_gemv_x(const void *x, const uint8_t *w, void *c, int m, int64_
 
 }  // namespace
 
+int64_t gemv_workspace_bytes(int64_t m, int64_t n, int64_t k, int x_dtype) {
+    (void)x_dtype;  // the partials are float32 for every activation type
+    if (m < 5 || m > 16 || n <= 0 || k <= 0) return 0;
+    return gemv_tile_workspace_bytes(static_cast<int>(m), n, k);
+}
+
 hipError_t launch_gemv(const void *x, int x_dtype, const uint8_t *w, void *c, int m, int64_t n,
-                       int64_t k, float alpha, float beta, const float *bias, hipStream_t s) {
+                       int64_t k, float alpha, float beta, const float *bias, hipStream_t s,
+                       void *ws, int64_t ws_bytes) {
     if (m == 0 || n == 0) return hipSuccess;
     bool handled = false;
-    const hipError_t e = launch_gemv_strip(&handled, x, x_dtype, w, c, m, n, k, alpha, beta, bias, s);
+    hipError_t e = launch_gemv_strip(&handled, x, x_dtype, w, c, m, n, k, alpha, beta, bias, s);
+    if (handled || e != hipSuccess) return e;
+    switch (x_dtype) {
+        case kDtypeBF16:
+            e = launch_gemv_tile<kDtypeBF16>(&handled, x, w, c, m, n, k, alpha, beta, bias, ws,
+                                             ws_bytes, s);
+            break;
+        case kDtypeF32:
+            e = launch_gemv_tile<kDtypeF32>(&handled, x, w, c, m, n, k, alpha, beta, bias, ws,
+                                            ws_bytes, s);
+            break;
+        default:
+            e = launch_gemv_tile<kDtypeI8>(&handled, x, w, c, m, n, k, alpha, beta, bias, ws,
+                                           ws_bytes, s);
+            break;
+    }
     if (handled || e != hipSuccess) return e;
     switch (x_dtype) {
         case kDtypeBF16: return launch_gemv_x<kDtypeBF16>(x, w, c, m, n, k, alpha, beta, bias, s);

@@ -12,6 +12,10 @@ namespace {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
+// Cache-policy operand of a buffer load: the non-temporal (streaming) hint, bit 1 of
+// the gfx950 cache-policy field.
+constexpr int kCpolNt = 2;
+
 // ---- activation fragments: 8 consecutive X[m, k0 .. k0+8) as bf16 (hi, lo) ----
 // Out-of-range lanes read from kZeroBlock / kPadLimb instead of selecting a value
 // after the load: the loads stay unconditional and nothing has to wait for them

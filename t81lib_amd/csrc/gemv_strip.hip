@@ -108,12 +108,13 @@ __device__ __forceinline__ float strip_keep(floatx4 v, int j) {
 }
 
 // S: sub-positions per quarter (range = 4*S limbs, S in {4, 8, 16}); NW: waves, one range
-// each at a time; R: loads per range, i.e. R * (16 / S) rows per workgroup.  kNat: limbs
+// each at a time; R: loads per range, i.e. R * (16 / S) rows per workgroup.  kNt: weight
+// loads carry the non-temporal hint (see launch_strip_x).  kNat: limbs
 // decoded in natural trit order (E and F tables, six MFMAs per limb) instead of padded
 // order (E table only, eight MFMAs) -- fewer MFMAs for two ORs per dword; the launch uses
 // it for one token over one 64-limb range or up to three 32-limb ranges, where it
 // measured faster (4096 x 14336: 7.03 -> 6.95 us; 3072 x 9216: 5.36 -> 5.09 us).
-template <int XT, int S, int NW, int R, bool kNat = false>
+template <int XT, int S, int NW, int R, bool kNat = false, bool kNt = false>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void gemv_strip_kernel(
     const void *__restrict__ x, const uint8_t *__restrict__ w, void *__restrict__ c, int M,
     int64_t N, int64_t K, int L, int nranges, int x_aligned, float alpha, float beta,
@@ -176,8 +177,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
         auto fetch = [&](int t) -> u32x4 {
             const uint32_t off = in_row ? lane_off + static_cast<uint32_t>(t * RPI) * row_bytes
                                         : kStripOob;
-            return __builtin_bit_cast(u32x4,
-                                      __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0));
+            return __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, kNt ? kCpolNt : 0));
         };
         u32x4 ring[D];  // load t lives in ring[t % D]
 #pragma unroll
@@ -283,58 +284,65 @@ struct StripArgs {
     hipStream_t s;
 };
 
-template <int XT, int S, int NW, int R, bool kNat = false>
+template <int XT, int S, int NW, int R, bool kNat = false, bool kNt = false>
 hipError_t launch_strip(const StripArgs &a) {
     constexpr int H = R * (16 / S);
     const int64_t blocks = (a.n + H - 1) / H;
-    gemv_strip_kernel<XT, S, NW, R, kNat><<<dim3(static_cast<unsigned>(blocks)), dim3(64 * NW), 0,
+    gemv_strip_kernel<XT, S, NW, R, kNat, kNt><<<dim3(static_cast<unsigned>(blocks)), dim3(64 * NW), 0,
                                        a.s>>>(a.x, a.w, a.c, a.m, a.n, a.k, a.L, a.nranges,
                                               a.aligned ? 1 : 0, a.alpha, a.beta, a.bias);
     return hipGetLastError();
 }
 
-template <int XT, int S, int R>
+template <int XT, int S, int R, bool kNt = false>
 hipError_t launch_strip_nw(int nw, const StripArgs &a) {
     switch (nw) {
-        case 1: return launch_strip<XT, S, 1, R>(a);
-        case 2: return launch_strip<XT, S, 2, R>(a);
-        case 3: return launch_strip<XT, S, 3, R>(a);
-        case 4: return launch_strip<XT, S, 4, R>(a);
-        case 5: return launch_strip<XT, S, 5, R>(a);
-        case 6: return launch_strip<XT, S, 6, R>(a);
-        case 7: return launch_strip<XT, S, 7, R>(a);
-        default: return launch_strip<XT, S, 8, R>(a);
+        case 1: return launch_strip<XT, S, 1, R, false, kNt>(a);
+        case 2: return launch_strip<XT, S, 2, R, false, kNt>(a);
+        case 3: return launch_strip<XT, S, 3, R, false, kNt>(a);
+        case 4: return launch_strip<XT, S, 4, R, false, kNt>(a);
+        case 5: return launch_strip<XT, S, 5, R, false, kNt>(a);
+        case 6: return launch_strip<XT, S, 6, R, false, kNt>(a);
+        case 7: return launch_strip<XT, S, 7, R, false, kNt>(a);
+        default: return launch_strip<XT, S, 8, R, false, kNt>(a);
     }
 }
 
 // Natural-order launches (bf16, one token, at most three ranges).
-template <int S, int R>
+template <int S, int R, bool kNt>
 hipError_t launch_strip_nat_nw(int nw, const StripArgs &a) {
     switch (nw) {
-        case 1: return launch_strip<kDtypeBF16, S, 1, R, true>(a);
-        case 2: return launch_strip<kDtypeBF16, S, 2, R, true>(a);
-        default: return launch_strip<kDtypeBF16, S, 3, R, true>(a);
+        case 1: return launch_strip<kDtypeBF16, S, 1, R, true, kNt>(a);
+        case 2: return launch_strip<kDtypeBF16, S, 2, R, true, kNt>(a);
+        default: return launch_strip<kDtypeBF16, S, 3, R, true, kNt>(a);
     }
 }
-template <int S>
+template <int S, bool kNt>
 hipError_t launch_strip_nat(int nw, int r, const StripArgs &a) {
-    if (r == 14) return launch_strip_nat_nw<S, 14>(nw, a);
-    if (r == 7) return launch_strip_nat_nw<S, 7>(nw, a);
-    if (r >= 16) return launch_strip_nat_nw<S, 16>(nw, a);
-    if (r >= 8) return launch_strip_nat_nw<S, 8>(nw, a);
-    return launch_strip_nat_nw<S, 4>(nw, a);
+    if (r == 14) return launch_strip_nat_nw<S, 14, kNt>(nw, a);
+    if (r == 7) return launch_strip_nat_nw<S, 7, kNt>(nw, a);
+    if (r >= 16) return launch_strip_nat_nw<S, 16, kNt>(nw, a);
+    if (r >= 8) return launch_strip_nat_nw<S, 8, kNt>(nw, a);
+    return launch_strip_nat_nw<S, 4, kNt>(nw, a);
 }
 
-template <int XT, int S>
+template <int XT, int S, bool kNt = false>
 hipError_t launch_strip_nr(int nw, int r, const StripArgs &a) {
     if constexpr (XT == kDtypeBF16) {
-        if (r == 14) return launch_strip_nw<XT, S, 14>(nw, a);
-        if (r == 7) return launch_strip_nw<XT, S, 7>(nw, a);
+        if (r == 14) return launch_strip_nw<XT, S, 14, kNt>(nw, a);
+        if (r == 7) return launch_strip_nw<XT, S, 7, kNt>(nw, a);
     }
-    if (r >= 16) return launch_strip_nw<XT, S, 16>(nw, a);
-    if (r >= 8) return launch_strip_nw<XT, S, 8>(nw, a);
-    return launch_strip_nw<XT, S, 4>(nw, a);
+    if (r >= 16) return launch_strip_nw<XT, S, 16, kNt>(nw, a);
+    if (r >= 8) return launch_strip_nw<XT, S, 8, kNt>(nw, a);
+    return launch_strip_nw<XT, S, 4, kNt>(nw, a);
 }
+
+// The weight loads of bf16 launches over at least this many packed bytes carry the
+// non-temporal hint.  Measured on the config-3 / config-4 decode shapes (rotating weight
+// copies, so every call streams from HBM): 4096 -> 14336, 14336 -> 4096, 3072 -> 9216 and
+// 3072 -> 16384 take 2-5 % less time at one token (2-5 % at four on the two largest);
+// 8192 -> 3072 (8.4 MB) takes 3-5 % more.
+constexpr int64_t kStripNtMinBytes = int64_t{9} << 20;
 
 // Fewer waves than this leave SIMDs idle: shorter strips are then worth their extra
 // activation reads.
@@ -394,8 +402,21 @@ hipError_t launch_strip_x(bool *handled, const void *x, const uint8_t *w, void *
         if (busiest(r - r / 8) < busiest(r)) r -= r / 8;
     }
     if constexpr (XT == kDtypeBF16) {
-        if (m == 1 && ((S == 8 && nranges <= 3) || (S == 16 && nranges == 1)))
-            return S == 16 ? launch_strip_nat<16>(nw, r, a) : launch_strip_nat<8>(nw, r, a);
+        const bool nt = n * L * kTrytes >= kStripNtMinBytes;
+        if (m == 1 && ((S == 8 && nranges <= 3) || (S == 16 && nranges == 1))) {
+            if (nt)
+                return S == 16 ? launch_strip_nat<16, true>(nw, r, a)
+                               : launch_strip_nat<8, true>(nw, r, a);
+            return S == 16 ? launch_strip_nat<16, false>(nw, r, a)
+                           : launch_strip_nat<8, false>(nw, r, a);
+        }
+        if (nt) {
+            switch (S) {
+                case 16: return launch_strip_nr<XT, 16, true>(nw, r, a);
+                case 8: return launch_strip_nr<XT, 8, true>(nw, r, a);
+                default: return launch_strip_nr<XT, 4, true>(nw, r, a);
+            }
+        }
     }
     switch (S) {
         case 16: return launch_strip_nr<XT, 16>(nw, r, a);

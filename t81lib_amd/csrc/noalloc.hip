@@ -1,6 +1,6 @@
 // t81lib_amd/csrc/noalloc.hip -- t81_hip_ternary_matmul_noalloc: the trit-dot matmul with
-// the K3 split-K workspace taken from a static device array, for callers that cannot
-// allocate device memory (code under HIP graph capture, serving loops that forbid it).
+// its split-K workspace (K3's partial tiles, K2's partials for 5..16 tokens) taken from a
+// static device array, for callers that cannot allocate device memory (code under HIP graph capture, serving loops that forbid it).
 //
 // `scratch` is a file-scope device array, reserved when the code object is loaded on a
 // device and held until the process ends, one copy per device at its own address.  In
@@ -58,8 +58,7 @@ int t81_hip_ternary_matmul_noalloc(int which, const void *x, int x_dtype, const 
     // Same workspace as t81_hip_ternary_matmul_ws is given by its callers (exactly
     // t81_hip_ternary_matmul_workspace_size bytes), so the split plan -- and with it the
     // order of every sum -- is the same, and so are the results, bit for bit.
-    const bool gemv = which == 2 || (which == 0 && m <= 16);
-    const int64_t need = gemv ? 0 : t81_hip_ternary_matmul_workspace_size(m, n, k, x_dtype);
+    const int64_t need = t81_hip_ternary_matmul_workspace_size(m, n, k, x_dtype);
     if (need > kScratchBytes)
         return t81hip::report_error(
             T81_HIP_EINVAL_SHAPE,

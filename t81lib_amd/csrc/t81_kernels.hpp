@@ -27,9 +27,12 @@ hipError_t launch_unpack(const uint8_t *packed, int8_t *out, int64_t rows, int64
                          int64_t cols, hipStream_t s);
 hipError_t launch_validate(const uint8_t *packed, int64_t count, int32_t *bad, hipStream_t s);
 
-// gemv.hip (K2): M <= 16
+// gemv.hip (K2): M <= 16.  ws (ws_bytes of device memory, may be null) lets 5..16
+// tokens split K over workgroups; gemv_workspace_bytes says how much a shape uses.
 hipError_t launch_gemv(const void *x, int x_dtype, const uint8_t *w, void *c, int m, int64_t n,
-                       int64_t k, float alpha, float beta, const float *bias, hipStream_t s);
+                       int64_t k, float alpha, float beta, const float *bias, hipStream_t s,
+                       void *ws = nullptr, int64_t ws_bytes = 0);
+int64_t gemv_workspace_bytes(int64_t m, int64_t n, int64_t k, int x_dtype);
 
 // gemv_strip.hip (K2, M <= 4): sets *handled = false (and launches nothing) when the
 // shape is outside what it covers

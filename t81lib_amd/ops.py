@@ -217,9 +217,10 @@ def ternary_matmul(x: torch.Tensor, w_packed: torch.Tensor, k: Optional[int] = N
     if which not in (0, 2, 3):
         raise ValueError("kernel must be 2 or 3")
     code = _MATMUL_CODES[x.dtype]
-    # K3 with few output tiles splits K over a workspace from torch's caching allocator
-    # (safe under graph capture); its size is 0 for every other shape.
-    ws_bytes = 0 if which == 2 else int(lib.t81_hip_ternary_matmul_workspace_size(m, n, k, code))
+    # K3 with few output tiles, and K2 for 5..16 tokens, split K over a workspace from
+    # torch's caching allocator (safe under graph capture); its size is 0 for every other
+    # shape.
+    ws_bytes = int(lib.t81_hip_ternary_matmul_workspace_size(m, n, k, code))
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes > 0 else None
     rc = lib.t81_hip_ternary_matmul_ws(which, x.data_ptr(), code, w_packed.data_ptr(),
                                        c.data_ptr(), m, n, k, alpha, beta, bias_ptr,

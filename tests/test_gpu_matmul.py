@@ -412,6 +412,46 @@ def test_k2_m5_to_16_full_check(gpu, orc, M, N, K, dtype):
         assert ok, f"{name}: {nbad} outside, worst {worst:.3g}"
 
 
+@pytest.mark.parametrize("M,N,K,dtype,splits", [
+    (9, 37, 6200, torch.bfloat16, 5),      # 33 sub-blocks: one active wave in the last split
+    (11, 3000, 9001, torch.bfloat16, 6),   # K % 8 != 0 (element loads)
+    (16, 4100, 14400, torch.int8, 10),     # rows past N in the last block
+    (13, 8192, 6144, torch.float32, 4),    # four row groups per workgroup
+    (12, 8193, 6144, torch.bfloat16, 0),   # wider than the tile kernel takes
+    (8, 3000, 9000, torch.bfloat16, 0),    # fewer tokens than it takes
+    (16, 14336, 4096, torch.int8, 0)])     # short K: the stream kernel
+def test_k2_tile_kernel_plans(gpu, orc, M, N, K, dtype, splits):
+    """K2 for 9..16 tokens over a long K with a workspace (gemv_tile_kernel; splits == 0:
+    a shape it leaves to the stream / wave kernels): every output against the oracle
+    (int8 bit-exact), run twice with identical bits (fixed summation order), and the
+    workspace size reported for its K splits."""
+    announce(f"K2 tile M={M} N={N} K={K} {dtype}")
+    lib = _lib.lib()
+    code = {torch.bfloat16: _lib.DTYPE_BF16, torch.float32: _lib.DTYPE_F32, torch.int8: _lib.DTYPE_I8}[dtype]
+    ws = lib.t81_hip_ternary_matmul_workspace_size(M, N, K, code)
+    assert ws == (4 * splits * M * N if splits > 1 else 0)
+    w, x, c, bias = make_problem(M, N, K, dtype, seed=3 * N + K + M)
+    packed = ops.quantize_pack(w.to(gpu), 0.45, _lib.THR_CPP)
+    packed_np = packed.cpu().numpy()
+    xg = x.to(gpu)
+    if dtype == torch.int8:
+        want = orc.trit_matmul_i64(x.numpy(), packed_np, K)
+        cg = torch.randint(-1000, 1000, (M, N), dtype=torch.int32, device=gpu)
+        outs = [ops.ternary_matmul(xg, packed, K, beta=1.0, c=cg.clone(), kernel=2) for _ in range(2)]
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(outs[0].cpu().numpy().astype(np.int64),
+                                      want + cg.cpu().numpy().astype(np.int64))
+    else:
+        cg, bg = c.to(gpu), bias.to(gpu)
+        outs = [ops.ternary_matmul(xg, packed, K, alpha=-1.25, beta=0.5, c=cg.clone(), bias=bg,
+                                   kernel=2) for _ in range(2)]
+        torch.cuda.synchronize()
+        ref, scale = oracle_matmul(orc, x, packed_np, K, -1.25, 0.5, c, bias)
+        ok, worst, nbad = fp_tolerance_ok(outs[0].cpu().numpy(), ref, scale, accum_rtol(K, dtype))
+        assert ok, f"{nbad} outside, worst {worst:.3g}"
+    assert torch.equal(outs[0], outs[1]), "two runs of the same call differ"
+
+
 @pytest.mark.parametrize("M,N,K,dtype", [(32, 4096, 14336, torch.bfloat16),
                                          (48, 1000, 4104, torch.float32),
                                          (20, 3000, 9000, torch.int8),

@@ -69,6 +69,10 @@ def _run_pair(gpu, M, N, K, dtype, seed):
     # int8 and float32: eight-wave splits of few tiles (int32 partials exact for int8)
     (torch.int8, [(20, 3000, 9000), (20, 1200, 4000)]),
     (torch.float32, [(48, 1000, 4104), (40, 700, 2000)]),
+    # K2 with 9..16 tokens over a long K: K split over workgroups, partials summed in
+    # split order
+    (torch.bfloat16, [(16, 4096, 14336), (9, 3000, 9000)]),
+    (torch.int8, [(12, 3072, 8192), (10, 2000, 7000)]),
 ])
 def test_noalloc_matches_workspace_entry_point(gpu, dtype, shapes):
     for i, (M, N, K) in enumerate(shapes):
