@@ -690,16 +690,24 @@ hipError_t launch_stream(const void *x, const uint8_t *w, void *c, int m, int64_
     return hipGetLastError();
 }
 
-// Rows per workgroup and waves splitting K for the stream kernel (timed on config-3/4
-// decode shapes): 9..16 tokens over >= 9216 rows share each activation fragment
-// between four row groups (llama.gate M = 16 14.4 -> 13.0 us); up to 8 tokens over a
-// long K (>= 40 sub-blocks) split it over eight waves (llama.down M = 8 21.2 ->
-// 15.6 us); else two row groups, four waves.
+// Rows per workgroup and waves splitting K for the stream kernel (a sweep of 1, 2, 4, 8
+// row groups x 4, 8, 16 waves on the config-3/4 decode shapes at 8 and 16 tokens):
+// at most 4096 rows take one row group per workgroup -- the grid then covers the CUs --
+// with eight waves over >= 32 sub-blocks (llama.down M = 8 15.7 -> 13.0 us, phi3.down
+// M = 16 13.3 -> 11.3 us) and four below (phi3.o M = 16 6.9 -> 6.0 us); 9..16 tokens
+// over >= 9216 rows share each activation fragment between four row groups (llama.gate
+// M = 16 14.4 -> 13.0 us); up to 8 tokens over a long K (>= 40 sub-blocks) split it
+// over eight waves; else two row groups, four waves.
 template <int XT, bool kAligned>
 hipError_t launch_stream_shape(const void *x, const uint8_t *w, void *c, int m, int64_t n,
                                int64_t k, int64_t L, float alpha, float beta, const float *bias,
                                hipStream_t s) {
     const int64_t nsb = (L + 3) / 4;
+    if (n <= 4096) {
+        if (nsb >= 32)
+            return launch_stream<XT, 1, kAligned, 8>(x, w, c, m, n, k, L, alpha, beta, bias, s);
+        return launch_stream<XT, 1, kAligned, 4>(x, w, c, m, n, k, L, alpha, beta, bias, s);
+    }
     if (m > 8 && n >= 9216)
         return launch_stream<XT, 4, kAligned, 4>(x, w, c, m, n, k, L, alpha, beta, bias, s);
     if (m <= 8 && nsb >= 40)
@@ -783,7 +791,11 @@ hipError_t launch_gemv_x(const void *x, const uint8_t *w, void *c, int m, int64_
     // small and every wave keeps at least two sub-blocks
     int wg = 1;
     while (wg <= 8 && max_run > 0 && nsb > max_run * wg) wg *= 2;
-    if (L > 0 && max_run > 0 && wg <= 8) {
+    // bf16 over many rows takes the stream kernel: 8+ tokens over >= 9216 rows (3072 ->
+    // 16384 at M = 8: 10.5 -> 8.7 us; even at 3072 -> 9216), 5+ over >= 14336 (4096 ->
+    // 14336 at M = 5: 11.2 -> 9.6 us; 3072 -> 9216 at M = 5 stays faster staged)
+    const bool wide = XT == kDtypeBF16 && ((m >= 8 && n >= 9216) || (m >= 5 && n >= 14336));
+    if (L > 0 && max_run > 0 && wg <= 8 && !wide) {
         while (wg < 8 && groups * wg < kTargetWaves && nsb >= 4 * wg) wg *= 2;
         const int W = wg < 4 ? 4 : wg;
         const int nsbw_max = static_cast<int>((nsb + wg - 1) / wg);

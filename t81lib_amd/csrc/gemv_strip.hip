@@ -109,12 +109,14 @@ __device__ __forceinline__ float strip_keep(floatx4 v, int j) {
 
 // S: sub-positions per quarter (range = 4*S limbs, S in {4, 8, 16}); NW: waves, one range
 // each at a time; R: loads per range, i.e. R * (16 / S) rows per workgroup.  kNt: weight
-// loads carry the non-temporal hint (see launch_strip_x).  kNat: limbs
+// loads carry the non-temporal hint (see launch_strip_x).  DEPTH: loads in flight per
+// wave (kStripDepth, three for the short natural-order strips).  kNat: limbs
 // decoded in natural trit order (E and F tables, six MFMAs per limb) instead of padded
 // order (E table only, eight MFMAs) -- fewer MFMAs for two ORs per dword; the launch uses
 // it for one token over one 64-limb range or up to three 32-limb ranges, where it
 // measured faster (4096 x 14336: 7.03 -> 6.95 us; 3072 x 9216: 5.36 -> 5.09 us).
-template <int XT, int S, int NW, int R, bool kNat = false, bool kNt = false>
+template <int XT, int S, int NW, int R, bool kNat = false, bool kNt = false,
+          int DEPTH = kStripDepth>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void gemv_strip_kernel(
     const void *__restrict__ x, const uint8_t *__restrict__ w, void *__restrict__ c, int M,
     int64_t N, int64_t K, int L, int nranges, int x_aligned, float alpha, float beta,
@@ -122,7 +124,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     static_assert(S == 4 || S == 8 || S == 16, "one matched entry per lane needs S >= 4");
     constexpr int RPI = 16 / S;  // rows per load (and tokens per MFMA)
     constexpr int H = R * RPI;   // rows per workgroup
-    constexpr int D = R < kStripDepth ? R : kStripDepth;
+    constexpr int D = R < DEPTH ? R : DEPTH;
     __shared__ __attribute__((aligned(16))) uint8_t lut[kLutBytes];
     __shared__ float red[NW][R][64];
 
@@ -284,11 +286,12 @@ struct StripArgs {
     hipStream_t s;
 };
 
-template <int XT, int S, int NW, int R, bool kNat = false, bool kNt = false>
+template <int XT, int S, int NW, int R, bool kNat = false, bool kNt = false,
+          int DEPTH = kStripDepth>
 hipError_t launch_strip(const StripArgs &a) {
     constexpr int H = R * (16 / S);
     const int64_t blocks = (a.n + H - 1) / H;
-    gemv_strip_kernel<XT, S, NW, R, kNat, kNt><<<dim3(static_cast<unsigned>(blocks)), dim3(64 * NW), 0,
+    gemv_strip_kernel<XT, S, NW, R, kNat, kNt, DEPTH><<<dim3(static_cast<unsigned>(blocks)), dim3(64 * NW), 0,
                                        a.s>>>(a.x, a.w, a.c, a.m, a.n, a.k, a.L, a.nranges,
                                               a.aligned ? 1 : 0, a.alpha, a.beta, a.bias);
     return hipGetLastError();
@@ -308,13 +311,17 @@ hipError_t launch_strip_nw(int nw, const StripArgs &a) {
     }
 }
 
-// Natural-order launches (bf16, one token, at most three ranges).
+// Natural-order launches (bf16, one token, at most three ranges).  Strips of at most
+// seven loads keep three of them in flight, not four: 4096 -> 14336 (seven loads)
+// 6.69 -> 6.45 us, 3072 -> 9216 (four) 4.94 -> 4.69 us; eight loads (3072 -> 16384)
+// measured 1 % slower with three.
 template <int S, int R, bool kNt>
 hipError_t launch_strip_nat_nw(int nw, const StripArgs &a) {
+    constexpr int kD = R <= 7 ? 3 : kStripDepth;
     switch (nw) {
-        case 1: return launch_strip<kDtypeBF16, S, 1, R, true, kNt>(a);
-        case 2: return launch_strip<kDtypeBF16, S, 2, R, true, kNt>(a);
-        default: return launch_strip<kDtypeBF16, S, 3, R, true, kNt>(a);
+        case 1: return launch_strip<kDtypeBF16, S, 1, R, true, kNt, kD>(a);
+        case 2: return launch_strip<kDtypeBF16, S, 2, R, true, kNt, kD>(a);
+        default: return launch_strip<kDtypeBF16, S, 3, R, true, kNt, kD>(a);
     }
 }
 template <int S, bool kNt>
