@@ -528,6 +528,42 @@ def run_spmm(torch, dev) -> list:
     return out
 
 
+DECODE_SHAPES = [("phi3.qkv", 3072, 9216), ("phi3.o", 3072, 3072), ("phi3.gate_up", 3072, 16384),
+                 ("phi3.down", 8192, 3072), ("llama.gate", 4096, 14336),
+                 ("llama.down", 14336, 4096)]
+
+
+def run_decode(torch, ops, lib, dev) -> dict:
+    """Config 3 (Phi-3 decode shapes) and the Llama-3-8B gate / down shapes at 1, 4, 8 and
+    16 tokens, through the product path (ops.ternary_matmul: K2, with the workspace its
+    K splits use): median microseconds per call over rotating weight copies (> 2 x MALL,
+    so every call streams from HBM), GB/s of algorithmic bytes, and each shape's 16-token
+    time over its one-token time."""
+    shapes = {}
+    for name, k, n in DECODE_SHAPES:
+        wbytes = 16 * n * ((k + 47) // 48)
+        copies = max(4, -(-2 * MALL_BYTES // wbytes) + 2)
+        wb = make_weights(torch, ops, lib, n, k, copies, dev, seed=3)
+        row = {"K": k, "N": n}
+        for m in (1, 4, 8, 16):
+            x = torch.randn((m, k), device=dev).to(torch.bfloat16)
+            out = torch.empty((m, n), device=dev)
+            d = time_graph(torch, lambda w: ops.ternary_matmul(x, w, k, c=out), wb, 256, 32,
+                           dist=True, min_launches=100, min_ms=20.0)
+            us = d["median_ms"] * 1e3
+            row[f"M{m}_us"] = round(us, 3)
+            row[f"M{m}_GBps"] = round(gemv_bytes(m, n, k) / (us * 1e-6) / 1e9, 1)
+            log(f"decode {name:13s} M={m:2d} {k:5d}->{n:5d}: {us:7.2f} us")
+            del x, out
+        row["M16_over_M1"] = round(row["M16_us"] / row["M1_us"], 3)
+        shapes[name] = row
+        del wb
+        torch.cuda.empty_cache()
+    return {"workload": "K2 decode, bf16 x, fp32 out, alpha=1 beta=0, median over rotating "
+                        "weight copies; config 3 (Phi-3) plus the Llama-3-8B gate / down shapes",
+            "shapes": shapes}
+
+
 def run_sweep(torch, ops, lib, dev) -> list:
     """Decode GEMV (config 3 + the Llama gate/down shapes) and prefill GEMM (config 4)."""
     rows = []
@@ -767,7 +803,7 @@ def main() -> int:
                     help="seconds of single-core reference CPU work for the baseline")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", choices=["gemv", "gemm", "pack", "copy", "read", "spmm", "launch",
-                                       "stack"],
+                                       "stack", "decode"],
                     default=None,
                     help="time one kernel only (for profiling runs); 'copy' times a plain "
                          "elementwise copy of the GEMV weight size, the calibration kernel "
@@ -982,6 +1018,7 @@ def main() -> int:
                               "sample": f"row blocks on {threads} threads, {sa * 1e3:.1f} ms"},
             }
 
+    decode = run_decode(torch, ops, _lib, dev) if only in (None, "decode") else None
     sweep = run_sweep(torch, ops, _lib, dev) if args.sweep else None
     spmm = run_spmm(torch, dev) if only == "spmm" else None
     stack = run_stack(torch, dev) if only == "stack" or (only is None and not args.no_stack) \
@@ -1054,6 +1091,8 @@ def main() -> int:
             line["pack"]["cpu_baseline"] = pack["cpu_baseline"]
     if floors:
         line["floors"] = floors
+    if decode:
+        line["decode"] = decode
     if sweep:
         line["sweep"] = sweep
     if spmm:

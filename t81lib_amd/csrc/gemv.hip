@@ -555,9 +555,24 @@ __global__ __launch_bounds__(256) void gemv_split_sum_kernel(
         const int cnt = N - n0 < 4 ? static_cast<int>(N - n0) : 4;
         float v[4];
         if (vec) {
-            float4 a = *reinterpret_cast<const float4 *>(part + base);
-            for (int sp = 1; sp < P; ++sp) {
-                const float4 b = *reinterpret_cast<const float4 *>(part + sp * total + base);
+            // four partials loaded at a time (all in flight), then added in split order
+            auto ld = [&](int sp) {
+                return *reinterpret_cast<const float4 *>(part + sp * total + base);
+            };
+            float4 a = ld(0);
+            int sp = 1;
+            for (; sp + 4 <= P; sp += 4) {
+                const float4 b[4] = {ld(sp), ld(sp + 1), ld(sp + 2), ld(sp + 3)};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    a.x += b[j].x;
+                    a.y += b[j].y;
+                    a.z += b[j].z;
+                    a.w += b[j].w;
+                }
+            }
+            for (; sp < P; ++sp) {
+                const float4 b = ld(sp);
                 a.x += b.x;
                 a.y += b.y;
                 a.z += b.z;
