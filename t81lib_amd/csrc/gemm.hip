@@ -611,6 +611,17 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
                         next[rb][j] = __builtin_bit_cast(bf16x8, raw);
                     }
             }
+            // Each MFMA followed by a few of the chunk's other instructions (two LDS
+            // reads, three VALU / SALU, one buffer load): with one wave per SIMD, issue is
+            // in order, so three MFMAs issued back to back (the default schedule) left the
+            // matrix pipe idle while the rest of the chunk issued after them.
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);   // LDS read
+                __builtin_amdgcn_sched_group_barrier(0x006, 3, 0);   // VALU, SALU
+                __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);   // buffer load
+            }
             __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
