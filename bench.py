@@ -875,31 +875,34 @@ def main() -> int:
                 f"p90 {gemv['p90_ms'] * 1e3:.2f})")
         if only in (None, "read"):
             # the read floor: a plain coalesced streaming read of the same weight copies
-            # (csrc/floors.hip), best of four grid sizes
+            # (csrc/floors.hip), best over grid sizes and loads in flight per thread
             import ctypes
 
             flib = ctypes.CDLL(os.path.join(ROOT, "t81lib_amd", "libt81_floors.so"))
             flib.t81_floor_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
-                                            ctypes.c_int, ctypes.c_void_p]
+                                            ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
             sink = torch.empty(8192, dtype=torch.int32, device=dev)
             best = None
-            for blocks in (256, 512, 1024, 2048, 4096):
-                def rd(wb, blocks=blocks):
-                    rc = flib.t81_floor_read(wb.data_ptr(), wbytes, sink.data_ptr(), blocks,
-                                             torch.cuda.current_stream().cuda_stream)
-                    if rc != 0:
-                        raise RuntimeError(f"t81_floor_read failed ({rc})")
-                r = time_graph(torch, rd, wbufs, max(args.steps, 256), 32, dist=True)
-                if best is None or r["median_ms"] < best[1]["median_ms"]:
-                    best = (blocks, r)
-            blocks, r = best
+            for unroll in (1, 4, 8):
+                for blocks in (256, 512, 1024, 2048, 4096):
+                    def rd(wb, blocks=blocks, unroll=unroll):
+                        rc = flib.t81_floor_read(wb.data_ptr(), wbytes, sink.data_ptr(), blocks,
+                                                 unroll, torch.cuda.current_stream().cuda_stream)
+                        if rc != 0:
+                            raise RuntimeError(f"t81_floor_read failed ({rc})")
+                    r = time_graph(torch, rd, wbufs, max(args.steps, 256), 32, dist=True)
+                    if best is None or r["median_ms"] < best[2]["median_ms"]:
+                        best = (blocks, unroll, r)
+            blocks, unroll, r = best
             floors["read"] = {"workload": f"plain coalesced read of one {wbytes}-byte weight "
                                           f"copy (16-byte loads, {blocks} workgroups of 256, "
-                                          f"best of 256-4096), {copies} rotating copies",
+                                          f"{unroll} loads in flight per thread; best of "
+                                          f"256-4096 workgroups x 1, 4, 8 loads), "
+                                          f"{copies} rotating copies",
                               "us": r["median_ms"] * 1e3,
                               "GBps": wbytes / (r["median_ms"] * 1e-3) / 1e9, **spread_us(r)}
             log(f"read floor {floors['read']['us']:.2f} us/launch, "
-                f"{floors['read']['GBps']:.0f} GB/s ({blocks} workgroups)")
+                f"{floors['read']['GBps']:.0f} GB/s ({blocks} workgroups, {unroll} in flight)")
         if only in (None, "copy"):
             # counter calibration and the measured copy bandwidth (read + write)
             elems = wbytes // 4

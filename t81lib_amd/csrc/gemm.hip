@@ -564,6 +564,10 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
     __builtin_amdgcn_s_waitcnt(0x0F74);
     __syncthreads();
     if (s_begin < s_end) decode_half(wcur, 0, a0);
+    u32x4 bq[4];
+    bq[0] = read_b(std::integral_constant<int, 0>(), 0, 0);
+    bq[1] = read_b(std::integral_constant<int, 0>(), 0, 1);
+    bq[2] = read_b(std::integral_constant<int, 0>(), 0, 2);
 
     // One k-step as 24 chunks of four MFMAs (chunks 0-11: half 0 with a0, 12-23: half 1
     // with a1), one B fragment each, read three chunks ahead.  Chunks are fenced so that
@@ -571,15 +575,17 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
     // chunks 12-19: half 0 of wnxt (the next step) into a0; table reads two chunks ahead
     // of their merge -- and of the loads: the tile of the next step (chunks 0-11), then
     // the weights of the step after it (chunk 12).  Issued after the tile loads, the
-    // weight loads can stay in flight across the end-of-step wait (vmcnt(4)), so they
-    // have a step and a half to land, not half a step.  (All loads are unconditional:
-    // past the last step they read zeros or unused weight bytes.)  Steps alternate
-    // between the two tile buffers, so the loop below runs two steps per iteration.
+    // weight loads can stay in flight across the step's wait (vmcnt(4)), so they have a
+    // step and a half to land, not half a step.  (All loads are unconditional: past the
+    // last step they read zeros or unused weight bytes.)  Steps alternate between the two
+    // tile buffers, so the loop below runs two steps per iteration.
+    // The step's barrier comes after chunk 20, whose B read is the last of this step's
+    // buffer: past it the next tile is complete (every wave's loads waited for) and no
+    // wave reads this buffer again, so chunks 21-23 read the next step's first three B
+    // fragments (the next step starts with its operands in registers, not waiting on LDS),
+    // and the next step may refill this buffer.  In an item's last step those three
+    // reads fetch bytes that are never used.
     auto step_body = [&](int step, auto bufc, auto otherc) {
-        u32x4 bq[4];
-        bq[0] = read_b(bufc, 0, 0);
-        bq[1] = read_b(bufc, 0, 1);
-        bq[2] = read_b(bufc, 0, 2);
         uint2 e[3][4];
         uint32_t pairs[4][12];
 #pragma unroll
@@ -587,6 +593,7 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
             const int p = g / 12;
             const int gg = g % 12;
             if (g + 3 < 24) bq[(g + 3) % 4] = read_b(bufc, (g + 3) / 12, (g + 3) % 12);
+            else bq[(g + 3) % 4] = read_b(otherc, 0, g + 3 - 24);
             if (gg < 8)
                 table_fetch((p == 0 ? wcur : wnxt)[gg / 2][2 * (1 - p) + (gg % 2)], e[gg % 3]);
             if (gg >= 2 && gg <= 9)
@@ -623,15 +630,17 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
                 __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);   // buffer load
             }
             __builtin_amdgcn_sched_barrier(0);
+            if (g == 20) {
+                // vmcnt(4): the tile loads are older than the four weight loads of step + 2
+                __builtin_amdgcn_s_waitcnt(0x0F74);
+                __syncthreads();
+            }
         }
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb) {
             wcur[rb] = wnxt[rb];
             wnxt[rb] = wnn[rb];
         }
-        // vmcnt(4): the tile loads are older than the four weight loads of step + 2
-        __builtin_amdgcn_s_waitcnt(0x0F74);
-        __syncthreads();
     };
     int step = s_begin;
     for (; step + 1 < s_end; step += 2) {
