@@ -46,6 +46,7 @@ namespace {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 template <int XT, int RN, int CM, int WN, int WM, int LK>
 struct GemmCfg {
@@ -717,7 +718,10 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
                         y[2] += bv.z;
                         y[3] += bv.w;
                     }
-                    *reinterpret_cast<float4 *>(cr + nb) = make_float4(y[0], y[1], y[2], y[3]);
+                    // non-temporal: C is not read again here, and every CU stores a whole
+                    // tile's C at about the same time (gate_up M = 2048 373 -> 363 us)
+                    const f32x4 yv = {y[0], y[1], y[2], y[3]};
+                    __builtin_nontemporal_store(yv, reinterpret_cast<f32x4 *>(cr + nb));
                 } else {
 #pragma unroll
                     for (int b = 0; b < 4; ++b) {

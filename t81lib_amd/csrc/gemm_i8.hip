@@ -348,7 +348,9 @@ __global__ __launch_bounds__(kI8Threads) void gemm_w4_i8_kernel(
                         y[2] += cv[2];
                         y[3] += cv[3];
                     }
-                    *reinterpret_cast<i32x4 *>(cr + nb) = i32x4{y[0], y[1], y[2], y[3]};
+                    // non-temporal, as the bf16 kernel's C (M = 2048 gate_up 296 -> 275 us)
+                    __builtin_nontemporal_store(i32x4{y[0], y[1], y[2], y[3]},
+                                                reinterpret_cast<i32x4 *>(cr + nb));
                 } else {
 #pragma unroll
                     for (int b = 0; b < 4; ++b) {
