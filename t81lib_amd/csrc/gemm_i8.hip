@@ -282,6 +282,16 @@ __global__ __launch_bounds__(kI8Threads) void gemm_w4_i8_kernel(
             for (int rb = 0; rb < 4; ++rb)
                 acc[rb][g % 4] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[P][rb][g / 4], bq[g % 3],
                                                                        acc[rb][g % 4], 0, 0, 0);
+            // each MFMA followed by a few of the chunk's other instructions (three LDS
+            // reads, four VALU / SALU, one buffer load), as in the bf16 kernel: issue is
+            // in order with one wave per SIMD (M = 2048 gate_up 278 -> 270 us)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);   // LDS read
+                __builtin_amdgcn_sched_group_barrier(0x006, 4, 0);   // VALU, SALU
+                __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);   // buffer load
+            }
             __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
