@@ -39,7 +39,12 @@ namespace {
 
 constexpr int kTq2Bytes = 66;
 constexpr int kTq2MaxWaves = 8;
-constexpr int kTq2Depth = 4;   // loads in flight per wave, refilled as each is decoded
+// Loads in flight per wave, refilled as each is decoded: three for one or two tokens
+// (S = 8), four above (llama.gate M = 1 6.99 -> 6.84 us with three; M = 4 7.90 -> 8.08).
+// The non-temporal hint that helps the limb strip kernel measured 6.99 -> 7.91 us here
+// (each piece's 4-byte tail load re-reads the line that the next piece's load streams).
+template <int S>
+constexpr int tq2_depth() { return S == 8 ? 3 : 4; }
 constexpr uint32_t kTq2Oob = 0x80000000u;
 constexpr int kTq2LutWords = 512;  // 256 entries x 8 bytes
 
@@ -119,7 +124,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     static_assert(S == 4 || S == 8, "one matched entry per lane");
     constexpr int RPI = 16 / S;
     constexpr int H = R * RPI;
-    constexpr int D = R < kTq2Depth ? R : kTq2Depth;
+    constexpr int D = R < tq2_depth<S>() ? R : tq2_depth<S>();
     __shared__ __attribute__((aligned(16))) uint32_t lut[kTq2LutWords];
     __shared__ float red[NW][R][64];
 
