@@ -358,7 +358,6 @@ constexpr int kW4StepK = 2 * kTrits;                // trits per k-step
 constexpr int kW4RowSlots = kW4StepK / 8 + 1;       // 16-byte slots per tile row (+1 pad)
 constexpr int kW4RowBytes = 16 * kW4RowSlots;       // 208
 constexpr int kW4TileBytes = kW4Tokens * kW4RowBytes;
-constexpr int kW4LoadsPerWave = kW4Tokens * kW4RowSlots / (64 * 4);   // 13
 constexpr uint32_t kW4Oob = 0x80000000u;
 constexpr int kW4StageStride = 68;   // floats per staged output row: 64 columns + 4 pad
 
@@ -376,23 +375,26 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void *base,
 }
 
 // Work items.  Weight rows [0, n1) run as whole 256 x 256 tiles (all k-steps, result
-// to C); rows [n1, N), with nsplit > 0, as split-K items: item (split sp, tile t of that
-// region) runs k-steps [sp * sps, (sp + 1) * sps) and stores its raw accumulators (no
-// alpha, beta, bias) to part in the order (sp, t, wave, block, a4, lane) as float4s --
-// every store is 1 KB contiguous; gemm_split_reduce_kernel then sums the splits in
-// order.  Half of
-// the split items come first and half last in the item order, so the workgroups that
-// start with a (shorter) split item finish their whole tiles half a tile out of step
-// with the others, and the C stores of the two halves do not all land at once.
+// to C).  Rows [n1, N) run either as split-K items (nsplit > 0): item (split sp, tile t of
+// that region) runs k-steps [sp * sps, (sp + 1) * sps) and stores its raw accumulators
+// (no alpha, beta, bias) to part in the order (sp, t, wave, block, a4, lane) as float4s
+// -- every store is 1 KB contiguous; gemm_split_reduce_kernel then sums the splits in
+// order -- or (half != 0) as half-width tiles of 256 rows x 128 tokens over all k-steps,
+// result to C: when those fill about one round of the CUs they need no workspace and no
+// second launch.  Half of the remainder's items come first and half last in the item
+// order, so the workgroups that start with a (shorter) remainder item finish their whole
+// tiles half a tile out of step with the others, and the C stores of the two halves do
+// not all land at once.
 template <int XT>
 __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
     const void *__restrict__ x, const uint8_t *__restrict__ w, void *__restrict__ c, int M, int N,
     int ldc, int K, int L, float alpha, float beta, const float *__restrict__ bias, int n1,
-    int sps, float4 *__restrict__ part, int nsplit) {
+    int sps, float4 *__restrict__ part, int nsplit, int half) {
     static_assert(XT == kDtypeBF16, "the LDS tile is filled straight from bf16 activations");
     // Two separate tile objects (not one array indexed by a run-time parity): the
     // loads into one buffer then provably do not alias the reads of the other, and
-    // the compiler need not wait for them before every LDS read.
+    // the compiler need not wait for them before every LDS read.  A half-width item
+    // uses the first half of each.
     // (The table's larger alignment places it at LDS address 0, so a table address is
     // just the byte field, with no base to add.)
     __shared__ __attribute__((aligned(1024))) uint8_t lut[kLutBytes];
@@ -404,6 +406,8 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
         if constexpr (decltype(bufc)::value == 0) return xs0;
         else return xs1;
     };
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
 
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -417,327 +421,412 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
     // new workgroup per tile started only after the C stores of the whole previous
     // round had drained (~15 us a round at M = 2048).
     const int tiles_m = (M + kW4Tokens - 1) / kW4Tokens;
+    const int tiles_mh = (M + kW4Tokens / 2 - 1) / (kW4Tokens / 2);   // half-width tiles
     const int tn1 = (n1 + kW4Rows - 1) / kW4Rows;        // row tiles of whole tiles
-    const int tn2 = (N - n1 + kW4Rows - 1) / kW4Rows;    // row tiles of split items
+    const int tn2 = (N - n1 + kW4Rows - 1) / kW4Rows;    // row tiles of the remainder
     const int full_items = tn1 * tiles_m;
     const int tiles2 = tn2 * tiles_m;
-    const int split_items = nsplit > 0 ? tiles2 * nsplit : 0;
-    const int head = split_items / 2;                    // split items placed first
-    const int total = full_items + split_items;
+    const int rem_items = half ? tn2 * tiles_mh : (nsplit > 0 ? tiles2 * nsplit : 0);
+    const int head = rem_items / 2;                      // remainder items placed first
+    const int total = full_items + rem_items;
     const int all_steps = (L + 1) / 2;
     lut_fill(lut, tid, kW4Threads);  // published by the first item's barrier
-    for (int q = static_cast<int>(blockIdx.x); q < total; q += static_cast<int>(gridDim.x)) {
-    // The lane index passes through an empty asm once per item, so the per-lane offsets
-    // derived from it are recomputed per item instead of being hoisted out of the loop
-    // and kept live across the epilogue (where they would spill).
-    int lane = tid & 63;
-    asm volatile("" : "+v"(lane));
-    const int r = lane & 31;
-    const int h = lane >> 5;
-    const bool split = q < head || q >= head + full_items;
-    const int item = __builtin_amdgcn_readfirstlane(q < head ? q : (split ? q - full_items : q - head));
-    const int sp = split ? item / tiles2 : 0;
-    const int tt = split ? item - sp * tiles2 : item;          // tile within its region
-    const int tiles_n = split ? tn2 : tn1;
-    const int tn = __builtin_amdgcn_readfirstlane(tt % tiles_n);
-    const int tm = __builtin_amdgcn_readfirstlane(tt / tiles_n);
-    const int nwg = (split ? n1 : 0) + tn * kW4Rows;
-    const int m0 = tm * kW4Tokens;
-    const int s_begin = split ? sp * sps : 0;
-    const int s_end = split && s_begin + sps < all_steps ? s_begin + sps : all_steps;
 
-    // Weights through a buffer based at the workgroup's first row: rows past N read
-    // zeros.  A limb index past L (odd L, last step) reads the next row's first limb
-    // or zeros; either decodes to finite trits that meet zero activations.
-    const __amdgpu_buffer_rsrc_t wsrc = uniform_rsrc(w + static_cast<int64_t>(nwg) * L * kTrytes,
-                                                   static_cast<int64_t>(N - nwg) * L * kTrytes);
-    uint32_t woff[4];
-#pragma unroll
-    for (int rb = 0; rb < 4; ++rb)
-        woff[rb] = (static_cast<uint32_t>(128 * wn + 32 * rb + r) * static_cast<uint32_t>(L) +
-                    static_cast<uint32_t>(h)) * kTrytes;
-    auto fetch_w = [&](int step, u32x4 (&dst)[4]) {
-        const uint32_t koff = static_cast<uint32_t>(step) * (2 * kTrytes);
+    // One item: 256 weight rows (nwg..) x 64 CB tokens (m0..) over k-steps
+    // [s_begin, s_end); wave (wn, wm) owns 128 rows x 32 CB tokens.  CB = 4: whole or
+    // split-K tiles; CB = 2: half-width tiles.
+    auto run_item = [&](auto cbc, int nwg, int m0, int s_begin, int s_end, bool split, int sp,
+                        int tt) {
+        constexpr int CB = decltype(cbc)::value;      // 32-token blocks per wave
+        constexpr int kTok = 64 * CB;                  // tokens per workgroup
+        constexpr int kTL = kTok * kW4RowSlots / 64;   // tile loads per workgroup (52, 26)
+        constexpr int LPW = (kTL + 3) / 4;             // per wave (13; 7, the last wave 5)
+        constexpr int NCH = 6 * CB;                    // chunks of four MFMAs per step
+        constexpr int HALF = 3 * CB;                   // chunks per half step
+        constexpr int NF = CB == 4 ? 8 : 4;            // chunks of a half that read the table
+        constexpr int FPC = 8 / NF;                    // weight dwords looked up per such chunk
+
+        // The lane index passes through an empty asm once per item, so the per-lane
+        // offsets derived from it are recomputed per item instead of being hoisted out of
+        // the loop and kept live across the epilogue (where they would spill).
+        int lane = tid & 63;
+        asm volatile("" : "+v"(lane));
+        const int r = lane & 31;
+        const int h = lane >> 5;
+
+        // Weights through a buffer based at the workgroup's first row: rows past N read
+        // zeros.  A limb index past L (odd L, last step) reads the next row's first limb
+        // or zeros; either decodes to finite trits that meet zero activations.
+        const __amdgpu_buffer_rsrc_t wsrc = uniform_rsrc(
+            w + static_cast<int64_t>(nwg) * L * kTrytes, static_cast<int64_t>(N - nwg) * L * kTrytes);
+        uint32_t woff[4];
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb)
-            dst[rb] = __builtin_bit_cast(
-                u32x4, __builtin_amdgcn_raw_buffer_load_b128(wsrc, woff[rb] + koff, 0, 0));
-    };
-
-    // Activation tile: load i of wave w fills slots q = 64 (13 w + i) + lane, tile row
-    // q / 13, slot q % 13.  Activations through a buffer based at token m0: tokens
-    // past M read zeros.
-    const __amdgpu_buffer_rsrc_t xsrc =
-        uniform_rsrc(static_cast<const uint16_t *>(x) + static_cast<int64_t>(m0) * K,
-                     static_cast<int64_t>(M - m0) * K * 2);
-    // Per-lane constants of the 13 loads: the byte offset of the chunk for k0 = 0 (or an
-    // out-of-range offset for a pad slot) and, packed four to a register, 8 * slot, the
-    // chunk's first trit within the step (past K the chunk loads zeros).
-    uint32_t tbase[kW4LoadsPerWave];
-    uint32_t tslot[(kW4LoadsPerWave + 3) / 4];
-#pragma unroll
-    for (int i = 0; i < (kW4LoadsPerWave + 3) / 4; ++i) tslot[i] = 0u;
-#pragma unroll
-    for (int i = 0; i < kW4LoadsPerWave; ++i) {
-        const uint32_t q = static_cast<uint32_t>(64 * (kW4LoadsPerWave * wave + i) + lane);
-        const uint32_t row = q / kW4RowSlots;
-        const uint32_t slot = q - row * kW4RowSlots;
-        tbase[i] = slot < kW4RowSlots - 1
-                       ? (row * static_cast<uint32_t>(K) + 8 * slot) * 2
-                       : kW4Oob;
-        tslot[i / 4] |= (8 * slot) << (8 * (i % 4));
-    }
-    // Load i of the wave's share of the tile of k-step `step` into LDS buffer buf (all
-    // zeros past the last step).
-    auto load_tile_part = [&](int step, auto bufc, int i) {
-        const int k0 = step * kW4StepK;
-        const uint32_t lim = k0 < K ? static_cast<uint32_t>(K - k0) : 0u;
-        const uint32_t slot8 = (tslot[i / 4] >> (8 * (i % 4))) & 0xFFu;
-        const uint32_t off = slot8 < lim ? tbase[i] + static_cast<uint32_t>(k0) * 2 : kW4Oob;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            xsrc,
-            (__attribute__((address_space(3))) void *)(
-                &tile(bufc)[16 * 64 * (kW4LoadsPerWave * wave + i)]),
-            16, off, 0, 0, 0);
-    };
-    auto load_tile = [&](int step, auto bufc) {
-#pragma unroll
-        for (int i = 0; i < kW4LoadsPerWave; ++i) load_tile_part(step, bufc, i);
-    };
-
-    // Half p of the lane's limbs -> A fragments J = 3p + j of the four row blocks.
-    auto decode_half = [&](const u32x4 (&wl)[4], int p, bf16x8 (&a)[4][3]) {
-#pragma unroll
-        for (int rb = 0; rb < 4; ++rb) {
-            uint32_t pairs[12];
-            decode_dword(lut, wl[rb][2 * p], pairs);
-            decode_dword(lut, wl[rb][2 * p + 1], pairs + 6);
-#pragma unroll
-            for (int j = 0; j < 3; ++j) {
-                const u32x4 raw = {pairs[4 * j], pairs[4 * j + 1], pairs[4 * j + 2],
-                                   pairs[4 * j + 3]};
-                a[rb][j] = __builtin_bit_cast(bf16x8, raw);
-            }
-        }
-    };
-
-    floatx16 acc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
-
-    // B lane (c, h): token 128 wm + 32 cb + c of the tile, trits 48h + 8J.. of the step.
-    const int brow = (128 * wm + r) * kW4RowBytes + 96 * h;
-    auto read_b = [&](auto bufc, int p, int g) -> u32x4 {
-        const int j = g / 4;
-        const int cb = g % 4;
-        return *reinterpret_cast<const u32x4 *>(
-            &tile(bufc)[brow + 32 * cb * kW4RowBytes + 16 * (3 * p + j)]);
-    };
-    // decode_dword in two parts, so the table reads can be issued a chunk ahead of the
-    // merge that needs them.
-    auto table_fetch = [&](uint32_t wd, uint2 (&e)[4]) {
-        const uint32_t w8 = wd << 3;
-        e[0] = *reinterpret_cast<const uint2 *>(lut + kLutE + (w8 & 0xFFu));
-        e[1] = *reinterpret_cast<const uint2 *>(lut + kLutF + ((w8 >> 8) & 0xFFu));
-        e[2] = *reinterpret_cast<const uint2 *>(lut + kLutE + ((w8 >> 16) & 0xFFu));
-        e[3] = *reinterpret_cast<const uint2 *>(lut + kLutF + (w8 >> 24));
-    };
-    auto table_merge = [&](const uint2 (&e)[4], uint32_t *out) {
-        out[0] = e[0].x;
-        out[1] = e[0].y | e[1].x;
-        out[2] = e[1].y;
-        out[3] = e[2].x;
-        out[4] = e[2].y | e[3].x;
-        out[5] = e[3].y;
-    };
-    u32x4 wcur[4], wnxt[4], wnn[4];
-    bf16x8 a0[4][3], a1[4][3];
-    if (s_begin < s_end) {
-        fetch_w(s_begin, wcur);
-        load_tile(s_begin, std::integral_constant<int, 0>());
-    }
-    fetch_w(s_begin + 1, wnxt);   // stays in flight across the barrier
-    // vmcnt(4): the tile's LDS writes have landed before the barrier publishes them
-    __builtin_amdgcn_s_waitcnt(0x0F74);
-    __syncthreads();
-    if (s_begin < s_end) decode_half(wcur, 0, a0);
-    u32x4 bq[4];
-    bq[0] = read_b(std::integral_constant<int, 0>(), 0, 0);
-    bq[1] = read_b(std::integral_constant<int, 0>(), 0, 1);
-    bq[2] = read_b(std::integral_constant<int, 0>(), 0, 2);
-
-    // One k-step as 24 chunks of four MFMAs (chunks 0-11: half 0 with a0, 12-23: half 1
-    // with a1), one B fragment each, read three chunks ahead.  Chunks are fenced so that
-    // each also carries its share of the decode -- chunks 0-7: half 1 of wcur into a1,
-    // chunks 12-19: half 0 of wnxt (the next step) into a0; table reads two chunks ahead
-    // of their merge -- and of the loads: the tile of the next step (chunks 0-11), then
-    // the weights of the step after it (chunk 12).  Issued after the tile loads, the
-    // weight loads can stay in flight across the step's wait (vmcnt(4)), so they have a
-    // step and a half to land, not half a step.  (All loads are unconditional: past the
-    // last step they read zeros or unused weight bytes.)  Steps alternate between the two
-    // tile buffers, so the loop below runs two steps per iteration.
-    // The step's barrier comes after chunk 20, whose B read is the last of this step's
-    // buffer: past it the next tile is complete (every wave's loads waited for) and no
-    // wave reads this buffer again, so chunks 21-23 read the next step's first three B
-    // fragments (the next step starts with its operands in registers, not waiting on LDS),
-    // and the next step may refill this buffer.  In an item's last step those three
-    // reads fetch bytes that are never used.
-    auto step_body = [&](int step, auto bufc, auto otherc) {
-        uint2 e[3][4];
-        uint32_t pairs[4][12];
-#pragma unroll
-        for (int g = 0; g < 24; ++g) {
-            const int p = g / 12;
-            const int gg = g % 12;
-            if (g + 3 < 24) bq[(g + 3) % 4] = read_b(bufc, (g + 3) / 12, (g + 3) % 12);
-            else bq[(g + 3) % 4] = read_b(otherc, 0, g + 3 - 24);
-            if (gg < 8)
-                table_fetch((p == 0 ? wcur : wnxt)[gg / 2][2 * (1 - p) + (gg % 2)], e[gg % 3]);
-            if (gg >= 2 && gg <= 9)
-                table_merge(e[(gg - 2) % 3], &pairs[(gg - 2) / 2][6 * ((gg - 2) % 2)]);
-            if (g < 12) load_tile_part(step + 1, otherc, g);
-            if (g == 11) load_tile_part(step + 1, otherc, 12);
-            if (g == 12) fetch_w(step + 2, wnn);
-            const bf16x8 b = __builtin_bit_cast(bf16x8, bq[g % 4]);
-            const bf16x8(&a)[4][3] = p == 0 ? a0 : a1;
+            woff[rb] = (static_cast<uint32_t>(128 * wn + 32 * rb + r) * static_cast<uint32_t>(L) +
+                        static_cast<uint32_t>(h)) * kTrytes;
+        auto fetch_w = [&](int step, u32x4 (&dst)[4]) {
+            const uint32_t koff = static_cast<uint32_t>(step) * (2 * kTrytes);
 #pragma unroll
             for (int rb = 0; rb < 4; ++rb)
-                acc[rb][gg % 4] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[rb][gg / 4], b,
-                                                                          acc[rb][gg % 4], 0, 0, 0);
-            if (gg == 11) {
-                bf16x8(&next)[4][3] = p == 0 ? a1 : a0;
+                dst[rb] = __builtin_bit_cast(
+                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(wsrc, woff[rb] + koff, 0, 0));
+        };
+
+        // Activation tile: load i of wave w fills slots q = 64 (LPW w + i) + lane, tile row
+        // q / 13, slot q % 13 (loads past kTL are not issued).  Activations through a
+        // buffer based at token m0: tokens past M read zeros.
+        const __amdgpu_buffer_rsrc_t xsrc =
+            uniform_rsrc(static_cast<const uint16_t *>(x) + static_cast<int64_t>(m0) * K,
+                         static_cast<int64_t>(M - m0) * K * 2);
+        // Per-lane constants of the loads: the byte offset of the chunk for k0 = 0 (or an
+        // out-of-range offset for a pad slot) and, packed four to a register, 8 * slot,
+        // the chunk's first trit within the step (past K the chunk loads zeros).
+        uint32_t tbase[LPW];
+        uint32_t tslot[(LPW + 3) / 4];
 #pragma unroll
-                for (int rb = 0; rb < 4; ++rb)
+        for (int i = 0; i < (LPW + 3) / 4; ++i) tslot[i] = 0u;
 #pragma unroll
-                    for (int j = 0; j < 3; ++j) {
-                        const u32x4 raw = {pairs[rb][4 * j], pairs[rb][4 * j + 1],
-                                           pairs[rb][4 * j + 2], pairs[rb][4 * j + 3]};
-                        next[rb][j] = __builtin_bit_cast(bf16x8, raw);
-                    }
+        for (int i = 0; i < LPW; ++i) {
+            const uint32_t q = static_cast<uint32_t>(64 * (LPW * wave + i) + lane);
+            const uint32_t row = q / kW4RowSlots;
+            const uint32_t slot = q - row * kW4RowSlots;
+            tbase[i] = slot < kW4RowSlots - 1
+                           ? (row * static_cast<uint32_t>(K) + 8 * slot) * 2
+                           : kW4Oob;
+            tslot[i / 4] |= (8 * slot) << (8 * (i % 4));
+        }
+        // Load i of the wave's share of the tile of k-step `step` into LDS buffer buf
+        // (all zeros past the last step).  The last wave's spare loads of a half-width
+        // tile (slots 26, 27: LDS bytes 26624..28671, inside the buffer and never read)
+        // load zeros -- an out-of-range offset, not a branch, which would split the
+        // chunk's scheduling region.
+        auto load_tile_part = [&](int step, auto bufc, int i) {
+            const bool spare = LPW * 4 != kTL && i >= kTL - 3 * LPW && LPW * wave + i >= kTL;
+            const int k0 = step * kW4StepK;
+            const uint32_t lim = k0 < K && !spare ? static_cast<uint32_t>(K - k0) : 0u;
+            const uint32_t slot8 = (tslot[i / 4] >> (8 * (i % 4))) & 0xFFu;
+            const uint32_t off = slot8 < lim ? tbase[i] + static_cast<uint32_t>(k0) * 2 : kW4Oob;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                xsrc,
+                (__attribute__((address_space(3))) void *)(
+                    &tile(bufc)[16 * 64 * (LPW * wave + i)]),
+                16, off, 0, 0, 0);
+        };
+        auto load_tile = [&](int step, auto bufc) {
+#pragma unroll
+            for (int i = 0; i < LPW; ++i) load_tile_part(step, bufc, i);
+        };
+
+        // Half p of the lane's limbs -> A fragments J = 3p + j of the four row blocks.
+        auto decode_half = [&](const u32x4 (&wl)[4], int p, bf16x8 (&a)[4][3]) {
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb) {
+                uint32_t pairs[12];
+                decode_dword(lut, wl[rb][2 * p], pairs);
+                decode_dword(lut, wl[rb][2 * p + 1], pairs + 6);
+#pragma unroll
+                for (int j = 0; j < 3; ++j) {
+                    const u32x4 raw = {pairs[4 * j], pairs[4 * j + 1], pairs[4 * j + 2],
+                                       pairs[4 * j + 3]};
+                    a[rb][j] = __builtin_bit_cast(bf16x8, raw);
+                }
             }
-            // Each MFMA followed by a few of the chunk's other instructions (two LDS
-            // reads, three VALU / SALU, one buffer load): with one wave per SIMD, issue is
-            // in order, so three MFMAs issued back to back (the default schedule) left the
-            // matrix pipe idle while the rest of the chunk issued after them.
+        };
+
+        floatx16 acc[4][CB];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);   // LDS read
-                __builtin_amdgcn_sched_group_barrier(0x006, 3, 0);   // VALU, SALU
-                __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);   // buffer load
-            }
-            __builtin_amdgcn_sched_barrier(0);
-            if (g == 20) {
-                // vmcnt(4): the tile loads are older than the four weight loads of step + 2
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < CB; ++j)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+        // B fragment gi of a step (gi < NCH): half p = gi / HALF, J = 3p + (gi % HALF) / CB,
+        // token block cb = gi % CB.  B lane (c, h): token 32 CB wm + 32 cb + c of the tile,
+        // trits 48h + 8J.. of the step.
+        const int brow = (32 * CB * wm + r) * kW4RowBytes + 96 * h;
+        auto read_b = [&](auto bufc, int gi) -> u32x4 {
+            const int p = gi / HALF;
+            const int gg = gi % HALF;
+            return *reinterpret_cast<const u32x4 *>(
+                &tile(bufc)[brow + 32 * (gg % CB) * kW4RowBytes + 16 * (3 * p + gg / CB)]);
+        };
+        // decode_dword in two parts, so the table reads can be issued ahead of the merge
+        // that needs them.
+        auto table_fetch = [&](uint32_t wd, uint2 (&e)[4]) {
+            const uint32_t w8 = wd << 3;
+            e[0] = *reinterpret_cast<const uint2 *>(lut + kLutE + (w8 & 0xFFu));
+            e[1] = *reinterpret_cast<const uint2 *>(lut + kLutF + ((w8 >> 8) & 0xFFu));
+            e[2] = *reinterpret_cast<const uint2 *>(lut + kLutE + ((w8 >> 16) & 0xFFu));
+            e[3] = *reinterpret_cast<const uint2 *>(lut + kLutF + (w8 >> 24));
+        };
+        auto table_merge = [&](const uint2 (&e)[4], uint32_t *out) {
+            out[0] = e[0].x;
+            out[1] = e[0].y | e[1].x;
+            out[2] = e[1].y;
+            out[3] = e[2].x;
+            out[4] = e[2].y | e[3].x;
+            out[5] = e[3].y;
+        };
+        u32x4 wcur[4], wnxt[4], wnn[4];
+        bf16x8 a0[4][3], a1[4][3];
+        if (s_begin < s_end) {
+            fetch_w(s_begin, wcur);
+            load_tile(s_begin, B0());
+        }
+        fetch_w(s_begin + 1, wnxt);   // stays in flight across the barrier
+        if constexpr (CB == 4) {
+            // vmcnt(4): the tile's LDS writes have landed before the barrier publishes them
+            __builtin_amdgcn_s_waitcnt(0x0F74);
+        } else {
+            // a half-width step is too short to cover its tile loads, so every step
+            // loads the tile of the step after next: here the second step's tile too.
+            // vmcnt(9): the first tile has landed (the second tile's loads -- five in
+            // the last wave -- and the four weight loads may still be in flight).
+            // One step only: vmcnt(4), the weight loads.
+            if (s_begin + 1 < s_end) {
+                load_tile(s_begin + 1, B1());
+                __builtin_amdgcn_s_waitcnt(0x0F79);
+            } else {
                 __builtin_amdgcn_s_waitcnt(0x0F74);
-                __syncthreads();
             }
         }
-#pragma unroll
-        for (int rb = 0; rb < 4; ++rb) {
-            wcur[rb] = wnxt[rb];
-            wnxt[rb] = wnn[rb];
-        }
-    };
-    int step = s_begin;
-    for (; step + 1 < s_end; step += 2) {
-        step_body(step, std::integral_constant<int, 0>(), std::integral_constant<int, 1>());
-        step_body(step + 1, std::integral_constant<int, 1>(), std::integral_constant<int, 0>());
-    }
-    if (step < s_end)  // odd step count: the last step, peeled (no join inside the loop)
-        step_body(step, std::integral_constant<int, 0>(), std::integral_constant<int, 1>());
+        __syncthreads();
+        if (s_begin < s_end) decode_half(wcur, 0, a0);
+        u32x4 bq[4];
+        bq[0] = read_b(B0(), 0);
+        bq[1] = read_b(B0(), 1);
+        bq[2] = read_b(B0(), 2);
 
-    if (split) {
-        float4 *dst =
-            part + (((static_cast<int64_t>(sp) * tiles2 + tt) * 4 + wave) * 64) * 64 + lane;
+        // One k-step as NCH chunks of four MFMAs (the first half with a0, the second with
+        // a1), one B fragment each, read three chunks ahead.  Chunks are fenced so that
+        // each also carries its share of the decode -- the first NF chunks of the first
+        // half: half 1 of wcur into a1; of the second half: half 0 of wnxt (the next
+        // step) into a0; table reads two chunks ahead of their merge -- and of the loads.
+        // Whole tiles (CB = 4): the tile of the next step (chunks 0-11), then the weights
+        // of the step after it (chunk 12); issued after the tile loads, the weight loads
+        // can stay in flight across the step's wait (vmcnt(4)), so they have a step and a
+        // half to land, not half a step.  Half-width tiles (CB = 2): the weights of the
+        // step after next (chunk 0), and, past the barrier, the tile of the step after
+        // next into this step's buffer (chunks 9-11; not in the item's last step, so no
+        // LDS write is left pending when the item ends).  (All other loads are
+        // unconditional: past the last step they read zeros or unused weight bytes.)
+        // Steps alternate between the two tile buffers, so the loop below runs two steps
+        // per iteration.
+        // The step's barrier comes after chunk NCH - 4, whose B read is the last of this
+        // step's buffer: past it the next tile is complete (every wave's loads waited
+        // for) and no wave reads this buffer again, so the last three chunks read the
+        // next step's first three B fragments (the next step starts with its operands in
+        // registers, not waiting on LDS), and the buffer may be refilled.  In an item's
+        // last step those three reads fetch bytes that are never used.
+        auto step_body = [&](int step, auto bufc, auto otherc) {
+            uint2 e[3][FPC][4];
+            uint32_t pairs[4][12];
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb)
+            for (int g = 0; g < NCH; ++g) {
+                const int p = g / HALF;
+                const int gg = g % HALF;
+                if (g + 3 < NCH) bq[(g + 3) % 4] = read_b(bufc, g + 3);
+                else bq[(g + 3) % 4] = read_b(otherc, g + 3 - NCH);
+                if (gg < NF) {
 #pragma unroll
-            for (int cb = 0; cb < 4; ++cb)
-#pragma unroll
-                for (int a4 = 0; a4 < 4; ++a4)
-                    dst[((rb * 4 + cb) * 4 + a4) * 64] =
-                        make_float4(acc[rb][cb][4 * a4], acc[rb][cb][4 * a4 + 1],
-                                    acc[rb][cb][4 * a4 + 2], acc[rb][cb][4 * a4 + 3]);
-        continue;
-    }
-
-    // ---- epilogue: lane (c, h) of block (rb, cb) holds rows 8 a4 + 4 h + b of token c ----
-    // The results go out 32 tokens x 64 weight rows at a time
-    // through the wave's LDS region: written there in the MFMA layout, read back as four
-    // tokens x 64 consecutive rows per instruction, so each global store (and each C read
-    // for beta) covers four 256-byte runs instead of 32 runs of 32 bytes.  A wave's LDS
-    // operations complete in order, so the region needs no barrier.
-    float *cdst = static_cast<float *>(c);
-    const int col0 = nwg;
-    const int ldv = ldc;
-    const int nv = N;
-    const float al = alpha;
-    const float be = beta;
-    const float *bi = bias;
-    const bool vec4 = ldv % 4 == 0 && (reinterpret_cast<uintptr_t>(cdst) & 15u) == 0;
-    float *st = cst[wave];
-    const int tq = lane >> 4;          // token within a group of four
-    const int tc = 4 * (lane & 15);    // first of the lane's four rows within the 64
-#pragma unroll
-    for (int cb = 0; cb < 4; ++cb) {
-#pragma unroll
-        for (int rp = 0; rp < 2; ++rp) {
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-#pragma unroll
-                for (int a4 = 0; a4 < 4; ++a4)
-                    *reinterpret_cast<float4 *>(&st[r * kW4StageStride + 32 * j + 8 * a4 + 4 * h]) =
-                        make_float4(acc[2 * rp + j][cb][4 * a4], acc[2 * rp + j][cb][4 * a4 + 1],
-                                    acc[2 * rp + j][cb][4 * a4 + 2], acc[2 * rp + j][cb][4 * a4 + 3]);
-            const int nb = col0 + 128 * wn + 64 * rp + tc;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int tok = 4 * i + tq;
-                const float4 v = *reinterpret_cast<const float4 *>(&st[tok * kW4StageStride + tc]);
-                const int m = m0 + 128 * wm + 32 * cb + tok;
-                if (m >= M) continue;
-                float *cr = cdst + static_cast<int64_t>(m) * ldv;
-                float y[4] = {al * v.x, al * v.y, al * v.z, al * v.w};
-                if (vec4 && nb + 3 < nv) {
-                    if (be != 0.0f) {
-                        const float4 cv = *reinterpret_cast<const float4 *>(cr + nb);
-                        y[0] += be * cv.x;
-                        y[1] += be * cv.y;
-                        y[2] += be * cv.z;
-                        y[3] += be * cv.w;
+                    for (int f2 = 0; f2 < FPC; ++f2) {
+                        const int f = gg * FPC + f2;
+                        table_fetch((p == 0 ? wcur : wnxt)[f / 2][2 * (1 - p) + (f % 2)],
+                                    e[gg % 3][f2]);
                     }
-                    if (bi != nullptr) {
-                        const float4 bv = *reinterpret_cast<const float4 *>(bi + nb);
-                        y[0] += bv.x;
-                        y[1] += bv.y;
-                        y[2] += bv.z;
-                        y[3] += bv.w;
+                }
+                if (gg >= 2 && gg < NF + 2) {
+#pragma unroll
+                    for (int f2 = 0; f2 < FPC; ++f2) {
+                        const int f = (gg - 2) * FPC + f2;
+                        table_merge(e[(gg - 2) % 3][f2], &pairs[f / 2][6 * (f % 2)]);
                     }
-                    // non-temporal: C is not read again here, and every CU stores a whole
-                    // tile's C at about the same time (gate_up M = 2048 373 -> 363 us)
-                    const f32x4 yv = {y[0], y[1], y[2], y[3]};
-                    __builtin_nontemporal_store(yv, reinterpret_cast<f32x4 *>(cr + nb));
+                }
+                if constexpr (CB == 4) {
+                    if (g < 12) load_tile_part(step + 1, otherc, g);
+                    if (g == 11) load_tile_part(step + 1, otherc, 12);
+                    if (g == 12) fetch_w(step + 2, wnn);
                 } else {
-#pragma unroll
-                    for (int b = 0; b < 4; ++b) {
-                        const int n = nb + b;
-                        if (n < nv) {
-                            float t = y[b];
-                            if (be != 0.0f) t = t + be * cr[n];
-                            if (bi != nullptr) t = t + bi[n];
-                            cr[n] = t;
+                    if (g == 0) fetch_w(step + 2, wnn);
+                    if (step + 1 < s_end) {
+                        if (g == 9) {
+                            load_tile_part(step + 2, bufc, 0);
+                            load_tile_part(step + 2, bufc, 1);
+                            load_tile_part(step + 2, bufc, 2);
+                        }
+                        if (g == 10) {
+                            load_tile_part(step + 2, bufc, 3);
+                            load_tile_part(step + 2, bufc, 4);
+                        }
+                        if (g == 11) {
+                            load_tile_part(step + 2, bufc, 5);
+                            load_tile_part(step + 2, bufc, 6);
                         }
                     }
                 }
+                const bf16x8 b = __builtin_bit_cast(bf16x8, bq[g % 4]);
+                const bf16x8(&a)[4][3] = p == 0 ? a0 : a1;
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb)
+                    acc[rb][gg % CB] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                        a[rb][gg / CB], b, acc[rb][gg % CB], 0, 0, 0);
+                if (gg == HALF - 1) {
+                    bf16x8(&next)[4][3] = p == 0 ? a1 : a0;
+#pragma unroll
+                    for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+                        for (int j = 0; j < 3; ++j) {
+                            const u32x4 raw = {pairs[rb][4 * j], pairs[rb][4 * j + 1],
+                                               pairs[rb][4 * j + 2], pairs[rb][4 * j + 3]};
+                            next[rb][j] = __builtin_bit_cast(bf16x8, raw);
+                        }
+                }
+                // Each MFMA followed by a few of the chunk's other instructions (two LDS
+                // reads, three VALU / SALU, one buffer load): with one wave per SIMD, issue
+                // is in order, so three MFMAs issued back to back (the default schedule)
+                // left the matrix pipe idle while the rest of the chunk issued after them.
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);   // LDS read
+                    __builtin_amdgcn_sched_group_barrier(0x006, 3, 0);   // VALU, SALU
+                    __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);   // buffer load
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                if (g == NCH - 4) {
+                    // vmcnt(4): the tile loads are older than the four weight loads of
+                    // step + 2
+                    __builtin_amdgcn_s_waitcnt(0x0F74);
+                    __syncthreads();
+                }
             }
-            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb) {
+                wcur[rb] = wnxt[rb];
+                wnxt[rb] = wnn[rb];
+            }
+        };
+        int step = s_begin;
+        for (; step + 1 < s_end; step += 2) {
+            step_body(step, B0(), B1());
+            step_body(step + 1, B1(), B0());
         }
-    }
+        if (step < s_end)  // odd step count: the last step, peeled (no join inside the loop)
+            step_body(step, B0(), B1());
+
+        if constexpr (CB == 4) {
+            if (split) {
+                float4 *dst =
+                    part + (((static_cast<int64_t>(sp) * tiles2 + tt) * 4 + wave) * 64) * 64 + lane;
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+                    for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+                        for (int a4 = 0; a4 < 4; ++a4)
+                            dst[((rb * 4 + cb) * 4 + a4) * 64] =
+                                make_float4(acc[rb][cb][4 * a4], acc[rb][cb][4 * a4 + 1],
+                                            acc[rb][cb][4 * a4 + 2], acc[rb][cb][4 * a4 + 3]);
+                return;
+            }
+        }
+
+        // ---- epilogue: lane (c, h) of block (rb, cb) holds rows 8 a4 + 4 h + b of token c ----
+        // The results go out 32 tokens x 64 weight rows at a time through the wave's LDS
+        // region: written there in the MFMA layout, read back as four tokens x 64
+        // consecutive rows per instruction, so each global store (and each C read for
+        // beta) covers four 256-byte runs instead of 32 runs of 32 bytes.  A wave's LDS
+        // operations complete in order, so the region needs no barrier.
+        float *cdst = static_cast<float *>(c);
+        const int col0 = nwg;
+        const int ldv = ldc;
+        const int nv = N;
+        const float al = alpha;
+        const float be = beta;
+        const float *bi = bias;
+        const bool vec4 = ldv % 4 == 0 && (reinterpret_cast<uintptr_t>(cdst) & 15u) == 0;
+        float *st = cst[wave];
+        const int tq = lane >> 4;          // token within a group of four
+        const int tc = 4 * (lane & 15);    // first of the lane's four rows within the 64
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) {
+#pragma unroll
+            for (int rp = 0; rp < 2; ++rp) {
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int a4 = 0; a4 < 4; ++a4)
+                        *reinterpret_cast<float4 *>(&st[r * kW4StageStride + 32 * j + 8 * a4 + 4 * h]) =
+                            make_float4(acc[2 * rp + j][cb][4 * a4], acc[2 * rp + j][cb][4 * a4 + 1],
+                                        acc[2 * rp + j][cb][4 * a4 + 2], acc[2 * rp + j][cb][4 * a4 + 3]);
+                const int nb = col0 + 128 * wn + 64 * rp + tc;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const int tok = 4 * i + tq;
+                    const float4 v = *reinterpret_cast<const float4 *>(&st[tok * kW4StageStride + tc]);
+                    const int m = m0 + 32 * CB * wm + 32 * cb + tok;
+                    if (m >= M) continue;
+                    float *cr = cdst + static_cast<int64_t>(m) * ldv;
+                    float y[4] = {al * v.x, al * v.y, al * v.z, al * v.w};
+                    if (vec4 && nb + 3 < nv) {
+                        if (be != 0.0f) {
+                            const float4 cv = *reinterpret_cast<const float4 *>(cr + nb);
+                            y[0] += be * cv.x;
+                            y[1] += be * cv.y;
+                            y[2] += be * cv.z;
+                            y[3] += be * cv.w;
+                        }
+                        if (bi != nullptr) {
+                            const float4 bv = *reinterpret_cast<const float4 *>(bi + nb);
+                            y[0] += bv.x;
+                            y[1] += bv.y;
+                            y[2] += bv.z;
+                            y[3] += bv.w;
+                        }
+                        // non-temporal: C is not read again here, and every CU stores a
+                        // whole tile's C at about the same time (gate_up M = 2048 373 -> 363 us)
+                        const f32x4 yv = {y[0], y[1], y[2], y[3]};
+                        __builtin_nontemporal_store(yv, reinterpret_cast<f32x4 *>(cr + nb));
+                    } else {
+#pragma unroll
+                        for (int b = 0; b < 4; ++b) {
+                            const int n = nb + b;
+                            if (n < nv) {
+                                float t = y[b];
+                                if (be != 0.0f) t = t + be * cr[n];
+                                if (bi != nullptr) t = t + bi[n];
+                                cr[n] = t;
+                            }
+                        }
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    };
+
+    for (int q = static_cast<int>(blockIdx.x); q < total; q += static_cast<int>(gridDim.x)) {
+        const bool rem = q < head || q >= head + full_items;
+        const int item =
+            __builtin_amdgcn_readfirstlane(q < head ? q : (rem ? q - full_items : q - head));
+        if (half && rem) {
+            const int tn = __builtin_amdgcn_readfirstlane(item % tn2);
+            const int tm = __builtin_amdgcn_readfirstlane(item / tn2);
+            run_item(std::integral_constant<int, 2>(), n1 + tn * kW4Rows, tm * (kW4Tokens / 2), 0,
+                     all_steps, false, 0, 0);
+        } else {
+            const bool split = rem;
+            const int sp = split ? item / tiles2 : 0;
+            const int tt = split ? item - sp * tiles2 : item;   // tile within its region
+            const int tiles_n = split ? tn2 : tn1;
+            const int tn = __builtin_amdgcn_readfirstlane(tt % tiles_n);
+            const int tm = __builtin_amdgcn_readfirstlane(tt / tiles_n);
+            const int s_begin = split ? sp * sps : 0;
+            const int s_end = split && s_begin + sps < all_steps ? s_begin + sps : all_steps;
+            run_item(std::integral_constant<int, 4>(), (split ? n1 : 0) + tn * kW4Rows,
+                     tm * kW4Tokens, s_begin, s_end, split, sp, tt);
+        }
     }  // work items
 }
 
@@ -836,6 +925,23 @@ int64_t gemm_rows_whole_rounds(int64_t m, int64_t n) {
     return n;
 }
 
+// Half-width tiles (256 weight rows x 128 tokens) over rows: their count, and whether
+// the rows [n1, n) left after whole rounds of big tiles run as one round of them -- three
+// quarters of the CUs or more, none waiting for a second round -- instead of as split-K
+// items (no workspace, no second launch).  Only after whole rounds: a half-width step
+// costs about as much outside its MFMAs as a whole one (the same 128 weight rows per wave
+// to decode), so with no whole tiles to run beside them (Llama down at M = 2048, every
+// row) they measured slower than split-K (199 -> 222 us); as gate_up's remainder at
+// M = 2048 they replace the split items and their sum (388 -> 382 us).
+int64_t gemm_half_tiles(int64_t m, int64_t rows) {
+    return ((rows + kW4Rows - 1) / kW4Rows) * ((m + kW4Tokens / 2 - 1) / (kW4Tokens / 2));
+}
+bool gemm_use_half(int64_t m, int64_t n, int64_t n1) {
+    const int64_t t = gemm_half_tiles(m, n - n1);
+    const int64_t cus = cu_count();
+    return n1 > 0 && n1 < n && m > 64 && t <= cus && 4 * t >= 3 * cus;
+}
+
 // How the big-tile kernel splits K for a shape: with few tiles (< 160), about one
 // workgroup per CU in total, at least four k-steps per split.  nsplit == 1: no split.
 struct SplitPlan {
@@ -860,23 +966,27 @@ int64_t split_workspace_bytes(const SplitPlan &p) {
 
 // Rows [0, n1) of W as whole big tiles and, with plan != nullptr (nsplit > 1) and part
 // (room for the plan's partial tiles), rows [n1, n) as split-K items, in one launch;
-// then the split partials are summed into C.  C rows are ldc elements apart.
+// then the split partials are summed into C.  With half, rows [n1, n) run instead as
+// half-width tiles (256 rows x 128 tokens, all k-steps) in the same launch.  C rows are
+// ldc elements apart.
 hipError_t launch_gemm_w4(const void *x, const uint8_t *w, void *c, int64_t m, int64_t n,
                           int64_t n1, int64_t ldc, int64_t k, float alpha, float beta,
                           const float *bias, hipStream_t s, const SplitPlan *plan = nullptr,
-                          void *part = nullptr) {
+                          void *part = nullptr, bool half = false) {
     const int64_t L = (k + kTrits - 1) / kTrits;
     const int64_t tiles_m = (m + kW4Tokens - 1) / kW4Tokens;
-    const bool split = plan != nullptr && plan->nsplit > 1 && part != nullptr && n1 < n;
+    const bool split = !half && plan != nullptr && plan->nsplit > 1 && part != nullptr && n1 < n;
+    const bool rem = half && n1 < n;
     const int64_t items = ((n1 + kW4Rows - 1) / kW4Rows) * tiles_m +
-                          (split ? plan->nsplit * plan->tiles : 0);
+                          (split ? plan->nsplit * plan->tiles : 0) +
+                          (rem ? gemm_half_tiles(m, n - n1) : 0);
     if (items <= 0) return hipSuccess;
     const int64_t cus = cu_count();
     gemm_w4_kernel<kDtypeBF16><<<dim3(items < cus ? items : cus), dim3(kW4Threads), 0, s>>>(
-        x, w, c, static_cast<int>(m), static_cast<int>(split ? n : n1), static_cast<int>(ldc),
-        static_cast<int>(k), static_cast<int>(L), alpha, beta, bias, static_cast<int>(n1),
-        split ? static_cast<int>(plan->sps) : 0, static_cast<float4 *>(part),
-        split ? static_cast<int>(plan->nsplit) : 0);
+        x, w, c, static_cast<int>(m), static_cast<int>(split || rem ? n : n1),
+        static_cast<int>(ldc), static_cast<int>(k), static_cast<int>(L), alpha, beta, bias,
+        static_cast<int>(n1), split ? static_cast<int>(plan->sps) : 0,
+        static_cast<float4 *>(part), split ? static_cast<int>(plan->nsplit) : 0, rem ? 1 : 0);
     if (!split) return hipGetLastError();
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -1005,6 +1115,11 @@ hipError_t launch_gemm_x(const void *x, const uint8_t *w, void *c, int64_t m, in
         const int64_t n1 = gemm_rows_whole_rounds(m, n);
         const int64_t L = (k + kTrits - 1) / kTrits;
         const bool w4 = XT == kDtypeBF16 && gemm_w4_fits(x, m, n, k);
+        if (w4 && gemm_use_half(m, n, n1))
+            // one launch: whole tiles for rows [0, n1), one round of half-width tiles for
+            // the rest
+            return launch_gemm_w4(x, w, c, m, n, n1, n, k, alpha, beta, bias, s, nullptr, nullptr,
+                                  true);
         if (w4 && ws != nullptr && n1 < n) {
             // one launch: whole tiles for rows [0, n1), split-K items for the rest
             const SplitPlan plan = gemm_split_plan(m, n - n1, k);
@@ -1073,7 +1188,11 @@ int64_t gemm_workspace_x(int64_t m, int64_t n, int64_t k) {
         const int64_t eight = gemm_t_workspace<XT, 2, 2, 4, 2>(m, n - n1, k);
         if constexpr (XT == kDtypeI8) return eight > i8 ? eight : i8;
         if constexpr (XT != kDtypeBF16) return eight;
-        const int64_t big = k % 8 == 0 ? split_workspace_bytes(gemm_split_plan(m, n - n1, k)) : 0;
+        // aligned activations whose remaining rows fill a round of half-width tiles run
+        // without a workspace
+        const int64_t big = k % 8 == 0 && !gemm_use_half(m, n, n1)
+                                ? split_workspace_bytes(gemm_split_plan(m, n - n1, k))
+                                : 0;
         return big > eight ? big : eight;
     }
 }

@@ -17,10 +17,11 @@ Paths covered (shapes taken from the configs):
 * K2 gemv.hip: 8, 12 and 16 tokens (activations staged in LDS, or streamed with
   two or four row groups per fragment);
 * K3 big-tile kernel (one wave per SIMD): config 4 at M = 2048 (gate_up: whole
-  256 x 256 tiles for the first 24576 rows, split-K items for the remaining 4096
-  in the same launch, an odd step count with the peeled last step), M = 512
-  (every tile split over the workspace) and M = 8192, plus small shapes with odd
-  and even step counts, ragged M and N and K past the last whole step.
+  256 x 256 tiles for the first 24576 rows, half-width 256 x 128 tiles for the
+  remaining 4096 in the same launch, an odd step count with the peeled last step),
+  M = 512 (every tile split over the workspace) and M = 8192, plus small shapes with
+  odd, even and single step counts, ragged M and N and K past the last whole step,
+  for whole, half-width and split-K items.
 
 Full-size K3 outputs are checked twice: a seeded sample of tokens x rows, drawn
 from every region of the launch, against the C oracle on the packed bytes, and
@@ -147,9 +148,9 @@ def _gpu_exact_product(xg_f64: torch.Tensor, packed: torch.Tensor, N: int, K: in
 
 K3_FULL = [
     # name, M, K, N
-    ("llama.gate_up", 2048, 4096, 28672),   # whole tiles + split items, odd step count
+    ("llama.gate_up", 2048, 4096, 28672),   # whole tiles + half-width tiles, odd steps
     ("llama.qkv", 2048, 4096, 6144),
-    ("llama.down", 2048, 14336, 4096),
+    ("llama.down", 2048, 14336, 4096),      # every tile split over the workspace
     ("llama.qkv", 512, 4096, 6144),         # every tile split over the workspace
     ("llama.down", 512, 14336, 4096),
     ("llama.qkv", 8192, 4096, 6144),
@@ -205,6 +206,9 @@ K3_SMALL = [
     (300, 256 * 160 + 13, 200), (512, 256 * 80, 192), (260, 256 * 81 + 7, 480),
     (512, 256 * 200 - 5, 96), (300, 1000, 4104), (260, 4096, 2000), (200, 700, 1536),
     (300, 256 * 160, 1536),
+    # whole rounds of 256 x 256 tiles, the remaining rows as one round of half-width
+    # 256 x 128 tiles (on 256 CUs: 192-256 of them), ragged M and N
+    (1900, 256 * 44 + 13, 200),
 ]
 
 
@@ -222,6 +226,50 @@ def test_k3_big_tile_integer_bf16_bit_exact(gpu, orc, M, N, K):
                                  bias=bias.to(gpu) if use_bias else None, kernel=3)
         want = expected(acc, alpha, beta, c.numpy(), bias.numpy() if use_bias else None)
         assert_bits(out.cpu().numpy(), want, f"alpha={alpha} beta={beta}")
+
+
+K3_HALF = [
+    # M, N, K: whole rounds of 256 x 256 tiles for the first 16384 rows, the rest as one
+    # round of half-width 256 x 128 tiles (on 256 CUs: 200 / 192 / 192 of them) in the
+    # same launch; one, three (K past the last whole step) and four steps; ragged N
+    (1000, 256 * 88 + 7, 96), (1000, 256 * 88, 200), (1000, 256 * 88 - 5, 384),
+]
+
+
+@pytest.mark.parametrize("M,N,K", K3_HALF)
+def test_k3_half_width_integer_bf16_bit_exact(gpu, orc, M, N, K):
+    """Every output against the float64 product of the unpacked trits on the GPU, a sample
+    from both regions against the C oracle, alpha / beta / bias, and no workspace asked
+    for (the half-width tiles need none)."""
+    announce(f"exact K3 half-width M={M} N={N} K={K}")
+    lib = _lib.lib()
+    assert lib.t81_hip_ternary_matmul_workspace_size(M, N, K, _lib.DTYPE_BF16) == 0
+    w, x, c, bias = int_problem(M, N, K, seed=M + N + K)
+    packed = ops.quantize_pack(w.to(gpu), 0.45, _lib.THR_CPP)
+    exact = _gpu_exact_product(x.to(torch.float64).to(gpu), packed, N, K)
+    n1 = whole_round_rows(M, N)
+    assert 0 < n1 < N, "shape expected to leave rows past whole rounds"
+    toks, rows = _sample(M, N, n1, seed=K)
+    acc_s = orc.trit_matmul_i64(x[torch.from_numpy(toks)].to(torch.int8).numpy(),
+                                packed.cpu().numpy()[rows], K)
+    tsel = torch.from_numpy(toks).to(gpu)
+    rsel = torch.from_numpy(rows).to(gpu)
+    np.testing.assert_array_equal(exact[tsel][:, rsel].cpu().numpy().astype(np.int64), acc_s)
+    xg, cg, bg = x.to(torch.bfloat16).to(gpu), c.to(gpu), bias.to(gpu)
+    for alpha, beta, use_bias in ((1.0, 0.0, False), (0.5, 1.0, True)):
+        out = ops.ternary_matmul(xg, packed, K, alpha=alpha, beta=beta,
+                                 c=cg.clone() if beta else None,
+                                 bias=bg if use_bias else None, kernel=3)
+        want = alpha * exact
+        if beta:
+            want = want + beta * cg.double()
+        if use_bias:
+            want = want + bg.double()
+        bad = int((out.double() != want).sum())
+        assert bad == 0, f"alpha={alpha} beta={beta}: {bad} of {M * N} outputs differ"
+        del out, want
+    del exact
+    torch.cuda.empty_cache()
 
 
 # ------------------------------------------------------------ K3, int8 activations --

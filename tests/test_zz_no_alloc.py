@@ -63,9 +63,10 @@ def _run_pair(gpu, M, N, K, dtype, seed):
 
 
 @pytest.mark.parametrize("dtype,shapes", [
-    # bf16: whole big tiles + split-K items in one launch (Llama gate_up at M = 2048, the
-    # full 64 MiB), then every tile split (qkv at M = 512), then a smaller split shape
-    (torch.bfloat16, [(2048, 28672, 4096), (512, 6144, 4096), (300, 1000, 4104)]),
+    # bf16: whole big tiles + split-K items in one launch (the rows past whole rounds too
+    # few for a round of half-width tiles; 32 MiB), then every tile split (qkv at
+    # M = 512), then a smaller split shape
+    (torch.bfloat16, [(300, 36864, 1536), (512, 6144, 4096), (300, 1000, 4104)]),
     # int8 and float32: eight-wave splits of few tiles (int32 partials exact for int8)
     (torch.int8, [(20, 3000, 9000), (20, 1200, 4000)]),
     (torch.float32, [(48, 1000, 4104), (40, 700, 2000)]),
@@ -86,7 +87,9 @@ def test_noalloc_matches_workspace_entry_point(gpu, dtype, shapes):
 def test_noalloc_without_split_and_rejection(gpu):
     lib = _lib.lib()
     announce("noalloc K2 and unsplit K3")
-    for M, N, K in ((4, 300, 4096), (2048, 8192, 1024)):
+    # K2; whole big tiles; whole big tiles + a round of half-width tiles (Llama gate_up
+    # at M = 2048)
+    for M, N, K in ((4, 300, 4096), (2048, 8192, 1024), (2048, 28672, 4096)):
         c_na, c_ws, need = _run_pair(gpu, M, N, K, torch.bfloat16, seed=M)
         assert need == 0
         assert torch.equal(c_na, c_ws)
