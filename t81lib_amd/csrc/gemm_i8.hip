@@ -15,9 +15,12 @@
 //    each); B lane (c, h) reads X[c, 96 s + 48 h + 16 J .. + 16], 16 bytes of the
 //    activation tile.  A lane's element e and the B lane's element e are the same k, so
 //    every MFMA pairs each trit with its own activation;
-//  * decode: a 32-entry LDS table maps a tryte u to the int8 word (t0, t1, t2, 0) (entries
-//    past 26 are zero); v_perm_b32 packs the words of four trytes into the three
-//    natural-order dwords of their twelve trits;
+//  * decode: a 64 KB LDS pair table maps two trytes (the weight dword's bytes 0-1 or 2-3,
+//    addressed as (w & 0x1F1F) << 3 -- two VALU ops) to their six int8 trits; a weight
+//    dword's two entries become the three natural-order dwords of its twelve trits with
+//    one v_perm_b32 and one v_alignbit_b32 (2 table reads and 6 VALU ops per dword, where
+//    a one-tryte table took 4 reads and 8: M = 2048 gate_up 274 -> 263 us, M = 8192
+//    1000 -> 954 us);
 //  * the activation tile of step s + 1 (256 tokens x 96 int8, rows of 7 16-byte slots,
 //    one a pad slot so that the 16-byte B reads of 16 lanes fall on distinct banks) goes
 //    straight from global memory into the other LDS buffer with buffer loads carrying
@@ -47,7 +50,8 @@ constexpr int kI8TileBytes = kI8Tokens * kI8RowBytes;
 constexpr int kI8LoadsPerWave = kI8Tokens * kI8RowSlots / (64 * 4);   // 7
 constexpr uint32_t kI8Oob = 0x80000000u;
 constexpr int kI8StageStride = 68;                // int32 per staged output row (64 + 4 pad)
-constexpr int kI8LutBytes = 32 * 4 + 16;          // 32 words + slack for invalid bytes
+// pair table: entry b0 + 256 b1 (8 bytes) for every pair of 5-bit byte values
+constexpr int kI8LutBytes = 32 * 256 * 8;
 
 static_assert(kI8Tokens * kI8RowSlots % (64 * 4) == 0, "tile loads must split evenly");
 
@@ -61,17 +65,23 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t i8_rsrc(const void *base, int6
         reinterpret_cast<void *>((static_cast<uint64_t>(hi) << 32) | lo), 0, n, 0x00020000);
 }
 
-// word u = int8 bytes (t0, t1, t2, 0) of tryte u (u = 13 + t0 + 3 t1 + 9 t2), zero past 26
+// Three int8 trits of tryte u (u = 13 + t0 + 3 t1 + 9 t2) in bytes 0-2, zero past 26.
+__device__ __forceinline__ uint32_t i8_trits(int u) {
+    if (u >= 27) return 0u;
+    return static_cast<uint32_t>(static_cast<uint8_t>(static_cast<int8_t>(trit_of(u, 0)))) |
+           static_cast<uint32_t>(static_cast<uint8_t>(static_cast<int8_t>(trit_of(u, 1)))) << 8 |
+           static_cast<uint32_t>(static_cast<uint8_t>(static_cast<int8_t>(trit_of(u, 2)))) << 16;
+}
+// Entry b0 + 256 b1 = the six trits of trytes b0, b1 in bytes 0-5 (bytes 6, 7 zero), for
+// b0, b1 < 32: a weight dword's bytes 0-1 (or 2-3) address theirs as (w & 0x1F1F) << 3.
+// Only those 1024 of the 8192 slots are ever read.
 __device__ __forceinline__ void i8_lut_fill(uint8_t *lds, int tid, int nthreads) {
     uint32_t *words = reinterpret_cast<uint32_t *>(lds);
-    for (int i = tid; i < kI8LutBytes / 4; i += nthreads) {
-        uint32_t v = 0u;
-        if (i < 27) {
-            v = static_cast<uint32_t>(static_cast<uint8_t>(static_cast<int8_t>(trit_of(i, 0)))) |
-                static_cast<uint32_t>(static_cast<uint8_t>(static_cast<int8_t>(trit_of(i, 1)))) << 8 |
-                static_cast<uint32_t>(static_cast<uint8_t>(static_cast<int8_t>(trit_of(i, 2)))) << 16;
-        }
-        words[i] = v;
+    for (int i = tid; i < 1024; i += nthreads) {
+        const int b0 = i & 31, b1 = i >> 5;
+        const uint32_t lo = i8_trits(b0), hi = i8_trits(b1);
+        words[2 * (b0 + 256 * b1)] = lo | (hi << 24);
+        words[2 * (b0 + 256 * b1) + 1] = hi >> 8;
     }
 }
 
@@ -175,19 +185,20 @@ __global__ __launch_bounds__(kI8Threads) void gemm_w4_i8_kernel(
         for (int i = 0; i < kI8LoadsPerWave; ++i) load_tile_part(step, bufc, i);
     };
 
-    // decode: table words of the four trytes of weight dword `wd`
+    // decode: the pair-table entries of weight dword `wd` (trytes 0-1, then 2-3)
     auto table_fetch = [&](uint32_t wd, uint32_t (&t)[4]) {
-        const uint32_t w4 = wd << 2;
-        t[0] = *reinterpret_cast<const uint32_t *>(lut + (w4 & 0x7Fu));
-        t[1] = *reinterpret_cast<const uint32_t *>(lut + ((w4 >> 8) & 0x7Fu));
-        t[2] = *reinterpret_cast<const uint32_t *>(lut + ((w4 >> 16) & 0x7Fu));
-        t[3] = *reinterpret_cast<const uint32_t *>(lut + ((w4 >> 24) & 0x7Fu));
+        const uint2 e0 = *reinterpret_cast<const uint2 *>(lut + ((wd << 3) & 0xF8F8u));
+        const uint2 e1 = *reinterpret_cast<const uint2 *>(lut + ((wd >> 13) & 0xF8F8u));
+        t[0] = e0.x;
+        t[1] = e0.y;
+        t[2] = e1.x;
+        t[3] = e1.y;
     };
-    // the twelve trits of those four words as three dwords, natural order
+    // the twelve trits of those entries (six bytes each) as three dwords, natural order
     auto table_merge = [&](const uint32_t (&t)[4], uint32_t *out) {
-        out[0] = __builtin_amdgcn_perm(t[1], t[0], 0x04020100u);
-        out[1] = __builtin_amdgcn_perm(t[2], t[1], 0x05040201u);
-        out[2] = __builtin_amdgcn_perm(t[3], t[2], 0x06050402u);
+        out[0] = t[0];
+        out[1] = __builtin_amdgcn_perm(t[2], t[1], 0x05040100u);
+        out[2] = __builtin_amdgcn_alignbit(t[3], t[2], 16);
     };
 
     i32x16 acc[4][4];
@@ -284,7 +295,9 @@ __global__ __launch_bounds__(kI8Threads) void gemm_w4_i8_kernel(
                                                                        acc[rb][g % 4], 0, 0, 0);
             // each MFMA followed by a few of the chunk's other instructions (three LDS
             // reads, four VALU / SALU, one buffer load), as in the bf16 kernel: issue is
-            // in order with one wave per SIMD (M = 2048 gate_up 278 -> 270 us)
+            // in order with one wave per SIMD (M = 2048 gate_up 278 -> 270 us with the
+            // one-tryte table; with the pair table two reads and three VALU measured the same
+            // or up to 2 % slower)
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
