@@ -416,17 +416,24 @@ __global__ __launch_bounds__(256) void gemm_split_reduce_i8_kernel(
     }
     __syncthreads();
     const int64_t n0 = static_cast<int64_t>(tt % tiles_n) * kI8Rows + 128 * wn;
+    // whole 16-byte quads as one vector store (and load, when accumulating)
+    const bool vec4 = ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(c) & 15u) == 0;
     for (int i = threadIdx.x; i < 32 * 32; i += 256) {
         const int tok = i >> 5, c4 = i & 31;
         const int64_t m = m0 + tok;
         if (m >= M) continue;
-        const i32x4 v = *reinterpret_cast<const i32x4 *>(&st[tok * kI8ReducePitch + 4 * c4]);
+        i32x4 v = *reinterpret_cast<const i32x4 *>(&st[tok * kI8ReducePitch + 4 * c4]);
         int32_t *cr = c + m * ldc;
         const int64_t nb = n0 + 4 * c4;
+        if (vec4 && nb + 3 < N) {
+            if (accumulate) v += *reinterpret_cast<const i32x4 *>(cr + nb);
+            *reinterpret_cast<i32x4 *>(cr + nb) = v;
+        } else {
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            const int64_t n = nb + b;
-            if (n < N) cr[n] = accumulate ? v[b] + cr[n] : v[b];
+            for (int b = 0; b < 4; ++b) {
+                const int64_t n = nb + b;
+                if (n < N) cr[n] = accumulate ? v[b] + cr[n] : v[b];
+            }
         }
     }
 }
