@@ -137,6 +137,50 @@ __host__ __device__ inline int wave_lds_bytes(int M, int nsbw_max, int planes) {
     return planes * M * wave_pitch(nsbw_max);
 }
 
+// bf16 activations of one 4-limb sub-block (16 tokens x 192 values) through a wave's own
+// LDS region.  Loaded as B fragments, lane (r, q) reads 16 bytes of token r, so each
+// 16-lane pass of a load touches 16 token rows and the address unit handles a cache line
+// per row; loaded as pieces, piece p = 64 i + lane (token p / 24, values 8 (p % 24) ..
+// + 8), a pass reads consecutive bytes of one or two rows.  The pieces go to LDS (rows of
+// 400 bytes, so the fragment reads of 16 lanes spread over the banks) and come back as the
+// fragments: llama.down at 16 tokens 17.0 -> 14.3 us.  Requires K % 8 == 0 and x 16-byte
+// aligned; tokens >= M and values past K are zero.
+constexpr int kXStagePitch = 4 * kTrits * 2 + 16;
+constexpr int kXStageBytes = 16 * kXStagePitch;   // per wave
+
+__device__ __forceinline__ void load_x_pieces(const void *x, int M, int64_t K, int64_t sb,
+                                              int64_t S, int lane, u32x4 (&xp)[6]) {
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+        const int p = 64 * i + lane;
+        const int t = p / 24;
+        const int64_t k = sb * (4 * kTrits) + 8 * (p - 24 * t);
+        const bool ok = t < M && sb < S && k < K;   // sub-block sb of S exists
+        const uint8_t *src = ok ? static_cast<const uint8_t *>(x) + (t * K + k) * 2
+                                : reinterpret_cast<const uint8_t *>(kZeroBlock);
+        xp[i] = *reinterpret_cast<const u32x4 *>(src);
+    }
+}
+
+// Writes the pieces to the wave's region xs and reads back lane (r, q)'s six fragments
+// (values 48 q + 8 j .. + 8 of token r).  The wave's own LDS operations complete in order,
+// so no barrier: a later call's writes come after this call's reads.
+template <typename T>
+__device__ __forceinline__ void stage_x_pieces(uint8_t *xs, int lane, const u32x4 (&xp)[6],
+                                               T (&frag)[6]) {
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+        const int p = 64 * i + lane;
+        const int t = p / 24;
+        *reinterpret_cast<u32x4 *>(xs + t * kXStagePitch + 16 * (p - 24 * t)) = xp[i];
+    }
+    const int r = lane & 15;
+    const int q = lane >> 4;
+#pragma unroll
+    for (int j = 0; j < 6; ++j)
+        frag[j] = *reinterpret_cast<const T *>(xs + r * kXStagePitch + 96 * q + 16 * j);
+}
+
 template <int XT, int W, int SU, int R>
 __global__ __launch_bounds__(64 * W) void gemv_wave_kernel(
     const void *__restrict__ x, const uint8_t *__restrict__ w, void *__restrict__ c, int M,
@@ -338,16 +382,20 @@ __global__ __launch_bounds__(64 * W) void gemv_wave_kernel(
 // gemv_stream_kernel: for M * K too large to stage, activations come straight from
 // global memory, fetched one sub-block ahead and issued before the weight prefetch
 // (so waiting for them never drains the weight loads).  The KS waves of a workgroup
-// split K round-robin; each activation fragment serves its G 16-row groups.
-template <int XT, int G, bool kAligned, int KS>
+// split K round-robin; each activation fragment serves its G 16-row groups.  kStage
+// (bf16, kAligned): the activations of a sub-block are loaded as pieces and become
+// fragments through the wave's LDS region (load_x_pieces).
+template <int XT, int G, bool kAligned, int KS, bool kStage>
 __global__ __launch_bounds__(64 * KS) void gemv_stream_kernel(const void *__restrict__ x,
                                                           const uint8_t *__restrict__ w,
                                                           void *__restrict__ c, int M, int64_t N,
                                                           int64_t K, int64_t L, float alpha,
                                                           float beta,
                                                           const float *__restrict__ bias) {
+    static_assert(!kStage || (XT == kDtypeBF16 && kAligned), "pieces are aligned bf16");
     __shared__ __attribute__((aligned(16))) uint8_t lut[kLutBytes];
     __shared__ __attribute__((aligned(16))) floatx4 red[KS * G * 64];
+    __shared__ __attribute__((aligned(16))) uint8_t xst[kStage ? KS * kXStageBytes : 16];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -360,15 +408,49 @@ __global__ __launch_bounds__(64 * KS) void gemv_stream_kernel(const void *__rest
     const bool xvalid = r < M;
     const int64_t xrow = static_cast<int64_t>(r) * K;
     bf16x8 bh[6], bl[6], nh[6], nl[6];
-    int64_t s = wave;
+    u32x4 xp[6];
+    uint8_t *xs = xst + wave * kXStageBytes;
+    // load_x_pieces and stage_x_pieces written out here: the compiler schedules this
+    // form's piece loads earlier among the MFMAs (llama.gate M = 16 12.35 us against 12.94)
+    auto load_pieces = [&](int64_t sb) {
 #pragma unroll
-    for (int j = 0; j < 6; ++j)
-        load_x8<XT, kAligned>(x, xrow, (4 * s + q) * kTrits + 8 * j, K,
-                              xvalid && (4 * s + q) < L, bh[j], bl[j]);
+        for (int i = 0; i < 6; ++i) {
+            const int P = 64 * i + lane;
+            const int t = P / 24;
+            const int64_t k = sb * (4 * kTrits) + 8 * (P - 24 * t);
+            const bool ok = t < M && sb < S && k < K;
+            const uint8_t *src = ok ? static_cast<const uint8_t *>(x) + (t * K + k) * 2
+                                    : reinterpret_cast<const uint8_t *>(kZeroBlock);
+            xp[i] = *reinterpret_cast<const u32x4 *>(src);
+        }
+    };
+    auto stage = [&]() {
+#pragma unroll
+        for (int i = 0; i < 6; ++i) {
+            const int P = 64 * i + lane;
+            const int t = P / 24;
+            *reinterpret_cast<u32x4 *>(xs + t * kXStagePitch + 16 * (P - 24 * t)) = xp[i];
+        }
+#pragma unroll
+        for (int j = 0; j < 6; ++j)
+            bh[j] = *reinterpret_cast<const bf16x8 *>(xs + r * kXStagePitch + 96 * q + 16 * j);
+    };
+    int64_t s = wave;
+    if constexpr (kStage) {
+        load_pieces(s);
+#pragma unroll
+        for (int j = 0; j < 6; ++j) bl[j] = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
+    } else {
+#pragma unroll
+        for (int j = 0; j < 6; ++j)
+            load_x8<XT, kAligned>(x, xrow, (4 * s + q) * kTrits + 8 * j, K,
+                                  xvalid && (4 * s + q) < L, bh[j], bl[j]);
+    }
     u32x4 wcur[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) wcur[g] = load_limb(w, n0 + 16 * g + r, 4 * s + q, N, L, L);
     lut_init(lut, tid, 64 * KS);
+    if constexpr (kStage) stage();
 
     floatx4 acc[G];
 #pragma unroll
@@ -376,10 +458,14 @@ __global__ __launch_bounds__(64 * KS) void gemv_stream_kernel(const void *__rest
 
     for (; s < S; s += KS) {
         const int64_t sn = s + KS;
+        if constexpr (kStage) {
+            load_pieces(sn);
+        } else {
 #pragma unroll
-        for (int j = 0; j < 6; ++j)
-            load_x8<XT, kAligned>(x, xrow, (4 * sn + q) * kTrits + 8 * j, K,
-                                  xvalid && sn < S && (4 * sn + q) < L, nh[j], nl[j]);
+            for (int j = 0; j < 6; ++j)
+                load_x8<XT, kAligned>(x, xrow, (4 * sn + q) * kTrits + 8 * j, K,
+                                      xvalid && sn < S && (4 * sn + q) < L, nh[j], nl[j]);
+        }
         u32x4 wnext[G];
 #pragma unroll
         for (int g = 0; g < G; ++g) wnext[g] = load_limb(w, n0 + 16 * g + r, 4 * sn + q, N, L, L);
@@ -388,10 +474,14 @@ __global__ __launch_bounds__(64 * KS) void gemv_stream_kernel(const void *__rest
             acc[g] = mfma_limb<XT>(lut, wcur[g], bh, bl, acc[g]);
             wcur[g] = wnext[g];
         }
+        if constexpr (kStage) {
+            stage();
+        } else {
 #pragma unroll
-        for (int j = 0; j < 6; ++j) {
-            bh[j] = nh[j];
-            bl[j] = nl[j];
+            for (int j = 0; j < 6; ++j) {
+                bh[j] = nh[j];
+                bl[j] = nl[j];
+            }
         }
     }
     reduce_store<XT, G, KS>(acc, red, wave, lane, M, N, n0, c, alpha, beta, bias);
@@ -429,8 +519,14 @@ __global__ __launch_bounds__(64 * NW) void gemv_tile_kernel(
     int64_t N, int64_t K, int L, int nsb, int nb, int x_aligned, float alpha, float beta,
     const float *__restrict__ bias, float *__restrict__ part) {
     constexpr int D = R < kDepth ? R : kDepth;
+    // aligned bf16 activations are staged through the wave's LDS region (load_x_pieces);
+    // the regions are dead past the start barrier, and the reduction reuses the space
+    constexpr int kRedBytes = NW * R * 64 * 16;
+    constexpr int kStageBytes = XT == kDtypeBF16 ? NW * kXStageBytes : 0;
     __shared__ __attribute__((aligned(16))) uint8_t lut[kLutBytes];
-    __shared__ __attribute__((aligned(16))) floatx4 red[NW * R * 64];
+    __shared__ __attribute__((aligned(16)))
+    uint8_t smem[kStageBytes > kRedBytes ? kStageBytes : kRedBytes];
+    floatx4 *red = reinterpret_cast<floatx4 *>(smem);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -464,13 +560,16 @@ __global__ __launch_bounds__(64 * NW) void gemv_tile_kernel(
     };
 
     XRaw xr[6];
+    u32x4 xp[6];
     u32x4 ring[D];  // load t lives in ring[t % D]
     if (active) {
         // B: the activations of token r for the lane's limb, issued before the weights
         const bool bvalid = r < M && in_row;
         const int64_t xrow = static_cast<int64_t>(r < M ? r : 0) * K;
         const int64_t kb = static_cast<int64_t>(limb) * kTrits;
-        if (x_aligned) {
+        if (XT == kDtypeBF16 && x_aligned) {
+            load_x_pieces(x, M, K, sb, nsb, lane, xp);
+        } else if (x_aligned) {
 #pragma unroll
             for (int j = 0; j < 6; ++j) xr[j] = load_x8_raw<XT, true>(x, xrow, kb + 8 * j, K, bvalid);
         } else {
@@ -481,6 +580,16 @@ __global__ __launch_bounds__(64 * NW) void gemv_tile_kernel(
         for (int t = 0; t < D; ++t) ring[t] = fetch(t);
     }
     lut_fill(lut, tid, 64 * NW);
+    if constexpr (XT == kDtypeBF16) {
+        if (active && x_aligned) {
+            // the barrier's wait for LDS operations ends every wave's fragment reads
+            // before any wave writes the reduction into the same space
+            u32x4 frag[6];
+            stage_x_pieces(smem + wave * kXStageBytes, lane, xp, frag);
+#pragma unroll
+            for (int j = 0; j < 6; ++j) xr[j].a = frag[j];
+        }
+    }
     __syncthreads();
 
     if (active) {
@@ -700,7 +809,18 @@ template <int XT, int G, bool kAligned, int KS>
 hipError_t launch_stream(const void *x, const uint8_t *w, void *c, int m, int64_t n, int64_t k,
                          int64_t L, float alpha, float beta, const float *bias, hipStream_t s) {
     const int64_t blocks = (n + 16 * G - 1) / (16 * G);
-    gemv_stream_kernel<XT, G, kAligned, KS><<<dim3(blocks), dim3(64 * KS), 0, s>>>(
+    // Staged pieces for one row group per workgroup or more than 8 tokens (llama.down M = 8
+    // 12.95 -> 11.43 us, phi3.down M = 8 8.26 -> 7.36, llama.gate M = 16 12.94 -> 12.26);
+    // at two row groups and up to 8 tokens the direct fragment loads, which then touch
+    // only M token rows, measured faster (llama.gate M = 5 9.53 against 10.66 staged).
+    if constexpr (XT == kDtypeBF16 && kAligned) {
+        if (G == 1 || m > 8) {
+            gemv_stream_kernel<XT, G, kAligned, KS, true><<<dim3(blocks), dim3(64 * KS), 0, s>>>(
+                x, w, c, m, n, k, L, alpha, beta, bias);
+            return hipGetLastError();
+        }
+    }
+    gemv_stream_kernel<XT, G, kAligned, KS, false><<<dim3(blocks), dim3(64 * KS), 0, s>>>(
         x, w, c, m, n, k, L, alpha, beta, bias);
     return hipGetLastError();
 }

@@ -85,7 +85,10 @@ LLAMA = {"qkv": (4096, 6144), "gate": (4096, 14336), "down": (14336, 4096)}
 K2_CASES = (
     [("phi3." + name, M, K, N) for name, (K, N) in PHI3.items() for M in (1, 4, 16)]
     + [("llama.gate", M, 4096, 14336) for M in (1, 2, 3, 8, 12, 16)]
-    + [("llama.down", M, 14336, 4096) for M in (1, 2, 4, 8, 16)]
+    + [("llama.down", M, 14336, 4096) for M in (1, 2, 4, 5, 8, 16)]
+    # staged activation pieces at few tokens (one row group per workgroup), and at
+    # 9..16 tokens over two row groups per workgroup
+    + [("phi3.down", 5, 8192, 3072), ("phi3.o", 12, 3072, 3072), ("wide", 10, 3072, 6144)]
     + [("llama.qkv", 1, 4096, 6144), ("ragged", 1, 4100, 77), ("ragged", 3, 1000, 333),
        ("ragged", 13, 5767, 300)]
 )
