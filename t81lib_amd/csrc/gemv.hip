@@ -737,10 +737,12 @@ TilePlan gemv_tile_plan(int64_t n, int64_t k) {
 
 // Whether the tile kernel takes this call, and the workspace its splits need.  Its time
 // hardly depends on M, and its K splits end in a second launch (about 3 us on top of the
-// main kernel at 16 tokens); measured against the stream / wave kernels it is faster
-// for 9..16 tokens over a long K (>= 32 sub-blocks) and at most 8192 rows -- 14336 ->
-// 4096 at 16 tokens 22.5 -> 17.6 us, 8192 -> 3072 13.7 -> 10.1 us -- and slower on
-// the wide and short-K config-3/4 shapes, which keep those kernels.
+// main kernel at 16 tokens); measured against the stream / wave kernels with fragment
+// loads it is faster for 9..16 tokens over a long K (>= 32 sub-blocks) and at most 8192
+// rows -- 14336 -> 4096 at 16 tokens 22.5 -> 17.6 us, 8192 -> 3072 13.7 -> 10.1 us --
+// and slower on the wide and short-K config-3/4 shapes, which keep those kernels.  bf16
+// activations with K % 8 == 0 and 16-byte aligned x take the stream kernel with staged
+// pieces instead (launch_gemv_tile declines them).
 bool gemv_tile_fits(int m, int64_t n, int64_t k) {
     const int64_t L = (k + kTrits - 1) / kTrits;
     const int64_t nsb = (L + 3) / 4;
@@ -798,6 +800,9 @@ hipError_t launch_gemv_tile(bool *handled, const void *x, const uint8_t *w, void
     constexpr int64_t kElem = XT == kDtypeF32 ? 4 : (XT == kDtypeBF16 ? 2 : 1);
     const bool aligned =
         (k % 8 == 0) && (reinterpret_cast<uintptr_t>(x) % (kElem == 1 ? 8 : 16) == 0);
+    // aligned bf16: the stream kernel with staged activation pieces, one launch, is faster
+    // (llama.down M = 16 13.2 us against 14.4 with the split sum; phi3.down 7.9 against 9.4)
+    if (XT == kDtypeBF16 && aligned) return hipSuccess;
     *handled = true;
     float *part = static_cast<float *>(ws);
     if (t.nw == 4)
@@ -838,6 +843,19 @@ hipError_t launch_stream_shape(const void *x, const uint8_t *w, void *c, int m, 
                                int64_t k, int64_t L, float alpha, float beta, const float *bias,
                                hipStream_t s) {
     const int64_t nsb = (L + 3) / 4;
+    if constexpr (XT == kDtypeBF16 && kAligned) {
+        // 9..16 tokens, staged pieces (their cost no longer grows with the tokens): eight
+        // waves, the row groups per workgroup by width -- a sweep of 1, 2, 4 groups x 4, 8,
+        // 16 waves at 9, 12 and 16 tokens: llama.gate M = 16 12.3 -> 10.1 us, phi3.qkv
+        // 9.8 -> 7.5, phi3.gate_up 10.7 -> 8.4, phi3.o 5.9 -> 4.9, 4096 -> 6144 8.6 -> 7.2
+        if (m > 8) {
+            if (n <= 4096)
+                return launch_stream<XT, 1, kAligned, 8>(x, w, c, m, n, k, L, alpha, beta, bias, s);
+            if (n < 9216)
+                return launch_stream<XT, 2, kAligned, 8>(x, w, c, m, n, k, L, alpha, beta, bias, s);
+            return launch_stream<XT, 4, kAligned, 8>(x, w, c, m, n, k, L, alpha, beta, bias, s);
+        }
+    }
     if (n <= 4096) {
         if (nsb >= 32)
             return launch_stream<XT, 1, kAligned, 8>(x, w, c, m, n, k, L, alpha, beta, bias, s);
@@ -929,7 +947,9 @@ hipError_t launch_gemv_x(const void *x, const uint8_t *w, void *c, int m, int64_
     // bf16 over many rows takes the stream kernel: 8+ tokens over >= 9216 rows (3072 ->
     // 16384 at M = 8: 10.5 -> 8.7 us; even at 3072 -> 9216), 5+ over >= 14336 (4096 ->
     // 14336 at M = 5: 11.2 -> 9.6 us; 3072 -> 9216 at M = 5 stays faster staged)
-    const bool wide = XT == kDtypeBF16 && ((m >= 8 && n >= 9216) || (m >= 5 && n >= 14336));
+    // ... and 9+ tokens with aligned bf16 activations, staged (see launch_stream_shape)
+    const bool wide = XT == kDtypeBF16 && ((m >= 8 && n >= 9216) || (m >= 5 && n >= 14336) ||
+                                           (m > 8 && aligned8));
     if (L > 0 && max_run > 0 && wg <= 8 && !wide) {
         while (wg < 8 && groups * wg < kTargetWaves && nsb >= 4 * wg) wg *= 2;
         const int W = wg < 4 ? 4 : wg;
@@ -968,9 +988,10 @@ hipError_t launch_gemv_x(const void *x, const uint8_t *w, void *c, int m, int64_
 }  // namespace
 
 int64_t gemv_workspace_bytes(int64_t m, int64_t n, int64_t k, int x_dtype) {
-    (void)x_dtype;  // the partials are float32 for every activation type
     if (m < 5 || m > 16 || n <= 0 || k <= 0) return 0;
-    return gemv_tile_workspace_bytes(static_cast<int>(m), n, k);
+    // bf16 with K % 8 == 0 runs the staged stream kernel in one launch instead
+    if (x_dtype == kDtypeBF16 && k % 8 == 0) return 0;
+    return gemv_tile_workspace_bytes(static_cast<int>(m), n, k);   // float32 partials
 }
 
 hipError_t launch_gemv(const void *x, int x_dtype, const uint8_t *w, void *c, int m, int64_t n,

@@ -413,7 +413,8 @@ def test_k2_m5_to_16_full_check(gpu, orc, M, N, K, dtype):
 
 
 @pytest.mark.parametrize("M,N,K,dtype,splits", [
-    (9, 37, 6200, torch.bfloat16, 5),      # 33 sub-blocks: one active wave in the last split
+    (9, 37, 6200, torch.float32, 5),       # 33 sub-blocks: one active wave in the last split
+    (16, 4096, 14336, torch.bfloat16, 0),  # aligned bf16: the staged stream kernel instead
     (11, 3000, 9001, torch.bfloat16, 6),   # K % 8 != 0 (element loads)
     (16, 4100, 14400, torch.int8, 10),     # rows past N in the last block
     (13, 8192, 6144, torch.float32, 4),    # four row groups per workgroup

@@ -70,9 +70,9 @@ def _run_pair(gpu, M, N, K, dtype, seed):
     # int8 and float32: eight-wave splits of few tiles (int32 partials exact for int8)
     (torch.int8, [(20, 3000, 9000), (20, 1200, 4000)]),
     (torch.float32, [(48, 1000, 4104), (40, 700, 2000)]),
-    # K2 with 9..16 tokens over a long K: K split over workgroups, partials summed in
-    # split order
-    (torch.bfloat16, [(16, 4096, 14336), (9, 3000, 9000)]),
+    # K2 with 9..16 tokens over a long K (float32 and int8 activations; aligned bf16 runs
+    # in one launch): K split over workgroups, partials summed in split order
+    (torch.float32, [(16, 4096, 14336), (9, 3000, 9000)]),
     (torch.int8, [(12, 3072, 8192), (10, 2000, 7000)]),
 ])
 def test_noalloc_matches_workspace_entry_point(gpu, dtype, shapes):
@@ -87,9 +87,9 @@ def test_noalloc_matches_workspace_entry_point(gpu, dtype, shapes):
 def test_noalloc_without_split_and_rejection(gpu):
     lib = _lib.lib()
     announce("noalloc K2 and unsplit K3")
-    # K2; whole big tiles; whole big tiles + a round of half-width tiles (Llama gate_up
-    # at M = 2048)
-    for M, N, K in ((4, 300, 4096), (2048, 8192, 1024), (2048, 28672, 4096)):
+    # K2 at 4 and 16 tokens; whole big tiles; whole big tiles + a round of half-width
+    # tiles (Llama gate_up at M = 2048)
+    for M, N, K in ((4, 300, 4096), (16, 4096, 14336), (2048, 8192, 1024), (2048, 28672, 4096)):
         c_na, c_ws, need = _run_pair(gpu, M, N, K, torch.bfloat16, seed=M)
         assert need == 0
         assert torch.equal(c_na, c_ws)
