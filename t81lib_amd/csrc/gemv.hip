@@ -814,12 +814,12 @@ template <int XT, int G, bool kAligned, int KS>
 hipError_t launch_stream(const void *x, const uint8_t *w, void *c, int m, int64_t n, int64_t k,
                          int64_t L, float alpha, float beta, const float *bias, hipStream_t s) {
     const int64_t blocks = (n + 16 * G - 1) / (16 * G);
-    // Staged pieces for one row group per workgroup or more than 8 tokens (llama.down M = 8
+    // Staged pieces for one row group per workgroup or 8+ tokens (llama.down M = 8
     // 12.95 -> 11.43 us, phi3.down M = 8 8.26 -> 7.36, llama.gate M = 16 12.94 -> 12.26);
-    // at two row groups and up to 8 tokens the direct fragment loads, which then touch
-    // only M token rows, measured faster (llama.gate M = 5 9.53 against 10.66 staged).
+    // at two row groups and fewer tokens the direct fragment loads, which then touch only
+    // M token rows, measured faster (llama.gate M = 5 9.53 against 10.66 staged).
     if constexpr (XT == kDtypeBF16 && kAligned) {
-        if (G == 1 || m > 8) {
+        if (G == 1 || m >= 8) {
             gemv_stream_kernel<XT, G, kAligned, KS, true><<<dim3(blocks), dim3(64 * KS), 0, s>>>(
                 x, w, c, m, n, k, L, alpha, beta, bias);
             return hipGetLastError();
@@ -844,11 +844,12 @@ hipError_t launch_stream_shape(const void *x, const uint8_t *w, void *c, int m, 
                                hipStream_t s) {
     const int64_t nsb = (L + 3) / 4;
     if constexpr (XT == kDtypeBF16 && kAligned) {
-        // 9..16 tokens, staged pieces (their cost no longer grows with the tokens): eight
+        // 8..16 tokens, staged pieces (their cost no longer grows with the tokens): eight
         // waves, the row groups per workgroup by width -- a sweep of 1, 2, 4 groups x 4, 8,
-        // 16 waves at 9, 12 and 16 tokens: llama.gate M = 16 12.3 -> 10.1 us, phi3.qkv
-        // 9.8 -> 7.5, phi3.gate_up 10.7 -> 8.4, phi3.o 5.9 -> 4.9, 4096 -> 6144 8.6 -> 7.2
-        if (m > 8) {
+        // 16 waves at 5, 8, 9, 12 and 16 tokens: llama.gate M = 16 12.3 -> 10.1 us, phi3.qkv
+        // 9.8 -> 7.5, phi3.gate_up 10.7 -> 8.4, phi3.o 5.9 -> 4.9, 4096 -> 6144 8.6 -> 7.2,
+        // phi3.qkv M = 8 8.3 -> 7.5; at 5 tokens the fragment loads stay faster
+        if (m >= 8) {
             if (n <= 4096)
                 return launch_stream<XT, 1, kAligned, 8>(x, w, c, m, n, k, L, alpha, beta, bias, s);
             if (n < 9216)
@@ -947,9 +948,9 @@ hipError_t launch_gemv_x(const void *x, const uint8_t *w, void *c, int m, int64_
     // bf16 over many rows takes the stream kernel: 8+ tokens over >= 9216 rows (3072 ->
     // 16384 at M = 8: 10.5 -> 8.7 us; even at 3072 -> 9216), 5+ over >= 14336 (4096 ->
     // 14336 at M = 5: 11.2 -> 9.6 us; 3072 -> 9216 at M = 5 stays faster staged)
-    // ... and 9+ tokens with aligned bf16 activations, staged (see launch_stream_shape)
+    // ... and 8+ tokens with aligned bf16 activations, staged (see launch_stream_shape)
     const bool wide = XT == kDtypeBF16 && ((m >= 8 && n >= 9216) || (m >= 5 && n >= 14336) ||
-                                           (m > 8 && aligned8));
+                                           (m >= 8 && aligned8));
     if (L > 0 && max_run > 0 && wg <= 8 && !wide) {
         while (wg < 8 && groups * wg < kTargetWaves && nsb >= 4 * wg) wg *= 2;
         const int W = wg < 4 ? 4 : wg;
