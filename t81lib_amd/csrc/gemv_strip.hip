@@ -115,18 +115,31 @@ __device__ __forceinline__ float strip_keep(floatx4 v, int j) {
 // order (E table only, eight MFMAs) -- fewer MFMAs for two ORs per dword; the launch uses
 // it for one token over one 64-limb range or up to three 32-limb ranges, where it
 // measured faster (4096 x 14336: 7.03 -> 6.95 us; 3072 x 9216: 5.36 -> 5.09 us).
+//
+// kStageB (bf16, aligned x; waves that stream more than one range): the B operand of a
+// range is loaded as consecutive 16-byte pieces of each token's values (piece p = 64 i +
+// lane: token p / (24 S), limb (p % (24 S)) / 6 of the range, values 8 (p % 6) ..) and
+// reaches the lanes through the wave's own LDS region (64 slots of 112 bytes, one per
+// (token, limb), so the fragment reads of 16 lanes fall on distinct banks).  Loaded as
+// fragments, each 16-lane pass touches 16 limbs 96 bytes apart.  Measured at four tokens:
+// 14336 -> 4096 9.38 -> 8.57 us, 8192 -> 3072 6.27 -> 6.01 us; slower where every wave
+// streams one range (4096 -> 14336 at one token 6.45 -> 8.73 us: the LDS round trip then
+// sits at the start of every wave's critical path).
 template <int XT, int S, int NW, int R, bool kNat = false, bool kNt = false,
-          int DEPTH = kStripDepth>
+          int DEPTH = kStripDepth, bool kStageB = false>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void gemv_strip_kernel(
     const void *__restrict__ x, const uint8_t *__restrict__ w, void *__restrict__ c, int M,
     int64_t N, int64_t K, int L, int nranges, int x_aligned, float alpha, float beta,
     const float *__restrict__ bias) {
     static_assert(S == 4 || S == 8 || S == 16, "one matched entry per lane needs S >= 4");
+    static_assert(!kStageB || (XT == kDtypeBF16 && !kNat), "staged B: bf16, padded order");
     constexpr int RPI = 16 / S;  // rows per load (and tokens per MFMA)
     constexpr int H = R * RPI;   // rows per workgroup
     constexpr int D = R < DEPTH ? R : DEPTH;
     __shared__ __attribute__((aligned(16))) uint8_t lut[kLutBytes];
     __shared__ float red[NW][R][64];
+    constexpr int kSlot = 112;
+    __shared__ __attribute__((aligned(16))) uint8_t xst[kStageB ? NW * 64 * kSlot : 16];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -162,7 +175,21 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
         const int64_t xrow = static_cast<int64_t>(mb < M ? mb : 0) * K;
         const int64_t kb = static_cast<int64_t>(limb) * kTrits;
         XRaw xr[6];
-        if (x_aligned) {
+        u32x4 xp[6];
+        if constexpr (kStageB) {
+#pragma unroll
+            for (int ii = 0; ii < 6; ++ii) {
+                const int p = 64 * ii + lane;
+                const int tk = p / (24 * S);
+                const int pp = p - tk * (24 * S);
+                const int64_t v =
+                    (static_cast<int64_t>(rg) * 4 * S + pp / 6) * kTrits + 8 * (pp % 6);
+                const bool ok = tk < M && v < K;
+                const uint8_t *src = ok ? static_cast<const uint8_t *>(x) + (tk * K + v) * 2
+                                        : reinterpret_cast<const uint8_t *>(kZeroBlock);
+                xp[ii] = *reinterpret_cast<const u32x4 *>(src);
+            }
+        } else if (x_aligned) {
 #pragma unroll
             for (int j = 0; j < 6; ++j)
                 xr[j] = load_x8_raw<XT, true>(x, xrow, kb + 8 * j, K, bvalid);
@@ -191,6 +218,23 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
             first = false;
         }
 
+        if constexpr (kStageB) {
+            // the wave's own region: its LDS operations complete in order, so the next
+            // range's writes come after these reads without a barrier
+            uint8_t *xs = xst + wave * 64 * kSlot;
+#pragma unroll
+            for (int ii = 0; ii < 6; ++ii) {
+                const int p = 64 * ii + lane;
+                const int tk = p / (24 * S);
+                const int pp = p - tk * (24 * S);
+                *reinterpret_cast<u32x4 *>(xs + (tk * 4 * S + pp / 6) * kSlot + 16 * (pp % 6)) =
+                    xp[ii];
+            }
+            const int slot = (i / S) * 4 * S + sub;
+#pragma unroll
+            for (int j = 0; j < 6; ++j)
+                xr[j].a = *reinterpret_cast<const u32x4 *>(xs + slot * kSlot + 16 * j);
+        }
         constexpr int kOps = kNat ? 6 : 8;  // MFMA operands per limb
         bf16x8 nh[6], nl[6], bh[kOps], bl[kOps];
 #pragma unroll
@@ -287,18 +331,28 @@ struct StripArgs {
 };
 
 template <int XT, int S, int NW, int R, bool kNat = false, bool kNt = false,
-          int DEPTH = kStripDepth>
+          int DEPTH = kStripDepth, bool kStageB = false>
 hipError_t launch_strip(const StripArgs &a) {
     constexpr int H = R * (16 / S);
     const int64_t blocks = (a.n + H - 1) / H;
-    gemv_strip_kernel<XT, S, NW, R, kNat, kNt, DEPTH><<<dim3(static_cast<unsigned>(blocks)), dim3(64 * NW), 0,
+    gemv_strip_kernel<XT, S, NW, R, kNat, kNt, DEPTH, kStageB><<<dim3(static_cast<unsigned>(blocks)), dim3(64 * NW), 0,
                                        a.s>>>(a.x, a.w, a.c, a.m, a.n, a.k, a.L, a.nranges,
                                               a.aligned ? 1 : 0, a.alpha, a.beta, a.bias);
     return hipGetLastError();
 }
 
-template <int XT, int S, int R, bool kNt = false>
+template <int XT, int S, int R, bool kNt = false, bool kStageB = false>
 hipError_t launch_strip_nw(int nw, const StripArgs &a) {
+    constexpr int D = kStripDepth;
+    if constexpr (kStageB) {
+        // staged B runs only where waves stream several ranges: five waves or more
+        switch (nw) {
+            case 5: return launch_strip<XT, S, 5, R, false, kNt, D, true>(a);
+            case 6: return launch_strip<XT, S, 6, R, false, kNt, D, true>(a);
+            case 7: return launch_strip<XT, S, 7, R, false, kNt, D, true>(a);
+            default: return launch_strip<XT, S, 8, R, false, kNt, D, true>(a);
+        }
+    }
     switch (nw) {
         case 1: return launch_strip<XT, S, 1, R, false, kNt>(a);
         case 2: return launch_strip<XT, S, 2, R, false, kNt>(a);
@@ -333,15 +387,15 @@ hipError_t launch_strip_nat(int nw, int r, const StripArgs &a) {
     return launch_strip_nat_nw<S, 4, kNt>(nw, a);
 }
 
-template <int XT, int S, bool kNt = false>
+template <int XT, int S, bool kNt = false, bool kStageB = false>
 hipError_t launch_strip_nr(int nw, int r, const StripArgs &a) {
     if constexpr (XT == kDtypeBF16) {
-        if (r == 14) return launch_strip_nw<XT, S, 14, kNt>(nw, a);
-        if (r == 7) return launch_strip_nw<XT, S, 7, kNt>(nw, a);
+        if (r == 14) return launch_strip_nw<XT, S, 14, kNt, kStageB>(nw, a);
+        if (r == 7) return launch_strip_nw<XT, S, 7, kNt, kStageB>(nw, a);
     }
-    if (r >= 16) return launch_strip_nw<XT, S, 16, kNt>(nw, a);
-    if (r >= 8) return launch_strip_nw<XT, S, 8, kNt>(nw, a);
-    return launch_strip_nw<XT, S, 4, kNt>(nw, a);
+    if (r >= 16) return launch_strip_nw<XT, S, 16, kNt, kStageB>(nw, a);
+    if (r >= 8) return launch_strip_nw<XT, S, 8, kNt, kStageB>(nw, a);
+    return launch_strip_nw<XT, S, 4, kNt, kStageB>(nw, a);
 }
 
 // The weight loads of bf16 launches over at least this many packed bytes carry the
@@ -416,6 +470,15 @@ hipError_t launch_strip_x(bool *handled, const void *x, const uint8_t *w, void *
                                : launch_strip_nat<8, true>(nw, r, a);
             return S == 16 ? launch_strip_nat<16, false>(nw, r, a)
                            : launch_strip_nat<8, false>(nw, r, a);
+        }
+        // staged B where waves stream several ranges (see gemv_strip_kernel); two to four
+        // tokens (S = 8, 4)
+        if (a.aligned && per_wave > 1 && S != 16) {
+            if (nt)
+                return S == 8 ? launch_strip_nr<XT, 8, true, true>(nw, r, a)
+                              : launch_strip_nr<XT, 4, true, true>(nw, r, a);
+            return S == 8 ? launch_strip_nr<XT, 8, false, true>(nw, r, a)
+                          : launch_strip_nr<XT, 4, false, true>(nw, r, a);
         }
         if (nt) {
             switch (S) {
