@@ -277,7 +277,8 @@ def test_k3_half_width_integer_bf16_bit_exact(gpu, orc, M, N, K):
 
 # ------------------------------------------------------------ K3, int8 activations --
 I8_FULL = [
-    # name, M, K, N: whole tiles + split-K items (gate_up), all split (M = 512), odd step
+    # name, M, K, N: whole tiles + a round of half-width tiles (gate_up), all split (M =
+    # 512), odd step
     # counts (K = 4096: 43 steps), long K (down), M = 8192
     ("llama.gate_up", 2048, 4096, 28672),
     ("llama.down", 2048, 14336, 4096),
@@ -289,6 +290,9 @@ I8_SMALL = [
     # whole step, even and odd step counts, more tiles than CUs, few tiles (split-K)
     (300, 256 * 160 + 13, 208), (260, 256 * 81 + 7, 480), (512, 256 * 200 - 5, 96),
     (65, 1000, 4096), (300, 1000, 4112), (100, 2000, 4800), (257, 700, 16),
+    # whole rounds for the first 16384 rows, the rest as one round of half-width tiles
+    # (200 / 192 of them on 256 CUs): two and three steps, ragged N
+    (1000, 256 * 88 + 7, 96), (1000, 256 * 88 - 5, 208),
 ]
 
 
