@@ -712,6 +712,26 @@ def summarize_trace(d: str, cmd: str, top: int = 8) -> str:
     return "\n".join(out) + "\n"
 
 
+def summarize_trace_by_grid(d: str, kernel_sub: str, cmd: str) -> str:
+    """Per-dispatch table of a `rocprofv3 --kernel-trace --output-format csv` run, grouped by
+    kernel and launch shape (grid x workgroup size, which tells apart the shapes one kernel
+    instance serves), for the kernels whose name contains kernel_sub, in first-launch order."""
+    groups: dict = {}
+    for r in _read_csv(_find(d, "kernel_trace.csv")):
+        if kernel_sub not in r["Kernel_Name"]:
+            continue
+        key = (r["Kernel_Name"], int(r["Grid_Size_X"]), int(r["Workgroup_Size_X"]))
+        groups.setdefault(key, []).append(
+            (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    out = [f"command: {cmd}", "",
+           f"{'calls':>6} {'avg_us':>8} {'min_us':>8} {'max_us':>8} {'workgroups':>10} "
+           f"{'threads':>7}  kernel"]
+    for (name, grid, wg), ts in groups.items():
+        out.append(f"{len(ts):6d} {sum(ts) / len(ts):8.2f} {min(ts):8.2f} {max(ts):8.2f} "
+                   f"{grid // wg:10d} {wg:7d}  {name[:100]}")
+    return "\n".join(out) + "\n"
+
+
 def _counter_median(d: str, kernel_sub: str, counter: str) -> tuple:
     import statistics
     vals = [float(r["Counter_Value"]) for r in _read_csv(_find(d, "counter_collection.csv"))
@@ -817,6 +837,9 @@ def main() -> int:
                     help="also time the config-3/4 shapes and print a table on stderr")
     ap.add_argument("--summarize-trace", metavar="DIR",
                     help="print the kernel table of a rocprofv3 csv --stats run and exit")
+    ap.add_argument("--summarize-trace-by-grid", nargs=2, metavar=("DIR", "KERNEL"),
+                    help="print the dispatches of a rocprofv3 csv --kernel-trace run grouped "
+                         "by kernel and launch shape, for kernels whose name contains KERNEL")
     ap.add_argument("--summarize-counters", nargs=2, metavar=("DIR", "KERNEL"),
                     help="print the median counters of a rocprofv3 csv --pmc run for the "
                          "kernels whose name contains KERNEL, and exit")
@@ -828,6 +851,10 @@ def main() -> int:
     args = ap.parse_args()
     if args.summarize_trace:
         sys.stdout.write(summarize_trace(args.summarize_trace, " | ".join(args.cmd)))
+        return 0
+    if args.summarize_trace_by_grid:
+        sys.stdout.write(summarize_trace_by_grid(*args.summarize_trace_by_grid,
+                                                 " | ".join(args.cmd)))
         return 0
     if args.summarize_counters:
         sys.stdout.write(summarize_counters(*args.summarize_counters, " | ".join(args.cmd)))
