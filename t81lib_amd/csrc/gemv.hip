@@ -830,6 +830,115 @@ hipError_t launch_stream(const void *x, const uint8_t *w, void *c, int m, int64_
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------------
+// gemv_stream2_kernel: 17..32 tokens (bf16, K % 8 == 0, 16-byte aligned x), the staged
+// stream kernel with two 16-token column blocks: each weight limb is decoded once and meets
+// both blocks' B fragments (six MFMAs each), so the weights stream once for all 32 tokens.
+// Staging, the fixed-order reduction and the stores as gemv_stream_kernel, per block (block
+// b holds tokens 16 b .. 16 b + 15).  A separate kernel, not a template parameter of the
+// other: the 8..16-token code generation stays as tuned.
+template <int G, int KS>
+__global__ __launch_bounds__(64 * KS) void gemv_stream2_kernel(const void *__restrict__ x,
+                                                           const uint8_t *__restrict__ w,
+                                                           void *__restrict__ c, int M,
+                                                           int64_t N, int64_t K, int64_t L,
+                                                           float alpha, float beta,
+                                                           const float *__restrict__ bias) {
+    constexpr int NB = 2;
+    __shared__ __attribute__((aligned(16))) uint8_t lut[kLutBytes];
+    __shared__ __attribute__((aligned(16))) floatx4 red[KS * G * NB * 64];
+    __shared__ __attribute__((aligned(16))) uint8_t xst[KS * NB * kXStageBytes];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int r = lane & 15;
+    const int q = lane >> 4;
+    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * (16 * G);
+    const int64_t S = (L + 3) / 4;
+
+    bf16x8 bh[NB][6], bl[6];
+    u32x4 xp[6 * NB];
+    uint8_t *xs = xst + wave * NB * kXStageBytes;
+#pragma unroll
+    for (int j = 0; j < 6; ++j) bl[j] = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
+    auto load_pieces = [&](int64_t sb) {
+#pragma unroll
+        for (int i = 0; i < 6 * NB; ++i) {
+            const int P = 64 * i + lane;
+            const int t = P / 24;
+            const int64_t k = sb * (4 * kTrits) + 8 * (P - 24 * t);
+            const bool ok = t < M && sb < S && k < K;
+            const uint8_t *src = ok ? static_cast<const uint8_t *>(x) + (t * K + k) * 2
+                                    : reinterpret_cast<const uint8_t *>(kZeroBlock);
+            xp[i] = *reinterpret_cast<const u32x4 *>(src);
+        }
+    };
+    auto stage = [&]() {
+#pragma unroll
+        for (int i = 0; i < 6 * NB; ++i) {
+            const int P = 64 * i + lane;
+            const int t = P / 24;
+            *reinterpret_cast<u32x4 *>(xs + t * kXStagePitch + 16 * (P - 24 * t)) = xp[i];
+        }
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int j = 0; j < 6; ++j)
+                bh[b][j] = *reinterpret_cast<const bf16x8 *>(
+                    xs + (16 * b + r) * kXStagePitch + 96 * q + 16 * j);
+    };
+    int64_t s = wave;
+    load_pieces(s);
+    u32x4 wcur[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) wcur[g] = load_limb(w, n0 + 16 * g + r, 4 * s + q, N, L, L);
+    lut_init(lut, tid, 64 * KS);
+    stage();
+
+    floatx4 acc[G][NB];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int b = 0; b < NB; ++b) acc[g][b] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    for (; s < S; s += KS) {
+        const int64_t sn = s + KS;
+        load_pieces(sn);
+        u32x4 wnext[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) wnext[g] = load_limb(w, n0 + 16 * g + r, 4 * sn + q, N, L, L);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            uint32_t pairs[24];
+#pragma unroll
+            for (int d = 0; d < 4; ++d) decode_dword(lut, wcur[g][d], pairs + 6 * d);
+#pragma unroll
+            for (int b = 0; b < NB; ++b)
+                acc[g][b] = mfma_pairs<kDtypeBF16>(pairs, bh[b], bl, acc[g][b]);
+            wcur[g] = wnext[g];
+        }
+        stage();
+    }
+
+    // per (row group, block): the KS partial tiles summed in wave order
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int b = 0; b < NB; ++b) red[((wave * G + g) * NB + b) * 64 + lane] = acc[g][b];
+    __syncthreads();
+    for (int e = wave; e < G * NB; e += KS) {
+        const int g = e / NB;
+        const int b = e % NB;
+        floatx4 v = red[(g * NB + b) * 64 + lane];
+#pragma unroll
+        for (int ww = 1; ww < KS; ++ww) v += red[((ww * G + g) * NB + b) * 64 + lane];
+        store_tile<kDtypeBF16>(v, lane, M - 16 * b, N, n0 + 16 * g,
+                               static_cast<float *>(c) + static_cast<int64_t>(16 * b) * N, alpha,
+                               beta, bias);
+    }
+}
+
 // Rows per workgroup and waves splitting K for the stream kernel (a sweep of 1, 2, 4, 8
 // row groups x 4, 8, 16 waves on the config-3/4 decode shapes at 8 and 16 tokens):
 // at most 4096 rows take one row group per workgroup -- the grid then covers the CUs --
@@ -987,6 +1096,39 @@ hipError_t launch_gemv_x(const void *x, const uint8_t *w, void *c, int m, int64_
 }
 
 }  // namespace
+
+// 17..32 tokens with aligned bf16 activations (called by the K3 launcher, which owns
+// M > 16): the two-block stream kernel, one launch, no workspace.  Row groups per workgroup
+// and waves from a sweep of 1, 2, 4 groups x 4, 8 waves at 17, 24 and 32 tokens on the
+// config-3/4 shapes, against the eight-wave GEMM kernel with its K split: at 32 tokens
+// llama.qkv 15.8 -> 9.9 us, 4096 -> 4096 13.9 -> 8.7, gate_up 35.1 -> 28.7, llama.down
+// 28.0 -> 19.6, phi3.o 15.2 -> 7.4, phi3.gate_up 20.7 -> 13.2 (bit-identical on integer
+// activations).  *handled is false for other shapes.
+hipError_t launch_gemv_two_blocks(bool *handled, const void *x, const uint8_t *w, void *c, int m,
+                                  int64_t n, int64_t k, float alpha, float beta,
+                                  const float *bias, hipStream_t s) {
+    *handled = false;
+    if (!gemv_two_blocks_fits(x, m, n, k)) return hipSuccess;
+    const int64_t L = (k + kTrits - 1) / kTrits;
+    *handled = true;
+    auto go = [&](auto gc, auto kc) {
+        constexpr int G = decltype(gc)::value, KS = decltype(kc)::value;
+        const int64_t blocks = (n + 16 * G - 1) / (16 * G);
+        gemv_stream2_kernel<G, KS><<<dim3(static_cast<unsigned>(blocks)), dim3(64 * KS), 0, s>>>(
+            x, w, c, m, n, k, L, alpha, beta, bias);
+        return hipGetLastError();
+    };
+    if (n <= 4096) return go(std::integral_constant<int, 1>(), std::integral_constant<int, 8>());
+    if (n < 9216) return go(std::integral_constant<int, 2>(), std::integral_constant<int, 8>());
+    return go(std::integral_constant<int, 2>(), std::integral_constant<int, 4>());
+}
+
+bool gemv_two_blocks_fits(const void *x, int64_t m, int64_t n, int64_t k) {
+    // 16-byte pieces of whole 8-value chunks; block offsets (16 rows x N) and grid in range
+    return m >= 17 && m <= 32 && n > 0 && k > 0 && k % 8 == 0 &&
+           reinterpret_cast<uintptr_t>(x) % 16 == 0 && (n + 15) / 16 < (int64_t(1) << 31) &&
+           k < (int64_t(1) << 31);
+}
 
 int64_t gemv_workspace_bytes(int64_t m, int64_t n, int64_t k, int x_dtype) {
     if (m < 5 || m > 16 || n <= 0 || k <= 0) return 0;

@@ -112,6 +112,34 @@ def test_k2_integer_bf16_bit_exact(gpu, orc, name, M, K, N):
         assert_bits(out.cpu().numpy(), want, f"alpha={alpha} beta={beta} bias={use_bias}")
 
 
+TWO_BLOCK_CASES = [
+    # 17..32 tokens through the K3 entry: the two-block stream kernel (one row group per
+    # workgroup up to 4096 rows, two below 9216, two with four waves above), ragged N and a
+    # K that ends inside a sub-block
+    ("llama.down", 17, 14336, 4096), ("llama.gate", 24, 4096, 14336), ("llama.qkv", 32, 4096, 6144),
+    ("phi3.o", 32, 3072, 3072), ("phi3.down", 32, 8192, 3072), ("phi3.gate_up", 32, 3072, 16384),
+    ("ragged", 29, 4104, 333),
+]
+
+
+@pytest.mark.parametrize("name,M,K,N", TWO_BLOCK_CASES)
+def test_two_block_integer_bf16_bit_exact(gpu, orc, name, M, K, N):
+    announce(f"exact two-block M={M} {name} K={K} N={N}")
+    lib = _lib.lib()
+    assert lib.t81_hip_ternary_matmul_workspace_size(M, N, K, _lib.DTYPE_BF16) == 0
+    w, x, c, bias = int_problem(M, N, K, seed=M * 131 + K + N)
+    packed = ops.quantize_pack(w.to(gpu), 0.45, _lib.THR_CPP)
+    acc = orc.trit_matmul_i64(x.to(torch.int8).numpy(), packed.cpu().numpy(), K)
+    xg = x.to(torch.bfloat16).to(gpu)
+    cg = c.to(gpu)
+    for alpha, beta, use_bias in ((1.0, 0.0, False), (0.5, 1.0, True), (-2.0, 0.5, True)):
+        out = ops.ternary_matmul(xg, packed, K, alpha=alpha, beta=beta,
+                                 c=cg.clone() if beta else None,
+                                 bias=bias.to(gpu) if use_bias else None, kernel=3)
+        want = expected(acc, alpha, beta, c.numpy(), bias.numpy() if use_bias else None)
+        assert_bits(out.cpu().numpy(), want, f"alpha={alpha} beta={beta} bias={use_bias}")
+
+
 # --------------------------------------------------------------------- K3 --
 def _sample(M, N, n1, seed, tokens=48, rows=96):
     """Tokens from every 256-token tile; rows from both the whole-tile region [0, n1)

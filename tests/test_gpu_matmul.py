@@ -453,13 +453,13 @@ def test_k2_tile_kernel_plans(gpu, orc, M, N, K, dtype, splits):
     assert torch.equal(outs[0], outs[1]), "two runs of the same call differ"
 
 
-@pytest.mark.parametrize("M,N,K,dtype", [(32, 4096, 14336, torch.bfloat16),
+@pytest.mark.parametrize("M,N,K,dtype", [(40, 4096, 14336, torch.bfloat16),
                                          (48, 1000, 4104, torch.float32),
                                          (20, 3000, 9000, torch.int8),
                                          (100, 2000, 4800, torch.int8),
                                          (64, 6144, 4096, torch.bfloat16),
                                          (300, 1500, 3000, torch.float32),
-                                         (32, 16384, 3072, torch.bfloat16),
+                                         (40, 16384, 3072, torch.bfloat16),
                                          (20, 20000, 2000, torch.int8)])
 def test_k3_eight_wave_split_k_full_check(gpu, orc, M, N, K, dtype):
     """Launches of the eight-wave kernel with few tiles (17 <= M <= 64, int8 and fp32
