@@ -109,8 +109,9 @@ int t81_hip_ternary_matmul_kernel(int which, const void *x, int x_dtype, const u
                                   float beta, const float *bias, void *stream);
 
 /* Same, with a caller-owned device workspace: which = 0 (by M, as
- * t81_hip_ternary_matmul), 2 or 3.  When K3 has few output tiles (bf16
- * activations, K % 8 == 0), or K2 runs 5..16 tokens, and workspace_bytes is at least
+ * t81_hip_ternary_matmul), 2 or 3.  When K3 has few output tiles for its shape, or K2
+ * runs 9..16 tokens over a long K with float32 or int8 activations (or bf16 with K not a
+ * multiple of 8), and workspace_bytes is at least
  * t81_hip_ternary_matmul_workspace_size(...), K is split over several workgroups
  * per tile: each writes its partial tile to the workspace and a second kernel sums
  * the partials in split order (deterministic).  NULL / 0 bytes: no split.  The
