@@ -77,6 +77,8 @@ SMALL = [
     (1, 64, 48), (1, 100, 1024), (4, 33, 1000), (16, 257, 3072), (3, 16, 4096), (16, 48, 97),
     (1, 7, 1), (2, 5, 47),
     (17, 64, 96), (64, 96, 1024), (100, 200, 300), (128, 512, 4096), (37, 45, 4097),
+    # 17..32 tokens, bf16: the two-block stream kernel (one and two row groups per workgroup)
+    (32, 300, 4104), (25, 6200, 1536),
 ]
 
 
