@@ -939,8 +939,10 @@ __global__ __launch_bounds__(64 * KS) void gemv_stream2_kernel(const void *__res
     }
 }
 
-// Rows per workgroup and waves splitting K for the stream kernel (a sweep of 1, 2, 4, 8
-// row groups x 4, 8, 16 waves on the config-3/4 decode shapes at 8 and 16 tokens):
+// Rows per workgroup and waves splitting K for the stream kernel.  Aligned bf16 at 8..16
+// tokens: the rule at the top of the function.  Otherwise (a sweep of 1, 2, 4, 8 row
+// groups x 4, 8, 16 waves on the config-3/4 decode shapes at 8 and 16 tokens, fragment
+// loads):
 // at most 4096 rows take one row group per workgroup -- the grid then covers the CUs --
 // with eight waves over >= 32 sub-blocks (llama.down M = 8 15.7 -> 13.0 us, phi3.down
 // M = 16 13.3 -> 11.3 us) and four below (phi3.o M = 16 6.9 -> 6.0 us); 9..16 tokens
