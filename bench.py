@@ -535,17 +535,18 @@ DECODE_SHAPES = [("phi3.qkv", 3072, 9216), ("phi3.o", 3072, 3072), ("phi3.gate_u
 
 def run_decode(torch, ops, lib, dev) -> dict:
     """Config 3 (Phi-3 decode shapes) and the Llama-3-8B gate / down shapes at 1, 4, 8 and
-    16 tokens, through the product path (ops.ternary_matmul: K2, with the workspace its
-    K splits use): median microseconds per call over rotating weight copies (> 2 x MALL,
-    so every call streams from HBM), GB/s of algorithmic bytes, and each shape's 16-token
-    time over its one-token time."""
+    16 tokens, and at 32 (config 5's decode batch), through the product path
+    (ops.ternary_matmul: K2 up to 16 tokens, with the workspace its K splits use; the K3
+    entry at 32, whose bf16 calls run K2's two-block stream kernel): median microseconds
+    per call over rotating weight copies (> 2 x MALL, so every call streams from HBM), GB/s
+    of algorithmic bytes, and each shape's 16-token time over its one-token time."""
     shapes = {}
     for name, k, n in DECODE_SHAPES:
         wbytes = 16 * n * ((k + 47) // 48)
         copies = max(4, -(-2 * MALL_BYTES // wbytes) + 2)
         wb = make_weights(torch, ops, lib, n, k, copies, dev, seed=3)
         row = {"K": k, "N": n}
-        for m in (1, 4, 8, 16):
+        for m in (1, 4, 8, 16, 32):
             x = torch.randn((m, k), device=dev).to(torch.bfloat16)
             out = torch.empty((m, n), device=dev)
             d = time_graph(torch, lambda w: ops.ternary_matmul(x, w, k, c=out), wb, 256, 32,
@@ -559,8 +560,9 @@ def run_decode(torch, ops, lib, dev) -> dict:
         shapes[name] = row
         del wb
         torch.cuda.empty_cache()
-    return {"workload": "K2 decode, bf16 x, fp32 out, alpha=1 beta=0, median over rotating "
-                        "weight copies; config 3 (Phi-3) plus the Llama-3-8B gate / down shapes",
+    return {"workload": "K2 decode at 1-16 tokens (32: the K3 entry, K2's two-block kernel), "
+                        "bf16 x, fp32 out, alpha=1 beta=0, median over rotating weight copies; "
+                        "config 3 (Phi-3) plus the Llama-3-8B gate / down shapes",
             "shapes": shapes}
 
 
@@ -712,21 +714,32 @@ def summarize_trace(d: str, cmd: str, top: int = 8) -> str:
     return "\n".join(out) + "\n"
 
 
-def summarize_trace_by_grid(d: str, kernel_sub: str, cmd: str) -> str:
+def summarize_trace_by_grid(d: str, kernel_sub: str, cmd: str, runs: bool = False) -> str:
     """Per-dispatch table of a `rocprofv3 --kernel-trace --output-format csv` run, grouped by
     kernel and launch shape (grid x workgroup size, which tells apart the shapes one kernel
-    instance serves), for the kernels whose name contains kernel_sub, in first-launch order."""
-    groups: dict = {}
-    for r in _read_csv(_find(d, "kernel_trace.csv")):
-        if kernel_sub not in r["Kernel_Name"]:
-            continue
+    instance serves), for the kernels whose name contains kernel_sub, in first-launch order.
+    runs: one row per run of consecutive such dispatches with the same key (in start order),
+    so that two shapes with one launch shape, timed one after the other, stay apart."""
+    rows = [r for r in _read_csv(_find(d, "kernel_trace.csv")) if kernel_sub in r["Kernel_Name"]]
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    groups: list = []
+    index: dict = {}
+    for r in rows:
         key = (r["Kernel_Name"], int(r["Grid_Size_X"]), int(r["Workgroup_Size_X"]))
-        groups.setdefault(key, []).append(
-            (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+        us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        if runs:
+            if not groups or groups[-1][0] != key:
+                groups.append((key, []))
+            groups[-1][1].append(us)
+        else:
+            if key not in index:
+                index[key] = len(groups)
+                groups.append((key, []))
+            groups[index[key]][1].append(us)
     out = [f"command: {cmd}", "",
            f"{'calls':>6} {'avg_us':>8} {'min_us':>8} {'max_us':>8} {'workgroups':>10} "
            f"{'threads':>7}  kernel"]
-    for (name, grid, wg), ts in groups.items():
+    for (name, grid, wg), ts in groups:
         out.append(f"{len(ts):6d} {sum(ts) / len(ts):8.2f} {min(ts):8.2f} {max(ts):8.2f} "
                    f"{grid // wg:10d} {wg:7d}  {name[:100]}")
     return "\n".join(out) + "\n"
@@ -840,6 +853,9 @@ def main() -> int:
     ap.add_argument("--summarize-trace-by-grid", nargs=2, metavar=("DIR", "KERNEL"),
                     help="print the dispatches of a rocprofv3 csv --kernel-trace run grouped "
                          "by kernel and launch shape, for kernels whose name contains KERNEL")
+    ap.add_argument("--runs", action="store_true",
+                    help="with --summarize-trace-by-grid: one row per run of consecutive "
+                         "dispatches instead of one per launch shape")
     ap.add_argument("--summarize-counters", nargs=2, metavar=("DIR", "KERNEL"),
                     help="print the median counters of a rocprofv3 csv --pmc run for the "
                          "kernels whose name contains KERNEL, and exit")
@@ -854,7 +870,7 @@ def main() -> int:
         return 0
     if args.summarize_trace_by_grid:
         sys.stdout.write(summarize_trace_by_grid(*args.summarize_trace_by_grid,
-                                                 " | ".join(args.cmd)))
+                                                 " | ".join(args.cmd), runs=args.runs))
         return 0
     if args.summarize_counters:
         sys.stdout.write(summarize_counters(*args.summarize_counters, " | ".join(args.cmd)))
