@@ -336,7 +336,9 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_kernel(
 //
 // A workgroup of four waves computes a 256 x 256 tile of C^T; wave (wn, wm) owns
 // 128 weight rows x 128 tokens, i.e. 4 x 4 blocks of v_mfma_f32_32x32x16_bf16
-// (256 accumulator registers).  A k-step is two limbs (96 trits):
+// (256 accumulator registers).  (RB = 3: 192-row tiles, three row blocks per wave, for
+// shapes whose 256-row tiles leave CUs idle; whole tiles only.)  A k-step is two limbs
+// (96 trits):
 //  * lane (r, h) loads all 16 bytes of limb 2s + h of row 32 rb + r, so one
 //    32-trit slice of the MFMA pairs trits 8J..8J+7 of limb 2s (h = 0) with the
 //    same trits of limb 2s + 1 (h = 1), J = 0..5; B lane (c, h) reads
@@ -385,12 +387,14 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void *base,
 // order, so the workgroups that start with a (shorter) remainder item finish their whole
 // tiles half a tile out of step with the others, and the C stores of the two halves do
 // not all land at once.
-template <int XT>
+template <int XT, int RB>
 __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
     const void *__restrict__ x, const uint8_t *__restrict__ w, void *__restrict__ c, int M, int N,
     int ldc, int K, int L, float alpha, float beta, const float *__restrict__ bias, int n1,
     int sps, float4 *__restrict__ part, int nsplit, int half) {
     static_assert(XT == kDtypeBF16, "the LDS tile is filled straight from bf16 activations");
+    static_assert(RB == 3 || RB == 4, "three or four 32-row blocks per wave");
+    constexpr int kRows = 64 * RB;   // weight rows per tile
     // Two separate tile objects (not one array indexed by a run-time parity): the
     // loads into one buffer then provably do not alias the reads of the other, and
     // the compiler need not wait for them before every LDS read.  A half-width item
@@ -422,8 +426,8 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
     // round had drained (~15 us a round at M = 2048).
     const int tiles_m = (M + kW4Tokens - 1) / kW4Tokens;
     const int tiles_mh = (M + kW4Tokens / 2 - 1) / (kW4Tokens / 2);   // half-width tiles
-    const int tn1 = (n1 + kW4Rows - 1) / kW4Rows;        // row tiles of whole tiles
-    const int tn2 = (N - n1 + kW4Rows - 1) / kW4Rows;    // row tiles of the remainder
+    const int tn1 = (n1 + kRows - 1) / kRows;        // row tiles of whole tiles
+    const int tn2 = (N - n1 + kRows - 1) / kRows;    // row tiles of the remainder
     const int full_items = tn1 * tiles_m;
     const int tiles2 = tn2 * tiles_m;
     const int rem_items = half ? tn2 * tiles_mh : (nsplit > 0 ? tiles2 * nsplit : 0);
@@ -432,8 +436,8 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
     const int all_steps = (L + 1) / 2;
     lut_fill(lut, tid, kW4Threads);  // published by the first item's barrier
 
-    // One item: 256 weight rows (nwg..) x 64 CB tokens (m0..) over k-steps
-    // [s_begin, s_end); wave (wn, wm) owns 128 rows x 32 CB tokens.  CB = 4: whole or
+    // One item: 64 RB weight rows (nwg..) x 64 CB tokens (m0..) over k-steps
+    // [s_begin, s_end); wave (wn, wm) owns 32 RB rows x 32 CB tokens.  CB = 4: whole or
     // split-K tiles; CB = 2: half-width tiles.
     auto run_item = [&](auto cbc, int nwg, int m0, int s_begin, int s_end, bool split, int sp,
                         int tt) {
@@ -443,8 +447,9 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
         constexpr int LPW = (kTL + 3) / 4;             // per wave (13; 7, the last wave 5)
         constexpr int NCH = 6 * CB;                    // chunks of four MFMAs per step
         constexpr int HALF = 3 * CB;                   // chunks per half step
-        constexpr int NF = CB == 4 ? 8 : 4;            // chunks of a half that read the table
-        constexpr int FPC = 8 / NF;                    // weight dwords looked up per such chunk
+        constexpr int NF = CB == 4 ? 2 * RB : RB;      // chunks of a half that read the table
+        constexpr int FPC = 2 * RB / NF;               // weight dwords looked up per such chunk
+        constexpr int kWaitW = 0x0F70 | RB;            // vmcnt(RB): all but the newest RB loads
 
         // The lane index passes through an empty asm once per item, so the per-lane
         // offsets derived from it are recomputed per item instead of being hoisted out of
@@ -459,15 +464,15 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
         // or zeros; either decodes to finite trits that meet zero activations.
         const __amdgpu_buffer_rsrc_t wsrc = uniform_rsrc(
             w + static_cast<int64_t>(nwg) * L * kTrytes, static_cast<int64_t>(N - nwg) * L * kTrytes);
-        uint32_t woff[4];
+        uint32_t woff[RB];
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb)
-            woff[rb] = (static_cast<uint32_t>(128 * wn + 32 * rb + r) * static_cast<uint32_t>(L) +
+        for (int rb = 0; rb < RB; ++rb)
+            woff[rb] = (static_cast<uint32_t>(32 * RB * wn + 32 * rb + r) * static_cast<uint32_t>(L) +
                         static_cast<uint32_t>(h)) * kTrytes;
-        auto fetch_w = [&](int step, u32x4 (&dst)[4]) {
+        auto fetch_w = [&](int step, u32x4 (&dst)[RB]) {
             const uint32_t koff = static_cast<uint32_t>(step) * (2 * kTrytes);
 #pragma unroll
-            for (int rb = 0; rb < 4; ++rb)
+            for (int rb = 0; rb < RB; ++rb)
                 dst[rb] = __builtin_bit_cast(
                     u32x4, __builtin_amdgcn_raw_buffer_load_b128(wsrc, woff[rb] + koff, 0, 0));
         };
@@ -518,9 +523,9 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
         };
 
         // Half p of the lane's limbs -> A fragments J = 3p + j of the four row blocks.
-        auto decode_half = [&](const u32x4 (&wl)[4], int p, bf16x8 (&a)[4][3]) {
+        auto decode_half = [&](const u32x4 (&wl)[RB], int p, bf16x8 (&a)[RB][3]) {
 #pragma unroll
-            for (int rb = 0; rb < 4; ++rb) {
+            for (int rb = 0; rb < RB; ++rb) {
                 uint32_t pairs[12];
                 decode_dword(lut, wl[rb][2 * p], pairs);
                 decode_dword(lut, wl[rb][2 * p + 1], pairs + 6);
@@ -533,9 +538,9 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
             }
         };
 
-        floatx16 acc[4][CB];
+        floatx16 acc[RB][CB];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < RB; ++i)
 #pragma unroll
             for (int j = 0; j < CB; ++j)
 #pragma unroll
@@ -568,27 +573,27 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
             out[4] = e[2].y | e[3].x;
             out[5] = e[3].y;
         };
-        u32x4 wcur[4], wnxt[4], wnn[4];
-        bf16x8 a0[4][3], a1[4][3];
+        u32x4 wcur[RB], wnxt[RB], wnn[RB];
+        bf16x8 a0[RB][3], a1[RB][3];
         if (s_begin < s_end) {
             fetch_w(s_begin, wcur);
             load_tile(s_begin, B0());
         }
         fetch_w(s_begin + 1, wnxt);   // stays in flight across the barrier
         if constexpr (CB == 4) {
-            // vmcnt(4): the tile's LDS writes have landed before the barrier publishes them
-            __builtin_amdgcn_s_waitcnt(0x0F74);
+            // vmcnt(RB): the tile's LDS writes have landed before the barrier publishes them
+            __builtin_amdgcn_s_waitcnt(kWaitW);
         } else {
             // a half-width step is too short to cover its tile loads, so every step
             // loads the tile of the step after next: here the second step's tile too.
             // vmcnt(9): the first tile has landed (the second tile's loads -- five in
             // the last wave -- and the four weight loads may still be in flight).
-            // One step only: vmcnt(4), the weight loads.
+            // One step only: vmcnt(RB), the weight loads.
             if (s_begin + 1 < s_end) {
                 load_tile(s_begin + 1, B1());
                 __builtin_amdgcn_s_waitcnt(0x0F79);
             } else {
-                __builtin_amdgcn_s_waitcnt(0x0F74);
+                __builtin_amdgcn_s_waitcnt(kWaitW);
             }
         }
         __syncthreads();
@@ -605,7 +610,7 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
         // step) into a0; table reads two chunks ahead of their merge -- and of the loads.
         // Whole tiles (CB = 4): the tile of the next step (chunks 0-11), then the weights
         // of the step after it (chunk 12); issued after the tile loads, the weight loads
-        // can stay in flight across the step's wait (vmcnt(4)), so they have a step and a
+        // can stay in flight across the step's wait (vmcnt(RB)), so they have a step and a
         // half to land, not half a step.  Half-width tiles (CB = 2): the weights of the
         // step after next (chunk 0), and, past the barrier, the tile of the step after
         // next into this step's buffer (chunks 9-11; not in the item's last step, so no
@@ -621,7 +626,7 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
         // last step those three reads fetch bytes that are never used.
         auto step_body = [&](int step, auto bufc, auto otherc) {
             uint2 e[3][FPC][4];
-            uint32_t pairs[4][12];
+            uint32_t pairs[RB][12];
 #pragma unroll
             for (int g = 0; g < NCH; ++g) {
                 const int p = g / HALF;
@@ -666,15 +671,15 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
                     }
                 }
                 const bf16x8 b = __builtin_bit_cast(bf16x8, bq[g % 4]);
-                const bf16x8(&a)[4][3] = p == 0 ? a0 : a1;
+                const bf16x8(&a)[RB][3] = p == 0 ? a0 : a1;
 #pragma unroll
-                for (int rb = 0; rb < 4; ++rb)
+                for (int rb = 0; rb < RB; ++rb)
                     acc[rb][gg % CB] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
                         a[rb][gg / CB], b, acc[rb][gg % CB], 0, 0, 0);
                 if (gg == HALF - 1) {
-                    bf16x8(&next)[4][3] = p == 0 ? a1 : a0;
+                    bf16x8(&next)[RB][3] = p == 0 ? a1 : a0;
 #pragma unroll
-                    for (int rb = 0; rb < 4; ++rb)
+                    for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
                         for (int j = 0; j < 3; ++j) {
                             const u32x4 raw = {pairs[rb][4 * j], pairs[rb][4 * j + 1],
@@ -687,7 +692,7 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
                 // is in order, so three MFMAs issued back to back (the default schedule)
                 // left the matrix pipe idle while the rest of the chunk issued after them.
 #pragma unroll
-                for (int k = 0; k < 4; ++k) {
+                for (int k = 0; k < RB; ++k) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
                     __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);   // LDS read
                     __builtin_amdgcn_sched_group_barrier(0x006, 3, 0);   // VALU, SALU
@@ -695,14 +700,14 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
                 }
                 __builtin_amdgcn_sched_barrier(0);
                 if (g == NCH - 4) {
-                    // vmcnt(4): the tile loads are older than the four weight loads of
+                    // vmcnt(RB): the tile loads are older than the RB weight loads of
                     // step + 2
-                    __builtin_amdgcn_s_waitcnt(0x0F74);
+                    __builtin_amdgcn_s_waitcnt(kWaitW);
                     __syncthreads();
                 }
             }
 #pragma unroll
-            for (int rb = 0; rb < 4; ++rb) {
+            for (int rb = 0; rb < RB; ++rb) {
                 wcur[rb] = wnxt[rb];
                 wnxt[rb] = wnn[rb];
             }
@@ -715,7 +720,7 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
         if (step < s_end)  // odd step count: the last step, peeled (no join inside the loop)
             step_body(step, B0(), B1());
 
-        if constexpr (CB == 4) {
+        if constexpr (CB == 4 && RB == 4) {
             if (split) {
                 float4 *dst =
                     part + (((static_cast<int64_t>(sp) * tiles2 + tt) * 4 + wave) * 64) * 64 + lane;
@@ -752,21 +757,24 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
 #pragma unroll
         for (int cb = 0; cb < CB; ++cb) {
 #pragma unroll
-            for (int rp = 0; rp < 2; ++rp) {
+            for (int rp = 0; rp < (RB + 1) / 2; ++rp) {
+                // rows of this pass: 64, or 32 for the third block of three
+                const int prow = 2 * rp + 1 < RB ? 64 : 32;
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
+                    if (2 * rp + j < RB)
 #pragma unroll
                     for (int a4 = 0; a4 < 4; ++a4)
                         *reinterpret_cast<float4 *>(&st[r * kW4StageStride + 32 * j + 8 * a4 + 4 * h]) =
                             make_float4(acc[2 * rp + j][cb][4 * a4], acc[2 * rp + j][cb][4 * a4 + 1],
                                         acc[2 * rp + j][cb][4 * a4 + 2], acc[2 * rp + j][cb][4 * a4 + 3]);
-                const int nb = col0 + 128 * wn + 64 * rp + tc;
+                const int nb = col0 + 32 * RB * wn + 64 * rp + tc;
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
                     const int tok = 4 * i + tq;
                     const float4 v = *reinterpret_cast<const float4 *>(&st[tok * kW4StageStride + tc]);
                     const int m = m0 + 32 * CB * wm + 32 * cb + tok;
-                    if (m >= M) continue;
+                    if (m >= M || tc >= prow) continue;
                     float *cr = cdst + static_cast<int64_t>(m) * ldv;
                     float y[4] = {al * v.x, al * v.y, al * v.z, al * v.w};
                     if (vec4 && nb + 3 < nv) {
@@ -811,10 +819,12 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
         const int item =
             __builtin_amdgcn_readfirstlane(q < head ? q : (rem ? q - full_items : q - head));
         if (half && rem) {
-            const int tn = __builtin_amdgcn_readfirstlane(item % tn2);
-            const int tm = __builtin_amdgcn_readfirstlane(item / tn2);
-            run_item(std::integral_constant<int, 2>(), n1 + tn * kW4Rows, tm * (kW4Tokens / 2), 0,
-                     all_steps, false, 0, 0);
+            if constexpr (RB == 4) {
+                const int tn = __builtin_amdgcn_readfirstlane(item % tn2);
+                const int tm = __builtin_amdgcn_readfirstlane(item / tn2);
+                run_item(std::integral_constant<int, 2>(), n1 + tn * kRows, tm * (kW4Tokens / 2),
+                         0, all_steps, false, 0, 0);
+            }
         } else {
             const bool split = rem;
             const int sp = split ? item / tiles2 : 0;
@@ -824,7 +834,7 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
             const int tm = __builtin_amdgcn_readfirstlane(tt / tiles_n);
             const int s_begin = split ? sp * sps : 0;
             const int s_end = split && s_begin + sps < all_steps ? s_begin + sps : all_steps;
-            run_item(std::integral_constant<int, 4>(), (split ? n1 : 0) + tn * kW4Rows,
+            run_item(std::integral_constant<int, 4>(), (split ? n1 : 0) + tn * kRows,
                      tm * kW4Tokens, s_begin, s_end, split, sp, tt);
         }
     }  // work items
@@ -964,6 +974,30 @@ int64_t split_workspace_bytes(const SplitPlan &p) {
     return p.nsplit > 1 ? p.nsplit * p.tiles * kW4Rows * kW4Tokens * 4 : 0;
 }
 
+// 192-row tiles (three 32-row blocks per wave) when a shape has fewer 256-row tiles than
+// CUs but 160 or more (no split), and its 192-row tiles still fit one round: every CU
+// then runs one tile of three quarters the work instead of three quarters of the CUs
+// one tile each (qkv at M = 2048: 192 -> 256 tiles).
+bool gemm_use_192(int64_t m, int64_t n) {
+    const int64_t tiles_m = (m + kW4Tokens - 1) / kW4Tokens;
+    const int64_t t4 = ((n + kW4Rows - 1) / kW4Rows) * tiles_m;
+    const int64_t t3 = ((n + 191) / 192) * tiles_m;
+    const int64_t cus = cu_count();
+    return m > 64 && t4 >= 160 && t4 < cus && t3 <= cus;
+}
+hipError_t launch_gemm_w4_192(const void *x, const uint8_t *w, void *c, int64_t m, int64_t n,
+                              int64_t ldc, int64_t k, float alpha, float beta, const float *bias,
+                              hipStream_t s) {
+    const int64_t L = (k + kTrits - 1) / kTrits;
+    const int64_t items = ((n + 191) / 192) * ((m + kW4Tokens - 1) / kW4Tokens);
+    const int64_t cus = cu_count();
+    gemm_w4_kernel<kDtypeBF16, 3><<<dim3(items < cus ? items : cus), dim3(kW4Threads), 0, s>>>(
+        x, w, c, static_cast<int>(m), static_cast<int>(n), static_cast<int>(ldc),
+        static_cast<int>(k), static_cast<int>(L), alpha, beta, bias, static_cast<int>(n), 0,
+        nullptr, 0, 0);
+    return hipGetLastError();
+}
+
 // Rows [0, n1) of W as whole big tiles and, with plan != nullptr (nsplit > 1) and part
 // (room for the plan's partial tiles), rows [n1, n) as split-K items, in one launch;
 // then the split partials are summed into C.  With half, rows [n1, n) run instead as
@@ -982,7 +1016,7 @@ hipError_t launch_gemm_w4(const void *x, const uint8_t *w, void *c, int64_t m, i
                           (rem ? gemm_half_tiles(m, n - n1) : 0);
     if (items <= 0) return hipSuccess;
     const int64_t cus = cu_count();
-    gemm_w4_kernel<kDtypeBF16><<<dim3(items < cus ? items : cus), dim3(kW4Threads), 0, s>>>(
+    gemm_w4_kernel<kDtypeBF16, 4><<<dim3(items < cus ? items : cus), dim3(kW4Threads), 0, s>>>(
         x, w, c, static_cast<int>(m), static_cast<int>(split || rem ? n : n1),
         static_cast<int>(ldc), static_cast<int>(k), static_cast<int>(L), alpha, beta, bias,
         static_cast<int>(n1), split ? static_cast<int>(plan->sps) : 0,
@@ -1122,6 +1156,8 @@ hipError_t launch_gemm_x(const void *x, const uint8_t *w, void *c, int64_t m, in
         const int64_t n1 = gemm_rows_whole_rounds(m, n);
         const int64_t L = (k + kTrits - 1) / kTrits;
         const bool w4 = XT == kDtypeBF16 && gemm_w4_fits(x, m, n, k);
+        if (w4 && gemm_use_192(m, n))
+            return launch_gemm_w4_192(x, w, c, m, n, n, k, alpha, beta, bias, s);
         if (w4 && gemm_use_half(m, n, n1))
             // one launch: whole tiles for rows [0, n1), one round of half-width tiles for
             // the rest

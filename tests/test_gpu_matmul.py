@@ -272,15 +272,16 @@ def test_k3_row_split_full_check(gpu, orc, dtype):
 
 
 @pytest.mark.parametrize("M,N,K", [(300, 256 * 160 + 13, 200), (512, 256 * 80, 192),
-                                   (260, 256 * 81 + 7, 480), (512, 256 * 200 - 5, 96)])
+                                   (260, 256 * 81 + 7, 480), (512, 256 * 200 - 5, 96),
+                                   (300, 192 * 128 - 5, 200)])
 def test_k3_big_tile_full_check(gpu, orc, M, N, K):
     """bf16 activations with K % 8 == 0 and at least 160 tiles of 256 x 256: the
     one-wave-per-SIMD kernel (activation tile loaded straight into LDS, two k-steps per
     loop iteration plus a peeled odd step).  Every output is checked: odd and even step
     counts, K past the last whole step, ragged M and N, alpha/beta/bias, (first case)
-    the rows past whole rounds as split-K items of the same launch, and (last case)
+    the rows past whole rounds as split-K items of the same launch, (fourth case)
     400 whole tiles on a grid of one workgroup per CU, so some workgroups take a second
-    tile."""
+    tile, and (last case) 192 tiles of 256 rows run as 256 tiles of 192 rows."""
     announce(f"K3 big tile M={M} N={N} K={K}")
     w, x, c, bias = make_problem(M, N, K, torch.bfloat16, seed=K)
     packed, out = run(gpu, w, x, c, bias, K, 0.75, 0.5, True, kernel=3)
