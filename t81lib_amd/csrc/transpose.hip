@@ -22,6 +22,13 @@
 // into the four output limbs.  Four consecutive threads write the four limbs of one output
 // row (64 contiguous bytes).  Every byte in and out is touched once: HBM-bound.  (Bytes
 // above 26 are not trytes; their output is unspecified.)
+//
+// Tile order: a tile's 64-byte input runs share 128-byte lines with the tile of the next
+// input limb group, and its 64-byte output runs with the tile of the next output limb
+// group.  Workgroups are dealt to the eight XCDs (each with its own L2) in turn, so the
+// grid is one-dimensional and workgroup b takes tile number (b / 8) within XCD b % 8's
+// contiguous share of the tiles, input limb group fastest: tiles sharing lines then run
+// on one XCD at about the same time (14336 x 4096: 16.4 -> 11.4 us).
 #include "t81_device.hpp"
 #include "t81_kernels.hpp"
 
@@ -63,12 +70,18 @@ __device__ __forceinline__ void byte_transpose4(uint32_t a, uint32_t b, uint32_t
 __global__ __launch_bounds__(256) void transpose_packed_kernel(const uint8_t *__restrict__ in,
                                                                uint8_t *__restrict__ out,
                                                                int64_t rows, int64_t cols,
-                                                               int64_t L, int64_t Lt) {
+                                                               int64_t L, int64_t Lt, int ny) {
     __shared__ __attribute__((aligned(16))) uint8_t tile[kTileRows * kPitch];
     __shared__ uint32_t lut[32];
     const int tid = threadIdx.x;
-    const int64_t lt0 = static_cast<int64_t>(blockIdx.x) * kOutLimbs;  // first output limb
-    const int64_t c0 = static_cast<int64_t>(blockIdx.y) * kTileLimbs;  // first input limb
+    // tile number tn (input limb group tn % ny, output limb group tn / ny) of workgroup wg
+    const int ntiles = static_cast<int>(gridDim.x);
+    const int wg = static_cast<int>(blockIdx.x);
+    const int xcd = wg & 7;
+    const int per = ntiles >> 3, extra = ntiles & 7;
+    const int tn = xcd * per + (xcd < extra ? xcd : extra) + (wg >> 3);
+    const int64_t lt0 = static_cast<int64_t>(tn / ny) * kOutLimbs;  // first output limb
+    const int64_t c0 = static_cast<int64_t>(tn % ny) * kTileLimbs;  // first input limb
     if (tid < 32) lut[tid] = digit_word(tid);
     __syncthreads();
 
@@ -142,9 +155,11 @@ hipError_t launch_transpose_packed(const uint8_t *in, uint8_t *out, int64_t rows
     if (rows == 0 || cols == 0) return hipSuccess;
     const int64_t L = (cols + kTrits - 1) / kTrits;
     const int64_t Lt = (rows + kTrits - 1) / kTrits;
-    const dim3 grid(static_cast<unsigned>((Lt + kOutLimbs - 1) / kOutLimbs),
-                    static_cast<unsigned>((L + kTileLimbs - 1) / kTileLimbs));
-    transpose_packed_kernel<<<grid, 256, 0, s>>>(in, out, rows, cols, L, Lt);
+    const int64_t nx = (Lt + kOutLimbs - 1) / kOutLimbs;
+    const int64_t ny = (L + kTileLimbs - 1) / kTileLimbs;
+    if (nx * ny > 0x7FFFFFFF) return hipErrorInvalidValue;   // tile numbers are ints
+    transpose_packed_kernel<<<dim3(static_cast<unsigned>(nx * ny)), 256, 0, s>>>(
+        in, out, rows, cols, L, Lt, static_cast<int>(ny));
     return hipGetLastError();
 }
 

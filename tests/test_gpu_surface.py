@@ -127,9 +127,11 @@ def test_linear_eval_vs_oracle(gpu, orc, tokens):
 
 
 @pytest.mark.parametrize("rows,cols", [(70, 200), (1, 1), (48, 48), (49, 97), (300, 1000),
-                                       (1000, 300), (96, 192), (5, 4097)])
+                                       (1000, 300), (96, 192), (5, 4097), (2500, 1300)])
 def test_transpose_packed_bit_exact(gpu, orc, rows, cols):
-    """T^T limbs equal the oracle's pack of the transposed unpacked trits (zero-padded)."""
+    """T^T limbs equal the oracle's pack of the transposed unpacked trits (zero-padded).
+    (2500 x 1300: 14 x 7 = 98 tiles, so the eight XCDs' shares of the tile order differ
+    in size.)"""
     announce(f"transpose_packed {rows}x{cols}")
     g = torch.Generator("cpu").manual_seed(rows * 1000 + cols)
     w = torch.randn(rows, cols, generator=g)
