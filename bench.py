@@ -535,9 +535,10 @@ DECODE_SHAPES = [("phi3.qkv", 3072, 9216), ("phi3.o", 3072, 3072), ("phi3.gate_u
 
 def run_decode(torch, ops, lib, dev) -> dict:
     """Config 3 (Phi-3 decode shapes) and the Llama-3-8B gate / down shapes at 1, 4, 8 and
-    16 tokens, and at 32 (config 5's decode batch), through the product path
+    16 tokens, and at 32 (config 5's decode batch) and 48, through the product path
     (ops.ternary_matmul: K2 up to 16 tokens, with the workspace its K splits use; the K3
-    entry at 32, whose bf16 calls run K2's two-block stream kernel): median microseconds
+    entry at 32 and 48, whose bf16 calls run K2's column-block stream kernel with two and
+    three 16-token blocks): median microseconds
     per call over rotating weight copies (> 2 x MALL, so every call streams from HBM), GB/s
     of algorithmic bytes, and each shape's 16-token time over its one-token time."""
     shapes = {}
@@ -546,7 +547,7 @@ def run_decode(torch, ops, lib, dev) -> dict:
         copies = max(4, -(-2 * MALL_BYTES // wbytes) + 2)
         wb = make_weights(torch, ops, lib, n, k, copies, dev, seed=3)
         row = {"K": k, "N": n}
-        for m in (1, 4, 8, 16, 32):
+        for m in (1, 4, 8, 16, 32, 48):
             x = torch.randn((m, k), device=dev).to(torch.bfloat16)
             out = torch.empty((m, n), device=dev)
             d = time_graph(torch, lambda w: ops.ternary_matmul(x, w, k, c=out), wb, 256, 32,
@@ -560,7 +561,8 @@ def run_decode(torch, ops, lib, dev) -> dict:
         shapes[name] = row
         del wb
         torch.cuda.empty_cache()
-    return {"workload": "K2 decode at 1-16 tokens (32: the K3 entry, K2's two-block kernel), "
+    return {"workload": "K2 decode at 1-16 tokens (32, 48: the K3 entry, K2's column-block "
+                        "kernel), "
                         "bf16 x, fp32 out, alpha=1 beta=0, median over rotating weight copies; "
                         "config 3 (Phi-3) plus the Llama-3-8B gate / down shapes",
             "shapes": shapes}

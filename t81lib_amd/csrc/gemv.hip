@@ -831,26 +831,36 @@ hipError_t launch_stream(const void *x, const uint8_t *w, void *c, int m, int64_
 }
 
 // ---------------------------------------------------------------------------------
-// gemv_stream2_kernel: 17..32 tokens (bf16, K % 8 == 0, 16-byte aligned x), the staged
-// stream kernel with two 16-token column blocks: each weight limb is decoded once and meets
-// both blocks' B fragments (six MFMAs each), so the weights stream once for all 32 tokens.
-// Staging, the fixed-order reduction and the stores as gemv_stream_kernel, per block (block
-// b holds tokens 16 b .. 16 b + 15).  A separate kernel, not a template parameter of the
-// other: the 8..16-token code generation stays as tuned.
-template <int G, int KS>
+// gemv_stream2_kernel: 17..48 tokens (bf16, K % 8 == 0, 16-byte aligned x), the staged
+// stream kernel with NB = 2 or 3 16-token column blocks: each weight limb is decoded once
+// and meets every block's B fragments (six MFMAs each), so the weights stream once for all
+// the tokens.  Staging, the fixed-order reduction and the stores as gemv_stream_kernel, per
+// block (block b holds tokens 16 b .. 16 b + 15).  A separate kernel, not a template
+// parameter of the other: the 8..16-token code generation stays as tuned.
+template <int G, int KS, int NB>
 __global__ __launch_bounds__(64 * KS) void gemv_stream2_kernel(const void *__restrict__ x,
                                                            const uint8_t *__restrict__ w,
                                                            void *__restrict__ c, int M,
                                                            int64_t N, int64_t K, int64_t L,
                                                            float alpha, float beta,
                                                            const float *__restrict__ bias) {
-    constexpr int NB = 2;
+    static_assert(NB == 2 || NB == 3, "two or three column blocks");
+    // NB = 3: each wave's partial tiles go into its own staging region (its last fragment
+    // reads come before them in the wave's LDS order), so eight waves fit in 154 KB
+    constexpr bool kAlias = NB >= 3;
+    static_assert(!kAlias || G * NB * 64 * 16 <= NB * kXStageBytes, "partials fit the region");
     __shared__ __attribute__((aligned(16))) uint8_t lut[kLutBytes];
-    __shared__ __attribute__((aligned(16))) floatx4 red[KS * G * NB * 64];
+    __shared__ __attribute__((aligned(16))) floatx4 red_own[kAlias ? 1 : KS * G * NB * 64];
     __shared__ __attribute__((aligned(16))) uint8_t xst[KS * NB * kXStageBytes];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
+    // partial tile (wave ww, row group g, block b)
+    auto red_at = [&](int ww, int g, int b) -> floatx4 & {
+        if constexpr (kAlias)
+            return reinterpret_cast<floatx4 *>(xst)[ww * (NB * kXStageBytes / 16) + (g * NB + b) * 64 + lane];
+        else return red_own[((ww * G + g) * NB + b) * 64 + lane];
+    };
     const int wave = tid >> 6;
     const int r = lane & 15;
     const int q = lane >> 4;
@@ -925,14 +935,14 @@ __global__ __launch_bounds__(64 * KS) void gemv_stream2_kernel(const void *__res
 #pragma unroll
     for (int g = 0; g < G; ++g)
 #pragma unroll
-        for (int b = 0; b < NB; ++b) red[((wave * G + g) * NB + b) * 64 + lane] = acc[g][b];
+        for (int b = 0; b < NB; ++b) red_at(wave, g, b) = acc[g][b];
     __syncthreads();
     for (int e = wave; e < G * NB; e += KS) {
         const int g = e / NB;
         const int b = e % NB;
-        floatx4 v = red[(g * NB + b) * 64 + lane];
+        floatx4 v = red_at(0, g, b);
 #pragma unroll
-        for (int ww = 1; ww < KS; ++ww) v += red[((ww * G + g) * NB + b) * 64 + lane];
+        for (int ww = 1; ww < KS; ++ww) v += red_at(ww, g, b);
         store_tile<kDtypeBF16>(v, lane, M - 16 * b, N, n0 + 16 * g,
                                static_cast<float *>(c) + static_cast<int64_t>(16 * b) * N, alpha,
                                beta, bias);
@@ -1099,35 +1109,48 @@ hipError_t launch_gemv_x(const void *x, const uint8_t *w, void *c, int m, int64_
 
 }  // namespace
 
-// 17..32 tokens with aligned bf16 activations (called by the K3 launcher, which owns
-// M > 16): the two-block stream kernel, one launch, no workspace.  Row groups per workgroup
-// and waves from a sweep of 1, 2, 4 groups x 4, 8 waves at 17, 24 and 32 tokens on the
-// config-3/4 shapes, against the eight-wave GEMM kernel with its K split: at 32 tokens
-// llama.qkv 15.8 -> 9.9 us, 4096 -> 4096 13.9 -> 8.7, gate_up 35.1 -> 28.7, llama.down
-// 28.0 -> 19.6, phi3.o 15.2 -> 7.4, phi3.gate_up 20.7 -> 13.2 (bit-identical on integer
-// activations).  *handled is false for other shapes.
-hipError_t launch_gemv_two_blocks(bool *handled, const void *x, const uint8_t *w, void *c, int m,
-                                  int64_t n, int64_t k, float alpha, float beta,
-                                  const float *bias, hipStream_t s) {
+// 17..48 tokens with aligned bf16 activations (called by the K3 launcher, which owns
+// M > 16): the column-block stream kernel, one launch, no workspace.  17..32 tokens, two
+// blocks: row groups per workgroup and waves from a sweep of 1, 2, 4 groups x 4, 8 waves
+// at 17, 24 and 32 tokens on the config-3/4 shapes, against the eight-wave GEMM kernel with
+// its K split: at 32 tokens llama.qkv 15.8 -> 9.9 us, 4096 -> 4096 13.9 -> 8.7, gate_up
+// 35.1 -> 28.7, llama.down 28.0 -> 19.6, phi3.o 15.2 -> 7.4, phi3.gate_up 20.7 -> 13.2.
+// 33..48 tokens, three blocks, eight waves (four measured slower: one wave per SIMD): at 48
+// tokens llama.gate 31.7 -> 26.6 us, llama.down 34.4 -> 28.3, llama.qkv 20.0 -> 13.6,
+// phi3.qkv 23.8 -> 20.1, phi3.o 19.1 -> 10.4, phi3.down 24.9 -> 17.0, phi3.gate_up
+// 28.2 -> 21.3.  (Four blocks at 49..64 tokens were slower than the GEMM kernel on the
+// long-K and widest shapes: each workgroup then reads 64 tokens' activations.)  Results
+// are bit-identical to the GEMM kernel's on integer activations.  *handled is false for
+// other shapes.
+hipError_t launch_gemv_column_blocks(bool *handled, const void *x, const uint8_t *w, void *c,
+                                     int m, int64_t n, int64_t k, float alpha, float beta,
+                                     const float *bias, hipStream_t s) {
     *handled = false;
-    if (!gemv_two_blocks_fits(x, m, n, k)) return hipSuccess;
+    if (!gemv_column_blocks_fits(x, m, n, k)) return hipSuccess;
     const int64_t L = (k + kTrits - 1) / kTrits;
     *handled = true;
-    auto go = [&](auto gc, auto kc) {
+    auto go = [&](auto gc, auto kc, auto nbc) {
         constexpr int G = decltype(gc)::value, KS = decltype(kc)::value;
+        constexpr int NB = decltype(nbc)::value;
         const int64_t blocks = (n + 16 * G - 1) / (16 * G);
-        gemv_stream2_kernel<G, KS><<<dim3(static_cast<unsigned>(blocks)), dim3(64 * KS), 0, s>>>(
-            x, w, c, m, n, k, L, alpha, beta, bias);
+        gemv_stream2_kernel<G, KS, NB><<<dim3(static_cast<unsigned>(blocks)), dim3(64 * KS), 0,
+                                         s>>>(x, w, c, m, n, k, L, alpha, beta, bias);
         return hipGetLastError();
     };
-    if (n <= 4096) return go(std::integral_constant<int, 1>(), std::integral_constant<int, 8>());
-    if (n < 9216) return go(std::integral_constant<int, 2>(), std::integral_constant<int, 8>());
-    return go(std::integral_constant<int, 2>(), std::integral_constant<int, 4>());
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
+    using I4 = std::integral_constant<int, 4>;
+    using I8 = std::integral_constant<int, 8>;
+    if (m > 32) return n <= 4096 ? go(I1(), I8(), I3()) : go(I2(), I8(), I3());
+    if (n <= 4096) return go(I1(), I8(), I2());
+    if (n < 9216) return go(I2(), I8(), I2());
+    return go(I2(), I4(), I2());
 }
 
-bool gemv_two_blocks_fits(const void *x, int64_t m, int64_t n, int64_t k) {
+bool gemv_column_blocks_fits(const void *x, int64_t m, int64_t n, int64_t k) {
     // 16-byte pieces of whole 8-value chunks; block offsets (16 rows x N) and grid in range
-    return m >= 17 && m <= 32 && n > 0 && k > 0 && k % 8 == 0 &&
+    return m >= 17 && m <= 48 && n > 0 && k > 0 && k % 8 == 0 &&
            reinterpret_cast<uintptr_t>(x) % 16 == 0 && (n + 15) / 16 < (int64_t(1) << 31) &&
            k < (int64_t(1) << 31);
 }

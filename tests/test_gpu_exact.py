@@ -113,18 +113,22 @@ def test_k2_integer_bf16_bit_exact(gpu, orc, name, M, K, N):
 
 
 TWO_BLOCK_CASES = [
-    # 17..32 tokens through the K3 entry: the two-block stream kernel (one row group per
-    # workgroup up to 4096 rows, two below 9216, two with four waves above), ragged N and a
-    # K that ends inside a sub-block
+    # 17..32 tokens through the K3 entry: the column-block stream kernel with two blocks (one
+    # row group per workgroup up to 4096 rows, two below 9216, two with four waves above),
+    # ragged N and a K that ends inside a sub-block
     ("llama.down", 17, 14336, 4096), ("llama.gate", 24, 4096, 14336), ("llama.qkv", 32, 4096, 6144),
     ("phi3.o", 32, 3072, 3072), ("phi3.down", 32, 8192, 3072), ("phi3.gate_up", 32, 3072, 16384),
     ("ragged", 29, 4104, 333),
+    # 33..48 tokens: three blocks, eight waves (one row group per workgroup up to 4096 rows,
+    # two above); a third block of one token, of 16, and ragged shapes
+    ("llama.down", 33, 14336, 4096), ("llama.gate", 48, 4096, 14336), ("llama.qkv", 40, 4096, 6144),
+    ("phi3.o", 48, 3072, 3072), ("phi3.down", 45, 8192, 3072), ("ragged", 37, 4104, 4133),
 ]
 
 
 @pytest.mark.parametrize("name,M,K,N", TWO_BLOCK_CASES)
 def test_two_block_integer_bf16_bit_exact(gpu, orc, name, M, K, N):
-    announce(f"exact two-block M={M} {name} K={K} N={N}")
+    announce(f"exact column-block M={M} {name} K={K} N={N}")
     lib = _lib.lib()
     assert lib.t81_hip_ternary_matmul_workspace_size(M, N, K, _lib.DTYPE_BF16) == 0
     w, x, c, bias = int_problem(M, N, K, seed=M * 131 + K + N)
