@@ -1129,7 +1129,7 @@ hipError_t launch_gemm_x(const void *x, const uint8_t *w, void *c, int64_t m, in
                          void *ws, int64_t ws_bytes) {
     constexpr int LK = 2;  // limbs per k-step
     if constexpr (XT == kDtypeBF16) {
-        // 17..48 tokens, aligned: the column-block stream kernel of K2 (gemv.hip), one launch
+        // 17..64 tokens, aligned: the column-block stream kernel of K2 (gemv.hip)
         bool handled = false;
         const hipError_t e = launch_gemv_column_blocks(&handled, x, w, c, static_cast<int>(m), n,
                                                        k, alpha, beta, bias, s);
@@ -1246,8 +1246,9 @@ int64_t gemm_workspace_bytes(int64_t m, int64_t n, int64_t k, int x_dtype) {
     if (m <= 0 || n <= 0 || k <= 0) return 0;
     switch (x_dtype) {
         case kDtypeBF16:
-            // 17..48 tokens with K % 8 == 0 take the column-block stream kernel: no workspace
-            if (m >= 17 && m <= 48 && k % 8 == 0) return 0;
+            // 17..48 tokens (64 with K <= 8192) with K % 8 == 0 take the column-block stream
+            // kernel: no workspace
+            if (m >= 17 && m <= (k <= 8192 ? 64 : 48) && k % 8 == 0) return 0;
             return gemm_workspace_x<kDtypeBF16>(m, n, k);
         case kDtypeF32: return gemm_workspace_x<kDtypeF32>(m, n, k);
         default: return gemm_workspace_x<kDtypeI8>(m, n, k);

@@ -1109,24 +1109,38 @@ hipError_t launch_gemv_x(const void *x, const uint8_t *w, void *c, int m, int64_
 
 }  // namespace
 
-// 17..48 tokens with aligned bf16 activations (called by the K3 launcher, which owns
-// M > 16): the column-block stream kernel, one launch, no workspace.  17..32 tokens, two
-// blocks: row groups per workgroup and waves from a sweep of 1, 2, 4 groups x 4, 8 waves
-// at 17, 24 and 32 tokens on the config-3/4 shapes, against the eight-wave GEMM kernel with
-// its K split: at 32 tokens llama.qkv 15.8 -> 9.9 us, 4096 -> 4096 13.9 -> 8.7, gate_up
-// 35.1 -> 28.7, llama.down 28.0 -> 19.6, phi3.o 15.2 -> 7.4, phi3.gate_up 20.7 -> 13.2.
-// 33..48 tokens, three blocks, eight waves (four measured slower: one wave per SIMD): at 48
-// tokens llama.gate 31.7 -> 26.6 us, llama.down 34.4 -> 28.3, llama.qkv 20.0 -> 13.6,
-// phi3.qkv 23.8 -> 20.1, phi3.o 19.1 -> 10.4, phi3.down 24.9 -> 17.0, phi3.gate_up
-// 28.2 -> 21.3.  (Four blocks at 49..64 tokens were slower than the GEMM kernel on the
-// long-K and widest shapes: each workgroup then reads 64 tokens' activations.)  Results
-// are bit-identical to the GEMM kernel's on integer activations.  *handled is false for
-// other shapes.
+// 17..48 tokens (64 with K <= 8192) with aligned bf16 activations (called by the K3
+// launcher, which owns M > 16): the column-block stream kernel, no workspace.  17..32
+// tokens, two blocks: row groups per workgroup and waves from a sweep of 1, 2, 4 groups x
+// 4, 8 waves at 17, 24 and 32 tokens on the config-3/4 shapes, against the eight-wave GEMM
+// kernel with its K split: at 32 tokens llama.qkv 15.8 -> 9.9 us, 4096 -> 4096 13.9 ->
+// 8.7, gate_up 35.1 -> 28.7, llama.down 28.0 -> 19.6, phi3.o 15.2 -> 7.4, phi3.gate_up
+// 20.7 -> 13.2. 33..48 tokens, three blocks, eight waves (four measured slower: one wave
+// per SIMD): at 48 tokens llama.gate 31.7 -> 26.6 us, llama.down 34.4 -> 28.3, llama.qkv
+// 20.0 -> 13.6, phi3.qkv 23.8 -> 20.1, phi3.o 19.1 -> 10.4, phi3.down 24.9 -> 17.0,
+// phi3.gate_up 28.2 -> 21.3.  49..64 tokens: two launches, tokens [0, 32) and [32, M)
+// (four blocks in one launch were slower than the GEMM kernel on the long-K and widest
+// shapes: each workgroup then reads 64 tokens' activations); at 64 tokens llama.gate 33.3
+// -> 30.2 us, llama.qkv 21.3 -> 19.5, phi3.qkv 26.0 -> 23.2, phi3.o 20.2 -> 14.1,
+// phi3.down 26.0 -> 23.4, phi3.gate_up 30.9 -> 24.4; K > 8192 keeps the GEMM kernel
+// (llama.down 34.6 -> 36.1 at 49 tokens).  Results are bit-identical to the GEMM kernel's
+// on integer activations.  *handled is false for other shapes.
 hipError_t launch_gemv_column_blocks(bool *handled, const void *x, const uint8_t *w, void *c,
                                      int m, int64_t n, int64_t k, float alpha, float beta,
                                      const float *bias, hipStream_t s) {
     *handled = false;
     if (!gemv_column_blocks_fits(x, m, n, k)) return hipSuccess;
+    if (m > 48) {
+        // tokens [32, m): x advances 32 rows of K bf16 values (16-byte aligned: K % 8 == 0)
+        bool h = false;
+        const hipError_t e =
+            launch_gemv_column_blocks(&h, x, w, c, 32, n, k, alpha, beta, bias, s);
+        if (e != hipSuccess) return e;
+        *handled = true;
+        return launch_gemv_column_blocks(&h, static_cast<const uint16_t *>(x) + 32 * k, w,
+                                         static_cast<float *>(c) + 32 * n, m - 32, n, k, alpha,
+                                         beta, bias, s);
+    }
     const int64_t L = (k + kTrits - 1) / kTrits;
     *handled = true;
     auto go = [&](auto gc, auto kc, auto nbc) {
@@ -1150,7 +1164,7 @@ hipError_t launch_gemv_column_blocks(bool *handled, const void *x, const uint8_t
 
 bool gemv_column_blocks_fits(const void *x, int64_t m, int64_t n, int64_t k) {
     // 16-byte pieces of whole 8-value chunks; block offsets (16 rows x N) and grid in range
-    return m >= 17 && m <= 48 && n > 0 && k > 0 && k % 8 == 0 &&
+    return m >= 17 && m <= (k <= 8192 ? 64 : 48) && n > 0 && k > 0 && k % 8 == 0 &&
            reinterpret_cast<uintptr_t>(x) % 16 == 0 && (n + 15) / 16 < (int64_t(1) << 31) &&
            k < (int64_t(1) << 31);
 }

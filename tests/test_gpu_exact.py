@@ -123,6 +123,8 @@ TWO_BLOCK_CASES = [
     # two above); a third block of one token, of 16, and ragged shapes
     ("llama.down", 33, 14336, 4096), ("llama.gate", 48, 4096, 14336), ("llama.qkv", 40, 4096, 6144),
     ("phi3.o", 48, 3072, 3072), ("phi3.down", 45, 8192, 3072), ("ragged", 37, 4104, 4133),
+    # 49..64 tokens: two launches (tokens 0..31, then the rest: 17..32 of them)
+    ("llama.gate", 64, 4096, 14336), ("phi3.o", 49, 3072, 3072), ("ragged", 57, 4104, 4133),
 ]
 
 

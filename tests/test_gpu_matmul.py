@@ -77,9 +77,9 @@ SMALL = [
     (1, 64, 48), (1, 100, 1024), (4, 33, 1000), (16, 257, 3072), (3, 16, 4096), (16, 48, 97),
     (1, 7, 1), (2, 5, 47),
     (17, 64, 96), (64, 96, 1024), (100, 200, 300), (128, 512, 4096), (37, 45, 4097),
-    # 17..48 tokens, bf16: the column-block stream kernel, two and three blocks (one and two
-    # row groups per workgroup)
-    (32, 300, 4104), (25, 6200, 1536), (40, 300, 4104), (48, 6200, 1536),
+    # 17..64 tokens, bf16: the column-block stream kernel, two and three blocks (one and two
+    # row groups per workgroup), and two launches at 49..64
+    (32, 300, 4104), (25, 6200, 1536), (40, 300, 4104), (48, 6200, 1536), (60, 300, 4104),
 ]
 
 
@@ -457,21 +457,22 @@ def test_k2_tile_kernel_plans(gpu, orc, M, N, K, dtype, splits):
     assert torch.equal(outs[0], outs[1]), "two runs of the same call differ"
 
 
-@pytest.mark.parametrize("M,N,K,dtype", [(56, 4096, 14336, torch.bfloat16),
+@pytest.mark.parametrize("M,N,K,dtype", [(56, 4096, 14340, torch.bfloat16),
+                                         (60, 4096, 14336, torch.bfloat16),
                                          (48, 1000, 4104, torch.float32),
                                          (20, 3000, 9000, torch.int8),
                                          (100, 2000, 4800, torch.int8),
-                                         (64, 6144, 4096, torch.bfloat16),
+                                         (64, 6144, 4100, torch.bfloat16),
                                          (300, 1500, 3000, torch.float32),
-                                         (50, 16384, 3072, torch.bfloat16),
+                                         (50, 16384, 3076, torch.bfloat16),
                                          (40, 1000, 4100, torch.bfloat16),
                                          (20, 20000, 2000, torch.int8)])
 def test_k3_eight_wave_split_k_full_check(gpu, orc, M, N, K, dtype):
     """Launches of the eight-wave kernel with few tiles (17 <= M <= 64, int8 and fp32
-    activations, unaligned K, bf16 above 48 tokens) split K: each split writes its raw sums
-    (int32 for int8, exact) as a row-major M x N matrix in the workspace and a second kernel
-    adds them in split order.  Every output against the oracle, with and without the workspace; int8
-    bit-exact."""
+    activations, bf16 with K % 8 != 0 or, past 48 tokens, K > 8192) split K: each split
+    writes its raw sums (int32 for int8, exact) as a row-major M x N matrix in the workspace
+    and a second kernel adds them in split order.  Every output against the oracle, with and
+    without the workspace; int8 bit-exact."""
     announce(f"K3 eight-wave split-K M={M} N={N} K={K} {dtype}")
     lib = _lib.lib()
     code = {torch.bfloat16: _lib.DTYPE_BF16, torch.float32: _lib.DTYPE_F32, torch.int8: _lib.DTYPE_I8}[dtype]
