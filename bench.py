@@ -568,6 +568,35 @@ def run_decode(torch, ops, lib, dev) -> dict:
             "shapes": shapes}
 
 
+def run_backward(torch, ops, lib, dev) -> list:
+    """Backward of the Llama gate layer (14336 x 4096): the transposed limbs T^T
+    (t81_hip_transpose_packed, graph-timed over rotating weight copies), then dx = dy T as
+    the forward product at M = 512 and 2048."""
+    rows = []
+    k, n = 4096, 14336
+    wb = make_weights(torch, ops, lib, n, k, 4, dev, seed=6)
+    ms = time_graph(torch, lambda w: ops.transpose_packed(w, n, k), wb, 64, 8)
+    tbytes = 16 * n * ((k + 47) // 48) + 16 * k * ((n + 47) // 48)
+    gbs = tbytes / (ms * 1e-3) / 1e9
+    rows.append({"shape": "transpose_packed llama.gate 14336x4096", "us": ms * 1e3, "GBps": gbs,
+                 "frac_hbm": gbs / HBM_PEAK_GBPS})
+    log(f"transpose_packed 14336x4096: {ms * 1e3:7.2f} us  {gbs:7.0f} GB/s")
+    wt = [ops.transpose_packed(w, n, k) for w in wb[:2]]
+    del wb
+    for m in (512, 2048):
+        dy = torch.randn((m, n), device=dev).to(torch.bfloat16)
+        dx = torch.empty((m, k), device=dev)
+        ms = time_graph(torch, lambda w: ops.ternary_matmul(dy, w, n, c=dx), wt, 8, 2)
+        tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+        rows.append({"shape": "backward dx = dy T, llama.gate", "M": m, "K": n, "N": k,
+                     "us": ms * 1e3, "TFLOPs": tf, "frac_mfma": tf / BF16_PEAK_TFLOPS})
+        log(f"backward dx=dyT llama.gate M={m:5d}: {ms * 1e3:8.1f} us  {tf:7.1f} TFLOP/s")
+        del dy, dx
+    del wt
+    torch.cuda.empty_cache()
+    return rows
+
+
 def run_sweep(torch, ops, lib, dev) -> list:
     """Decode GEMV (config 3 + the Llama gate/down shapes) and prefill GEMM (config 4)."""
     rows = []
@@ -624,28 +653,7 @@ def run_sweep(torch, ops, lib, dev) -> list:
                  "limb_products_per_s": products / (ms2 * 1e-3)})
     log(f"reference matmul_input pack_cols + gemm_limb: {ms2 * 1e3:8.1f} us")
     del wr, xr, cr
-    # backward of the Llama gate layer (14336 x 4096): T^T limbs, then dx = dy T as K3
-    k, n = 4096, 14336
-    wb = make_weights(torch, ops, lib, n, k, 4, dev, seed=6)
-    ms = time_graph(torch, lambda w: ops.transpose_packed(w, n, k), wb, 64, 8)
-    tbytes = 16 * n * ((k + 47) // 48) + 16 * k * ((n + 47) // 48)
-    gbs = tbytes / (ms * 1e-3) / 1e9
-    rows.append({"shape": "transpose_packed llama.gate 14336x4096", "us": ms * 1e3, "GBps": gbs,
-                 "frac_hbm": gbs / HBM_PEAK_GBPS})
-    log(f"transpose_packed 14336x4096: {ms * 1e3:7.2f} us  {gbs:7.0f} GB/s")
-    wt = [ops.transpose_packed(w, n, k) for w in wb[:2]]
-    del wb
-    for m in (512, 2048):
-        dy = torch.randn((m, n), device=dev).to(torch.bfloat16)
-        dx = torch.empty((m, k), device=dev)
-        ms = time_graph(torch, lambda w: ops.ternary_matmul(dy, w, n, c=dx), wt, 8, 2)
-        tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
-        rows.append({"shape": "backward dx = dy T, llama.gate", "M": m, "K": n, "N": k,
-                     "us": ms * 1e3, "TFLOPs": tf, "frac_mfma": tf / BF16_PEAK_TFLOPS})
-        log(f"backward dx=dyT llama.gate M={m:5d}: {ms * 1e3:8.1f} us  {tf:7.1f} TFLOP/s")
-        del dy, dx
-    del wt
-    torch.cuda.empty_cache()
+    rows.extend(run_backward(torch, ops, lib, dev))
     # TQ2_0 / TQ1_0 codecs over an 8192 x 3072 float32 matrix
     src = [torch.randn((8192, 3072), device=dev) for _ in range(4)]
     for quant in ("TQ2_0", "TQ1_0"):
@@ -838,14 +846,15 @@ def main() -> int:
                     help="seconds of single-core reference CPU work for the baseline")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", choices=["gemv", "gemm", "pack", "copy", "read", "spmm", "launch",
-                                       "stack", "decode"],
+                                       "stack", "decode", "backward"],
                     default=None,
                     help="time one kernel only (for profiling runs); 'copy' times a plain "
                          "elementwise copy of the GEMV weight size, the calibration kernel "
                          "for the HBM byte counters; 'read' a plain reduction over the GEMV "
                          "weight copies (the read floor); 'launch' a one-element fill, the "
                          "per-launch floor of a graph of back-to-back kernels; 'stack' runs "
-                         "config 5, the 32-layer decoder, prefill + greedy decode tokens/s")
+                         "config 5, the 32-layer decoder, prefill + greedy decode tokens/s; "
+                         "'backward' the transposed limbs and dx = dy T of the Llama gate layer")
     ap.add_argument("--no-stack", action="store_true",
                     help="skip config 5 (the decoder stack) in the default run")
     ap.add_argument("--sweep", action="store_true",
@@ -1069,6 +1078,7 @@ def main() -> int:
     decode = run_decode(torch, ops, _lib, dev) if only in (None, "decode") else None
     sweep = run_sweep(torch, ops, _lib, dev) if args.sweep else None
     spmm = run_spmm(torch, dev) if only == "spmm" else None
+    backward = run_backward(torch, ops, _lib, dev) if only == "backward" else None
     stack = run_stack(torch, dev) if only == "stack" or (only is None and not args.no_stack) \
         else None
 
@@ -1145,6 +1155,8 @@ def main() -> int:
         line["sweep"] = sweep
     if spmm:
         line["spmm"] = spmm
+    if backward:
+        line["backward"] = backward
     if stack:
         line["stack"] = stack
     print(json.dumps(line), flush=True)
