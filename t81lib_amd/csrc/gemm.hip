@@ -1128,11 +1128,11 @@ hipError_t launch_gemm_x(const void *x, const uint8_t *w, void *c, int64_t m, in
                          int64_t k, float alpha, float beta, const float *bias, hipStream_t s,
                          void *ws, int64_t ws_bytes) {
     constexpr int LK = 2;  // limbs per k-step
-    if constexpr (XT == kDtypeBF16) {
+    if constexpr (XT == kDtypeBF16 || XT == kDtypeI8) {
         // 17..64 tokens, aligned: the column-block stream kernel of K2 (gemv.hip)
         bool handled = false;
-        const hipError_t e = launch_gemv_column_blocks(&handled, x, w, c, static_cast<int>(m), n,
-                                                       k, alpha, beta, bias, s);
+        const hipError_t e = launch_gemv_column_blocks(&handled, x, XT, w, c, static_cast<int>(m),
+                                                       n, k, alpha, beta, bias, s);
         if (handled || e != hipSuccess) return e;
     }
     if (m <= 32)
@@ -1251,7 +1251,10 @@ int64_t gemm_workspace_bytes(int64_t m, int64_t n, int64_t k, int x_dtype) {
             if (m >= 17 && m <= (k <= 8192 ? 64 : 48) && k % 8 == 0) return 0;
             return gemm_workspace_x<kDtypeBF16>(m, n, k);
         case kDtypeF32: return gemm_workspace_x<kDtypeF32>(m, n, k);
-        default: return gemm_workspace_x<kDtypeI8>(m, n, k);
+        default:
+            // int8 the same with K % 16 == 0
+            if (m >= 17 && m <= (k <= 8192 ? 64 : 48) && k % 16 == 0) return 0;
+            return gemm_workspace_x<kDtypeI8>(m, n, k);
     }
 }
 

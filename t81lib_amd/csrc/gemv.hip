@@ -837,7 +837,7 @@ hipError_t launch_stream(const void *x, const uint8_t *w, void *c, int m, int64_
 // the tokens.  Staging, the fixed-order reduction and the stores as gemv_stream_kernel, per
 // block (block b holds tokens 16 b .. 16 b + 15).  A separate kernel, not a template
 // parameter of the other: the 8..16-token code generation stays as tuned.
-template <int G, int KS, int NB>
+template <int G, int KS, int NB, int XT>
 __global__ __launch_bounds__(64 * KS) void gemv_stream2_kernel(const void *__restrict__ x,
                                                            const uint8_t *__restrict__ w,
                                                            void *__restrict__ c, int M,
@@ -845,6 +845,14 @@ __global__ __launch_bounds__(64 * KS) void gemv_stream2_kernel(const void *__res
                                                            float alpha, float beta,
                                                            const float *__restrict__ bias) {
     static_assert(NB == 2 || NB == 3, "two or three column blocks");
+    static_assert(XT == kDtypeBF16 || XT == kDtypeI8, "bf16, or int8 widened to bf16 in LDS");
+    // A piece is 16 bytes of one token's activations: 8 bf16 or 16 int8 values (int8 is
+    // widened to bf16 as it is staged, so the LDS layout and the fragment reads are the
+    // same; the fp32 sums of integers stay exact under the ABI's K <= 131071).
+    constexpr int kVals = XT == kDtypeI8 ? 16 : 8;        // values per piece
+    constexpr int kPieces = 4 * kTrits / kVals;           // pieces per token and sub-block
+    constexpr int kLanePieces = 16 * kPieces / 64;        // per lane and block: 6 or 3
+    constexpr int kElem = XT == kDtypeI8 ? 1 : 2;
     // NB = 3: each wave's partial tiles go into its own staging region (its last fragment
     // reads come before them in the wave's LDS order), so eight waves fit in 154 KB
     constexpr bool kAlias = NB >= 3;
@@ -868,28 +876,45 @@ __global__ __launch_bounds__(64 * KS) void gemv_stream2_kernel(const void *__res
     const int64_t S = (L + 3) / 4;
 
     bf16x8 bh[NB][6], bl[6];
-    u32x4 xp[6 * NB];
+    u32x4 xp[kLanePieces * NB];
     uint8_t *xs = xst + wave * NB * kXStageBytes;
 #pragma unroll
     for (int j = 0; j < 6; ++j) bl[j] = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
     auto load_pieces = [&](int64_t sb) {
 #pragma unroll
-        for (int i = 0; i < 6 * NB; ++i) {
+        for (int i = 0; i < kLanePieces * NB; ++i) {
             const int P = 64 * i + lane;
-            const int t = P / 24;
-            const int64_t k = sb * (4 * kTrits) + 8 * (P - 24 * t);
+            const int t = P / kPieces;
+            const int64_t k = sb * (4 * kTrits) + kVals * (P - kPieces * t);
             const bool ok = t < M && sb < S && k < K;
-            const uint8_t *src = ok ? static_cast<const uint8_t *>(x) + (t * K + k) * 2
+            const uint8_t *src = ok ? static_cast<const uint8_t *>(x) + (t * K + k) * kElem
                                     : reinterpret_cast<const uint8_t *>(kZeroBlock);
             xp[i] = *reinterpret_cast<const u32x4 *>(src);
         }
     };
     auto stage = [&]() {
 #pragma unroll
-        for (int i = 0; i < 6 * NB; ++i) {
+        for (int i = 0; i < kLanePieces * NB; ++i) {
             const int P = 64 * i + lane;
-            const int t = P / 24;
-            *reinterpret_cast<u32x4 *>(xs + t * kXStagePitch + 16 * (P - 24 * t)) = xp[i];
+            const int t = P / kPieces;
+            uint8_t *dst = xs + t * kXStagePitch + 16 * (kVals / 8) * (P - kPieces * t);
+            if constexpr (XT == kDtypeI8) {
+                // 16 int8 -> 16 bf16 (exact: |v| <= 128 needs 8 significant bits)
+                uint32_t h[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const uint32_t wd = xp[i][e / 2];
+                    const int sh = 16 * (e % 2);
+                    const float f0 = static_cast<float>(static_cast<int8_t>((wd >> sh) & 0xFFu));
+                    const float f1 =
+                        static_cast<float>(static_cast<int8_t>((wd >> (sh + 8)) & 0xFFu));
+                    h[e] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xFFFF0000u);
+                }
+                *reinterpret_cast<u32x4 *>(dst) = u32x4{h[0], h[1], h[2], h[3]};
+                *reinterpret_cast<u32x4 *>(dst + 16) = u32x4{h[4], h[5], h[6], h[7]};
+            } else {
+                *reinterpret_cast<u32x4 *>(dst) = xp[i];
+            }
         }
 #pragma unroll
         for (int b = 0; b < NB; ++b)
@@ -943,7 +968,7 @@ __global__ __launch_bounds__(64 * KS) void gemv_stream2_kernel(const void *__res
         floatx4 v = red_at(0, g, b);
 #pragma unroll
         for (int ww = 1; ww < KS; ++ww) v += red_at(ww, g, b);
-        store_tile<kDtypeBF16>(v, lane, M - 16 * b, N, n0 + 16 * g,
+        store_tile<XT>(v, lane, M - 16 * b, N, n0 + 16 * g,
                                static_cast<float *>(c) + static_cast<int64_t>(16 * b) * N, alpha,
                                beta, bias);
     }
@@ -1125,46 +1150,56 @@ hipError_t launch_gemv_x(const void *x, const uint8_t *w, void *c, int m, int64_
 // phi3.down 26.0 -> 23.4, phi3.gate_up 30.9 -> 24.4; K > 8192 keeps the GEMM kernel
 // (llama.down 34.6 -> 36.1 at 49 tokens).  Results are bit-identical to the GEMM kernel's
 // on integer activations.  *handled is false for other shapes.
-hipError_t launch_gemv_column_blocks(bool *handled, const void *x, const uint8_t *w, void *c,
-                                     int m, int64_t n, int64_t k, float alpha, float beta,
-                                     const float *bias, hipStream_t s) {
+hipError_t launch_gemv_column_blocks(bool *handled, const void *x, int x_dtype,
+                                     const uint8_t *w, void *c, int m, int64_t n, int64_t k,
+                                     float alpha, float beta, const float *bias, hipStream_t s) {
     *handled = false;
-    if (!gemv_column_blocks_fits(x, m, n, k)) return hipSuccess;
+    if (!gemv_column_blocks_fits(x, x_dtype, m, n, k)) return hipSuccess;
     if (m > 48) {
-        // tokens [32, m): x advances 32 rows of K bf16 values (16-byte aligned: K % 8 == 0)
+        // tokens [32, m): x advances 32 rows of K values (16-byte aligned by the K rule), C
+        // 32 rows of N four-byte values
+        const int64_t elem = x_dtype == kDtypeI8 ? 1 : 2;
         bool h = false;
         const hipError_t e =
-            launch_gemv_column_blocks(&h, x, w, c, 32, n, k, alpha, beta, bias, s);
+            launch_gemv_column_blocks(&h, x, x_dtype, w, c, 32, n, k, alpha, beta, bias, s);
         if (e != hipSuccess) return e;
         *handled = true;
-        return launch_gemv_column_blocks(&h, static_cast<const uint16_t *>(x) + 32 * k, w,
-                                         static_cast<float *>(c) + 32 * n, m - 32, n, k, alpha,
-                                         beta, bias, s);
+        return launch_gemv_column_blocks(&h, static_cast<const uint8_t *>(x) + 32 * k * elem,
+                                         x_dtype, w, static_cast<float *>(c) + 32 * n, m - 32,
+                                         n, k, alpha, beta, bias, s);
     }
     const int64_t L = (k + kTrits - 1) / kTrits;
     *handled = true;
-    auto go = [&](auto gc, auto kc, auto nbc) {
+    auto go = [&](auto xc, auto gc, auto kc, auto nbc) {
+        constexpr int XT = decltype(xc)::value;
         constexpr int G = decltype(gc)::value, KS = decltype(kc)::value;
         constexpr int NB = decltype(nbc)::value;
         const int64_t blocks = (n + 16 * G - 1) / (16 * G);
-        gemv_stream2_kernel<G, KS, NB><<<dim3(static_cast<unsigned>(blocks)), dim3(64 * KS), 0,
-                                         s>>>(x, w, c, m, n, k, L, alpha, beta, bias);
+        gemv_stream2_kernel<G, KS, NB, XT><<<dim3(static_cast<unsigned>(blocks)), dim3(64 * KS),
+                                             0, s>>>(x, w, c, m, n, k, L, alpha, beta, bias);
         return hipGetLastError();
     };
-    using I1 = std::integral_constant<int, 1>;
-    using I2 = std::integral_constant<int, 2>;
-    using I3 = std::integral_constant<int, 3>;
-    using I4 = std::integral_constant<int, 4>;
-    using I8 = std::integral_constant<int, 8>;
-    if (m > 32) return n <= 4096 ? go(I1(), I8(), I3()) : go(I2(), I8(), I3());
-    if (n <= 4096) return go(I1(), I8(), I2());
-    if (n < 9216) return go(I2(), I8(), I2());
-    return go(I2(), I4(), I2());
+    auto shape = [&](auto xc) {
+        using I1 = std::integral_constant<int, 1>;
+        using I2 = std::integral_constant<int, 2>;
+        using I3 = std::integral_constant<int, 3>;
+        using I4 = std::integral_constant<int, 4>;
+        using I8 = std::integral_constant<int, 8>;
+        if (m > 32) return n <= 4096 ? go(xc, I1(), I8(), I3()) : go(xc, I2(), I8(), I3());
+        if (n <= 4096) return go(xc, I1(), I8(), I2());
+        if (n < 9216) return go(xc, I2(), I8(), I2());
+        return go(xc, I2(), I4(), I2());
+    };
+    if (x_dtype == kDtypeI8) return shape(std::integral_constant<int, kDtypeI8>());
+    return shape(std::integral_constant<int, kDtypeBF16>());
 }
 
-bool gemv_column_blocks_fits(const void *x, int64_t m, int64_t n, int64_t k) {
-    // 16-byte pieces of whole 8-value chunks; block offsets (16 rows x N) and grid in range
-    return m >= 17 && m <= (k <= 8192 ? 64 : 48) && n > 0 && k > 0 && k % 8 == 0 &&
+bool gemv_column_blocks_fits(const void *x, int x_dtype, int64_t m, int64_t n, int64_t k) {
+    // 16-byte pieces of whole 8-value (bf16) or 16-value (int8) chunks; block offsets
+    // (16 rows x N) and grid in range
+    const int64_t chunk = x_dtype == kDtypeI8 ? 16 : 8;
+    return (x_dtype == kDtypeBF16 || x_dtype == kDtypeI8) && m >= 17 &&
+           m <= (k <= 8192 ? 64 : 48) && n > 0 && k > 0 && k % chunk == 0 &&
            reinterpret_cast<uintptr_t>(x) % 16 == 0 && (n + 15) / 16 < (int64_t(1) << 31) &&
            k < (int64_t(1) << 31);
 }

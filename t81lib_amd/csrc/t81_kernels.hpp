@@ -29,13 +29,13 @@ hipError_t launch_validate(const uint8_t *packed, int64_t count, int32_t *bad, h
 
 // gemv.hip (K2): M <= 16.  ws (ws_bytes of device memory, may be null) lets 5..16
 // tokens split K over workgroups; gemv_workspace_bytes says how much a shape uses.
-// 17..48 tokens (64 with K <= 8192), aligned bf16 (K % 8 == 0, 16-byte aligned x): the
-// column-block stream kernel of gemv.hip (two or three 16-token blocks; 49..64 tokens as two
-// launches); the K3 launcher tries it first.
-bool gemv_column_blocks_fits(const void *x, int64_t m, int64_t n, int64_t k);
-hipError_t launch_gemv_column_blocks(bool *handled, const void *x, const uint8_t *w, void *c,
-                                     int m, int64_t n, int64_t k, float alpha, float beta,
-                                     const float *bias, hipStream_t s);
+// 17..48 tokens (64 with K <= 8192), bf16 (K % 8 == 0) or int8 (K % 16 == 0) activations
+// at a 16-byte aligned x: the column-block stream kernel of gemv.hip (two or three 16-token
+// blocks; 49..64 tokens as two launches); the K3 launcher tries it first.
+bool gemv_column_blocks_fits(const void *x, int x_dtype, int64_t m, int64_t n, int64_t k);
+hipError_t launch_gemv_column_blocks(bool *handled, const void *x, int x_dtype,
+                                     const uint8_t *w, void *c, int m, int64_t n, int64_t k,
+                                     float alpha, float beta, const float *bias, hipStream_t s);
 hipError_t launch_gemv(const void *x, int x_dtype, const uint8_t *w, void *c, int m, int64_t n,
                        int64_t k, float alpha, float beta, const float *bias, hipStream_t s,
                        void *ws = nullptr, int64_t ws_bytes = 0);

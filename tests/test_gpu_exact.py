@@ -357,6 +357,33 @@ def test_k3_int8_big_tile_bit_exact(gpu, orc, M, N, K):
     np.testing.assert_array_equal(out.cpu().numpy().astype(np.int64), want + c.numpy())
 
 
+I8_COLUMN_BLOCK_CASES = [
+    # M, N, K: int8 activations at 17..64 tokens (K % 16 == 0) through the K3 entry: the
+    # column-block stream kernel with int8 widened to bf16 in LDS (two blocks, three, two
+    # launches at 49..64), one and two row groups per workgroup, ragged N, |x| up to 128
+    (17, 4096, 14336), (32, 14336, 4096), (40, 3072, 3072), (48, 3072, 8192), (64, 6144, 4096),
+    (57, 1000, 4112),
+]
+
+
+@pytest.mark.parametrize("M,N,K", I8_COLUMN_BLOCK_CASES)
+def test_column_block_int8_bit_exact(gpu, orc, M, N, K):
+    """int32 results equal the int64 oracle with beta = 0 and 1; no workspace asked for."""
+    announce(f"exact column-block int8 M={M} N={N} K={K}")
+    lib = _lib.lib()
+    assert lib.t81_hip_ternary_matmul_workspace_size(M, N, K, _lib.DTYPE_I8) == 0
+    w, x, c = _int8_problem(M, N, K, seed=M * 5 + N + K)
+    x[0, :16] = -128                      # the int8 extreme widens exactly too
+    packed = ops.quantize_pack(w.to(gpu), 0.45, _lib.THR_CPP)
+    want = orc.trit_matmul_i64(x.numpy(), packed.cpu().numpy(), K)
+    xg = x.to(gpu)
+    out = ops.ternary_matmul(xg, packed, K, kernel=3)
+    assert out.dtype == torch.int32
+    np.testing.assert_array_equal(out.cpu().numpy().astype(np.int64), want)
+    out = ops.ternary_matmul(xg, packed, K, beta=1.0, c=c.to(gpu), kernel=3)
+    np.testing.assert_array_equal(out.cpu().numpy().astype(np.int64), want + c.numpy())
+
+
 @pytest.mark.parametrize("name,M,K,N", I8_FULL)
 def test_k3_int8_config4_bit_exact(gpu, orc, name, M, K, N):
     """Config-4 shapes with int8 activations: every output against a float64 product of the

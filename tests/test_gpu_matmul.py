@@ -466,13 +466,13 @@ def test_k2_tile_kernel_plans(gpu, orc, M, N, K, dtype, splits):
                                          (300, 1500, 3000, torch.float32),
                                          (50, 16384, 3076, torch.bfloat16),
                                          (40, 1000, 4100, torch.bfloat16),
-                                         (20, 20000, 2000, torch.int8)])
+                                         (20, 20000, 2008, torch.int8)])
 def test_k3_eight_wave_split_k_full_check(gpu, orc, M, N, K, dtype):
-    """Launches of the eight-wave kernel with few tiles (17 <= M <= 64, int8 and fp32
-    activations, bf16 with K % 8 != 0 or, past 48 tokens, K > 8192) split K: each split
-    writes its raw sums (int32 for int8, exact) as a row-major M x N matrix in the workspace
-    and a second kernel adds them in split order.  Every output against the oracle, with and
-    without the workspace; int8 bit-exact."""
+    """Launches of the eight-wave kernel with few tiles (17 <= M <= 64: fp32 activations,
+    int8 with K % 16 != 0, bf16 with K % 8 != 0 or, past 48 tokens, K > 8192) split K: each
+    split writes its raw sums (int32 for int8, exact) as a row-major M x N matrix in the
+    workspace and a second kernel adds them in split order.  Every output against the
+    oracle, with and without the workspace; int8 bit-exact."""
     announce(f"K3 eight-wave split-K M={M} N={N} K={K} {dtype}")
     lib = _lib.lib()
     code = {torch.bfloat16: _lib.DTYPE_BF16, torch.float32: _lib.DTYPE_F32, torch.int8: _lib.DTYPE_I8}[dtype]
