@@ -831,10 +831,10 @@ hipError_t launch_stream(const void *x, const uint8_t *w, void *c, int m, int64_
 }
 
 // ---------------------------------------------------------------------------------
-// gemv_stream2_kernel: 17..48 tokens (bf16, K % 8 == 0, 16-byte aligned x), the staged
-// stream kernel with NB = 2 or 3 16-token column blocks: each weight limb is decoded once
-// and meets every block's B fragments (six MFMAs each), so the weights stream once for all
-// the tokens.  Staging, the fixed-order reduction and the stores as gemv_stream_kernel, per
+// gemv_stream2_kernel: 17..48 tokens (49..64 as two launches) of bf16 (K % 8 == 0) or int8
+// (K % 16 == 0) activations at a 16-byte aligned x: the staged stream kernel with NB = 2 or
+// 3 16-token column blocks: each weight limb is decoded once and meets every block's B
+// fragments (six MFMAs each), so the weights stream once for all the tokens.  Staging, the fixed-order reduction and the stores as gemv_stream_kernel, per
 // block (block b holds tokens 16 b .. 16 b + 15).  A separate kernel, not a template
 // parameter of the other: the 8..16-token code generation stays as tuned.
 template <int G, int KS, int NB, int XT>
