@@ -392,7 +392,14 @@ __global__ __launch_bounds__(64 * KS) void gemv_stream_kernel(const void *__rest
                                                           int64_t K, int64_t L, float alpha,
                                                           float beta,
                                                           const float *__restrict__ bias) {
-    static_assert(!kStage || (XT == kDtypeBF16 && kAligned), "pieces are aligned bf16");
+    static_assert(!kStage || ((XT == kDtypeBF16 || XT == kDtypeI8) && kAligned),
+                  "pieces are aligned bf16, or int8 widened to bf16 as they are staged");
+    // a piece: 16 bytes of one token's activations, 8 bf16 or 16 int8 values (the int8
+    // launch also needs K % 16 == 0 and a 16-byte aligned x)
+    constexpr int kVals = XT == kDtypeI8 ? 16 : 8;
+    constexpr int kPieces = 4 * kTrits / kVals;        // per token and sub-block: 24 or 12
+    constexpr int kLanePieces = 16 * kPieces / 64;     // per lane: 6 or 3
+    constexpr int kElemB = XT == kDtypeI8 ? 1 : 2;
     __shared__ __attribute__((aligned(16))) uint8_t lut[kLutBytes];
     __shared__ __attribute__((aligned(16))) floatx4 red[KS * G * 64];
     __shared__ __attribute__((aligned(16))) uint8_t xst[kStage ? KS * kXStageBytes : 16];
@@ -414,22 +421,39 @@ __global__ __launch_bounds__(64 * KS) void gemv_stream_kernel(const void *__rest
     // form's piece loads earlier among the MFMAs (llama.gate M = 16 12.35 us against 12.94)
     auto load_pieces = [&](int64_t sb) {
 #pragma unroll
-        for (int i = 0; i < 6; ++i) {
+        for (int i = 0; i < kLanePieces; ++i) {
             const int P = 64 * i + lane;
-            const int t = P / 24;
-            const int64_t k = sb * (4 * kTrits) + 8 * (P - 24 * t);
+            const int t = P / kPieces;
+            const int64_t k = sb * (4 * kTrits) + kVals * (P - kPieces * t);
             const bool ok = t < M && sb < S && k < K;
-            const uint8_t *src = ok ? static_cast<const uint8_t *>(x) + (t * K + k) * 2
+            const uint8_t *src = ok ? static_cast<const uint8_t *>(x) + (t * K + k) * kElemB
                                     : reinterpret_cast<const uint8_t *>(kZeroBlock);
             xp[i] = *reinterpret_cast<const u32x4 *>(src);
         }
     };
     auto stage = [&]() {
 #pragma unroll
-        for (int i = 0; i < 6; ++i) {
+        for (int i = 0; i < kLanePieces; ++i) {
             const int P = 64 * i + lane;
-            const int t = P / 24;
-            *reinterpret_cast<u32x4 *>(xs + t * kXStagePitch + 16 * (P - 24 * t)) = xp[i];
+            const int t = P / kPieces;
+            uint8_t *dst = xs + t * kXStagePitch + 16 * (kVals / 8) * (P - kPieces * t);
+            if constexpr (XT == kDtypeI8) {
+                // 16 int8 -> 16 bf16 (exact: |v| <= 128 needs 8 significant bits)
+                uint32_t h[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const uint32_t wd = xp[i][e / 2];
+                    const int sh = 16 * (e % 2);
+                    const float f0 = static_cast<float>(static_cast<int8_t>((wd >> sh) & 0xFFu));
+                    const float f1 =
+                        static_cast<float>(static_cast<int8_t>((wd >> (sh + 8)) & 0xFFu));
+                    h[e] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xFFFF0000u);
+                }
+                *reinterpret_cast<u32x4 *>(dst) = u32x4{h[0], h[1], h[2], h[3]};
+                *reinterpret_cast<u32x4 *>(dst + 16) = u32x4{h[4], h[5], h[6], h[7]};
+            } else {
+                *reinterpret_cast<u32x4 *>(dst) = xp[i];
+            }
         }
 #pragma unroll
         for (int j = 0; j < 6; ++j)
@@ -803,6 +827,9 @@ hipError_t launch_gemv_tile(bool *handled, const void *x, const uint8_t *w, void
     // aligned bf16: the stream kernel with staged activation pieces, one launch, is faster
     // (llama.down M = 16 13.2 us against 14.4 with the split sum; phi3.down 7.9 against 9.4)
     if (XT == kDtypeBF16 && aligned) return hipSuccess;
+    // int8 at 8+ tokens with 16-value pieces: the same staged stream kernel
+    if (XT == kDtypeI8 && m >= 8 && k % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0)
+        return hipSuccess;
     *handled = true;
     float *part = static_cast<float *>(ws);
     if (t.nw == 4)
@@ -820,6 +847,14 @@ hipError_t launch_stream(const void *x, const uint8_t *w, void *c, int m, int64_
     // M token rows, measured faster (llama.gate M = 5 9.53 against 10.66 staged).
     if constexpr (XT == kDtypeBF16 && kAligned) {
         if (G == 1 || m >= 8) {
+            gemv_stream_kernel<XT, G, kAligned, KS, true><<<dim3(blocks), dim3(64 * KS), 0, s>>>(
+                x, w, c, m, n, k, L, alpha, beta, bias);
+            return hipGetLastError();
+        }
+    }
+    if constexpr (XT == kDtypeI8 && kAligned) {
+        // int8, 8+ tokens: the same staging, the values widened to bf16 (16-value pieces)
+        if (m >= 8 && k % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0) {
             gemv_stream_kernel<XT, G, kAligned, KS, true><<<dim3(blocks), dim3(64 * KS), 0, s>>>(
                 x, w, c, m, n, k, L, alpha, beta, bias);
             return hipGetLastError();
@@ -989,7 +1024,12 @@ hipError_t launch_stream_shape(const void *x, const uint8_t *w, void *c, int m, 
                                int64_t k, int64_t L, float alpha, float beta, const float *bias,
                                hipStream_t s) {
     const int64_t nsb = (L + 3) / 4;
-    if constexpr (XT == kDtypeBF16 && kAligned) {
+    // int8 with K % 16 == 0 and a 16-byte aligned x stages its pieces like bf16
+    bool staged = false;
+    if constexpr (XT == kDtypeBF16 && kAligned) staged = true;
+    if constexpr (XT == kDtypeI8 && kAligned)
+        staged = k % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
+    if (staged) {
         // 8..16 tokens, staged pieces (their cost no longer grows with the tokens): eight
         // waves, the row groups per workgroup by width -- a sweep of 1, 2, 4 groups x 4, 8,
         // 16 waves at 5, 8, 9, 12 and 16 tokens: llama.gate M = 16 12.3 -> 10.1 us, phi3.qkv
@@ -1095,8 +1135,11 @@ hipError_t launch_gemv_x(const void *x, const uint8_t *w, void *c, int m, int64_
     // 16384 at M = 8: 10.5 -> 8.7 us; even at 3072 -> 9216), 5+ over >= 14336 (4096 ->
     // 14336 at M = 5: 11.2 -> 9.6 us; 3072 -> 9216 at M = 5 stays faster staged)
     // ... and 8+ tokens with aligned bf16 activations, staged (see launch_stream_shape)
-    const bool wide = XT == kDtypeBF16 && ((m >= 8 && n >= 9216) || (m >= 5 && n >= 14336) ||
-                                           (m >= 8 && aligned8));
+    const bool stage_i8 = XT == kDtypeI8 && m >= 8 && k % 16 == 0 &&
+                          reinterpret_cast<uintptr_t>(x) % 16 == 0;
+    const bool wide = (XT == kDtypeBF16 && ((m >= 8 && n >= 9216) || (m >= 5 && n >= 14336) ||
+                                            (m >= 8 && aligned8))) ||
+                      stage_i8;
     if (L > 0 && max_run > 0 && wg <= 8 && !wide) {
         while (wg < 8 && groups * wg < kTargetWaves && nsb >= 4 * wg) wg *= 2;
         const int W = wg < 4 ? 4 : wg;
@@ -1208,6 +1251,7 @@ int64_t gemv_workspace_bytes(int64_t m, int64_t n, int64_t k, int x_dtype) {
     if (m < 5 || m > 16 || n <= 0 || k <= 0) return 0;
     // bf16 with K % 8 == 0 runs the staged stream kernel in one launch instead
     if (x_dtype == kDtypeBF16 && k % 8 == 0) return 0;
+    if (x_dtype == kDtypeI8 && m >= 8 && k % 16 == 0) return 0;   // the same, 16-value pieces
     return gemv_tile_workspace_bytes(static_cast<int>(m), n, k);   // float32 partials
 }
 

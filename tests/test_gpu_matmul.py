@@ -420,7 +420,8 @@ def test_k2_m5_to_16_full_check(gpu, orc, M, N, K, dtype):
     (9, 37, 6200, torch.float32, 5),       # 33 sub-blocks: one active wave in the last split
     (16, 4096, 14336, torch.bfloat16, 0),  # aligned bf16: the staged stream kernel instead
     (11, 3000, 9001, torch.bfloat16, 6),   # K % 8 != 0 (element loads)
-    (16, 4100, 14400, torch.int8, 10),     # rows past N in the last block
+    (16, 4100, 14400, torch.int8, 0),      # int8, K % 16 == 0: the staged stream kernel
+    (16, 4100, 14408, torch.int8, -1),     # rows past N in the last block (-1: any split)
     (13, 8192, 6144, torch.float32, 4),    # four row groups per workgroup
     (12, 8193, 6144, torch.bfloat16, 0),   # wider than the tile kernel takes
     (8, 3000, 9000, torch.bfloat16, 0),    # fewer tokens than it takes
@@ -434,7 +435,10 @@ def test_k2_tile_kernel_plans(gpu, orc, M, N, K, dtype, splits):
     lib = _lib.lib()
     code = {torch.bfloat16: _lib.DTYPE_BF16, torch.float32: _lib.DTYPE_F32, torch.int8: _lib.DTYPE_I8}[dtype]
     ws = lib.t81_hip_ternary_matmul_workspace_size(M, N, K, code)
-    assert ws == (4 * splits * M * N if splits > 1 else 0)
+    if splits >= 0:
+        assert ws == (4 * splits * M * N if splits > 1 else 0)
+    else:
+        assert ws > 0 and ws % (4 * M * N) == 0, "shape expected to split K"
     w, x, c, bias = make_problem(M, N, K, dtype, seed=3 * N + K + M)
     packed = ops.quantize_pack(w.to(gpu), 0.45, _lib.THR_CPP)
     packed_np = packed.cpu().numpy()
