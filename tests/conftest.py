@@ -84,6 +84,58 @@ def accum_rtol(k: int, dtype) -> float:
     return min(bound, NORTH_STAR_RTOL[name])
 
 
+def fixed_point_activations(M: int, K: int, amax: int, seed: int):
+    """float32 activations x = a + b / 256 with integers |a| <= amax and |b| <= 127.
+
+    Each x holds at most 11 significant bits, so the kernels' split x = hi + lo into two
+    bfloat16 values is exact, every product x * t is a multiple of 2^-8, and as long as
+    (256 amax + 127) K < 2^24 every partial sum, in any order, is a multiple of 2^-8
+    below 2^16 in magnitude: float32 adds them without rounding.  A float32 kernel must
+    then reproduce the integer oracle bit for bit.  Returns (a int8, b int8, x float32)."""
+    assert (256 * amax + 127) * K < 2 ** 24, "activations too large for exact float32 sums"
+    rng = np.random.default_rng(seed)
+    a = rng.integers(-amax, amax + 1, (M, K), dtype=np.int64).astype(np.int8)
+    b = rng.integers(-127, 128, (M, K), dtype=np.int64).astype(np.int8)
+    x = (a.astype(np.float64) + b.astype(np.float64) / 256.0).astype(np.float32)
+    return a, b, x
+
+
+def fixed_point_acc256(orc, a, b, packed, K: int) -> np.ndarray:
+    """256 * (x @ T^T) as int64 from the integer oracle, by linearity: 256 (a T) + b T."""
+    return 256 * orc.trit_matmul_i64(a, packed, K) + orc.trit_matmul_i64(b, packed, K)
+
+
+def _frac_bits(v: float) -> int:
+    q = 0
+    while v * 2.0 ** q != np.floor(v * 2.0 ** q):
+        q += 1
+        assert q <= 16, f"{v} is not a short binary fraction"
+    return q
+
+
+def fixed_point_expected(acc256, alpha: float, beta: float, c=None, bias=None) -> np.ndarray:
+    """alpha * acc256 / 256 + beta * c + bias as float32, exactly.  c and bias hold
+    integers; the terms share a grid of 2^-f and the asserted bound keeps every partial
+    sum of them, in any order, on that grid within float32's 24 bits."""
+    f = max(8 + _frac_bits(alpha), _frac_bits(beta))
+    y = alpha * (acc256.astype(np.float64) / 256.0)
+    mag = np.abs(y)
+    if beta != 0.0:
+        cd = np.asarray(c, np.float64)
+        assert np.array_equal(cd, np.floor(cd)), "C must hold integers"
+        y = y + beta * cd
+        mag = mag + np.abs(beta * cd)
+    if bias is not None:
+        bd = np.asarray(bias, np.float64)
+        assert np.array_equal(bd, np.floor(bd)), "bias must hold integers"
+        y = y + bd
+        mag = mag + np.abs(bd)
+    assert float(mag.max(initial=0.0)) < 2.0 ** (24 - f), "epilogue would round in float32"
+    out = y.astype(np.float32)
+    assert np.array_equal(out.astype(np.float64), y)
+    return out
+
+
 def fp_tolerance_ok(got, ref, scale, rtol, atol=1e-6):
     """|got - ref| <= rtol * scale + atol elementwise, scale = sum_k |alpha x_k t_k| + |beta c| + |bias|
     (a relative tolerance on the terms that were summed, so cancellation in a sum does not

@@ -414,3 +414,35 @@ def test_k3_int8_config4_bit_exact(gpu, orc, name, M, K, N):
         del out, want
     del exact
     torch.cuda.empty_cache()
+
+
+I8_STREAM_CASES = [
+    # M, N, K: int8 activations at 8..16 tokens through K2 (K % 16 == 0, 16-byte aligned x:
+    # the staged stream kernel), at the 8-token switch-over and at 9..15 tokens with masked
+    # token columns, for one, two and four row groups per workgroup; K = 14400 ends inside
+    # a sub-block
+    (8, 14336, 4096), (8, 4096, 14336), (12, 4100, 3072), (9, 257, 14400), (15, 9216, 3072),
+    (11, 3072, 8192),
+]
+
+
+@pytest.mark.parametrize("M,N,K,offset", [c + (0,) for c in I8_STREAM_CASES]
+                         + [(8, 14336, 4096, 1), (8, 4096, 14336, 1)])
+def test_k2_int8_stream_bit_exact(gpu, orc, M, N, K, offset):
+    """int32 results equal the int64 oracle with beta = 0 and 1, with |x| up to 128; offset 1
+    puts x one byte past a 16-byte boundary at the 8-token switch-over (no staging: element
+    loads)."""
+    announce(f"exact K2 int8 M={M} N={N} K={K} offset={offset}")
+    w, x, c = _int8_problem(M, N, K, seed=M * 11 + N + K)
+    x[0, :16] = -128
+    packed = ops.quantize_pack(w.to(gpu), 0.45, _lib.THR_CPP)
+    want = orc.trit_matmul_i64(x.numpy(), packed.cpu().numpy(), K)
+    store = torch.zeros(M * K + 16, dtype=torch.int8, device=gpu)
+    xg = store[offset:offset + M * K].view(M, K)
+    xg.copy_(x.to(gpu))
+    assert xg.data_ptr() % 16 == offset
+    out = ops.ternary_matmul(xg, packed, K, kernel=2)
+    assert out.dtype == torch.int32
+    np.testing.assert_array_equal(out.cpu().numpy().astype(np.int64), want)
+    out = ops.ternary_matmul(xg, packed, K, beta=1.0, c=c.to(gpu), kernel=2)
+    np.testing.assert_array_equal(out.cpu().numpy().astype(np.int64), want + c.numpy())

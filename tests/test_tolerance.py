@@ -76,3 +76,40 @@ def test_bound_values():
     assert accum_rtol(4096, "bf16") == pytest.approx(2 * (4096 + 16) * 2.0 ** -24)
     assert accum_rtol(48, "f32") == pytest.approx(2 * (96 + 16) * 2.0 ** -24 + 2.0 ** -16)
     assert accum_rtol(10 ** 6, "bf16") == 1e-2 and accum_rtol(14336, "f32") == 1e-3
+
+
+def _bf16_rne(x: np.ndarray) -> np.ndarray:
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return u.astype(np.uint32).view(np.float32)
+
+
+@pytest.mark.parametrize("K", [97, 4096, 14336])
+def test_fixed_point_pin_rejects_dropped_lo_plane(orc, K):
+    """The bit-exact float32 tests (tests/test_gpu_exact_f32.py) catch a kernel that drops
+    the lo bfloat16 plane of float32 activations, which the summation-bound tolerance lets
+    through at long K.  The correct hi + lo split reproduces the expected bits."""
+    from conftest import fixed_point_acc256, fixed_point_activations, fixed_point_expected
+
+    M, N = 4, 384
+    amax = 7 if (256 * 7 + 127) * K < 2 ** 24 else 3
+    a, b, x = fixed_point_activations(M, K, amax, seed=K)
+    w = np.random.default_rng(K + 1).standard_normal((N, K)).astype(np.float32)
+    packed = orc.pack_rows(w, np.float32(0.45), 0)
+    want = fixed_point_expected(fixed_point_acc256(orc, a, b, packed, K), 0.5, 0.0)
+
+    hi = _bf16_rne(x)
+    lo = _bf16_rne(x - hi)
+    assert np.array_equal(hi.astype(np.float64) + lo, x.astype(np.float64)), "split must be exact"
+    split = 0.5 * (orc.trit_matmul_f64(hi.astype(np.float64), packed, K)
+                   + orc.trit_matmul_f64(lo.astype(np.float64), packed, K))
+    assert np.array_equal(split.astype(np.float32).view(np.uint32), want.view(np.uint32))
+
+    dropped = (0.5 * orc.trit_matmul_f64(hi.astype(np.float64), packed, K)).astype(np.float32)
+    differ = float((dropped.view(np.uint32) != want.view(np.uint32)).mean())
+    assert differ > 0.95, f"lo plane dropped: only {differ:.1%} of outputs differ"
+    if K >= 4096:
+        # the summation-bound tolerance alone accepts this mutant on most outputs at long K
+        scale = 0.5 * orc.trit_matmul_abs_f64(x.astype(np.float64), packed, K)
+        _, _, nbad = fp_tolerance_ok(dropped, want.astype(np.float64), scale, accum_rtol(K, "f32"))
+        assert nbad < 0.5 * dropped.size
