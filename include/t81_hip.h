@@ -233,6 +233,55 @@ int t81_hip_tq2_matmul(const void *x, int x_dtype, const uint8_t *w, float *c, i
                        int64_t n, int64_t k, float alpha, float beta, const float *bias,
                        void *stream);
 
+/* ---- the reference's own TQ1_0 row codec (src/t81/core/gguf_quants.h:14-168) ----
+ * A row of n values is ceil(n / 8) uint16 words; word w holds trits 8w .. 8w + 7 as
+ * base-3 digits d = {+1: 0, 0: 1, -1: 2}, trit 8w + i weighted 3^i (pad trits 0), and
+ * the row has one float scale.  This is not the llama.cpp block format above. */
+#define T81_TQ1_TRITS_PER_BLOCK 8 /* gguf_quants.h:14 */
+#define T81_TQ1_BLOCK_ROWS 32     /* gguf_quants.h:15: rows per scale in a tensor payload */
+
+/* rows x cols float32 (row-major) -> rows x ceil(cols / 8) words (row-major).  Row r uses
+ * scale s = scales_in[r] when scales_in is given and scales_in[r] > 0, else max |v| over
+ * the row (NaN values skipped); trit of v * (1 / s) with the value clamped to [-1, 1] (NaN
+ * to +1) against threshold clamped to [0, 0.9999]; all trits 0 when s <= 0.  The scale
+ * used goes to scales_out[r] when scales_out is given.  values 4-byte, dst 2-byte aligned.
+ * Replaces: quantize_row_tq1_0 + compute_scale, gguf_quants.h:55-64, 116-144, one call
+ *           per row, as the quantize_row_tq1_0 binding makes it (python/bindings.cpp:519-540). */
+int t81_hip_tq1_quantize_rows(const float *values, int64_t rows, int64_t cols, float threshold,
+                              const float *scales_in, float *scales_out, uint16_t *dst,
+                              void *stream);
+
+/* rows x ceil(cols / 8) words -> rows x cols float32: trit * scales[r] (zeros when
+ * scales[r] == 0); only the low 8 base-3 digits of a word are read.
+ * Replaces: dequantize_row_tq1_0, gguf_quants.h:146-168 (binding dequant_row_tq1_0,
+ *           python/bindings.cpp:542-559). */
+int t81_hip_tq1_dequantize_rows(const uint16_t *src, int64_t rows, int64_t cols,
+                                const float *scales, float *dst, void *stream);
+
+/* Tensor payload: groups of max(1, block_rows) rows, each a little-endian IEEE half scale,
+ * 8 reserved bytes when refinements != 0 (the TQ2_0 variant), then the group's rows of
+ * words (2 * ceil(cols / 8) bytes each).  Any alignment.  Size of a whole payload: */
+int64_t t81_hip_tq1_payload_bytes(int64_t rows, int64_t cols, int64_t block_rows,
+                                  int refinements);
+
+/* Writes such a payload (t81_hip_tq1_payload_bytes bytes): per group h = half(max |v|)
+ * (round to nearest even), zero reserved bytes, each row quantized as
+ * t81_hip_tq1_quantize_rows with scales_in = float(h).
+ * No reference counterpart: the reference reads these payloads but has no writer. */
+int t81_hip_tq1_quantize_payload(const float *values, int64_t rows, int64_t cols,
+                                 int64_t block_rows, int refinements, float threshold,
+                                 uint8_t *payload, void *stream);
+
+/* payload (payload_bytes bytes) -> rows x cols float32.  A payload shorter than the layout
+ * returns T81_HIP_EINVAL_SHAPE with the binding's message for the first check its
+ * sequential walk fails: "buffer truncated while reading scale", "... while skipping
+ * refinement bytes" or "... while reading quantized rows".
+ * Replaces: dequant_tensor_tq1_impl behind dequant_tq1_0 (refinements 0) and dequant_tq2_0
+ *           (refinements 1), python/bindings.cpp:561-638, 975-995. */
+int t81_hip_tq1_dequantize_payload(const uint8_t *payload, int64_t payload_bytes, int64_t rows,
+                                   int64_t cols, int64_t block_rows, int refinements, float *dst,
+                                   void *stream);
+
 /* Sparse ternary x dense (COO entries, list order significant):
  *     C[r, :] = beta == 0 ? 0 : float(double(C[r, :]) * beta), then for each entry e in
  *     list order: C[row_e, k] = float(double(C[row_e, k]) + double(value_e) * alpha *

@@ -33,6 +33,7 @@ TRITS = 48
 TRYTES = 16
 
 _u8p = ctypes.POINTER(ctypes.c_uint8)
+_u16p = ctypes.POINTER(ctypes.c_uint16)
 _i8p = ctypes.POINTER(ctypes.c_int8)
 _f32p = ctypes.POINTER(ctypes.c_float)
 _f64p = ctypes.POINTER(ctypes.c_double)
@@ -111,6 +112,15 @@ def _load_oracle() -> ctypes.CDLL:
     lib.orc_tq_dequantize.argtypes = [_u8p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int, _f32p]
     lib.orc_tq2_matmul_f64.argtypes = [_f64p, ctypes.c_int64, ctypes.c_int64, _u8p,
                                        ctypes.c_int64, _f64p, _f64p]
+    lib.orc_tq1r_scale.restype = ctypes.c_float
+    lib.orc_tq1r_scale.argtypes = [_f32p, ctypes.c_int64]
+    lib.orc_tq1r_quantize_row.restype = ctypes.c_float
+    lib.orc_tq1r_quantize_row.argtypes = [_f32p, ctypes.c_int64, ctypes.c_float, ctypes.c_float,
+                                          _u16p]
+    lib.orc_tq1r_dequantize_row.argtypes = [_u16p, ctypes.c_int64, ctypes.c_float, _f32p]
+    lib.orc_tq1r_dequant_tensor.restype = ctypes.c_int
+    lib.orc_tq1r_dequant_tensor.argtypes = [_u8p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+                                            ctypes.c_int64, ctypes.c_int, _f32p]
     return lib
 
 
@@ -329,6 +339,73 @@ def tq2_matmul_f64(x: np.ndarray, w_tq2: np.ndarray, K: int) -> tuple[np.ndarray
     return out, scale
 
 
+# ------------------------------------- TQ1_0 row codec (gguf_quants.h) --
+TQ1_TRITS_PER_BLOCK = 8
+TQ1_BLOCK_ROWS = 32
+TQ1R_ERRORS = {1: "buffer truncated while reading scale",
+               2: "buffer truncated while skipping refinement bytes",
+               3: "buffer truncated while reading quantized rows"}
+
+
+def tq1r_words(n: int) -> int:
+    return (int(n) + TQ1_TRITS_PER_BLOCK - 1) // TQ1_TRITS_PER_BLOCK
+
+
+def tq1r_scale(v: np.ndarray) -> float:
+    v = np.ascontiguousarray(v, np.float32).reshape(-1)
+    return float(np.float32(lib().orc_tq1r_scale(_ptr(v, _f32p), v.size)))
+
+
+def tq1r_quantize_row(v: np.ndarray, threshold: float = 0.45, scale: float = 0.0
+                      ) -> tuple[float, np.ndarray]:
+    """(scale used, ceil(n / 8) uint16 words) for one row."""
+    v = np.ascontiguousarray(v, np.float32).reshape(-1)
+    out = np.zeros(tq1r_words(v.size), np.uint16)
+    used = lib().orc_tq1r_quantize_row(_ptr(v, _f32p), v.size, threshold, scale, _ptr(out, _u16p))
+    return float(np.float32(used)), out
+
+
+def tq1r_dequantize_row(words: np.ndarray, n: int, scale: float) -> np.ndarray:
+    words = np.ascontiguousarray(words, np.uint16).reshape(-1)
+    assert words.size >= tq1r_words(n)
+    out = np.zeros(n, np.float32)
+    lib().orc_tq1r_dequantize_row(_ptr(words, _u16p), n, scale, _ptr(out, _f32p))
+    return out
+
+
+def tq1r_dequant_tensor(buf, rows: int, cols: int, block_rows: int = TQ1_BLOCK_ROWS,
+                        refinements: bool = False) -> tuple[int, np.ndarray]:
+    """(0 or the failing check 1 / 2 / 3 of TQ1R_ERRORS, or -1 for negative sizes,
+    rows x cols float32 as far as decoded)."""
+    b = np.ascontiguousarray(np.frombuffer(bytes(buf), np.uint8))
+    out = np.zeros((max(rows, 0), max(cols, 0)), np.float32)
+    rc = lib().orc_tq1r_dequant_tensor(_ptr(b, _u8p) if b.size else None, b.size, rows, cols,
+                                       block_rows, int(bool(refinements)), _ptr(out, _f32p))
+    return int(rc), out
+
+
+def tq1r_payload(values: np.ndarray, block_rows: int = TQ1_BLOCK_ROWS, refinements: bool = False,
+                 threshold: float = 0.45) -> bytes:
+    """The tensor payload dequant_tq1_0 / dequant_tq2_0 read, written with the row codec:
+    per group of block_rows rows h = float16(max |v| of the group), 8 zero bytes when
+    `refinements`, then each row's words from quantize_row_tq1_0 with the scale
+    float(h)."""
+    values = np.ascontiguousarray(values, np.float32)
+    rows, cols = values.shape
+    group = max(1, int(block_rows))
+    parts = []
+    for g0 in range(0, rows, group):
+        blk = values[g0:g0 + group]
+        h = f32_to_f16_bits(tq1r_scale(blk))
+        parts.append(np.array([h], np.uint16).tobytes())
+        if refinements:
+            parts.append(bytes(8))
+        s = f16_bits_to_f32(h)
+        for r in range(blk.shape[0]):
+            parts.append(tq1r_quantize_row(blk[r], threshold, s)[1].tobytes())
+    return b"".join(parts)
+
+
 # ------------------------------------------------ the compiled reference --
 def _cpu_has_avx512f() -> bool:
     try:
@@ -376,6 +453,35 @@ class Ref:
                                      ctypes.c_float]
         lib.t81ref_addcmul.argtypes = [_f32p, _f32p, _f32p, ctypes.c_float, _f32p,
                                        ctypes.c_longlong]
+        lib.t81ref_tq1_compute_scale.restype = ctypes.c_float
+        lib.t81ref_tq1_compute_scale.argtypes = [_f32p, ctypes.c_longlong]
+        lib.t81ref_tq1_quantize_row.argtypes = [_f32p, ctypes.c_longlong, ctypes.c_float,
+                                                ctypes.c_float, _u16p]
+        lib.t81ref_tq1_dequantize_row.argtypes = [_u16p, ctypes.c_longlong, ctypes.c_float,
+                                                  _f32p]
+        lib.t81ref_tq1_half_to_float.restype = ctypes.c_float
+        lib.t81ref_tq1_half_to_float.argtypes = [ctypes.c_uint16]
+
+    def tq1_compute_scale(self, v) -> float:
+        v = np.ascontiguousarray(v, np.float32).reshape(-1)
+        return float(np.float32(self.lib.t81ref_tq1_compute_scale(_ptr(v, _f32p), v.size)))
+
+    def tq1_quantize_row(self, v, threshold: float, scale: float) -> np.ndarray:
+        """quantize_row_tq1_0 as it stands (the scale argument passed through)."""
+        v = np.ascontiguousarray(v, np.float32).reshape(-1)
+        out = np.zeros(tq1r_words(v.size), np.uint16)
+        self.lib.t81ref_tq1_quantize_row(_ptr(v, _f32p), v.size, threshold, scale,
+                                         _ptr(out, _u16p))
+        return out
+
+    def tq1_dequantize_row(self, words, n: int, scale: float) -> np.ndarray:
+        words = np.ascontiguousarray(words, np.uint16).reshape(-1)
+        out = np.zeros(n, np.float32)
+        self.lib.t81ref_tq1_dequantize_row(_ptr(words, _u16p), n, scale, _ptr(out, _f32p))
+        return out
+
+    def tq1_half_to_float(self, bits: int) -> np.float32:
+        return np.float32(self.lib.t81ref_tq1_half_to_float(int(bits)))
 
     def spmm_simple(self, values, rows_idx, cols_idx, rows: int, cols: int, B, C, N: int,
                     alpha: float = 1.0, beta: float = 0.0):

@@ -19,6 +19,8 @@
 //   random_limb (mt19937_64 + uniform_int(0,26))  tests/unit/test_limb_basic.cpp:58-66 (restated)
 //   t81::linalg::detail::where / clamp / lerp / addcmul on Backend::CPU
 //                                                 src/linalg/gemm_dispatch.cpp:239-322
+//   t81::core::gguf::compute_scale / quantize_row_tq1_0 / dequantize_row_tq1_0 /
+//   half_to_float                                 src/t81/core/gguf_quants.h:55-168
 
 #include <array>
 #include <cstdint>
@@ -27,6 +29,7 @@
 #include <span>
 #include <stdexcept>
 
+#include <t81/core/gguf_quants.h>
 #include <t81/linalg/gemm.hpp>
 #include <t81/linalg/gemm_gpu.hpp>
 #include <t81/sparse/simple.hpp>
@@ -231,5 +234,21 @@ int t81ref_spmm_simple(const long long *values, const int *row_idx, const int *c
         return -1;
     }
 }
+
+// ---- the TQ1_0 row codec of src/t81/core/gguf_quants.h, called as it stands ----
+float t81ref_tq1_compute_scale(const float *values, long long n) {
+    return t81::core::gguf::compute_scale(values, n);
+}
+
+void t81ref_tq1_quantize_row(const float *values, long long n, float threshold, float scale,
+                             std::uint16_t *dst) {
+    t81::core::gguf::quantize_row_tq1_0(values, n, threshold, scale, dst);
+}
+
+void t81ref_tq1_dequantize_row(const std::uint16_t *src, long long n, float scale, float *dst) {
+    t81::core::gguf::dequantize_row_tq1_0(src, n, scale, dst);
+}
+
+float t81ref_tq1_half_to_float(std::uint16_t bits) { return t81::core::gguf::half_to_float(bits); }
 
 } // extern "C"

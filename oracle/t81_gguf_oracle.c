@@ -255,3 +255,115 @@ void orc_tq2_matmul_f64(const double *x, int64_t M, int64_t K, const uint8_t *w,
         }
     }
 }
+
+/* ---- t81::core::gguf row codec (src/t81/core/gguf_quants.h): 8 trits per 13-bit
+ * block stored as uint16, one float scale per row, and the tensor framing of the
+ * dequant_tq1_0 / dequant_tq2_0 bindings (python/bindings.cpp:561-638).  Pinned
+ * against the compiled header (oracle/_ref) in tests/test_gguf_oracle.py. ---- */
+
+/* compute_scale (gguf_quants.h:55-64): the largest |v| that compares greater than the
+ * running maximum, starting from 0; NaN never does. */
+float orc_tq1r_scale(const float *v, int64_t n) {
+    float m = 0.0f;
+    for (int64_t i = 0; i < n; ++i) {
+        const float a = fabsf(v[i]);
+        if (a > m) m = a;
+    }
+    return m;
+}
+
+/* quantize_trit (:23-32) after clamp_threshold (:19-21, std::clamp keeps NaN): fmin /
+ * fmax take the non-NaN operand, so a NaN value clamps to +1. */
+static int tq1r_trit(float v, float thr) {
+    const float c = isnan(v) ? 1.0f : (v > 1.0f ? 1.0f : (v < -1.0f ? -1.0f : v));
+    if (c >= thr) return 1;
+    if (c <= -thr) return -1;
+    return 0;
+}
+
+static float tq1r_clamp_threshold(float t) {
+    return t < 0.0f ? 0.0f : (0.9999f < t ? 0.9999f : t);
+}
+
+/* quantize_row_tq1_0 (:116-144): scale = supplied if > 0 else compute_scale; each block of
+ * 8 values becomes digits d_i = {+1: 0, 0: 1, -1: 2} of trit(v * (1 / scale)) (trit 0
+ * past the row or when scale <= 0), stored as sum_i d_i 3^i (digit 0 least
+ * significant).  Returns the scale used. */
+float orc_tq1r_quantize_row(const float *v, int64_t n, float threshold, float supplied,
+                            uint16_t *dst) {
+    if (n <= 0 || dst == NULL) return 0.0f;
+    const float scale = supplied > 0.0f ? supplied : orc_tq1r_scale(v, n);
+    const float thr = tq1r_clamp_threshold(threshold);
+    const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+    const int64_t blocks = (n + 7) / 8;
+    for (int64_t b = 0; b < blocks; ++b) {
+        unsigned word = 0;
+        for (int i = 7; i >= 0; --i) {
+            const int64_t k = b * 8 + i;
+            int t = 0;
+            if (k < n && scale > 0.0f) t = tq1r_trit(v[k] * inv, thr);
+            word = word * 3u + (unsigned)(t > 0 ? 0 : (t < 0 ? 2 : 1));
+        }
+        dst[b] = (uint16_t)(word & 0x1FFFu);
+    }
+    return scale;
+}
+
+/* dequantize_row_tq1_0 (:146-168): scale == 0 gives zeros; else value = trit * scale with
+ * the low 8 base-3 digits of each word (digit 0 -> +1, 2 -> -1, else 0). */
+void orc_tq1r_dequantize_row(const uint16_t *src, int64_t n, float scale, float *dst) {
+    if (n <= 0 || dst == NULL || src == NULL) return;
+    if (scale == 0.0f) {
+        for (int64_t i = 0; i < n; ++i) dst[i] = 0.0f;
+        return;
+    }
+    for (int64_t i = 0; i < n; ++i) {
+        unsigned w = src[i / 8];
+        for (int64_t d = 0; d < i % 8; ++d) w /= 3u;
+        const unsigned digit = w % 3u;
+        const float t = digit == 0 ? 1.0f : (digit == 2 ? -1.0f : 0.0f);
+        dst[i] = t * scale;
+    }
+}
+
+/* dequant_tensor_tq1_impl (python/bindings.cpp:561-638): groups of max(1, block_rows)
+ * rows, each a little-endian float16 scale, 8 skipped bytes when `refinements`, then
+ * each row's ceil(cols / 8) uint16 words.  Returns 0, or the first check that fails as
+ * the binding meets it: 1 "buffer truncated while reading scale", 2 "... while skipping
+ * refinement bytes", 3 "... while reading quantized rows"; -1 negative rows / cols.
+ * Rows decoded before the failure are left in dst. */
+int orc_tq1r_dequant_tensor(const uint8_t *buf, int64_t nbytes, int64_t rows, int64_t cols,
+                            int64_t block_rows, int refinements, float *dst) {
+    if (rows < 0 || cols < 0) return -1;
+    const int64_t words = (cols + 7) / 8;
+    const int64_t row_bytes = words * 2;
+    const int64_t group = block_rows > 1 ? block_rows : 1;
+    int64_t off = 0;
+    int64_t r = 0;
+    uint16_t row[4096];
+    while (r < rows) {
+        if (off + 2 > nbytes) return 1;
+        const uint16_t h = (uint16_t)(buf[off] | (buf[off + 1] << 8));
+        off += 2;
+        if (refinements) {
+            if (off + 8 > nbytes) return 2;
+            off += 8;
+        }
+        const float scale = orc_f16_bits_to_f32(h);
+        const int64_t in_group = group < rows - r ? group : rows - r;
+        for (int64_t g = 0; g < in_group; ++g) {
+            if (off + row_bytes > nbytes) return 3;
+            for (int64_t w0 = 0; w0 < words; w0 += 4096) {
+                const int64_t cnt = words - w0 < 4096 ? words - w0 : 4096;
+                for (int64_t i = 0; i < cnt; ++i)
+                    row[i] = (uint16_t)(buf[off + 2 * (w0 + i)] | (buf[off + 2 * (w0 + i) + 1] << 8));
+                const int64_t c0 = w0 * 8;
+                const int64_t nc = cols - c0 < cnt * 8 ? cols - c0 : cnt * 8;
+                orc_tq1r_dequantize_row(row, nc, scale, dst + r * cols + c0);
+            }
+            off += row_bytes;
+            ++r;
+        }
+    }
+    return 0;
+}

@@ -59,6 +59,11 @@ EXPORTS = (
     "t81_hip_tq_quantize",
     "t81_hip_tq_dequantize",
     "t81_hip_tq2_matmul",
+    "t81_hip_tq1_quantize_rows",
+    "t81_hip_tq1_dequantize_rows",
+    "t81_hip_tq1_payload_bytes",
+    "t81_hip_tq1_quantize_payload",
+    "t81_hip_tq1_dequantize_payload",
     "t81_hip_spmm_plan_create",
     "t81_hip_spmm_plan_apply",
     "t81_hip_spmm_plan_info",
@@ -135,6 +140,16 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.t81_hip_tq_dequantize.argtypes = [_vp, _vp, _i64, _i64, _i, _vp]
     lib.t81_hip_tq2_matmul.restype = _i
     lib.t81_hip_tq2_matmul.argtypes = [_vp, _i, _vp, _vp, _i64, _i64, _i64, _f, _f, _vp, _vp]
+    lib.t81_hip_tq1_quantize_rows.restype = _i
+    lib.t81_hip_tq1_quantize_rows.argtypes = [_vp, _i64, _i64, _f, _vp, _vp, _vp, _vp]
+    lib.t81_hip_tq1_dequantize_rows.restype = _i
+    lib.t81_hip_tq1_dequantize_rows.argtypes = [_vp, _i64, _i64, _vp, _vp, _vp]
+    lib.t81_hip_tq1_payload_bytes.restype = _i64
+    lib.t81_hip_tq1_payload_bytes.argtypes = [_i64, _i64, _i64, _i]
+    lib.t81_hip_tq1_quantize_payload.restype = _i
+    lib.t81_hip_tq1_quantize_payload.argtypes = [_vp, _i64, _i64, _i64, _i, _f, _vp, _vp]
+    lib.t81_hip_tq1_dequantize_payload.restype = _i
+    lib.t81_hip_tq1_dequantize_payload.argtypes = [_vp, _i64, _i64, _i64, _i64, _i, _vp, _vp]
     lib.t81_hip_spmm_plan_create.restype = _i
     lib.t81_hip_spmm_plan_create.argtypes = [_vp, _vp, _vp, _i64, _i, _i,
                                              ctypes.POINTER(ctypes.c_void_p),

@@ -22,7 +22,7 @@ FLOORS_LIB = os.path.join(HERE, "libt81_floors.so")
 ARCH = "gfx950"
 
 SOURCES = ["abi.hip", "pack.hip", "gemv.hip", "gemv_strip.hip", "gemm.hip", "gemm_i8.hip",
-           "limb.hip", "elementwise.hip", "tq.hip", "gemv_tq2.hip", "transpose.hip",
+           "limb.hip", "elementwise.hip", "tq.hip", "tq_row.hip", "gemv_tq2.hip", "transpose.hip",
            "spmm.hip", "noalloc.hip"]
 
 # -packed-fp32-ops: no v_pk_*_f32 from the compiler (they are never written by hand either).

@@ -411,6 +411,88 @@ int t81_hip_tq_dequantize(const uint8_t *src, float *dst, int64_t rows, int64_t 
                   "t81_hip_tq_dequantize");
 }
 
+// ---- the TQ1_0 row codec of src/t81/core/gguf_quants.h and its tensor payload ----
+int t81_hip_tq1_quantize_rows(const float *values, int64_t rows, int64_t cols, float threshold,
+                              const float *scales_in, float *scales_out, uint16_t *dst,
+                              void *stream) {
+    if (rows < 0 || cols < 0) return fail(T81_HIP_EINVAL_SHAPE, "rows and cols must be non-negative");
+    if (too_many(rows, cols) || rows > INT_MAX) return fail(T81_HIP_EINVAL_SHAPE, "rows x cols too large");
+    if (rows > 0 && cols > 0 && (values == nullptr || dst == nullptr))
+        return fail(T81_HIP_EINVAL_POINTER, "null data pointer");
+    if (reinterpret_cast<uintptr_t>(values) % 4 != 0 || reinterpret_cast<uintptr_t>(dst) % 2 != 0 ||
+        reinterpret_cast<uintptr_t>(scales_in) % 4 != 0 ||
+        reinterpret_cast<uintptr_t>(scales_out) % 4 != 0)
+        return fail(T81_HIP_EINVAL_POINTER, "misaligned values, words or scales pointer");
+    if (int rc = require_device("t81_hip_tq1_quantize_rows")) return rc;
+    return finish(t81hip::launch_tq1r_quantize_rows(values, rows, cols, threshold, scales_in,
+                                                    scales_out, dst,
+                                                    static_cast<hipStream_t>(stream)),
+                  "t81_hip_tq1_quantize_rows");
+}
+
+int t81_hip_tq1_dequantize_rows(const uint16_t *src, int64_t rows, int64_t cols,
+                                const float *scales, float *dst, void *stream) {
+    if (rows < 0 || cols < 0) return fail(T81_HIP_EINVAL_SHAPE, "rows and cols must be non-negative");
+    if (too_many(rows, cols)) return fail(T81_HIP_EINVAL_SHAPE, "rows x cols too large");
+    if (rows > 0 && cols > 0 && (src == nullptr || dst == nullptr || scales == nullptr))
+        return fail(T81_HIP_EINVAL_POINTER, "null data pointer");
+    if (reinterpret_cast<uintptr_t>(src) % 2 != 0 || reinterpret_cast<uintptr_t>(dst) % 4 != 0 ||
+        reinterpret_cast<uintptr_t>(scales) % 4 != 0)
+        return fail(T81_HIP_EINVAL_POINTER, "misaligned words, output or scales pointer");
+    if (int rc = require_device("t81_hip_tq1_dequantize_rows")) return rc;
+    return finish(t81hip::launch_tq1r_dequantize_rows(src, rows, cols, scales, dst,
+                                                      static_cast<hipStream_t>(stream)),
+                  "t81_hip_tq1_dequantize_rows");
+}
+
+int64_t t81_hip_tq1_payload_bytes(int64_t rows, int64_t cols, int64_t block_rows,
+                                  int refinements) {
+    if (rows < 0 || cols < 0) return fail(T81_HIP_EINVAL_SHAPE, "rows and cols must be non-negative");
+    if (too_many(rows, cols)) return fail(T81_HIP_EINVAL_SHAPE, "rows x cols too large");
+    return t81hip::tq1r_payload_bytes(rows, cols, block_rows, refinements != 0);
+}
+
+int t81_hip_tq1_quantize_payload(const float *values, int64_t rows, int64_t cols,
+                                 int64_t block_rows, int refinements, float threshold,
+                                 uint8_t *payload, void *stream) {
+    if (rows < 0 || cols < 0) return fail(T81_HIP_EINVAL_SHAPE, "rows and cols must be non-negative");
+    if (too_many(rows, cols) || rows > INT_MAX) return fail(T81_HIP_EINVAL_SHAPE, "rows x cols too large");
+    if (rows > 0 && (payload == nullptr || (cols > 0 && values == nullptr)))
+        return fail(T81_HIP_EINVAL_POINTER, "null data pointer");
+    if (reinterpret_cast<uintptr_t>(values) % 4 != 0)
+        return fail(T81_HIP_EINVAL_POINTER, "float32 data must be 4-byte aligned");
+    if (int rc = require_device("t81_hip_tq1_quantize_payload")) return rc;
+    return finish(t81hip::launch_tq1r_quantize_payload(values, rows, cols, block_rows,
+                                                       refinements != 0, threshold, payload,
+                                                       static_cast<hipStream_t>(stream)),
+                  "t81_hip_tq1_quantize_payload");
+}
+
+// python/bindings.cpp:561-638: the binding's checks, in its order and with its messages.
+int t81_hip_tq1_dequantize_payload(const uint8_t *payload, int64_t payload_bytes, int64_t rows,
+                                   int64_t cols, int64_t block_rows, int refinements, float *dst,
+                                   void *stream) {
+    if (rows < 0 || cols < 0) return fail(T81_HIP_EINVAL_SHAPE, "rows and cols must be non-negative");
+    if (payload_bytes < 0) return fail(T81_HIP_EINVAL_SHAPE, "payload size must be non-negative");
+    if (payload == nullptr && payload_bytes > 0)
+        return fail(T81_HIP_EINVAL_POINTER, "buffer pointer is null");
+    if (too_many(rows, cols)) return fail(T81_HIP_EINVAL_SHAPE, "rows x cols too large");
+    switch (t81hip::tq1r_payload_check(payload_bytes, rows, cols, block_rows, refinements != 0)) {
+        case 1: return fail(T81_HIP_EINVAL_SHAPE, "buffer truncated while reading scale");
+        case 2: return fail(T81_HIP_EINVAL_SHAPE, "buffer truncated while skipping refinement bytes");
+        case 3: return fail(T81_HIP_EINVAL_SHAPE, "buffer truncated while reading quantized rows");
+        default: break;
+    }
+    if (rows > 0 && cols > 0 && dst == nullptr) return fail(T81_HIP_EINVAL_POINTER, "null data pointer");
+    if (reinterpret_cast<uintptr_t>(dst) % 4 != 0)
+        return fail(T81_HIP_EINVAL_POINTER, "float32 data must be 4-byte aligned");
+    if (int rc = require_device("t81_hip_tq1_dequantize_payload")) return rc;
+    return finish(t81hip::launch_tq1r_dequantize_payload(payload, rows, cols, block_rows,
+                                                         refinements != 0, dst,
+                                                         static_cast<hipStream_t>(stream)),
+                  "t81_hip_tq1_dequantize_payload");
+}
+
 int t81_hip_tq2_matmul(const void *x, int x_dtype, const uint8_t *w, float *c, int64_t m,
                        int64_t n, int64_t k, float alpha, float beta, const float *bias,
                        void *stream) {

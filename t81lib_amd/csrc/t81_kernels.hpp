@@ -68,6 +68,24 @@ hipError_t launch_tq_quantize(const float *src, uint8_t *dst, int64_t rows, int6
 hipError_t launch_tq_dequantize(const uint8_t *src, float *dst, int64_t rows, int64_t cols,
                                 int quant, hipStream_t s);
 
+// tq_row.hip: the TQ1_0 row codec (8 trits per uint16 word, a float scale per row) and the
+// grouped tensor payload; payload_check returns the binding's first failing check (0 none,
+// 1 scale, 2 reserved bytes, 3 rows)
+int64_t tq1r_payload_bytes(int64_t rows, int64_t n, int64_t block_rows, bool refinements);
+int tq1r_payload_check(int64_t nbytes, int64_t rows, int64_t n, int64_t block_rows,
+                       bool refinements);
+hipError_t launch_tq1r_quantize_rows(const float *values, int64_t rows, int64_t n, float thr,
+                                     const float *scales_in, float *scales_out, uint16_t *dst,
+                                     hipStream_t s);
+hipError_t launch_tq1r_dequantize_rows(const uint16_t *src, int64_t rows, int64_t n,
+                                       const float *scales, float *dst, hipStream_t s);
+hipError_t launch_tq1r_dequantize_payload(const uint8_t *payload, int64_t rows, int64_t n,
+                                          int64_t block_rows, bool refinements, float *dst,
+                                          hipStream_t s);
+hipError_t launch_tq1r_quantize_payload(const float *values, int64_t rows, int64_t n,
+                                        int64_t block_rows, bool refinements, float thr,
+                                        uint8_t *payload, hipStream_t s);
+
 // gemv_tq2.hip: matmul straight from TQ2_0 weights (tokens in groups of four)
 bool tq2_matmul_fits(int64_t n, int64_t k);
 hipError_t launch_tq2_matmul(const void *x, int x_dtype, const uint8_t *w, float *c, int64_t m,

@@ -1,0 +1,322 @@
+// t81lib_amd/csrc/tq_row.hip -- the reference's own TQ1_0 row codec
+// (src/t81/core/gguf_quants.h:14-168) and the tensor payload its dequant_tq1_0 /
+// dequant_tq2_0 bindings read (python/bindings.cpp:561-638).
+//
+// Word format: 8 trits per uint16, digit d = {+1: 0, 0: 1, -1: 2}, word = sum_i d_i 3^i
+// with trit i of the word (values 8w + i of the row) as digit i; the words of a row of
+// n values are ceil(n / 8), pad trits 0.  A row has one float scale: quantize uses
+// the caller's scale when it is > 0, else max |v| of the row (NaN values never win the
+// comparison), then trit(v * (1 / scale)) with |v| clamped to 1 (a NaN product clamps
+// to +1, as std::fmin / std::fmax return the non-NaN operand) and the threshold
+// clamped to [0, 0.9999]; decode gives trit * scale (all zeros when scale == 0).
+//
+// Tensor payload: groups of block_rows rows, each a little-endian IEEE half scale,
+// 8 reserved bytes in the TQ2_0 variant, then the group's rows of words, byte-packed
+// (the payload need not be aligned).  The writer here (no reference counterpart; the
+// reference only reads such payloads) stores h = half(max |v| of the group) and
+// quantizes each row with the scale float(h), as a caller of quantize_row_tq1_0
+// would.
+//
+// All three kernels are bound by HBM: a word is 32 bytes of float32 on one side and
+// 2 bytes on the other.  One thread per word, consecutive threads on consecutive words.
+#include <hip/hip_runtime.h>
+
+#include "t81_device.hpp"
+#include "t81_kernels.hpp"
+
+#pragma clang fp contract(off)
+
+namespace t81hip {
+
+namespace {
+
+constexpr int kWordTrits = 8;
+
+__device__ __forceinline__ int tq1r_trit(float v, float thr) {
+    const float c = v != v ? 1.0f : (v > 1.0f ? 1.0f : (v < -1.0f ? -1.0f : v));
+    if (c >= thr) return 1;
+    if (c <= -thr) return -1;
+    return 0;
+}
+
+__device__ __forceinline__ uint32_t tq1r_digit(int t) { return t > 0 ? 0u : (t < 0 ? 2u : 1u); }
+
+// IEEE half bits -> float32 bits, exactly (subnormals normalised, NaN payload kept).
+__host__ __device__ __forceinline__ float half_bits_to_float(uint32_t h) {
+    const uint32_t sign = (h & 0x8000u) << 16;
+    const uint32_t e = (h >> 10) & 0x1Fu;
+    uint32_t m = h & 0x3FFu;
+    uint32_t bits;
+    if (e == 0x1Fu) {
+        bits = sign | 0x7F800000u | (m << 13);
+    } else if (e == 0) {
+        if (m == 0) {
+            bits = sign;
+        } else {
+            // m * 2^-24: shift the leading one up to bit 10, one exponent step per shift
+            int shift = 0;
+            while ((m & 0x400u) == 0) {
+                m <<= 1;
+                ++shift;
+            }
+            bits = sign | (static_cast<uint32_t>(113 - shift) << 23) | ((m & 0x3FFu) << 13);
+        }
+    } else {
+        bits = sign | ((e + 112u) << 23) | (m << 13);
+    }
+    return __builtin_bit_cast(float, bits);
+}
+
+// Max of non-NaN |v| over the workgroup (256 threads), from per-thread maxima >= 0.
+__device__ __forceinline__ float block_max(float m, float *red) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float o = __shfl_xor(m, off, 64);
+        m = o > m ? o : m;
+    }
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    float r = red[0];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) r = red[w] > r ? red[w] : r;
+    return r;
+}
+
+__device__ __forceinline__ float abs_max_strided(const float *v, int64_t n) {
+    float m = 0.0f;
+    for (int64_t i = threadIdx.x; i < n; i += 256) {
+        const float a = fabsf(v[i]);
+        m = a > m ? a : m;
+    }
+    return m;
+}
+
+// Word w of a row: trits of v[8w .. 8w + 8) (those below n), digit 0 least significant.
+__device__ __forceinline__ uint32_t quantize_word(const float *v, int64_t n, int64_t w,
+                                                  float scale, float inv, float thr) {
+    float x[kWordTrits];
+    const int64_t k0 = w * kWordTrits;
+    if (k0 + kWordTrits <= n && (reinterpret_cast<uintptr_t>(v + k0) & 15u) == 0) {
+        const floatx4 a = *reinterpret_cast<const floatx4 *>(v + k0);
+        const floatx4 b = *reinterpret_cast<const floatx4 *>(v + k0 + 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[i] = a[i], x[4 + i] = b[i];
+    } else {
+#pragma unroll
+        for (int i = 0; i < kWordTrits; ++i) x[i] = k0 + i < n ? v[k0 + i] : 0.0f;
+    }
+    uint32_t word = 0;
+#pragma unroll
+    for (int i = kWordTrits - 1; i >= 0; --i) {
+        const int t = (k0 + i < n && scale > 0.0f) ? tq1r_trit(x[i] * inv, thr) : 0;
+        word = word * 3u + tq1r_digit(t);
+    }
+    return word & 0x1FFFu;
+}
+
+// Trit i (0..7) of a word's low 8 base-3 digits times scale.
+__device__ __forceinline__ void decode_word(uint32_t word, float scale, float *out, int count) {
+#pragma unroll
+    for (int i = 0; i < kWordTrits; ++i) {
+        const uint32_t d = word % 3u;
+        word /= 3u;
+        if (i < count) {
+            const float t = d == 0 ? 1.0f : (d == 2 ? -1.0f : 0.0f);
+            out[i] = scale == 0.0f ? 0.0f : t * scale;
+        }
+    }
+}
+
+// One workgroup per row: the scale (caller's when > 0, else the row's max |v|), then
+// the row's words.
+__global__ __launch_bounds__(256) void tq1r_quantize_rows_kernel(
+    const float *__restrict__ values, int64_t n, float thr, const float *__restrict__ scales_in,
+    float *__restrict__ scales_out, uint16_t *__restrict__ dst) {
+    __shared__ float red[4];
+    const int64_t row = blockIdx.x;
+    const float *v = values + row * n;
+    float scale = scales_in != nullptr ? scales_in[row] : 0.0f;
+    if (!(scale > 0.0f)) scale = block_max(abs_max_strided(v, n), red);
+    if (scales_out != nullptr && threadIdx.x == 0) scales_out[row] = scale;
+    const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+    const int64_t words = (n + kWordTrits - 1) / kWordTrits;
+    uint16_t *out = dst + row * words;
+    for (int64_t w = threadIdx.x; w < words; w += 256)
+        out[w] = static_cast<uint16_t>(quantize_word(v, n, w, scale, inv, thr));
+}
+
+__global__ __launch_bounds__(256) void tq1r_dequantize_rows_kernel(
+    const uint16_t *__restrict__ src, int64_t rows, int64_t n, int64_t words,
+    const float *__restrict__ scales, float *__restrict__ dst) {
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (idx >= rows * words) return;
+    const int64_t row = idx / words;
+    const int64_t w = idx - row * words;
+    const int64_t k0 = w * kWordTrits;
+    const int count = static_cast<int>(n - k0 < kWordTrits ? n - k0 : kWordTrits);
+    float out[kWordTrits];
+    decode_word(src[idx], scales[row], out, count);
+    float *o = dst + row * n + k0;
+#pragma unroll
+    for (int i = 0; i < kWordTrits; ++i)
+        if (i < count) o[i] = out[i];
+}
+
+struct PayloadLayout {
+    int64_t group;      // rows per group (>= 1, at most max(rows, 1))
+    int64_t header;     // 2 (+ 8 reserved bytes)
+    int64_t row_bytes;  // 2 * words
+    int64_t stride;     // bytes per whole group
+};
+
+__global__ __launch_bounds__(256) void tq1r_dequantize_payload_kernel(
+    const uint8_t *__restrict__ payload, int64_t rows, int64_t n, int64_t words, PayloadLayout lay,
+    float *__restrict__ dst) {
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (idx >= rows * words) return;
+    const int64_t row = idx / words;
+    const int64_t w = idx - row * words;
+    const int64_t g = row / lay.group;
+    const uint8_t *grp = payload + g * lay.stride;
+    const float scale = half_bits_to_float(static_cast<uint32_t>(grp[0]) |
+                                           (static_cast<uint32_t>(grp[1]) << 8));
+    const uint8_t *p = grp + lay.header + (row - g * lay.group) * lay.row_bytes + 2 * w;
+    const uint32_t word = static_cast<uint32_t>(p[0]) | (static_cast<uint32_t>(p[1]) << 8);
+    const int64_t k0 = w * kWordTrits;
+    const int count = static_cast<int>(n - k0 < kWordTrits ? n - k0 : kWordTrits);
+    float out[kWordTrits];
+    decode_word(word, scale, out, count);
+    float *o = dst + row * n + k0;
+#pragma unroll
+    for (int i = 0; i < kWordTrits; ++i)
+        if (i < count) o[i] = out[i];
+}
+
+// One workgroup per group: h = half(max |v| over the group's rows, contiguous in the
+// input), round to nearest even; the reserved bytes are zeroed.
+__global__ __launch_bounds__(256) void tq1r_payload_scales_kernel(
+    const float *__restrict__ values, int64_t rows, int64_t n, PayloadLayout lay,
+    uint8_t *__restrict__ payload) {
+    __shared__ float red[4];
+    const int64_t g = blockIdx.x;
+    const int64_t r0 = g * lay.group;
+    const int64_t nr = rows - r0 < lay.group ? rows - r0 : lay.group;
+    const float m = block_max(abs_max_strided(values + r0 * n, nr * n), red);
+    uint8_t *grp = payload + g * lay.stride;
+    if (threadIdx.x == 0) {
+        const uint16_t h = __builtin_bit_cast(uint16_t, static_cast<_Float16>(m));
+        grp[0] = static_cast<uint8_t>(h & 0xFFu);
+        grp[1] = static_cast<uint8_t>(h >> 8);
+    }
+    if (threadIdx.x >= 2 && threadIdx.x < lay.header) grp[threadIdx.x] = 0;
+}
+
+// One workgroup per row, scale read back from its group's half: quantize_row_tq1_0
+// with that scale (<= 0 falls back to the row's own max, as the reference does).
+__global__ __launch_bounds__(256) void tq1r_payload_rows_kernel(
+    const float *__restrict__ values, int64_t n, float thr, PayloadLayout lay,
+    uint8_t *__restrict__ payload) {
+    __shared__ float red[4];
+    const int64_t row = blockIdx.x;
+    const int64_t g = row / lay.group;
+    uint8_t *grp = payload + g * lay.stride;
+    const float *v = values + row * n;
+    float scale = half_bits_to_float(static_cast<uint32_t>(grp[0]) |
+                                     (static_cast<uint32_t>(grp[1]) << 8));
+    if (!(scale > 0.0f)) scale = block_max(abs_max_strided(v, n), red);
+    const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+    const int64_t words = (n + kWordTrits - 1) / kWordTrits;
+    uint8_t *out = grp + lay.header + (row - g * lay.group) * lay.row_bytes;
+    for (int64_t w = threadIdx.x; w < words; w += 256) {
+        const uint32_t word = quantize_word(v, n, w, scale, inv, thr);
+        out[2 * w] = static_cast<uint8_t>(word & 0xFFu);
+        out[2 * w + 1] = static_cast<uint8_t>(word >> 8);
+    }
+}
+
+PayloadLayout layout(int64_t rows, int64_t n, int64_t block_rows, bool refinements) {
+    PayloadLayout lay;
+    const int64_t cap = rows > 1 ? rows : 1;
+    lay.group = block_rows < 1 ? 1 : (block_rows > cap ? cap : block_rows);
+    lay.header = refinements ? 10 : 2;
+    lay.row_bytes = 2 * ((n + kWordTrits - 1) / kWordTrits);
+    lay.stride = lay.header + lay.group * lay.row_bytes;
+    return lay;
+}
+
+float clamp_threshold(float t) { return t < 0.0f ? 0.0f : (0.9999f < t ? 0.9999f : t); }
+
+unsigned grid_of(int64_t threads) { return static_cast<unsigned>((threads + 255) / 256); }
+
+}  // namespace
+
+int64_t tq1r_payload_bytes(int64_t rows, int64_t n, int64_t block_rows, bool refinements) {
+    if (rows <= 0) return 0;
+    const PayloadLayout lay = layout(rows, n, block_rows, refinements);
+    const int64_t groups = (rows + lay.group - 1) / lay.group;
+    const int64_t last = rows - (groups - 1) * lay.group;
+    return (groups - 1) * lay.stride + lay.header + last * lay.row_bytes;
+}
+
+int tq1r_payload_check(int64_t nbytes, int64_t rows, int64_t n, int64_t block_rows,
+                       bool refinements) {
+    if (rows <= 0 || nbytes >= tq1r_payload_bytes(rows, n, block_rows, refinements)) return 0;
+    const PayloadLayout lay = layout(rows, n, block_rows, refinements);
+    // every group before g0 ends at or before g0 * stride <= nbytes: the first failing
+    // check of the binding's sequential walk lies in group g0 or the one after it
+    const int64_t groups = (rows + lay.group - 1) / lay.group;
+    int64_t g = nbytes / lay.stride;
+    if (g > groups - 1) g = groups - 1;
+    for (; g < groups; ++g) {
+        const int64_t off = g * lay.stride;
+        if (off + 2 > nbytes) return 1;
+        if (refinements && off + 10 > nbytes) return 2;
+        const int64_t nr = rows - g * lay.group < lay.group ? rows - g * lay.group : lay.group;
+        if (off + lay.header + nr * lay.row_bytes > nbytes) return 3;
+    }
+    return 0;
+}
+
+hipError_t launch_tq1r_quantize_rows(const float *values, int64_t rows, int64_t n, float thr,
+                                     const float *scales_in, float *scales_out, uint16_t *dst,
+                                     hipStream_t s) {
+    if (rows == 0 || n == 0) return hipSuccess;
+    tq1r_quantize_rows_kernel<<<dim3(static_cast<unsigned>(rows)), 256, 0, s>>>(
+        values, n, clamp_threshold(thr), scales_in, scales_out, dst);
+    return hipGetLastError();
+}
+
+hipError_t launch_tq1r_dequantize_rows(const uint16_t *src, int64_t rows, int64_t n,
+                                       const float *scales, float *dst, hipStream_t s) {
+    const int64_t words = (n + kWordTrits - 1) / kWordTrits;
+    if (rows * words == 0) return hipSuccess;
+    tq1r_dequantize_rows_kernel<<<grid_of(rows * words), 256, 0, s>>>(src, rows, n, words,
+                                                                       scales, dst);
+    return hipGetLastError();
+}
+
+hipError_t launch_tq1r_dequantize_payload(const uint8_t *payload, int64_t rows, int64_t n,
+                                          int64_t block_rows, bool refinements, float *dst,
+                                          hipStream_t s) {
+    const int64_t words = (n + kWordTrits - 1) / kWordTrits;
+    if (rows * words == 0) return hipSuccess;
+    tq1r_dequantize_payload_kernel<<<grid_of(rows * words), 256, 0, s>>>(
+        payload, rows, n, words, layout(rows, n, block_rows, refinements), dst);
+    return hipGetLastError();
+}
+
+hipError_t launch_tq1r_quantize_payload(const float *values, int64_t rows, int64_t n,
+                                        int64_t block_rows, bool refinements, float thr,
+                                        uint8_t *payload, hipStream_t s) {
+    if (rows == 0) return hipSuccess;
+    const PayloadLayout lay = layout(rows, n, block_rows, refinements);
+    const int64_t groups = (rows + lay.group - 1) / lay.group;
+    tq1r_payload_scales_kernel<<<dim3(static_cast<unsigned>(groups)), 256, 0, s>>>(
+        values, rows, n, lay, payload);
+    if (n > 0)
+        tq1r_payload_rows_kernel<<<dim3(static_cast<unsigned>(rows)), 256, 0, s>>>(
+            values, n, clamp_threshold(thr), lay, payload);
+    return hipGetLastError();
+}
+
+}  // namespace t81hip

@@ -124,3 +124,87 @@ def tq2_matmul(x: torch.Tensor, w_tq2: torch.Tensor, k: int, alpha: float = 1.0,
                                              c.data_ptr(), m, n, k, alpha, beta, bias_ptr,
                                              _stream()))
     return c
+
+
+# ---- the reference's own TQ1_0 row codec (src/t81/core/gguf_quants.h), batched ----
+TQ1_TRITS_PER_BLOCK = 8   # gguf_quants.h:14
+TQ1_BLOCK_ROWS = 32       # gguf_quants.h:15
+
+
+def _cuda_f32(t: torch.Tensor) -> torch.Tensor:
+    if not t.is_cuda:
+        t = t.to("cuda")
+    return t.to(torch.float32).contiguous()
+
+
+def quantize_rows_tq1_0(matrix: torch.Tensor, threshold: float = 0.45,
+                        scales: Optional[torch.Tensor] = None
+                        ) -> "tuple[torch.Tensor, torch.Tensor]":
+    """(rows, cols) floats -> (scales float32 (rows,), words uint16 (rows, ceil(cols / 8))):
+    quantize_row_tq1_0 (gguf_quants.h:116-144) on every row in one launch.  Row r uses
+    scales[r] when given and > 0, else its max |v|; the scales used are returned."""
+    src = _cuda_f32(matrix)
+    if src.ndim != 2:
+        raise ValueError("quantize_rows_tq1_0 expects a 2-D tensor")
+    rows, cols = src.shape
+    s_in = None
+    if scales is not None:
+        s_in = _cuda_f32(scales).reshape(-1)
+        if s_in.numel() != rows:
+            raise ValueError("scales must have one value per row")
+    s_out = torch.zeros(rows, dtype=torch.float32, device=src.device)
+    words = torch.empty((rows, (cols + 7) // 8), dtype=torch.uint16, device=src.device)
+    _lib.check(_lib.lib().t81_hip_tq1_quantize_rows(
+        src.data_ptr(), rows, cols, float(threshold),
+        s_in.data_ptr() if s_in is not None else None, s_out.data_ptr(), words.data_ptr(),
+        _stream()))
+    return s_out, words
+
+
+def dequant_rows_tq1_0(words: torch.Tensor, cols: int, scales: torch.Tensor) -> torch.Tensor:
+    """(rows, ceil(cols / 8)) uint16 words and per-row scales -> (rows, cols) float32
+    (dequantize_row_tq1_0, gguf_quants.h:146-168, on every row)."""
+    if not words.is_cuda:
+        words = words.to("cuda")
+    if words.dtype not in (torch.uint16, torch.int16) or words.ndim != 2:
+        raise ValueError("words must be a 2-D uint16 tensor")
+    words = words.contiguous()
+    rows = words.shape[0]
+    if words.shape[1] < (cols + 7) // 8:
+        raise ValueError("packed buffer too small for the requested column count")
+    if words.shape[1] != (cols + 7) // 8:
+        words = words[:, :(cols + 7) // 8].contiguous()
+    s = _cuda_f32(scales).reshape(-1)
+    if s.numel() != rows:
+        raise ValueError("scales must have one value per row")
+    out = torch.empty((rows, int(cols)), dtype=torch.float32, device=words.device)
+    _lib.check(_lib.lib().t81_hip_tq1_dequantize_rows(words.data_ptr(), rows, cols, s.data_ptr(),
+                                                      out.data_ptr(), _stream()))
+    return out
+
+
+def tq1_payload_bytes(rows: int, cols: int, block_rows: int = TQ1_BLOCK_ROWS,
+                      refinements: bool = False) -> int:
+    n = int(_lib.lib().t81_hip_tq1_payload_bytes(rows, cols, block_rows, int(refinements)))
+    if n < 0:
+        _lib.check(n)
+    return n
+
+
+def quantize_tq1_0_payload(matrix: torch.Tensor, block_rows: int = TQ1_BLOCK_ROWS,
+                           refinements: bool = False, threshold: float = 0.45) -> torch.Tensor:
+    """(rows, cols) floats -> the uint8 payload t81lib.dequant_tq1_0 (refinements False) or
+    dequant_tq2_0 (True) reads: per group of block_rows rows a float16 scale
+    h = half(max |v|), 8 zero bytes with refinements, then each row's words from
+    quantize_row_tq1_0 with the scale float(h).  The reference has no writer for this
+    payload; this one composes its row codec the way a caller of the binding would."""
+    src = _cuda_f32(matrix)
+    if src.ndim != 2:
+        raise ValueError("quantize_tq1_0_payload expects a 2-D tensor")
+    rows, cols = src.shape
+    out = torch.empty(tq1_payload_bytes(rows, cols, block_rows, refinements), dtype=torch.uint8,
+                      device=src.device)
+    _lib.check(_lib.lib().t81_hip_tq1_quantize_payload(src.data_ptr(), rows, cols, block_rows,
+                                                       int(refinements), float(threshold),
+                                                       out.data_ptr(), _stream()))
+    return out

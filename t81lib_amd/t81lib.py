@@ -1,8 +1,9 @@
 """The reference's ``t81lib`` extension-module surface for the packed path, on the GPU.
 
 Same names, argument meanings, defaults and exception types as the pybind11
-module (python/bindings.cpp:759-765 constants, :769-810 ``gemm_ternary``,
-:405-517 quantize/pack, :640-686 unpack, :888-940 ``spmm_simple``).  Arguments may be NumPy arrays /
+module (python/bindings.cpp:759-767 constants, :769-810 ``gemm_ternary``,
+:405-517 quantize/pack, :519-638 and :961-995 the TQ1_0 row codec, :640-686 unpack,
+:888-940 ``spmm_simple``).  Arguments may be NumPy arrays /
 buffers (copied to the GPU, results copied back -- the host-span contract of
 ``rocm_gemm_ternary``, src/linalg/gemm_rocm.cpp:335-396) or GPU torch tensors
 (used in place, no copies).  Every computation runs on the GPU; there is no
@@ -23,6 +24,8 @@ TRYTES_PER_LIMB = 16
 BYTES_PER_LIMB = 16
 HAS_CUDA_BACKEND = False
 HAS_METAL_BACKEND = False
+TQ1_TRITS_PER_BLOCK = 8   # src/t81/core/gguf_quants.h:14
+TQ1_BLOCK_ROWS = 32       # src/t81/core/gguf_quants.h:15
 
 
 def _has_rocm() -> bool:
@@ -153,6 +156,108 @@ def unpack_packed_limbs(packed: Any, rows: int, cols: int):
     return _return_like(ops.unpack(t, rows, cols), host)
 
 
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _tq1_words(cols: int) -> int:
+    return (int(cols) + TQ1_TRITS_PER_BLOCK - 1) // TQ1_TRITS_PER_BLOCK
+
+
+def _forcecast(obj: Any, np_dtype, t_dtype: torch.dtype) -> tuple[torch.Tensor, bool]:
+    """The array as a contiguous GPU tensor of the given type, converted the way pybind11's
+    forcecast converts (numpy's unsafe cast); (tensor, was_host)."""
+    if isinstance(obj, torch.Tensor) and obj.device.type == "cuda":
+        if obj.dtype != t_dtype:
+            if t_dtype == torch.uint16:
+                obj = (obj.to(torch.int64) & 0xFFFF).to(torch.int32).to(torch.uint16)
+            else:
+                obj = obj.to(t_dtype)
+        return obj.contiguous(), False
+    arr = obj.numpy() if isinstance(obj, torch.Tensor) else np.asarray(obj)
+    arr = np.ascontiguousarray(arr.astype(np_dtype, copy=False))
+    return torch.from_numpy(arr).to(device=_device()), True
+
+
+def quantize_row_tq1_0(row: Any, threshold: float = 0.45, scale: float = 0.0):
+    """One row of floats -> (scale, uint16 TQ1_0 words) (python/bindings.cpp:519-540 over
+    quantize_row_tq1_0, src/t81/core/gguf_quants.h:116-144).  The returned scale is the
+    argument when it is not <= 0 (a NaN argument is returned as given, while the words use
+    the row's max |v|, as the binding does), else the row's max |v|."""
+    t, host = _forcecast(row, np.float32, torch.float32)
+    if t.ndim != 1:
+        raise ValueError("quantize_row_tq1_0 requires a 1-D float array")
+    n = t.numel()
+    scale32 = float(np.float32(scale))
+    threshold32 = float(np.float32(threshold))
+    words = torch.empty(_tq1_words(n), dtype=torch.uint16, device=t.device)
+    if n == 0:
+        actual = 0.0 if scale32 <= 0.0 else scale32
+        return actual, _return_like(words, host)
+    s_in = torch.tensor([scale32], dtype=torch.float32, device=t.device)
+    s_out = torch.empty(1, dtype=torch.float32, device=t.device)
+    _lib.check(_lib.lib().t81_hip_tq1_quantize_rows(t.data_ptr(), 1, n, threshold32,
+                                                     s_in.data_ptr(), s_out.data_ptr(),
+                                                     words.data_ptr(), _stream()))
+    actual = float(s_out.item()) if scale32 <= 0.0 else scale32
+    return actual, _return_like(words, host)
+
+
+def dequant_row_tq1_0(blocks: Any, cols: int, scale: float):
+    """TQ1_0 words -> cols float32 values (python/bindings.cpp:542-559 over
+    dequantize_row_tq1_0, src/t81/core/gguf_quants.h:146-168)."""
+    if cols < 0:
+        raise ValueError("cols must be non-negative")
+    t, host = _forcecast(blocks, np.uint16, torch.uint16)
+    need = _tq1_words(cols)
+    if t.numel() < need:
+        raise ValueError("packed buffer too small for the requested column count")
+    out = torch.empty(int(cols), dtype=torch.float32, device=t.device)
+    if cols > 0:
+        s = torch.tensor([float(np.float32(scale))], dtype=torch.float32, device=t.device)
+        _lib.check(_lib.lib().t81_hip_tq1_dequantize_rows(t.reshape(-1).data_ptr(), 1, cols,
+                                                          s.data_ptr(), out.data_ptr(),
+                                                          _stream()))
+    return _return_like(out, host)
+
+
+def _payload_bytes(buffer: Any) -> tuple[torch.Tensor, bool]:
+    if isinstance(buffer, torch.Tensor):
+        if buffer.element_size() != 1:
+            raise ValueError("buffer must be observed as bytes")
+        t, host = _as_device(buffer, buffer.dtype)
+        return t.contiguous().reshape(-1).view(torch.uint8), host
+    view = memoryview(buffer)
+    if view.itemsize != 1:
+        raise ValueError("buffer must be observed as bytes")
+    arr = np.frombuffer(view.tobytes(), np.uint8)
+    return torch.from_numpy(arr.copy()).to(device=_device()), True
+
+
+def _dequant_tensor(buffer: Any, rows: int, cols: int, block_rows: int, refinements: bool):
+    if rows < 0 or cols < 0:
+        raise ValueError("rows and cols must be non-negative")
+    data, host = _payload_bytes(buffer)
+    out = torch.empty((int(rows), int(cols)), dtype=torch.float32, device=data.device)
+    _lib.check(_lib.lib().t81_hip_tq1_dequantize_payload(
+        data.data_ptr() if data.numel() else None, data.numel(), rows, cols, block_rows,
+        int(refinements), out.data_ptr() if out.numel() else None, _stream()))
+    return _return_like(out, host)
+
+
+def dequant_tq1_0(buffer: Any, rows: int, cols: int, block_rows: int = TQ1_BLOCK_ROWS):
+    """A whole TQ1_0 row-codec tensor payload -> (rows, cols) float32: per group of
+    block_rows rows a float16 scale, then the rows' words (python/bindings.cpp:561-638,
+    975-984)."""
+    return _dequant_tensor(buffer, rows, cols, block_rows, False)
+
+
+def dequant_tq2_0(buffer: Any, rows: int, cols: int, block_rows: int = TQ1_BLOCK_ROWS):
+    """As dequant_tq1_0 with 8 reserved refinement bytes after each group's scale, skipped
+    (python/bindings.cpp:986-995)."""
+    return _dequant_tensor(buffer, rows, cols, block_rows, True)
+
+
 def _float_span(obj: Any, count: int) -> tuple[torch.Tensor, Any]:
     """(GPU float32 tensor, host array to write back or None), with the buffer checks and
     messages of make_float_span (python/bindings.cpp:112-134), which the binding applies
@@ -213,5 +318,7 @@ def spmm_simple(values: Any, row_indices: Any, col_indices: Any, rows: int, cols
 __all__ = [
     "TRITS_PER_LIMB", "TRYTES_PER_LIMB", "BYTES_PER_LIMB", "HAS_CUDA_BACKEND",
     "HAS_METAL_BACKEND", "gemm_ternary", "quantize_to_trits", "dequantize_trits",
-    "pack_dense_matrix", "unpack_packed_limbs", "spmm_simple",
+    "pack_dense_matrix", "unpack_packed_limbs", "spmm_simple", "TQ1_TRITS_PER_BLOCK",
+    "TQ1_BLOCK_ROWS", "quantize_row_tq1_0", "dequant_row_tq1_0", "dequant_tq1_0",
+    "dequant_tq2_0",
 ]

@@ -24,6 +24,24 @@ source.  Vectors:
                              repeated entries, int64 values near +-2^63, NaN / inf /
                              denormal operands, beta == 0 over NaN, and out-of-range
                              indices (``_rc`` -1: C as the reference leaves it on throw)
+
+and tests/golden/tq1_row_vectors.npz (``tq1_main``), the TQ1_0 row codec of
+src/t81/core/gguf_quants.h compiled as it stands:
+
+* ``q_*``   quantize_row_tq1_0 on ragged rows with NaN / +-inf / -0.0 / denormal values,
+            values at +-threshold * scale and one ulp either side, thresholds outside
+            [0, 0.9999] and NaN, supplied scales 0 / negative / NaN / inf / denormal; the
+            returned scale follows the binding (python/bindings.cpp:531-539)
+* ``d_*``   dequantize_row_tq1_0: the trits of every word 0 .. 65535 (the low 8 base-3
+            digits of an out-of-range word), and 2048 words at scales 0, -0, +-1.5,
+            +-inf, NaN, denormal, 3e38
+* ``h_*``   half_to_float on all 65536 half patterns
+* ``p_*``   tensor payloads (groups of block_rows rows: a half scale, 8 reserved bytes for
+            the TQ2_0 variant, the rows' words) decoded row by row with the compiled
+            dequantize_row_tq1_0 and half_to_float; the framing and its truncation checks
+            follow python/bindings.cpp:561-638 (that file needs pybind11 and is not built
+            here), ``p_rc`` naming the first failing check (1 scale, 2 reserved bytes,
+            3 rows) of payloads cut short
 """
 
 from __future__ import annotations
@@ -201,5 +219,125 @@ def main() -> None:
     print(f"wrote {path} ({os.path.getsize(path)} bytes, SIMD path {ref.simd_path()})")
 
 
+def tq1_quantize_cases():
+    """(threshold, scale, values) for quantize_row_tq1_0."""
+    g = np.random.default_rng(1081)
+    f32 = np.float32
+    cases = []
+    for n in (1, 7, 8, 9, 15, 16, 17, 33, 100, 257, 1000):
+        cases.append((0.45, 0.0, g.standard_normal(n).astype(f32)))
+    v = g.standard_normal(64).astype(f32)
+    for thr in (0.5, 0.0, -0.3, -0.0, 0.9999, 1.0, 1.5, np.nan, 1e-8, 0.45000002):
+        cases.append((thr, 0.0, v))
+    for sc in (-1.0, 2.5, np.nan, np.inf, 1e-40, 1e-30, 0.37):
+        cases.append((0.45, sc, v))
+    # values at +-threshold (scale 1) and one ulp either side
+    t = f32(0.45)
+    edge = np.array([t, -t, np.nextafter(t, f32(1)), np.nextafter(t, f32(0)),
+                     -np.nextafter(t, f32(1)), -np.nextafter(t, f32(0)), 1.0, -1.0,
+                     1.5, -7.0, 0.0, -0.0], f32)
+    cases.append((0.45, 1.0, edge))
+    cases.append((0.45, 0.0, np.concatenate([edge, np.array([1.0], f32)])))
+    sp = np.array([np.nan, np.inf, -np.inf, -0.0, 0.0, 1e-45, -1e-40, 3e38, -3e38, 0.5, -0.5,
+                   np.nan, 2.0, -2.0, 1e-38, 0.25, 0.75], f32)
+    for sc in (0.0, 1.0, np.inf):
+        cases.append((0.45, sc, sp))
+    cases.append((0.45, 0.0, np.array([np.nan, np.nan, 0.0, -0.0], f32)))   # scale 0
+    cases.append((0.45, 0.0, np.zeros(20, f32)))
+    cases.append((0.45, 0.0, np.array([1e-42, -3e-43, 0.0, 1e-44, -1e-42], f32)))  # denormal max
+    cases.append((0.3, 0.0, (g.standard_normal(333) * 1e-3).astype(f32)))
+    return cases
+
+
+def tq1_main() -> None:
+    ref = oracle.ref("generic")
+    if ref is None:
+        raise SystemExit("oracle/_ref/libt81ref_generic.so is not built (needs /root/reference)")
+    out: dict[str, np.ndarray] = {}
+    # quantize: values concatenated, offsets per case
+    qs = tq1_quantize_cases()
+    vals, offs, woffs, words, thr, sc, ret = [], [0], [0], [], [], [], []
+    for t, s_, v in qs:
+        w = ref.tq1_quantize_row(v, t, s_)
+        s32 = np.float32(s_)
+        ret.append(s32 if not s32 <= 0 else np.float32(ref.tq1_compute_scale(v)))
+        vals.append(v)
+        offs.append(offs[-1] + v.size)
+        words.append(w)
+        woffs.append(woffs[-1] + w.size)
+        thr.append(t)
+        sc.append(s_)
+    out.update(q_values=np.concatenate(vals), q_offsets=np.array(offs, np.int64),
+               q_words=np.concatenate(words), q_word_offsets=np.array(woffs, np.int64),
+               q_threshold=np.array(thr, np.float32), q_scale=np.array(sc, np.float32),
+               q_returned_scale=np.array(ret, np.float32))
+    # dequantize: the trits of every word (scale 1), and a sample of words at each scale
+    all_words = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    out["d_trits"] = ref.tq1_dequantize_row(all_words, 8 * 65536, 1.0).astype(np.int8)
+    sample = np.concatenate([np.arange(1024), np.random.default_rng(1083).integers(
+        1024, 65536, 1024)]).astype(np.uint16)
+    scales = np.array([0.0, -0.0, 1.5, -1.5, np.inf, -np.inf, np.nan, 1e-42, 3e38], np.float32)
+    out["d_words"] = sample
+    out["d_scales"] = scales
+    out["d_values"] = np.stack([ref.tq1_dequantize_row(sample, 8 * sample.size, float(s_))
+                                for s_ in scales])
+    ragged = []
+    for n in (0, 1, 5, 8, 13, 100):
+        ragged.append(ref.tq1_dequantize_row(all_words[:64], n, 1.25))
+    out["d_ragged"] = np.concatenate(ragged)
+    out["h_values"] = np.array([ref.tq1_half_to_float(h) for h in range(65536)], np.float32)
+    # tensor payloads written with the row codec, decoded with the compiled row decoder
+    g = np.random.default_rng(1082)
+    pay, poffs, pmeta, pvals, pvoffs = [], [0], [], [], [0]
+    for rows, cols, block_rows, refine in ((5, 13, 32, 0), (70, 100, 32, 1), (33, 8, 7, 0),
+                                           (9, 1, 1, 1), (4, 17, 0, 0), (6, 40, -5, 1),
+                                           (3, 24, 1000, 0), (0, 10, 32, 0), (4, 0, 2, 1),
+                                           (40, 16, 32, 0)):
+        m = g.standard_normal((rows, cols)).astype(np.float32)
+        if rows > 3 and cols:
+            m[3] *= 1e-9                                  # a tiny row in a big group
+        buf = bytearray(oracle.tq1r_payload(m, block_rows, bool(refine)))
+        group = max(1, block_rows)
+        stride = 2 + 8 * refine + 2 * ((cols + 7) // 8) * group
+        if rows >= 9 and len(buf) > stride:              # crafted scales: NaN, inf, subnormal
+            for gi, h in enumerate((0x7E01, 0xFC00, 0x0003)):
+                if gi * stride + 1 < len(buf):
+                    buf[gi * stride:gi * stride + 2] = np.array([h], np.uint16).tobytes()
+        want = np.zeros((rows, cols), np.float32)
+        wpr = (cols + 7) // 8
+        for r in range(rows):
+            gi, i = divmod(r, group)
+            o = gi * stride
+            h = int(np.frombuffer(bytes(buf[o:o + 2]), np.uint16)[0])
+            ro = o + 2 + 8 * refine + i * 2 * wpr
+            wr = np.frombuffer(bytes(buf[ro:ro + 2 * wpr]), np.uint16)
+            want[r] = ref.tq1_dequantize_row(wr, cols, float(ref.tq1_half_to_float(h)))
+        pay.append(np.frombuffer(bytes(buf), np.uint8))
+        poffs.append(poffs[-1] + len(buf))
+        pmeta.append((rows, cols, block_rows, refine))
+        pvals.append(want.reshape(-1))
+        pvoffs.append(pvoffs[-1] + want.size)
+    out.update(p_bytes=np.concatenate(pay), p_offsets=np.array(poffs, np.int64),
+               p_meta=np.array(pmeta, np.int64), p_values=np.concatenate(pvals),
+               p_value_offsets=np.array(pvoffs, np.int64))
+    # truncated payloads: (case index, length) -> the first failing check
+    cuts = []
+    for ci, (rows, cols, block_rows, refine) in enumerate(pmeta):
+        full = poffs[ci + 1] - poffs[ci]
+        for cut in sorted({0, 1, 2, 3, 9, 10, 11, full // 2, full - 1}):
+            if 0 <= cut < full:
+                rc, _ = oracle.tq1r_dequant_tensor(bytes(pay[ci][:cut]), rows, cols, block_rows,
+                                                   bool(refine))
+                cuts.append((ci, cut, rc))
+    out["p_cuts"] = np.array(cuts, np.int64)
+    path = os.path.join(HERE, "tq1_row_vectors.npz")
+    np.savez_compressed(path, **out)
+    print(f"wrote {path} ({os.path.getsize(path)} bytes)")
+
+
 if __name__ == "__main__":
-    main()
+    if len(sys.argv) > 1 and sys.argv[1] == "tq1":
+        tq1_main()
+    else:
+        main()
+        tq1_main()

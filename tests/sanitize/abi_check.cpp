@@ -231,6 +231,56 @@ int main() {
     expect("tq2_matmul negative", t81_hip_tq2_matmul(p, 1, u8, f, kMin, 4, 256, 1, 0, nullptr, nullptr),
            {T81_HIP_EINVAL_SHAPE});
 
+    // ---- TQ1_0 row codec and its tensor payload ----
+    auto *u16 = reinterpret_cast<uint16_t *>(buf);
+    expect("tq1 rows negative", t81_hip_tq1_quantize_rows(f, kMin, 8, 0.45f, nullptr, nullptr, u16,
+                                                          nullptr),
+           {T81_HIP_EINVAL_SHAPE}, "non-negative");
+    expect("tq1 rows huge", t81_hip_tq1_quantize_rows(f, kMax, kMax, 0.45f, nullptr, nullptr, u16,
+                                                      nullptr),
+           {T81_HIP_EINVAL_SHAPE}, "too large");
+    expect("tq1 rows null", t81_hip_tq1_quantize_rows(nullptr, 2, 8, 0.45f, nullptr, nullptr, u16,
+                                                      nullptr),
+           {T81_HIP_EINVAL_POINTER});
+    expect("tq1 rows align", t81_hip_tq1_quantize_rows(f, 2, 8, 0.45f, nullptr, nullptr,
+                                                       reinterpret_cast<uint16_t *>(buf + 1),
+                                                       nullptr),
+           {T81_HIP_EINVAL_POINTER});
+    expect("tq1 dequant negative", t81_hip_tq1_dequantize_rows(u16, 1, kMin, f, f, nullptr),
+           {T81_HIP_EINVAL_SHAPE}, "non-negative");
+    expect("tq1 dequant null scales", t81_hip_tq1_dequantize_rows(u16, 1, 8, nullptr, f, nullptr),
+           {T81_HIP_EINVAL_POINTER});
+    if (t81_hip_tq1_payload_bytes(5, 13, 32, 0) != 2 + 5 * 4 ||
+        t81_hip_tq1_payload_bytes(70, 100, 32, 1) != 3 * 10 + 70 * 26 ||
+        t81_hip_tq1_payload_bytes(3, 8, kMin, 0) != 3 * 4 || t81_hip_tq1_payload_bytes(0, 8, 1, 1) != 0 ||
+        t81_hip_tq1_payload_bytes(2, 8, kMax, 1) != 10 + 2 * 2) {
+        ++g_failures;
+        std::fprintf(stderr, "FAIL tq1_payload_bytes values\n");
+    }
+    expect("tq1 payload bytes huge",
+           static_cast<int>(t81_hip_tq1_payload_bytes(kMax, kMax, kMax, 1)), {T81_HIP_EINVAL_SHAPE});
+    expect("tq1 payload scale", t81_hip_tq1_dequantize_payload(u8, 1, 4, 8, 2, 0, f, nullptr),
+           {T81_HIP_EINVAL_SHAPE}, "buffer truncated while reading scale");
+    expect("tq1 payload refinements", t81_hip_tq1_dequantize_payload(u8, 9, 4, 8, 2, 1, f, nullptr),
+           {T81_HIP_EINVAL_SHAPE}, "buffer truncated while skipping refinement bytes");
+    expect("tq1 payload rows", t81_hip_tq1_dequantize_payload(u8, 13, 4, 8, 2, 1, f, nullptr),
+           {T81_HIP_EINVAL_SHAPE}, "buffer truncated while reading quantized rows");
+    expect("tq1 payload second scale", t81_hip_tq1_dequantize_payload(u8, 6, 4, 8, 2, 0, f, nullptr),
+           {T81_HIP_EINVAL_SHAPE}, "buffer truncated while reading scale");
+    expect("tq1 payload extreme group", t81_hip_tq1_dequantize_payload(u8, 3, 4, 8, kMax, 0, f, nullptr),
+           {T81_HIP_EINVAL_SHAPE}, "buffer truncated while reading quantized rows");
+    expect("tq1 payload negative", t81_hip_tq1_dequantize_payload(u8, 64, kMin, 8, 2, 0, f, nullptr),
+           {T81_HIP_EINVAL_SHAPE}, "non-negative");
+    expect("tq1 payload huge", t81_hip_tq1_dequantize_payload(u8, kMax, kMax, kMax, kMin, 1, f, nullptr),
+           {T81_HIP_EINVAL_SHAPE}, "too large");
+    expect("tq1 payload null", t81_hip_tq1_dequantize_payload(nullptr, 4, 1, 8, 2, 0, f, nullptr),
+           {T81_HIP_EINVAL_POINTER});
+    expect("tq1 payload writer negative",
+           t81_hip_tq1_quantize_payload(f, kMin, 4, 32, 0, 0.45f, u8, nullptr), {T81_HIP_EINVAL_SHAPE});
+    expect("tq1 payload writer null",
+           t81_hip_tq1_quantize_payload(f, 2, 4, 32, 0, 0.45f, nullptr, nullptr),
+           {T81_HIP_EINVAL_POINTER});
+
     // ---- sparse ----
     t81_hip_spmm_plan *plan = nullptr;
     int64_t bad = 0;

@@ -160,3 +160,163 @@ def test_tq2_matmul_closed_form():
     y, scale = oracle.tq2_matmul_f64(x, packed, 600)
     np.testing.assert_allclose(y, x @ dense.T, rtol=1e-12, atol=1e-9)
     np.testing.assert_allclose(scale, np.abs(x) @ np.abs(dense).T, rtol=1e-12)
+
+
+# ---------------------------------------------- TQ1_0 row codec (gguf_quants.h) --
+TQ1R = __import__("os").path.join(__import__("os").path.dirname(__file__), "golden",
+                                  "tq1_row_vectors.npz")
+
+
+@pytest.fixture(scope="module")
+def tq1g():
+    return np.load(TQ1R)
+
+
+def _cases(g, prefix, key, okey):
+    offs = g[f"{prefix}_{okey}"]
+    arr = g[f"{prefix}_{key}"]
+    return [arr[offs[i]:offs[i + 1]] for i in range(offs.size - 1)]
+
+
+def _same_bits(a, b) -> bool:
+    a = np.asarray(a, np.float32)
+    b = np.asarray(b, np.float32)
+    return bool(((a.view(np.uint32) == b.view(np.uint32)) | (np.isnan(a) & np.isnan(b))).all())
+
+
+def test_tq1r_constants():
+    assert oracle.TQ1_TRITS_PER_BLOCK == 8 and oracle.TQ1_BLOCK_ROWS == 32  # gguf_quants.h:14-15
+    assert oracle.tq1r_words(0) == 0 and oracle.tq1r_words(8) == 1 and oracle.tq1r_words(9) == 2
+
+
+def test_tq1r_quantize_golden(tq1g):
+    vals = _cases(tq1g, "q", "values", "offsets")
+    words = _cases(tq1g, "q", "words", "word_offsets")
+    for i, (v, w) in enumerate(zip(vals, words)):
+        thr, sc = float(tq1g["q_threshold"][i]), float(tq1g["q_scale"][i])
+        used, got = oracle.tq1r_quantize_row(v, thr, sc)
+        np.testing.assert_array_equal(got, w, err_msg=f"case {i} thr={thr} scale={sc}")
+        # the binding returns the argument unless it is <= 0 (NaN is returned as given)
+        s32 = np.float32(sc)
+        ret = s32 if not s32 <= 0 else np.float32(oracle.tq1r_scale(v))
+        assert _same_bits(ret, tq1g["q_returned_scale"][i])
+        if s32 <= 0 or np.isnan(s32):
+            assert _same_bits(used, oracle.tq1r_scale(v))
+
+
+def test_tq1r_dequantize_golden(tq1g):
+    words = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    trits = oracle.tq1r_dequantize_row(words, 8 * 65536, 1.0)
+    np.testing.assert_array_equal(trits.astype(np.int8), tq1g["d_trits"])
+    for s_, want in zip(tq1g["d_scales"], tq1g["d_values"]):
+        got = oracle.tq1r_dequantize_row(tq1g["d_words"], 8 * tq1g["d_words"].size, float(s_))
+        assert _same_bits(got, want), f"scale {s_}"
+    ragged = [oracle.tq1r_dequantize_row(words[:64], n, 1.25) for n in (0, 1, 5, 8, 13, 100)]
+    np.testing.assert_array_equal(np.concatenate(ragged), tq1g["d_ragged"])
+
+
+def test_tq1r_half_to_float_golden_and_numpy(tq1g):
+    halfs = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = np.array([oracle.f16_bits_to_f32(h) for h in halfs], np.float32)
+    # (NaN compared as NaN: a float returned through ctypes passes a double, which quiets
+    # a signalling NaN on the way)
+    assert _same_bits(got, tq1g["h_values"])
+    fin = ~np.isnan(got)
+    np.testing.assert_array_equal(got[fin], halfs.view(np.float16).astype(np.float32)[fin])
+
+
+def _payload_cases(g):
+    pays = _cases(g, "p", "bytes", "offsets")
+    vals = _cases(g, "p", "values", "value_offsets")
+    return [(tuple(int(v) for v in m), p, v) for m, p, v in zip(g["p_meta"], pays, vals)]
+
+
+def test_tq1r_payload_golden(tq1g):
+    for (rows, cols, block_rows, refine), pay, want in _payload_cases(tq1g):
+        rc, got = oracle.tq1r_dequant_tensor(pay.tobytes(), rows, cols, block_rows, bool(refine))
+        assert rc == 0
+        assert _same_bits(got.reshape(-1), want), (rows, cols, block_rows, refine)
+    cases = _payload_cases(tq1g)
+    for ci, cut, rc_want in tq1g["p_cuts"]:
+        (rows, cols, block_rows, refine), pay, _ = cases[ci]
+        rc, _ = oracle.tq1r_dequant_tensor(pay[:cut].tobytes(), rows, cols, block_rows,
+                                           bool(refine))
+        assert rc == rc_want, (ci, cut)
+
+
+class _ShortRead(Exception):
+    pass
+
+
+def _stream_decode(buf: bytes, rows: int, cols: int, block_rows: int, refine: bool) -> int:
+    """A brute-force reader that consumes the payload field by field, in the order the
+    binding's loop reads it (python/bindings.cpp:596-635), and reports the kind of the
+    first field it cannot read in full: 1 scale, 2 reserved bytes, 3 a row."""
+    import io
+
+    f = io.BytesIO(buf)
+
+    def take(n, kind):
+        if len(f.read(n)) != n:
+            raise _ShortRead(kind)
+
+    group = max(1, block_rows)
+    done = 0
+    try:
+        while done < rows:
+            take(2, 1)
+            if refine:
+                take(8, 2)
+            for _ in range(min(group, rows - done)):
+                take(2 * ((cols + 7) // 8), 3)
+                done += 1
+    except _ShortRead as e:
+        return int(e.args[0])
+    return 0
+
+
+@pytest.mark.parametrize("rows,cols,block_rows,refine", [
+    (5, 13, 32, 0), (70, 100, 32, 1), (33, 8, 7, 0), (9, 1, 1, 1), (4, 0, 2, 1), (6, 40, -5, 1),
+    (3, 24, 1000, 0), (1, 17, 32, 1)])
+def test_tq1r_truncation_every_cut(rows, cols, block_rows, refine):
+    m = np.random.default_rng(rows * cols + 1).standard_normal((rows, cols)).astype(np.float32)
+    pay = oracle.tq1r_payload(m, block_rows, bool(refine))
+    for cut in range(len(pay) + 1):
+        rc, _ = oracle.tq1r_dequant_tensor(pay[:cut], rows, cols, block_rows, bool(refine))
+        assert rc == _stream_decode(pay[:cut], rows, cols, block_rows, bool(refine)), cut
+    assert oracle.tq1r_dequant_tensor(b"", -1, 3)[0] == -1
+
+
+def test_tq1r_word_code_closed_form():
+    """Every digit pattern of 8 trits round-trips, the word equals sum_i d_i 3^i with
+    d = {+1: 0, 0: 1, -1: 2}, and the 6561 valid words are a bijection."""
+    digits = np.array(np.meshgrid(*[np.arange(3)] * 8, indexing="ij")).reshape(8, -1).T
+    trits = np.where(digits == 0, 1, np.where(digits == 2, -1, 0)).astype(np.float32)
+    words = np.empty(len(trits), np.uint16)
+    for i, t in enumerate(trits):
+        used, w = oracle.tq1r_quantize_row(t, 0.45, 1.0)
+        words[i] = w[0]
+    np.testing.assert_array_equal(words, (digits * 3 ** np.arange(8)).sum(1))
+    assert np.unique(words).size == 6561 and words.max() == 6560
+    back = oracle.tq1r_dequantize_row(words, 8 * words.size, 1.0).reshape(-1, 8)
+    np.testing.assert_array_equal(back, trits)
+
+
+@pytest.mark.skipif("not __import__('oracle').ref()", reason="oracle/_ref not built here")
+def test_tq1r_matches_compiled_reference_live():
+    ref = oracle.ref()
+    g = np.random.default_rng(7)
+    specials = np.array([np.nan, np.inf, -np.inf, -0.0, 1e-45, -1e-40, 3e38], np.float32)
+    for i in range(300):
+        n = int(g.integers(0, 90))
+        v = (g.standard_normal(n) * 10.0 ** g.integers(-6, 3)).astype(np.float32)
+        if n and i % 3 == 0:
+            v[g.integers(0, n, 3)] = g.choice(specials, 3)
+        thr = float(g.choice([0.45, 0.5, 0.0, 1.2, -0.1, np.nan, g.random()]))
+        sc = float(g.choice([0.0, -1.0, np.nan, np.inf, 1e-40, g.random() * 3]))
+        np.testing.assert_array_equal(oracle.tq1r_quantize_row(v, thr, sc)[1],
+                                      ref.tq1_quantize_row(v, thr, sc), err_msg=f"case {i}")
+        assert _same_bits(oracle.tq1r_scale(v), ref.tq1_compute_scale(v))
+        w = g.integers(0, 65536, oracle.tq1r_words(n)).astype(np.uint16)
+        s_ = float(g.choice([0.0, -0.0, 1.0, -2.5, np.inf, np.nan, 1e-42, g.standard_normal()]))
+        assert _same_bits(oracle.tq1r_dequantize_row(w, n, s_), ref.tq1_dequantize_row(w, n, s_))
