@@ -70,7 +70,8 @@ def time_graph(torch, launch, buffers, steps: int, warmup: int, dist: bool = Fal
     HIP graphs so the GPU runs them back to back on one stream: a graph of one launch per
     buffer (replayed steps // len(buffers) times) plus one of the remaining launches.
     `warmup` untimed launches (whole rotations) run first, then a synchronisation, then one
-    more untimed rotation ahead of the start event; the timed region ends with a
+    more untimed rotation ahead of the start event (the graph of the remaining launches is
+    replayed once untimed too, so no timed replay is a first one); the timed region ends with a
     synchronisation and is timed with HIP events on the launch stream.  Returns ms per
     launch; with dist=True a dict that adds the spread: each replay of the rotation graph
     timed on its own, over at least `min_launches` launches and `min_ms` of GPU time
@@ -90,6 +91,8 @@ def time_graph(torch, launch, buffers, steps: int, warmup: int, dist: bool = Fal
     torch.cuda.synchronize()
     for _ in range(-(-warmup // n)):
         full.replay()
+    if rest is not None:          # the partial graph's first replay is not timed either
+        rest.replay()
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
@@ -533,7 +536,7 @@ DECODE_SHAPES = [("phi3.qkv", 3072, 9216), ("phi3.o", 3072, 3072), ("phi3.gate_u
                  ("llama.down", 14336, 4096)]
 
 
-def run_decode(torch, ops, lib, dev) -> dict:
+def run_decode(torch, ops, lib, dev, only_case=None) -> dict:
     """Config 3 (Phi-3 decode shapes) and the Llama-3-8B gate / down shapes at 1, 4, 8 and
     16 tokens, and at 32 (config 5's decode batch) and 48, through the product path
     (ops.ternary_matmul: K2 up to 16 tokens, with the workspace its K splits use; the K3
@@ -542,12 +545,13 @@ def run_decode(torch, ops, lib, dev) -> dict:
     per call over rotating weight copies (> 2 x MALL, so every call streams from HBM), GB/s
     of algorithmic bytes, and each shape's 16-token time over its one-token time."""
     shapes = {}
-    for name, k, n in DECODE_SHAPES:
+    todo = DECODE_SHAPES if only_case is None else [("case", only_case[0], only_case[1])]
+    for name, k, n in todo:
         wbytes = 16 * n * ((k + 47) // 48)
         copies = max(4, -(-2 * MALL_BYTES // wbytes) + 2)
         wb = make_weights(torch, ops, lib, n, k, copies, dev, seed=3)
         row = {"K": k, "N": n}
-        for m in (1, 4, 8, 16, 32, 48):
+        for m in ((1, 4, 8, 16, 32, 48) if only_case is None else (only_case[2],)):
             x = torch.randn((m, k), device=dev).to(torch.bfloat16)
             out = torch.empty((m, n), device=dev)
             d = time_graph(torch, lambda w: ops.ternary_matmul(x, w, k, c=out), wb, 256, 32,
@@ -557,7 +561,8 @@ def run_decode(torch, ops, lib, dev) -> dict:
             row[f"M{m}_GBps"] = round(gemv_bytes(m, n, k) / (us * 1e-6) / 1e9, 1)
             log(f"decode {name:13s} M={m:2d} {k:5d}->{n:5d}: {us:7.2f} us")
             del x, out
-        row["M16_over_M1"] = round(row["M16_us"] / row["M1_us"], 3)
+        if only_case is None:
+            row["M16_over_M1"] = round(row["M16_us"] / row["M1_us"], 3)
         shapes[name] = row
         del wb
         torch.cuda.empty_cache()
@@ -566,6 +571,97 @@ def run_decode(torch, ops, lib, dev) -> dict:
                         "bf16 x, fp32 out, alpha=1 beta=0, median over rotating weight copies; "
                         "config 3 (Phi-3) plus the Llama-3-8B gate / down shapes",
             "shapes": shapes}
+
+
+PREFILL_SHAPES = [("llama.qkv", 4096, 6144), ("llama.gate_up", 4096, 28672),
+                  ("llama.down", 14336, 4096)]
+
+
+def run_prefill(torch, ops, lib, dev) -> dict:
+    """Config 4: the three Llama-3-8B prefill shapes at M = 512, 2048 and 8192 tokens, bf16
+    activations ~ N(0,1), with (alpha, beta) = (1, 0) and (0.5, 1) over a float32 C ~ N(0,1)
+    (read and written in place), through the product path (ops.ternary_matmul with its
+    workspace): exactly 100 timed launches after 20 untimed ones, over two weight copies,
+    plus >= 50 ms of spread samples.  TFLOP/s of 2 M N K and the fraction of the bf16
+    matrix-core peak, from the mean over the 100 timed launches (median alongside)."""
+    cases = []
+    for name, k, n in PREFILL_SHAPES:
+        wb = make_weights(torch, ops, lib, n, k, 2, dev, seed=4)
+        for m in (512, 2048, 8192):
+            x = torch.randn((m, k), device=dev).to(torch.bfloat16)
+            c = torch.randn((m, n), device=dev)
+            for alpha, beta in ((1.0, 0.0), (0.5, 1.0)):
+                d = time_graph(torch, lambda w: ops.ternary_matmul(x, w, k, alpha=alpha, beta=beta,
+                                                                   c=c), wb, 100, 20, dist=True)
+                flops = 2.0 * m * n * k
+                tf = flops / (d["ms"] * 1e-3) / 1e12
+                cases.append({"shape": name, "M": m, "K": k, "N": n, "alpha": alpha, "beta": beta,
+                              "ms": round(d["ms"], 5), "median_ms": round(d["median_ms"], 5),
+                              "timed_launches": d["timed_launches"], "tflops": round(tf, 1),
+                              "frac": round(tf / BF16_PEAK_TFLOPS, 4),
+                              "tokens_per_s_equiv": round(m / (d["ms"] * 1e-3))})
+                log(f"prefill {name:14s} M={m:5d} a={alpha} b={beta}: {d['ms'] * 1e3:8.1f} us "
+                    f"(median {d['median_ms'] * 1e3:8.1f})  {tf:7.1f} TFLOP/s  "
+                    f"{tf / BF16_PEAK_TFLOPS:.3f}")
+            del x, c
+        del wb
+        torch.cuda.empty_cache()
+    return {"workload": "config 4: K3 prefill GEMM on the Llama-3-8B qkv / gate_up / down shapes "
+                        "at M = 512, 2048, 8192, bf16 x, fp32 C, (alpha, beta) = (1, 0) and "
+                        "(0.5, 1); 100 timed launches each",
+            "peak_tflops": BF16_PEAK_TFLOPS, "cases": cases}
+
+
+def run_limb(torch, ops, lib, dev, cpu_budget: float, with_cpu: bool) -> dict:
+    """Config 1, the reference's own CPU case: gemm_ternary_cpu_impl's shape with the limb GEMM
+    K4 (A = W as 1024 x 22 limbs, B = the column-packed activations 22 x 64, C 1024 x 64,
+    alpha 1, beta 0): limb products per second over 100 timed launches, and the compiled
+    reference timed on the same product in the same run."""
+    M, N, K = 1024, 64, 1024
+    kl = (K + 47) // 48
+    A = make_weights(torch, ops, lib, M, K, 2, dev, seed=7)
+    x = torch.randn((N, K), device=dev)
+    B = ops.pack_cols(x, 0.5, lib.THR_TORCH)
+    C = torch.zeros((M, N), device=dev)
+    d = time_graph(torch, lambda a: ops.gemm_limb(a, B, C, M, N, kl * 48), A, 100, 10, dist=True)
+    products = M * N * kl
+    out = {"workload": "config 1: K4 limb GEMM in gemm_ternary_cpu_impl's orientation, A = W "
+                       "1024 x 22 limbs (from_float at 0.45 of W/0.02), B = X^T 22 x 64 limbs "
+                       "(quantized at 0.5, column-packed), C 1024 x 64 fp32, alpha 1 beta 0",
+           "us": d["ms"] * 1e3, "timed_launches": d["timed_launches"],
+           "limb_products_per_s": products / (d["ms"] * 1e-3), "limb_products": products,
+           "timing": spread_us(d)}
+    if with_cpu:
+        import numpy as np
+
+        r, kind = _reference_lib()
+        a_np, b_np = A[0].cpu().numpy(), B.cpu().numpy()
+        times = []
+        for _ in range(3):
+            c0 = np.zeros((M, N), np.float32)
+            t0 = time.perf_counter()
+            if r is not None:
+                r.gemm_ternary(a_np, b_np, c0, M, N, kl * 48)
+            else:
+                import oracle
+
+                oracle.gemm_limb(a_np, b_np, c0, M, N, kl * 48)
+            times.append(time.perf_counter() - t0)
+            if sum(times) > cpu_budget:
+                break
+        sec = float(np.median(times))
+        what = (f"the compiled reference gemm_ternary_cpu_impl ({r.variant}, SIMD "
+                f"{r.simd_path()})" if r is not None else
+                "the oracle's C restatement of gemm_ternary_cpu_impl")
+        out["cpu_baseline"] = {
+            "value": products / sec, "unit": "limb products/s", "cores": 1, "kind": kind,
+            "sample": f"{what} on the whole config-1 product ({products} limb products), "
+                      f"median of {len(times)}: {sec:.2f} s"}
+    log(f"limb GEMM config 1: {out['us']:.1f} us, "
+        f"{out['limb_products_per_s'] / 1e9:.2f} G limb products/s")
+    del A, B, C, x
+    torch.cuda.empty_cache()
+    return out
 
 
 def run_backward(torch, ops, lib, dev) -> list:
@@ -827,14 +923,26 @@ def read_traffic(path: str = TRAFFIC_FILE):
 
 
 def cpu_model() -> str:
+    """The host CPU as /proc/cpuinfo names it: model name, vendor, family / model /
+    stepping numbers and the SIMD extensions the reference path can use."""
+    fields = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                if ":" not in line:
+                    if fields:
+                        break          # the first processor's block is enough
+                    continue
+                key, val = (p.strip() for p in line.split(":", 1))
+                fields.setdefault(key, val)
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    flags = fields.get("flags", "").split()
+    simd = [f for f in ("avx2", "avx512f", "avx512bw", "avx512_vnni", "avx512_bf16") if f in flags]
+    return (f"{fields.get('model name', 'unknown')} ({fields.get('vendor_id', '?')}, family "
+            f"{fields.get('cpu family', '?')} model {fields.get('model', '?')} stepping "
+            f"{fields.get('stepping', '?')}, {fields.get('cache size', '?')} cache, "
+            f"{' '.join(simd) or 'no avx2'})")
 
 
 def main() -> int:
@@ -846,7 +954,8 @@ def main() -> int:
                     help="seconds of single-core reference CPU work for the baseline")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", choices=["gemv", "gemm", "pack", "copy", "read", "spmm", "launch",
-                                       "stack", "decode", "backward"],
+                                       "stack", "decode", "backward", "prefill", "limb",
+                                       "pack3072"],
                     default=None,
                     help="time one kernel only (for profiling runs); 'copy' times a plain "
                          "elementwise copy of the GEMV weight size, the calibration kernel "
@@ -855,6 +964,8 @@ def main() -> int:
                          "per-launch floor of a graph of back-to-back kernels; 'stack' runs "
                          "config 5, the 32-layer decoder, prefill + greedy decode tokens/s; "
                          "'backward' the transposed limbs and dx = dy T of the Llama gate layer")
+    ap.add_argument("--decode-case", nargs=3, type=int, metavar=("K", "N", "M"), default=None,
+                    help="with --only decode: time this one shape and token count only")
     ap.add_argument("--no-stack", action="store_true",
                     help="skip config 5 (the decoder stack) in the default run")
     ap.add_argument("--sweep", action="store_true",
@@ -873,6 +984,9 @@ def main() -> int:
     ap.add_argument("--summarize-traffic", nargs=4, metavar=("KFETCH", "KWRITE", "CFETCH", "CWRITE"),
                     help="print calibrated HBM bytes per GEMV launch from rocprofv3 --pmc "
                          "FETCH_SIZE / WRITE_SIZE runs of the GEMV and of the copy, and exit")
+    ap.add_argument("--traffic-kernel", choices=["gemv", "pack"], default="gemv",
+                    help="with --summarize-traffic: the K2 headline launch (gemv) or K1 on "
+                         "8192 x 3072 (pack, from --only pack runs)")
     ap.add_argument("--cmd", action="append", default=[],
                     help="command line(s) that produced the profile, for the summary")
     args = ap.parse_args()
@@ -889,8 +1003,12 @@ def main() -> int:
     if args.summarize_traffic:
         K, N = 4096, 14336
         wb = 16 * N * ((K + 47) // 48)
-        sys.stdout.write(summarize_traffic("gemv", *args.summarize_traffic, copy_bytes=wb,
-                                           algo_bytes=gemv_bytes(1, N, K), cmds=args.cmd))
+        if args.traffic_kernel == "pack":
+            kernel, algo = "quantize_pack_rows_kernel", 4 * 8192 * 3072 + 16 * 8192 * 64
+        else:
+            kernel, algo = "gemv", gemv_bytes(1, N, K)
+        sys.stdout.write(summarize_traffic(kernel, *args.summarize_traffic, copy_bytes=wb,
+                                           algo_bytes=algo, cmds=args.cmd))
         return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the packed-ternary path is a single-GPU kernel set "
@@ -1016,19 +1134,34 @@ def main() -> int:
             f"(median {gemm_i8['median_ms']:.3f})")
 
     # ------------------------------------------------------------- K1 pack --
+    # config 2: W ~ N(0, 0.02) with 1 % outliers x 10, threshold 0.45 (C++ form)
     PR, PC = 8192, 3072
     pack = None
-    if only in (None, "pack"):
-        pbytes = 4 * PR * PC + 16 * PR * ((PC + 47) // 48)
+    pack3072 = None
+
+    def time_pack(rows, cols, which):
+        pbytes = 4 * rows * cols + 16 * rows * ((cols + 47) // 48)
         pcopies = max(4, -(-2 * MALL_BYTES // pbytes) + 2)
-        srcs = [torch.randn((PR, PC), device=dev) * 0.02 for _ in range(pcopies)]
-        pout = torch.empty((PR, (PC + 47) // 48, 16), dtype=torch.uint8, device=dev)
+        gen = torch.Generator(dev).manual_seed(rows + cols)
+        srcs = []
+        for _ in range(pcopies):
+            w = torch.randn((rows, cols), device=dev, generator=gen) * 0.02
+            w = torch.where(torch.rand((rows, cols), device=dev, generator=gen) < 0.01, w * 10, w)
+            srcs.append(w)
+        pout = torch.empty((rows, (cols + 47) // 48, 16), dtype=torch.uint8, device=dev)
         plaunch = lambda s: ops.quantize_pack(s, 0.45, _lib.THR_CPP, out=pout)  # noqa: E731
-        pack = time_graph(torch, plaunch, srcs, max(128, args.steps // 8), 8, dist=True)
-        pack["sha256"] = sha256_tensors(torch, srcs[0])
+        r = time_graph(torch, plaunch, srcs, max(128, args.steps // 8), 8, dist=True)
+        r["sha256"] = sha256_tensors(torch, srcs[0])
         del srcs
         torch.cuda.empty_cache()
-        log(f"pack {pack['ms'] * 1e3:.2f} us/call")
+        log(f"pack {rows}x{cols} ({which}) {r['ms'] * 1e3:.2f} us/call "
+            f"(median {r['median_ms'] * 1e3:.2f})")
+        return r
+
+    if only in (None, "pack"):
+        pack = time_pack(PR, PC, "8192x3072")
+    if only in (None, "pack3072"):
+        pack3072 = time_pack(3072, 3072, "3072x3072")
 
     # ------------------------------------------------------------ CPU baselines --
     cpu = None
@@ -1075,7 +1208,11 @@ def main() -> int:
                               "sample": f"row blocks on {threads} threads, {sa * 1e3:.1f} ms"},
             }
 
-    decode = run_decode(torch, ops, _lib, dev) if only in (None, "decode") else None
+    limb = run_limb(torch, ops, _lib, dev, 0.25 * args.cpu_budget, not args.no_cpu and only is None) \
+        if only in (None, "limb") else None
+    prefill = run_prefill(torch, ops, _lib, dev) if only in (None, "prefill") else None
+    decode = run_decode(torch, ops, _lib, dev, args.decode_case) \
+        if only in (None, "decode") else None
     sweep = run_sweep(torch, ops, _lib, dev) if args.sweep else None
     spmm = run_spmm(torch, dev) if only == "spmm" else None
     backward = run_backward(torch, ops, _lib, dev) if only == "backward" else None
@@ -1147,6 +1284,22 @@ def main() -> int:
                         "timing": spread_us(pack), "inputs_sha256": pack["sha256"]}
         if "cpu_baseline" in pack:
             line["pack"]["cpu_baseline"] = pack["cpu_baseline"]
+    if pack3072:
+        pbytes3 = 4 * 3072 * 3072 + 16 * 3072 * 64
+        gbs3 = pbytes3 / (pack3072["ms"] * 1e-3) / 1e9
+        entry = {"workload": "K1 quantize+pack 3072x3072 fp32 (config 2)",
+                 "us": pack3072["ms"] * 1e3, "timed_launches": pack3072["timed_launches"],
+                 "roofline": {"bound": "hbm", "achieved": gbs3, "peak": HBM_PEAK_GBPS,
+                              "unit": "GB/s", "frac": gbs3 / HBM_PEAK_GBPS},
+                 "timing": spread_us(pack3072), "inputs_sha256": pack3072["sha256"]}
+        if "pack" in line:
+            line["pack"]["config2_3072x3072"] = entry
+        else:
+            line["pack"] = {"config2_3072x3072": entry}
+    if limb:
+        line["limb"] = limb
+    if prefill:
+        line["prefill"] = prefill
     if floors:
         line["floors"] = floors
     if decode:
