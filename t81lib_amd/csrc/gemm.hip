@@ -362,6 +362,7 @@ constexpr int kW4RowBytes = 16 * kW4RowSlots;       // 208
 constexpr int kW4TileBytes = kW4Tokens * kW4RowBytes;
 constexpr uint32_t kW4Oob = 0x80000000u;
 constexpr int kW4StageStride = 68;   // floats per staged output row: 64 columns + 4 pad
+constexpr int kW4StageBytes = 4 * 32 * kW4StageStride * 4;   // four waves' staging regions
 
 // A raw buffer descriptor over [base, base + bytes) (clamped to 2^31 - 1 bytes) whose
 // fields are forced into scalar registers: the loads then need no per-lane
@@ -394,6 +395,12 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
     int sps, float4 *__restrict__ part, int nsplit, int half) {
     static_assert(XT == kDtypeBF16, "the LDS tile is filled straight from bf16 activations");
     static_assert(RB == 3 || RB == 4, "three or four 32-row blocks per wave");
+    if constexpr (RB == 3) {
+        // the 192-row instance has no remainder path: every row is in a whole tile
+        n1 = N;
+        nsplit = 0;
+        half = 0;
+    }
     constexpr int kRows = 64 * RB;   // weight rows per tile
     // Two separate tile objects (not one array indexed by a run-time parity): the
     // loads into one buffer then provably do not alias the reads of the other, and
@@ -404,8 +411,16 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
     __shared__ __attribute__((aligned(1024))) uint8_t lut[kLutBytes];
     __shared__ __attribute__((aligned(16))) uint8_t xs0[kW4TileBytes];
     __shared__ __attribute__((aligned(16))) uint8_t xs1[kW4TileBytes];
-    // Epilogue staging, one region per wave: 32 tokens x 64 weight rows of results.
-    __shared__ __attribute__((aligned(16))) float cst[4][32 * kW4StageStride];
+    // Epilogue staging, one region per wave (32 tokens x 64 weight rows of results), in the
+    // first tile buffer: past an item's last barrier no tile byte that is used is read or
+    // written any more (the last step's tile loads have landed and its last B reads fetch
+    // unused bytes), and each item starts with a barrier, so no wave's next tile loads
+    // overwrite a region another wave is still using.  The static LDS is then the table
+    // and the two tiles only, below the bound for global -> LDS load targets wherever the
+    // compiler places them.
+    static_assert(kW4StageBytes <= kW4TileBytes, "the epilogue staging must fit a tile buffer");
+    // (the table plus the most alignment padding any placement can add: 1024 bytes)
+    static_assert(1024 + 2 * kW4TileBytes + 1024 <= kLdsDmaLimit, "LDS-load targets past 128 KiB");
     auto tile = [&](auto bufc) -> uint8_t * {
         if constexpr (decltype(bufc)::value == 0) return xs0;
         else return xs1;
@@ -443,13 +458,19 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
                         int tt) {
         constexpr int CB = decltype(cbc)::value;      // 32-token blocks per wave
         constexpr int kTok = 64 * CB;                  // tokens per workgroup
+        // every wave is past the previous item's epilogue (staged in xs0) before this
+        // item's tile loads
+        __syncthreads();
         constexpr int kTL = kTok * kW4RowSlots / 64;   // tile loads per workgroup (52, 26)
         constexpr int LPW = (kTL + 3) / 4;             // per wave (13; 7, the last wave 5)
         constexpr int NCH = 6 * CB;                    // chunks of four MFMAs per step
         constexpr int HALF = 3 * CB;                   // chunks per half step
         constexpr int NF = CB == 4 ? 2 * RB : RB;      // chunks of a half that read the table
         constexpr int FPC = 2 * RB / NF;               // weight dwords looked up per such chunk
-        constexpr int kWaitW = 0x0F70 | RB;            // vmcnt(RB): all but the newest RB loads
+        constexpr int kWLoads = RB;                    // loads of fetch_w: one per row block
+        constexpr int kWaitW = waitcnt_vm<kWLoads>();  // all but the newest fetch_w
+        // the half-width prologue's two tiles: all but the newest fetch_w and tile loads
+        constexpr int kWaitTwo = waitcnt_vm<kWLoads + LPW>();
 
         // The lane index passes through an empty asm once per item, so the per-lane
         // offsets derived from it are recomputed per item instead of being hoisted out of
@@ -586,12 +607,12 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
         } else {
             // a half-width step is too short to cover its tile loads, so every step
             // loads the tile of the step after next: here the second step's tile too.
-            // vmcnt(9): the first tile has landed (the second tile's loads -- five in
-            // the last wave -- and the four weight loads may still be in flight).
-            // One step only: vmcnt(RB), the weight loads.
+            // Issued after the first tile: the weights of the second step (kWLoads loads)
+            // and the second tile (LPW loads, every wave, spare ones included), which may
+            // stay in flight.  One step only: the weight loads.
             if (s_begin + 1 < s_end) {
                 load_tile(s_begin + 1, B1());
-                __builtin_amdgcn_s_waitcnt(0x0F79);
+                __builtin_amdgcn_s_waitcnt(kWaitTwo);
             } else {
                 __builtin_amdgcn_s_waitcnt(kWaitW);
             }
@@ -751,7 +772,7 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
         const float be = beta;
         const float *bi = bias;
         const bool vec4 = ldv % 4 == 0 && (reinterpret_cast<uintptr_t>(cdst) & 15u) == 0;
-        float *st = cst[wave];
+        float *st = reinterpret_cast<float *>(xs0) + wave * (32 * kW4StageStride);
         const int tq = lane >> 4;          // token within a group of four
         const int tc = 4 * (lane & 15);    // first of the lane's four rows within the 64
 #pragma unroll
@@ -819,6 +840,7 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
         const int item =
             __builtin_amdgcn_readfirstlane(q < head ? q : (rem ? q - full_items : q - head));
         if (half && rem) {
+            // (unreachable for RB = 3, whose remainder is forced empty above)
             if constexpr (RB == 4) {
                 const int tn = __builtin_amdgcn_readfirstlane(item % tn2);
                 const int tm = __builtin_amdgcn_readfirstlane(item / tn2);

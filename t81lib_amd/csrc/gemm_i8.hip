@@ -50,6 +50,7 @@ constexpr int kI8RowBytes = 16 * kI8RowSlots;     // 112
 constexpr int kI8TileBytes = kI8Tokens * kI8RowBytes;
 constexpr uint32_t kI8Oob = 0x80000000u;
 constexpr int kI8StageStride = 68;                // int32 per staged output row (64 + 4 pad)
+constexpr int kI8StageWave = 32 * kI8StageStride * 4;   // bytes of one wave's staging region
 // pair table: entry b0 + 256 b1 (8 bytes) for every pair of 5-bit byte values
 constexpr int kI8LutBytes = 32 * 256 * 8;
 
@@ -105,7 +106,16 @@ __global__ __launch_bounds__(kI8Threads) void gemm_w4_i8_kernel(
     __shared__ __attribute__((aligned(1024))) uint8_t lut[kI8LutBytes];
     __shared__ __attribute__((aligned(16))) uint8_t xs0[kI8TileBytes];
     __shared__ __attribute__((aligned(16))) uint8_t xs1[kI8TileBytes];
-    __shared__ __attribute__((aligned(16))) int32_t cst[4][32 * kI8StageStride];
+    // Epilogue staging, one region per wave, in the tile buffers (waves 0-2 in the first,
+    // wave 3 in the second): past an item's last barrier the tiles are dead, and each item
+    // starts with a barrier, so no wave's next tile loads overwrite a region another wave
+    // is still using.  The static LDS is then the table and the two tiles only, below the
+    // bound for global -> LDS load targets wherever the compiler places them.
+    static_assert(3 * kI8StageWave <= kI8TileBytes && kI8StageWave <= kI8TileBytes,
+                  "the epilogue staging must fit the tile buffers");
+    // (+ 1024: the most alignment padding any placement of the three objects can add)
+    static_assert(kI8LutBytes + 2 * kI8TileBytes + 1024 <= kLdsDmaLimit,
+                  "LDS-load targets past 128 KiB");
     auto tile = [&](auto bufc) -> uint8_t * {
         if constexpr (decltype(bufc)::value == 0) return xs0;
         else return xs1;
@@ -140,6 +150,12 @@ __global__ __launch_bounds__(kI8Threads) void gemm_w4_i8_kernel(
         constexpr int LPW = (kTL + 3) / 4;                 // per wave (7; 4, the last wave 2)
         constexpr int NCH = 3 * CB;                        // chunks of four MFMAs per step
         constexpr int NFC = CB == 4 ? 8 : 4;               // chunks that issue table reads
+        constexpr int kWLoads = 4;                         // loads of fetch_w: one per row block
+        // all but the newest fetch_w: the tile loads issued before it have landed
+        constexpr int kWaitW = waitcnt_vm<kWLoads>();
+        // every wave is past the previous item's epilogue (staged in the tile buffers)
+        // before this item's tile loads
+        __syncthreads();
         constexpr int FR = 8 / NFC;                        // ... for FR x 2 row blocks each
         // The lane index passes through an empty asm once per item (its derived offsets are
         // recomputed per item, not kept live across the epilogue).
@@ -268,7 +284,7 @@ __global__ __launch_bounds__(kI8Threads) void gemm_w4_i8_kernel(
             load_tile(s_begin, B0());
         }
         fetch_w(s_begin + 2, wn2);            // stays in flight across the barrier
-        __builtin_amdgcn_s_waitcnt(0x0F74);   // vmcnt(4): the tile has landed before the barrier
+        __builtin_amdgcn_s_waitcnt(kWaitW);   // the tile has landed before the barrier
         __syncthreads();
         if (s_begin < s_end) {
             // the first step's J = 0 operands and dwords 4, 5 of its J = 1 operands
@@ -337,9 +353,9 @@ __global__ __launch_bounds__(kI8Threads) void gemm_w4_i8_kernel(
                 wnxt[rb] = wn2[rb];
                 wn2[rb] = wn3[rb];
             }
-            // vmcnt(4): this step's tile loads (and everything older) have landed; the
-            // weights of step + 3 stay in flight
-            __builtin_amdgcn_s_waitcnt(0x0F74);
+            // this step's tile loads (and everything older) have landed; the weights of
+            // step + 3, issued after them, stay in flight
+            __builtin_amdgcn_s_waitcnt(kWaitW);
             __syncthreads();
         };
         int step = s_begin;
@@ -370,7 +386,7 @@ __global__ __launch_bounds__(kI8Threads) void gemm_w4_i8_kernel(
         // epilogue through the wave's LDS region, as in the bf16 kernel
         const int col0 = nwg;
         const bool vec4 = ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(c) & 15u) == 0;
-        int32_t *st = cst[wave];
+        int32_t *st = reinterpret_cast<int32_t *>(wave < 3 ? xs0 + wave * kI8StageWave : xs1);
         const int tq = lane >> 4;
         const int tc = 4 * (lane & 15);
 #pragma unroll
