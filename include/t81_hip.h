@@ -110,8 +110,8 @@ int t81_hip_ternary_matmul_kernel(int which, const void *x, int x_dtype, const u
 
 /* Same, with a caller-owned device workspace: which = 0 (by M, as
  * t81_hip_ternary_matmul), 2 or 3.  When K3 has few output tiles for its shape, or K2
- * runs 9..16 tokens over a long K with float32 or int8 activations (or bf16 with K not a
- * multiple of 8), and workspace_bytes is at least
+ * runs 9..16 tokens over a long K with float32 activations, int8 ones with K not a
+ * multiple of 16, or bf16 ones with K not a multiple of 8, and workspace_bytes is at least
  * t81_hip_ternary_matmul_workspace_size(...), K is split over several workgroups
  * per tile: each writes its partial tile to the workspace and a second kernel sums
  * the partials in split order (deterministic).  NULL / 0 bytes: no split.  The
@@ -124,7 +124,9 @@ int t81_hip_ternary_matmul_ws(int which, const void *x, int x_dtype, const uint8
                               void *stream);
 
 /* Bytes of workspace t81_hip_ternary_matmul_ws uses for this shape on the current
- * device (0: the shape does not split).  Never fails. */
+ * device (0: the shape does not split).  Never fails.  It does not look at x's
+ * alignment: int8 activations at 8+ tokens with K % 16 == 0 report 0, and such a call
+ * runs in one launch with no split whether or not x is 16-byte aligned. */
 int64_t t81_hip_ternary_matmul_workspace_size(int64_t m, int64_t n, int64_t k, int x_dtype);
 
 /* Same as t81_hip_ternary_matmul_ws(which, ...) given a workspace of exactly

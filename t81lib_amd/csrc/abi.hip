@@ -121,6 +121,16 @@ int check_matmul(const void *x, int x_dtype, const uint8_t *w, void *c, int64_t 
 
 int t81hip::report_error(int code, const char *msg) { return fail(code, msg); }
 
+int t81hip::check_matmul_args(int which, const void *x, int x_dtype, const uint8_t *w, void *c,
+                              int64_t m, int64_t n, int64_t k, float alpha, float beta,
+                              const float *bias) {
+    if (int rc = check_matmul(x, x_dtype, w, c, m, n, k, alpha, beta, bias)) return rc;
+    if (which == 2 && m > 16) return fail(T81_HIP_EINVAL_SHAPE, "the GEMV kernel takes M <= 16");
+    if (which != 0 && which != 2 && which != 3)
+        return fail(T81_HIP_EINVAL_SHAPE, "kernel must be 0, 2 or 3");
+    return T81_HIP_OK;
+}
+
 extern "C" {
 
 int t81_hip_available(void) {

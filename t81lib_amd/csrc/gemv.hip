@@ -385,7 +385,7 @@ __global__ __launch_bounds__(64 * W) void gemv_wave_kernel(
 // split K round-robin; each activation fragment serves its G 16-row groups.  kStage
 // (bf16, kAligned): the activations of a sub-block are loaded as pieces and become
 // fragments through the wave's LDS region (load_x_pieces).
-template <int XT, int G, bool kAligned, int KS, bool kStage>
+template <int XT, int G, bool kAligned, int KS, bool kStage, bool kDeep = false>
 __global__ __launch_bounds__(64 * KS) void gemv_stream_kernel(const void *__restrict__ x,
                                                           const uint8_t *__restrict__ w,
                                                           void *__restrict__ c, int M, int64_t N,
@@ -394,6 +394,7 @@ __global__ __launch_bounds__(64 * KS) void gemv_stream_kernel(const void *__rest
                                                           const float *__restrict__ bias) {
     static_assert(!kStage || ((XT == kDtypeBF16 || XT == kDtypeI8) && kAligned),
                   "pieces are aligned bf16, or int8 widened to bf16 as they are staged");
+    static_assert(!kDeep || kStage, "two sub-blocks in flight: the staged form only");
     // a piece: 16 bytes of one token's activations, 8 bf16 or 16 int8 values (the int8
     // launch also needs K % 16 == 0 and a 16-byte aligned x)
     constexpr int kVals = XT == kDtypeI8 ? 16 : 8;
@@ -460,6 +461,57 @@ __global__ __launch_bounds__(64 * KS) void gemv_stream_kernel(const void *__rest
             bh[j] = *reinterpret_cast<const bf16x8 *>(xs + r * kXStagePitch + 96 * q + 16 * j);
     };
     int64_t s = wave;
+    if constexpr (kDeep) {
+        // Two sub-blocks in flight.  Iteration i (sub-block s_i = wave + i KS): issue the
+        // pieces of s_{i+2} into slot i % 2 (whose pieces of s_i were staged the iteration
+        // before), run the MFMAs of s_i with the weights in slot i % 2 (loaded two
+        // iterations ago), load the weights of s_{i+2} into that slot, then stage the
+        // pieces of s_{i+1} (issued an iteration ago): every load has two iterations to
+        // land, and no register of a load in flight is copied.  Two iterations per pass
+        // keep the slots static.  (Fencing the loads at the top of the iteration with
+        // sched_barrier measured slower: llama.down M = 8 12.6 -> 13.2 us.)
+        floatx4 acc[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) acc[g] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 6; ++j) bl[j] = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
+        u32x4 xa[6], xb[6];
+        u32x4 wa[G], wb[G];
+        auto pieces_to = [&](int64_t sb, u32x4 (&dst)[6]) {
+            load_pieces(sb);
+#pragma unroll
+            for (int i = 0; i < kLanePieces; ++i) dst[i] = xp[i];
+        };
+        auto stage_from = [&](const u32x4 (&src)[6]) {
+#pragma unroll
+            for (int i = 0; i < kLanePieces; ++i) xp[i] = src[i];
+            stage();
+        };
+        auto weights_to = [&](int64_t sb, u32x4 (&dst)[G]) {
+#pragma unroll
+            for (int g = 0; g < G; ++g) dst[g] = load_limb(w, n0 + 16 * g + r, 4 * sb + q, N, L, L);
+        };
+        pieces_to(s, xa);
+        weights_to(s, wa);
+        pieces_to(s + KS, xb);
+        weights_to(s + KS, wb);
+        lut_init(lut, tid, 64 * KS);
+        stage_from(xa);
+        auto iter = [&](int64_t si, u32x4 (&xs_now)[6], u32x4 (&xs_next)[6], u32x4 (&wn)[G]) {
+            pieces_to(si + 2 * KS, xs_now);
+#pragma unroll
+            for (int g = 0; g < G; ++g) acc[g] = mfma_limb<XT>(lut, wn[g], bh, bl, acc[g]);
+            weights_to(si + 2 * KS, wn);
+            stage_from(xs_next);
+        };
+        for (; s < S; s += 2 * KS) {
+            iter(s, xa, xb, wa);
+            if (s + KS >= S) break;
+            iter(s + KS, xb, xa, wb);
+        }
+        reduce_store<XT, G, KS>(acc, red, wave, lane, M, N, n0, c, alpha, beta, bias);
+        return;
+    }
     if constexpr (kStage) {
         load_pieces(s);
 #pragma unroll
@@ -853,10 +905,19 @@ hipError_t launch_stream(const void *x, const uint8_t *w, void *c, int m, int64_
         }
     }
     if constexpr (XT == kDtypeI8 && kAligned) {
-        // int8, 8+ tokens: the same staging, the values widened to bf16 (16-value pieces)
+        // int8, 8+ tokens: the same staging, the values widened to bf16 (16-value pieces).
+        // One row group per workgroup (<= 4096 rows) keeps two sub-blocks in flight: with
+        // three pieces per lane the second slot is cheap (llama.down M = 8 14.5 -> 12.6 us,
+        // M = 16 14.5 -> 13.1, 3072 -> 3072 5.5 -> 5.4; the wider, two- and four-group
+        // shapes measured slower, 10.1 -> 11.7 on llama.gate, as did bf16, whose six
+        // pieces per lane double the slot: llama.down M = 16 13.2 -> 13.4)
         if (m >= 8 && k % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0) {
-            gemv_stream_kernel<XT, G, kAligned, KS, true><<<dim3(blocks), dim3(64 * KS), 0, s>>>(
-                x, w, c, m, n, k, L, alpha, beta, bias);
+            if constexpr (G == 1)
+                gemv_stream_kernel<XT, G, kAligned, KS, true, true>
+                    <<<dim3(blocks), dim3(64 * KS), 0, s>>>(x, w, c, m, n, k, L, alpha, beta, bias);
+            else
+                gemv_stream_kernel<XT, G, kAligned, KS, true>
+                    <<<dim3(blocks), dim3(64 * KS), 0, s>>>(x, w, c, m, n, k, L, alpha, beta, bias);
             return hipGetLastError();
         }
     }

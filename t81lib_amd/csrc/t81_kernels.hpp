@@ -15,6 +15,11 @@ constexpr int kDtypeF16 = 3;
 
 // abi.hip: records msg as the calling thread's last error and returns code
 int report_error(int code, const char *msg);
+// The argument checks of t81_hip_ternary_matmul_ws (0 or the code it would return, with
+// its error text recorded).
+int check_matmul_args(int which, const void *x, int x_dtype, const uint8_t *w, void *c,
+                      int64_t m, int64_t n, int64_t k, float alpha, float beta,
+                      const float *bias);
 
 // pack.hip
 hipError_t launch_quantize_pack_rows(const void *w, int dtype, uint8_t *out, int64_t rows,
@@ -27,8 +32,9 @@ hipError_t launch_unpack(const uint8_t *packed, int8_t *out, int64_t rows, int64
                          int64_t cols, hipStream_t s);
 hipError_t launch_validate(const uint8_t *packed, int64_t count, int32_t *bad, hipStream_t s);
 
-// gemv.hip (K2): M <= 16.  ws (ws_bytes of device memory, may be null) lets 5..16
-// tokens split K over workgroups; gemv_workspace_bytes says how much a shape uses.
+// gemv.hip (K2): M <= 16.  ws (ws_bytes of device memory, may be null) lets 9..16 tokens
+// over a long K split it over workgroups (float32 activations, int8 with K % 16 != 0,
+// bf16 with K % 8 != 0); gemv_workspace_bytes says how much a shape uses.
 // 17..48 tokens (64 with K <= 8192), bf16 (K % 8 == 0) or int8 (K % 16 == 0) activations
 // at a 16-byte aligned x: the column-block stream kernel of gemv.hip (two or three 16-token
 // blocks; 49..64 tokens as two launches); the K3 launcher tries it first.

@@ -108,3 +108,58 @@ def test_noalloc_without_split_and_rejection(gpu):
     assert "static scratch" in _lib.last_error()
     torch.cuda.synchronize()
     assert torch.equal(c, before)
+
+
+def test_noalloc_bad_arguments_before_scratch_check(gpu):
+    """Argument errors are reported as t81_hip_ternary_matmul_ws reports them, before the
+    scratch-size check."""
+    lib = _lib.lib()
+    s = torch.cuda.current_stream().cuda_stream
+    rc = lib.t81_hip_ternary_matmul_noalloc(0, None, 9, None, None, 1, 1, 48, 1.0, 0.0, None, s)
+    assert rc == _lib.EINVAL_DTYPE and "activations must be" in _lib.last_error()
+    x = torch.zeros((17, 48), dtype=torch.bfloat16, device=gpu)
+    w = torch.full((8, 1, 16), 13, dtype=torch.uint8, device=gpu)
+    c = torch.zeros((17, 8), device=gpu)
+    rc = lib.t81_hip_ternary_matmul_noalloc(2, x.data_ptr(), _lib.DTYPE_BF16, w.data_ptr(),
+                                            c.data_ptr(), 17, 8, 48, 1.0, 0.0, None, s)
+    assert rc == _lib.EINVAL_SHAPE and "M <= 16" in _lib.last_error()
+    rc = lib.t81_hip_ternary_matmul_noalloc(2, None, _lib.DTYPE_BF16, None, None, 17, 8, 48, 1.0,
+                                            0.0, None, s)
+    assert rc == _lib.EINVAL_POINTER   # the pointer checks come first, as in the _ws form
+
+
+@pytest.mark.parametrize("dtype,M,N,K", [(torch.float32, 48, 1000, 4104),
+                                         (torch.bfloat16, 512, 6144, 4096),
+                                         (torch.float32, 16, 4096, 14336)])
+def test_noalloc_under_graph_capture(gpu, dtype, M, N, K):
+    """A split shape captured in a HIP graph through the no-allocation entry point: every
+    replay equals the workspace entry point's eager result bit for bit, with eager calls
+    on other shapes (which overwrite the shared scratch) and synchronisations between the
+    replays."""
+    announce(f"noalloc graph capture {dtype} M={M} N={N} K={K}")
+    lib = _lib.lib()
+    x, packed, c, bias, alpha, beta = _problem(gpu, M, N, K, dtype, seed=M * 3 + K)
+    code = _code(dtype)
+    need = lib.t81_hip_ternary_matmul_workspace_size(M, N, K, code)
+    assert 0 < need <= SCRATCH
+    c_na, c_ws, _ = _run_pair(gpu, M, N, K, dtype, seed=M * 3 + K)   # eager, same inputs
+    assert torch.equal(c_na.view(torch.int32), c_ws.view(torch.int32))
+    bptr = bias.data_ptr() if bias is not None else None
+    c_g = c.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc = lib.t81_hip_ternary_matmul_noalloc(0, x.data_ptr(), code, packed.data_ptr(),
+                                                c_g.data_ptr(), M, N, K, alpha, beta, bptr,
+                                                torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc)
+    for i in range(3):
+        c_g.copy_(c)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(c_g.view(torch.int32), c_ws.view(torch.int32)), \
+            f"replay {i + 1}: {int((c_g != c_ws).sum())} outputs differ"
+        # an eager split call on another shape reuses (overwrites) the scratch in between
+        other = _run_pair(gpu, 40, 700, 2000, torch.float32, seed=i)
+        assert torch.equal(other[0].view(torch.int32), other[1].view(torch.int32))
+    del graph
