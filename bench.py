@@ -573,6 +573,62 @@ def run_decode(torch, ops, lib, dev, only_case=None) -> dict:
             "shapes": shapes}
 
 
+def run_gemv_valu(torch, ops, lib, dev) -> dict:
+    """The north-star form of K2 beside the matrix-core one, same box, same run: the one-token
+    GEMV at 4096 -> 14336 (the headline shape) over the same rotating weight copies, as
+    ops.ternary_matmul (K2: LDS-table decode, v_mfma_f32_16x16x32_bf16, LDS row sums) and as
+    t81_floor_gemv_valu (the same table decode, v_dot2c_f32_bf16 products in each lane, DPP
+    row sums per weight row, no matrix cores; csrc/floors.hip), best of 256-4096
+    workgroups x 1, 2, 4 rows in flight per wave.  Integer activations (exact in bf16) make
+    both outputs exact, so they must agree bit for bit; medians over graph replays."""
+    import ctypes
+
+    K, N = 4096, 14336
+    wbytes = 16 * N * ((K + 47) // 48)
+    copies = max(8, -(-2 * MALL_BYTES // wbytes) + 4)
+    wbufs = make_weights(torch, ops, lib, N, K, copies, dev, seed=1)
+    g = torch.Generator(dev).manual_seed(9)
+    x = torch.randint(-64, 65, (1, K), generator=g, device=dev).to(torch.bfloat16)
+    flib = ctypes.CDLL(os.path.join(ROOT, "t81lib_amd", "libt81_floors.so"))
+    flib.t81_floor_gemv_valu.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                         ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                         ctypes.c_void_p]
+    y_m = torch.empty((1, N), device=dev)
+    y_v = torch.empty((1, N), device=dev)
+    ops.ternary_matmul(x, wbufs[0], K, c=y_m, kernel=2)
+
+    def valu(wb, blocks, depth):
+        rc = flib.t81_floor_gemv_valu(x.data_ptr(), wb.data_ptr(), y_v.data_ptr(), N, K, blocks,
+                                      depth, torch.cuda.current_stream().cuda_stream)
+        if rc != 0:
+            raise RuntimeError(f"t81_floor_gemv_valu failed ({rc})")
+
+    valu(wbufs[0], 1024, 2)
+    torch.cuda.synchronize()
+    exact = bool(torch.equal(y_m.view(torch.int32), y_v.view(torch.int32)))
+    mfma = time_graph(torch, lambda wb: ops.ternary_matmul(x, wb, K, c=y_m, kernel=2), wbufs,
+                      256, 32, dist=True)
+    best = None
+    for blocks in (256, 512, 1024, 2048, 4096):
+        for depth in (1, 2, 4):
+            r = time_graph(torch, lambda wb: valu(wb, blocks, depth), wbufs, 256, 32, dist=True)
+            if best is None or r["median_ms"] < best[2]["median_ms"]:
+                best = (blocks, depth, r)
+    blocks, depth, r = best
+    out = {"workload": f"one-token GEMV {K}->{N}, bf16 integer-valued x, {copies} rotating "
+                       f"weight copies",
+           "mfma_us": mfma["median_ms"] * 1e3, "valu_us": r["median_ms"] * 1e3,
+           "valu_config": {"workgroups": blocks, "rows_in_flight_per_wave": depth},
+           "mfma_GBps": gemv_bytes(1, N, K) / (mfma["median_ms"] * 1e-3) / 1e9,
+           "valu_GBps": gemv_bytes(1, N, K) / (r["median_ms"] * 1e-3) / 1e9,
+           "valu_over_mfma": r["median_ms"] / mfma["median_ms"], "outputs_bit_identical": exact}
+    log(f"gemv A/B {K}->{N}: matrix cores {out['mfma_us']:.2f} us, VALU {out['valu_us']:.2f} us "
+        f"({blocks} workgroups, {depth} rows in flight), identical={exact}")
+    del wbufs
+    torch.cuda.empty_cache()
+    return out
+
+
 PREFILL_SHAPES = [("llama.qkv", 4096, 6144), ("llama.gate_up", 4096, 28672),
                   ("llama.down", 14336, 4096)]
 
@@ -955,7 +1011,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", choices=["gemv", "gemm", "pack", "copy", "read", "spmm", "launch",
                                        "stack", "decode", "backward", "prefill", "limb",
-                                       "pack3072"],
+                                       "pack3072", "gemv_valu"],
                     default=None,
                     help="time one kernel only (for profiling runs); 'copy' times a plain "
                          "elementwise copy of the GEMV weight size, the calibration kernel "
@@ -1211,6 +1267,7 @@ def main() -> int:
     limb = run_limb(torch, ops, _lib, dev, 0.25 * args.cpu_budget, not args.no_cpu and only is None) \
         if only in (None, "limb") else None
     prefill = run_prefill(torch, ops, _lib, dev) if only in (None, "prefill") else None
+    gemv_valu = run_gemv_valu(torch, ops, _lib, dev) if only in (None, "gemv_valu") else None
     decode = run_decode(torch, ops, _lib, dev, args.decode_case) \
         if only in (None, "decode") else None
     sweep = run_sweep(torch, ops, _lib, dev) if args.sweep else None
@@ -1300,6 +1357,8 @@ def main() -> int:
         line["limb"] = limb
     if prefill:
         line["prefill"] = prefill
+    if gemv_valu:
+        line["gemv_valu_ab"] = gemv_valu
     if floors:
         line["floors"] = floors
     if decode:
