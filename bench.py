@@ -184,6 +184,21 @@ def time_eager(torch, launch, n: int, steps: int, warmup: int, ahead: int = 64,
             "launches_per_sample": 32}
 
 
+def abi_launch(lib, x, x_dtype: int, wbufs, out, m: int, n: int, k: int, which: int = 3,
+               alpha: float = 1.0, beta: float = 0.0):
+    """launch(i, stream) for time_eager: t81_hip_ternary_matmul_kernel (which = 2 or 3) on weight copy i, for a
+    shape that needs no workspace (the C ABI call every consumer of the library makes)."""
+    fn = lib.lib().t81_hip_ternary_matmul_kernel
+    wptrs = [w.data_ptr() for w in wbufs]
+    xp, op = x.data_ptr(), out.data_ptr()
+
+    def launch(i, sh):
+        rc = fn(which, xp, x_dtype, wptrs[i], op, m, n, k, alpha, beta, None, sh)
+        if rc != 0:
+            lib.check(rc)
+    return launch
+
+
 def spread_us(d: dict) -> dict:
     """The spread of a time_graph(dist=True) result, in microseconds."""
     return {"median_us": d["median_ms"] * 1e3, "p10_us": d["p10_ms"] * 1e3,
@@ -1231,10 +1246,12 @@ def main() -> int:
         gw = make_weights(torch, ops, _lib, GN, GK, 2, dev, seed=2)
         gx = torch.randn((GM, GK), device=dev).to(torch.bfloat16)
         gout = torch.empty((GM, GN), device=dev)
-        glaunch = lambda wb: ops.ternary_matmul(gx, wb, GK, c=gout, kernel=3)  # noqa: E731
         # exactly 100 timed launches (and >= 50 ms of spread samples) whatever --steps is,
-        # after 20 untimed ones that bring the clocks to their loaded state
-        gemm = time_graph(torch, glaunch, gw, 100, 20, dist=True)
+        # after 20 untimed ones that bring the clocks to their loaded state; issued one by
+        # one through the C ABI, as the headline leg (this shape needs no workspace)
+        assert _lib.lib().t81_hip_ternary_matmul_workspace_size(GM, GN, GK, _lib.DTYPE_BF16) == 0
+        gemm = time_eager(torch, abi_launch(_lib, gx, _lib.DTYPE_BF16, gw, gout, GM, GN, GK),
+                          len(gw), 100, 20, ahead=4)
         gemm["sha256"] = sha256_tensors(torch, gw[0], gx)
         del gw, gx, gout
         torch.cuda.empty_cache()
@@ -1247,8 +1264,9 @@ def main() -> int:
         gw = make_weights(torch, ops, _lib, GN, GK, 2, dev, seed=2)
         gx8 = torch.randint(-128, 128, (GM, GK), device=dev, dtype=torch.int8)
         gout8 = torch.empty((GM, GN), device=dev, dtype=torch.int32)
-        glaunch8 = lambda wb: ops.ternary_matmul(gx8, wb, GK, c=gout8, kernel=3)  # noqa: E731
-        gemm_i8 = time_graph(torch, glaunch8, gw, 100, 20, dist=True)
+        assert _lib.lib().t81_hip_ternary_matmul_workspace_size(GM, GN, GK, _lib.DTYPE_I8) == 0
+        gemm_i8 = time_eager(torch, abi_launch(_lib, gx8, _lib.DTYPE_I8, gw, gout8, GM, GN, GK),
+                             len(gw), 100, 20, ahead=4)
         gemm_i8["sha256"] = sha256_tensors(torch, gw[0], gx8)
         del gw, gx8, gout8
         torch.cuda.empty_cache()
@@ -1271,8 +1289,18 @@ def main() -> int:
             w = torch.where(torch.rand((rows, cols), device=dev, generator=gen) < 0.01, w * 10, w)
             srcs.append(w)
         pout = torch.empty((rows, (cols + 47) // 48, 16), dtype=torch.uint8, device=dev)
-        plaunch = lambda s: ops.quantize_pack(s, 0.45, _lib.THR_CPP, out=pout)  # noqa: E731
-        r = time_graph(torch, plaunch, srcs, max(128, args.steps // 8), 8, dist=True)
+        qp = _lib.lib().t81_hip_quantize_pack
+        sptrs = [t.data_ptr() for t in srcs]
+        outp = pout.data_ptr()
+
+        def plaunch(i, sh):
+            rc = qp(sptrs[i], _lib.DTYPE_F32, outp, rows, cols, 0.45, _lib.THR_CPP, sh)
+            if rc != 0:
+                _lib.check(rc)
+
+        # launches issued one by one through the C ABI (host ~3.5 us per call, the kernel
+        # ~9-20 us), as the other legs
+        r = time_eager(torch, plaunch, len(srcs), max(128, args.steps // 8), 8)
         r["sha256"] = sha256_tensors(torch, srcs[0])
         del srcs
         torch.cuda.empty_cache()
