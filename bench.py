@@ -65,10 +65,12 @@ def _capture(torch, launch, items, stream):
 
 
 def time_graph(torch, launch, buffers, steps: int, warmup: int, dist: bool = False,
-               min_launches: int = 100, min_ms: float = 50.0):
+               min_launches: int = 100, min_ms: float = 50.0, min_graph: int = 128):
     """Times exactly `steps` launches of `launch`, rotating through `buffers`, captured in
-    HIP graphs so the GPU runs them back to back on one stream: a graph of one launch per
-    buffer (replayed steps // len(buffers) times) plus one of the remaining launches.
+    HIP graphs so the GPU runs them back to back on one stream: a graph of at least
+    `min_graph` launches cycling through the buffers (a whole number of rotations; a graph
+    replay costs ~10-20 us at its boundary on this runtime, so a graph holds many launches),
+    replayed steps // its size times, plus one graph of the remaining launches.
     `warmup` untimed launches (whole rotations) run first, then a synchronisation, then one
     more untimed rotation ahead of the start event (the graph of the remaining launches is
     replayed once untimed too, so no timed replay is a first one); the timed region ends with a
@@ -79,13 +81,14 @@ def time_graph(torch, launch, buffers, steps: int, warmup: int, dist: bool = Fal
     import numpy as np
 
     steps = max(1, int(steps))
-    n = len(buffers)
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):
-        for i in range(min(max(warmup, 1), n)):   # eager warm-up outside any capture
+        for i in range(min(max(warmup, 1), len(buffers))):   # eager warm-up, no capture
             launch(buffers[i])
     torch.cuda.synchronize()
+    buffers = list(buffers) * max(1, -(-min_graph // len(buffers)))
+    n = len(buffers)
     full = _capture(torch, launch, buffers, stream)
     rest = _capture(torch, launch, buffers[: steps % n], stream) if steps % n else None
     torch.cuda.synchronize()
@@ -185,15 +188,22 @@ def time_eager(torch, launch, n: int, steps: int, warmup: int, ahead: int = 64,
 
 
 def abi_launch(lib, x, x_dtype: int, wbufs, out, m: int, n: int, k: int, which: int = 3,
-               alpha: float = 1.0, beta: float = 0.0):
-    """launch(i, stream) for time_eager: t81_hip_ternary_matmul_kernel (which = 2 or 3) on weight copy i, for a
-    shape that needs no workspace (the C ABI call every consumer of the library makes)."""
-    fn = lib.lib().t81_hip_ternary_matmul_kernel
+               alpha: float = 1.0, beta: float = 0.0, torch=None):
+    """launch(i, stream) for time_eager: t81_hip_ternary_matmul_ws (which = 0, 2 or 3) on
+    weight copy i, with a workspace of the size the shape asks for allocated once here (the
+    C ABI call every consumer of the library makes; out is C, read when beta != 0)."""
+    L = lib.lib()
+    fn = L.t81_hip_ternary_matmul_ws
     wptrs = [w.data_ptr() for w in wbufs]
     xp, op = x.data_ptr(), out.data_ptr()
+    need = int(L.t81_hip_ternary_matmul_workspace_size(m, n, k, x_dtype))
+    ws = None
+    if need > 0:
+        ws = torch.empty(need, dtype=torch.uint8, device=out.device)
+    wsp = ws.data_ptr() if ws is not None else None
 
-    def launch(i, sh):
-        rc = fn(which, xp, x_dtype, wptrs[i], op, m, n, k, alpha, beta, None, sh)
+    def launch(i, sh, ws=ws):
+        rc = fn(which, xp, x_dtype, wptrs[i], op, m, n, k, alpha, beta, None, wsp, need, sh)
         if rc != 0:
             lib.check(rc)
     return launch
@@ -706,9 +716,9 @@ PREFILL_SHAPES = [("llama.qkv", 4096, 6144), ("llama.gate_up", 4096, 28672),
 def run_prefill(torch, ops, lib, dev) -> dict:
     """Config 4: the three Llama-3-8B prefill shapes at M = 512, 2048 and 8192 tokens, bf16
     activations ~ N(0,1), with (alpha, beta) = (1, 0) and (0.5, 1) over a float32 C ~ N(0,1)
-    (read and written in place), through the product path (ops.ternary_matmul with its
-    workspace): exactly 100 timed launches after 20 untimed ones, over two weight copies,
-    plus >= 50 ms of spread samples.  TFLOP/s of 2 M N K and the fraction of the bf16
+    (read and written in place), through the C ABI (t81_hip_ternary_matmul_ws with the
+    workspace the shape asks for): exactly 100 timed launches issued one by one after 20
+    untimed ones, over two weight copies, plus >= 50 ms of spread samples.  TFLOP/s of 2 M N K and the fraction of the bf16
     matrix-core peak, from the mean over the 100 timed launches (median alongside)."""
     cases = []
     for name, k, n in PREFILL_SHAPES:
@@ -717,8 +727,9 @@ def run_prefill(torch, ops, lib, dev) -> dict:
             x = torch.randn((m, k), device=dev).to(torch.bfloat16)
             c = torch.randn((m, n), device=dev)
             for alpha, beta in ((1.0, 0.0), (0.5, 1.0)):
-                d = time_graph(torch, lambda w: ops.ternary_matmul(x, w, k, alpha=alpha, beta=beta,
-                                                                   c=c), wb, 100, 20, dist=True)
+                d = time_eager(torch, abi_launch(lib, x, lib.DTYPE_BF16, wb, c, m, n, k, which=3,
+                                                 alpha=alpha, beta=beta, torch=torch),
+                               len(wb), 100, 20, ahead=4)
                 flops = 2.0 * m * n * k
                 tf = flops / (d["ms"] * 1e-3) / 1e12
                 cases.append({"shape": name, "M": m, "K": k, "N": n, "alpha": alpha, "beta": beta,

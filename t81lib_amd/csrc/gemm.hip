@@ -388,7 +388,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void *base,
 // order, so the workgroups that start with a (shorter) remainder item finish their whole
 // tiles half a tile out of step with the others, and the C stores of the two halves do
 // not all land at once.
-template <int XT, int RB>
+template <int XT, int RB, bool kBeta>
 __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
     const void *__restrict__ x, const uint8_t *__restrict__ w, void *__restrict__ c, int M, int N,
     int ldc, int K, int L, float alpha, float beta, const float *__restrict__ bias, int n1,
@@ -775,10 +775,38 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
         float *st = reinterpret_cast<float *>(xs0) + wave * (32 * kW4StageStride);
         const int tq = lane >> 4;          // token within a group of four
         const int tc = 4 * (lane & 15);    // first of the lane's four rows within the 64
+        // With beta != 0 (the kBeta instance) the C values of each pass (32 tokens x 64
+        // rows) are loaded one pass ahead, so only the first pass waits for them: issued
+        // inside the pass, every pass had waited for its own C reads (gate_up M = 2048 with
+        // beta = 1: 444.7 -> 417.5 us, M = 8192 1794 -> 1610 us).  The beta = 0 instance
+        // has none of this code (with it, beta = 0 ran ~1 % slower).
+        constexpr int kRP = (RB + 1) / 2;
+        constexpr int kPasses = CB * kRP;
+        auto c_pass = [&](int p, float4 (&cv)[8]) {
+            const int cb = p / kRP;
+            const int rp = p % kRP;
+            const int prow = 2 * rp + 1 < RB ? 64 : 32;
+            const int nb = col0 + 32 * RB * wn + 64 * rp + tc;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int tok = 4 * i + tq;
+                const int m = m0 + 32 * CB * wm + 32 * cb + tok;
+                const bool ok = vec4 && m < M && tc < prow && nb + 3 < nv;
+                cv[i] = ok ? *reinterpret_cast<const float4 *>(cdst + static_cast<int64_t>(m) * ldv + nb)
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        };
+        float4 cva[8], cvb[8];
+        if constexpr (kBeta) c_pass(0, cva);
 #pragma unroll
         for (int cb = 0; cb < CB; ++cb) {
 #pragma unroll
-            for (int rp = 0; rp < (RB + 1) / 2; ++rp) {
+            for (int rp = 0; rp < kRP; ++rp) {
+                const int pass = cb * kRP + rp;
+                float4 (&cvc)[8] = pass % 2 == 0 ? cva : cvb;
+                float4 (&cvn)[8] = pass % 2 == 0 ? cvb : cva;
+                if constexpr (kBeta)
+                    if (pass + 1 < kPasses) c_pass(pass + 1, cvn);
                 // rows of this pass: 64, or 32 for the third block of three
                 const int prow = 2 * rp + 1 < RB ? 64 : 32;
 #pragma unroll
@@ -799,8 +827,8 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
                     float *cr = cdst + static_cast<int64_t>(m) * ldv;
                     float y[4] = {al * v.x, al * v.y, al * v.z, al * v.w};
                     if (vec4 && nb + 3 < nv) {
-                        if (be != 0.0f) {
-                            const float4 cv = *reinterpret_cast<const float4 *>(cr + nb);
+                        if constexpr (kBeta) {
+                            const float4 cv = cvc[i];
                             y[0] += be * cv.x;
                             y[1] += be * cv.y;
                             y[2] += be * cv.z;
@@ -1013,7 +1041,9 @@ hipError_t launch_gemm_w4_192(const void *x, const uint8_t *w, void *c, int64_t 
     const int64_t L = (k + kTrits - 1) / kTrits;
     const int64_t items = ((n + 191) / 192) * ((m + kW4Tokens - 1) / kW4Tokens);
     const int64_t cus = cu_count();
-    gemm_w4_kernel<kDtypeBF16, 3><<<dim3(items < cus ? items : cus), dim3(kW4Threads), 0, s>>>(
+    auto kernel = beta != 0.0f ? gemm_w4_kernel<kDtypeBF16, 3, true>
+                               : gemm_w4_kernel<kDtypeBF16, 3, false>;
+    kernel<<<dim3(items < cus ? items : cus), dim3(kW4Threads), 0, s>>>(
         x, w, c, static_cast<int>(m), static_cast<int>(n), static_cast<int>(ldc),
         static_cast<int>(k), static_cast<int>(L), alpha, beta, bias, static_cast<int>(n), 0,
         nullptr, 0, 0);
@@ -1038,7 +1068,11 @@ hipError_t launch_gemm_w4(const void *x, const uint8_t *w, void *c, int64_t m, i
                           (rem ? gemm_half_tiles(m, n - n1) : 0);
     if (items <= 0) return hipSuccess;
     const int64_t cus = cu_count();
-    gemm_w4_kernel<kDtypeBF16, 4><<<dim3(items < cus ? items : cus), dim3(kW4Threads), 0, s>>>(
+    // (split items store raw sums: beta is applied by the split sum, and the whole tiles of
+    // the same launch take the kBeta instance)
+    auto kernel = beta != 0.0f ? gemm_w4_kernel<kDtypeBF16, 4, true>
+                               : gemm_w4_kernel<kDtypeBF16, 4, false>;
+    kernel<<<dim3(items < cus ? items : cus), dim3(kW4Threads), 0, s>>>(
         x, w, c, static_cast<int>(m), static_cast<int>(split || rem ? n : n1),
         static_cast<int>(ldc), static_cast<int>(k), static_cast<int>(L), alpha, beta, bias,
         static_cast<int>(n1), split ? static_cast<int>(plan->sps) : 0,

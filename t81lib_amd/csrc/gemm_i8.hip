@@ -95,7 +95,7 @@ __device__ __forceinline__ void i8_lut_fill(uint8_t *lds, int tid, int nthreads)
 // kHalf: the instance with the half-width path (compiled apart, so that the whole-tile
 // instance keeps its register allocation: the combined one spills 27 scalar registers and
 // ran M = 8192 gate_up 1.2 % slower).
-template <bool kHalf>
+template <bool kHalf, bool kAcc>
 __global__ __launch_bounds__(kI8Threads) void gemm_w4_i8_kernel(
     const int8_t *__restrict__ x, const uint8_t *__restrict__ w, int32_t *__restrict__ c, int M,
     int N, int ldc, int K, int L, int accumulate, int n1, int sps, i32x4 *__restrict__ part,
@@ -389,10 +389,32 @@ __global__ __launch_bounds__(kI8Threads) void gemm_w4_i8_kernel(
         int32_t *st = reinterpret_cast<int32_t *>(wave < 3 ? xs0 + wave * kI8StageWave : xs1);
         const int tq = lane >> 4;
         const int tc = 4 * (lane & 15);
+        // Accumulating (the kAcc instance): each pass's C values are loaded one pass ahead,
+        // as in the bf16 kernel, so only the first pass waits for them.
+        constexpr int kPasses = CB * 2;
+        auto c_pass = [&](int p, i32x4 (&cv)[8]) {
+            const int cb = p / 2;
+            const int rp = p % 2;
+            const int nb = col0 + 128 * wn + 64 * rp + tc;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int m = m0 + 32 * CB * wm + 32 * cb + 4 * i + tq;
+                const bool ok = vec4 && m < M && nb + 3 < N;
+                cv[i] = ok ? *reinterpret_cast<const i32x4 *>(c + static_cast<int64_t>(m) * ldc + nb)
+                           : i32x4{0, 0, 0, 0};
+            }
+        };
+        i32x4 cva[8], cvb[8];
+        if constexpr (kAcc) c_pass(0, cva);
 #pragma unroll
         for (int cb = 0; cb < CB; ++cb) {
 #pragma unroll
             for (int rp = 0; rp < 2; ++rp) {
+                const int pass = 2 * cb + rp;
+                i32x4 (&cvc)[8] = pass % 2 == 0 ? cva : cvb;
+                i32x4 (&cvn)[8] = pass % 2 == 0 ? cvb : cva;
+                if constexpr (kAcc)
+                    if (pass + 1 < kPasses) c_pass(pass + 1, cvn);
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -410,8 +432,8 @@ __global__ __launch_bounds__(kI8Threads) void gemm_w4_i8_kernel(
                     int32_t *cr = c + static_cast<int64_t>(m) * ldc;
                     int32_t y[4] = {v[0], v[1], v[2], v[3]};
                     if (vec4 && nb + 3 < N) {
-                        if (accumulate) {
-                            const i32x4 cv = *reinterpret_cast<const i32x4 *>(cr + nb);
+                        if constexpr (kAcc) {
+                            const i32x4 cv = cvc[i];
                             y[0] += cv[0];
                             y[1] += cv[1];
                             y[2] += cv[2];
@@ -424,7 +446,7 @@ __global__ __launch_bounds__(kI8Threads) void gemm_w4_i8_kernel(
 #pragma unroll
                         for (int b = 0; b < 4; ++b) {
                             const int n = nb + b;
-                            if (n < N) cr[n] = accumulate ? y[b] + cr[n] : y[b];
+                            if (n < N) cr[n] = kAcc ? y[b] + cr[n] : y[b];
                         }
                     }
                 }
@@ -599,17 +621,21 @@ hipError_t launch_gemm_i8(const void *x, const uint8_t *w, int32_t *c, int64_t m
     if (items <= 0) return hipSuccess;
     const int64_t cus = cu_count();
     const dim3 grid(static_cast<unsigned>(items < cus ? items : cus));
-    if (p.half)
-        gemm_w4_i8_kernel<true><<<grid, dim3(kI8Threads), 0, s>>>(
+    // (split items store raw partials; the split sum adds C)
+    if (p.half) {
+        auto kernel = accumulate ? gemm_w4_i8_kernel<true, true> : gemm_w4_i8_kernel<true, false>;
+        kernel<<<grid, dim3(kI8Threads), 0, s>>>(
             static_cast<const int8_t *>(x), w, c, static_cast<int>(m), static_cast<int>(n),
             static_cast<int>(n), static_cast<int>(k), static_cast<int>(L), accumulate ? 1 : 0,
             static_cast<int>(p.n1), 0, nullptr, 0);
-    else
-        gemm_w4_i8_kernel<false><<<grid, dim3(kI8Threads), 0, s>>>(
+    } else {
+        auto kernel = accumulate ? gemm_w4_i8_kernel<false, true> : gemm_w4_i8_kernel<false, false>;
+        kernel<<<grid, dim3(kI8Threads), 0, s>>>(
             static_cast<const int8_t *>(x), w, c, static_cast<int>(m), static_cast<int>(n),
             static_cast<int>(n), static_cast<int>(k), static_cast<int>(L), accumulate ? 1 : 0,
             static_cast<int>(p.n1), split ? static_cast<int>(p.sps) : 0, static_cast<i32x4 *>(ws),
             split ? static_cast<int>(p.nsplit) : 0);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || !split) return e;
     gemm_split_reduce_i8_kernel<<<dim3(static_cast<unsigned>(p.tiles * 16)), dim3(256), 0, s>>>(
