@@ -1143,6 +1143,18 @@ SplitPlan gemm_t_plan(int64_t m, int64_t n, int64_t k) {
     return small_split_plan(tiles, (L + LK - 1) / LK, CM == 1 && tiles >= 64 ? 2 : 1);
 }
 
+// Up to 64 tokens over a long K: the eight-wave kernel takes four limbs per k-step instead
+// of two, so each step's loads (issued one step ahead) meet twice the MFMA work and a launch
+// waits at half as many barriers.  A sweep of two, four and six limbs (float32 at 17..64
+// tokens, bf16 at 49 and 64) on 14336 -> 4096, 11008 -> 4096, 8192 -> 3072, 8192 -> 8192:
+// four wins over K = 14336 (float32 M = 17 29.9 -> 25.1 us, M = 32 34.6 -> 30.9, M = 64
+// 48.7 -> 45.9; bf16 M = 49 34.4 -> 29.4, M = 64 35.8 -> 31.0) and K = 8192 at <= 32
+// tokens (M = 17 on 8192 -> 8192 31.4 -> 27.6), not at 33..64 tokens over K = 8192 (8192 ->
+// 3072 M = 64 30.9 -> 31.6) nor over K = 4096 (4096 -> 6144 M = 48 22.3 -> 34.8, the
+// float32 tiles then fill 102 KB of LDS and a CU holds one workgroup); six measured slower
+// than four except on 8192 -> 8192.
+bool gemm_small_long_k(int64_t m, int64_t k) { return m <= 32 ? k >= 8192 : k > 8192; }
+
 // Rows [0, n) of W and columns [0, n) of C, whose rows are ldc elements apart.  With a
 // workspace of at least nsplit * m * n * 4 bytes, a launch of few tiles splits K.
 template <int XT, int RN, int CM, int WN, int WM, int LK>
@@ -1190,6 +1202,15 @@ hipError_t launch_gemm_x(const void *x, const uint8_t *w, void *c, int64_t m, in
         const hipError_t e = launch_gemv_column_blocks(&handled, x, XT, w, c, static_cast<int>(m),
                                                        n, k, alpha, beta, bias, s);
         if (handled || e != hipSuccess) return e;
+    }
+    // 17..64 tokens that the column-block kernel does not take (float32, long K, unaligned
+    // x): the eight-wave kernel, four limbs per k-step over a long K (gemm_small_long_k)
+    if (m <= 64 && gemm_small_long_k(m, k)) {
+        if (m <= 32)
+            return launch_gemm_t<XT, 2, 1, 4, 1, 2 * LK>(x, w, c, m, n, n, k, alpha, beta, bias, s,
+                                                         ws, ws_bytes);
+        return launch_gemm_t<XT, 2, 2, 4, 1, 2 * LK>(x, w, c, m, n, n, k, alpha, beta, bias, s, ws,
+                                                     ws_bytes);
     }
     if (m <= 32)
         return launch_gemm_t<XT, 2, 1, 4, 1, LK>(x, w, c, m, n, n, k, alpha, beta, bias, s, ws,
@@ -1261,16 +1282,20 @@ hipError_t launch_gemm(const void *x, int x_dtype, const uint8_t *w, void *c, in
 namespace {
 
 // Workspace of an eight-wave launch over m x n: nsplit row-major m x n partials.
-template <int XT, int RN, int CM, int WN, int WM>
+template <int XT, int RN, int CM, int WN, int WM, int LK = 2>
 int64_t gemm_t_workspace(int64_t m, int64_t n, int64_t k) {
-    const SplitPlan p = gemm_t_plan<XT, RN, CM, WN, WM, 2>(m, n, k);
+    const SplitPlan p = gemm_t_plan<XT, RN, CM, WN, WM, LK>(m, n, k);
     return p.nsplit > 1 ? p.nsplit * m * n * 4 : 0;
 }
 
 template <int XT>
 int64_t gemm_workspace_x(int64_t m, int64_t n, int64_t k) {
-    if (m <= 32) return gemm_t_workspace<XT, 2, 1, 4, 1>(m, n, k);
-    if (m <= 64) return gemm_t_workspace<XT, 2, 2, 4, 1>(m, n, k);
+    if (m <= 32)
+        return gemm_small_long_k(m, k) ? gemm_t_workspace<XT, 2, 1, 4, 1, 4>(m, n, k)
+                                       : gemm_t_workspace<XT, 2, 1, 4, 1>(m, n, k);
+    if (m <= 64)
+        return gemm_small_long_k(m, k) ? gemm_t_workspace<XT, 2, 2, 4, 1, 4>(m, n, k)
+                                       : gemm_t_workspace<XT, 2, 2, 4, 1>(m, n, k);
     if constexpr (XT == kDtypeF32) {
         return gemm_t_workspace<XT, 2, 4, 4, 1>(m, n, k);
     } else {

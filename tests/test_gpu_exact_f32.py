@@ -16,7 +16,9 @@ by a bit-exact result; float activations enter at t81/torch/__init__.py:241-246)
 * K2 wave / stream kernels at 5..8 tokens;
 * K2 tile kernel at 9..16 tokens over K >= 6144 with its split sum in the workspace,
   and the stream kernel for the wider shapes it leaves;
-* K3 eight-wave kernel at 17..64 tokens, with the K split over a workspace and without;
+* K3 eight-wave kernel at 17..64 tokens, on aligned x (vector loads) and on x one element
+  off 16-byte alignment (element loads), two or four limbs per k-step (four over a long
+  K), with the K split over a workspace and without;
 * K3 at M > 64, including the config-4 shape 4096 -> 6144 at M = 512, every output
   against a float64 product of the unpacked trits on the GPU (exact) and a sample
   against the C oracle.
@@ -65,11 +67,17 @@ def assert_bits(got: np.ndarray, want: np.ndarray, what: str) -> None:
                              f"{i}: got {got[i]!r}, want {want[i]!r}")
 
 
-def run_cases(gpu, orc, M, N, K, seed, kernel, what):
+def run_cases(gpu, orc, M, N, K, seed, kernel, what, offset=0):
+    """offset: x starts that many float32 elements into its buffer (1 moves it off the
+    16-byte alignment the staged kernels need)."""
     w, a, b, x, c, bias = problem(M, N, K, seed)
     packed = ops.quantize_pack(w.to(gpu), 0.45, _lib.THR_CPP)
     acc = fixed_point_acc256(orc, a, b, packed.cpu().numpy(), K)
-    xg, cg, bg = x.to(gpu), c.to(gpu), bias.to(gpu)
+    store = torch.zeros(M * K + 4, dtype=torch.float32, device=gpu)
+    xg = store[offset:offset + M * K].view(M, K)
+    xg.copy_(x.to(gpu))
+    assert xg.data_ptr() % 16 == 4 * offset
+    cg, bg = c.to(gpu), bias.to(gpu)
     for alpha, beta, use_bias in EPILOGUES:
         out = ops.ternary_matmul(xg, packed, K, alpha=alpha, beta=beta,
                                  c=cg.clone() if beta else None,
@@ -119,20 +127,36 @@ def test_gemv_tile_f32_bit_exact(gpu, orc, M, K, N, split):
     run_cases(gpu, orc, M, N, K, seed=M * 41 + K + N, kernel=2, what="K2 tile")
 
 
+# ---------------------------------------------- K3 eight-wave, aligned x, 17..64 --
+ALIGNED = [(17, 4100, 3000), (24, 3072, 3072), (32, 4096, 14336), (32, 14336, 4096),
+           (33, 3072, 9216), (40, 8192, 3072), (32, 8192, 3072), (48, 4104, 1000),
+           (49, 4096, 6144), (64, 14336, 4096), (64, 3072, 16384), (20, 1000, 37)]
+
+
+@pytest.mark.parametrize("M,K,N", ALIGNED)
+def test_k3_small_m_aligned_f32_bit_exact(gpu, orc, M, K, N):
+    """17..64 tokens at a 16-byte aligned x: the eight-wave kernel's vector-load path, two
+    limbs per k-step, four over K >= 8192 (<= 32 tokens) or K > 8192, split over the
+    workspace."""
+    announce(f"exact f32 K3 aligned M={M} K={K} N={N}")
+    run_cases(gpu, orc, M, N, K, seed=M * 53 + K + N, kernel=3, what="aligned")
+
+
 # ------------------------------------------------------ K3 eight-wave, 17..64 --
 EIGHT = [(48, 4104, 1000), (32, 3000, 4096), (64, 4096, 6144), (17, 4100, 3000),
-         (20, 14336, 4096), (33, 3072, 9216), (64, 8192, 3072)]
+         (20, 14336, 4096), (33, 3072, 9216), (64, 8192, 3072), (17, 8192, 8192)]
 
 
 @pytest.mark.parametrize("M,K,N", EIGHT)
 def test_k3_eight_wave_f32_bit_exact(gpu, orc, M, K, N):
-    """17..64 tokens: with the workspace (K split, partial sums added in split order by a
-    second kernel) and without it (one launch over all of K)."""
+    """17..64 tokens with x one element off 16-byte alignment (element loads): with the
+    workspace (K split, partial sums added in split order by a second kernel) and without
+    it (one launch over all of K)."""
     announce(f"exact f32 K3 eight-wave M={M} K={K} N={N}")
     lib = _lib.lib()
     assert lib.t81_hip_ternary_matmul_workspace_size(M, N, K, _lib.DTYPE_F32) > 0
     packed, acc, xg, cg, bg, c, bias = run_cases(gpu, orc, M, N, K, seed=M * 43 + K + N,
-                                                 kernel=3, what="split-K")
+                                                 kernel=3, what="split-K", offset=1)
     s = torch.cuda.current_stream().cuda_stream
     for alpha, beta, use_bias in EPILOGUES:
         plain = cg.clone()
