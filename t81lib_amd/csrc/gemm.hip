@@ -1139,8 +1139,10 @@ SplitPlan gemm_t_plan(int64_t m, int64_t n, int64_t k) {
     const int64_t L = (k + kTrits - 1) / kTrits;
     const int64_t tiles = ((n + Cfg::kBN - 1) / Cfg::kBN) * ((m + Cfg::kBM - 1) / Cfg::kBM);
     // 32-token tiles over wide N (>= 64 tiles): two workgroups per CU, whose partials
-    // are small at this M (llama.gate_up M = 32: 47 -> 35 us); elsewhere one.
-    return small_split_plan(tiles, (L + LK - 1) / LK, CM == 1 && tiles >= 64 ? 2 : 1);
+    // are small at this M (llama.gate_up M = 32: 47 -> 35 us); the 128-row tiles of a long
+    // K (gemm_small_rows) too; elsewhere one.
+    const bool two = (CM == 1 && tiles >= 64) || (RN == 1 && LK == 4);
+    return small_split_plan(tiles, (L + LK - 1) / LK, two ? 2 : 1);
 }
 
 // Up to 64 tokens over a long K: the eight-wave kernel takes four limbs per k-step instead
@@ -1154,6 +1156,19 @@ SplitPlan gemm_t_plan(int64_t m, int64_t n, int64_t k) {
 // float32 tiles then fill 102 KB of LDS and a CU holds one workgroup); six measured slower
 // than four except on 8192 -> 8192.
 bool gemm_small_long_k(int64_t m, int64_t k) { return m <= 32 ? k >= 8192 : k > 8192; }
+
+// On that path, 128-row tiles (two workgroups per CU) instead of 256-row ones where the
+// 256-row grid has fewer than 64 tiles: more workgroups share the K split, and two per CU
+// hide each other's step latency.  Not for float32 at 33..64 tokens, whose 64-token tiles
+// of two planes already fill 102 KB of LDS (14336 -> 4096 at 64 tokens 45.9 -> 63.5 us).
+// Same box, against 256-row tiles: bf16 14336 -> 4096 at 49 / 64 tokens 29.3 / 31.0 ->
+// 25.9 / 26.8 us, 11008 -> 4096 23.9 / 25.1 -> 23.7 / 23.4; float32 at 17 / 32 tokens
+// 14336 -> 4096 25.2 / 31.1 -> 24.0 / 27.2, 8192 -> 8192 27.7 / 32.7 -> 24.8 / 28.2,
+// 8192 -> 3072 18.1 / 21.1 -> 17.1 / 19.5.
+template <int XT>
+bool gemm_small_rows(int64_t m, int64_t n) {
+    return (XT != kDtypeF32 || m <= 32) && n < 64 * 256;
+}
 
 // Rows [0, n) of W and columns [0, n) of C, whose rows are ldc elements apart.  With a
 // workspace of at least nsplit * m * n * 4 bytes, a launch of few tiles splits K.
@@ -1206,11 +1221,16 @@ hipError_t launch_gemm_x(const void *x, const uint8_t *w, void *c, int64_t m, in
     // 17..64 tokens that the column-block kernel does not take (float32, long K, unaligned
     // x): the eight-wave kernel, four limbs per k-step over a long K (gemm_small_long_k)
     if (m <= 64 && gemm_small_long_k(m, k)) {
+        const bool rows128 = gemm_small_rows<XT>(m, n);
         if (m <= 32)
-            return launch_gemm_t<XT, 2, 1, 4, 1, 2 * LK>(x, w, c, m, n, n, k, alpha, beta, bias, s,
-                                                         ws, ws_bytes);
-        return launch_gemm_t<XT, 2, 2, 4, 1, 2 * LK>(x, w, c, m, n, n, k, alpha, beta, bias, s, ws,
-                                                     ws_bytes);
+            return rows128 ? launch_gemm_t<XT, 1, 1, 4, 1, 2 * LK>(x, w, c, m, n, n, k, alpha, beta,
+                                                                   bias, s, ws, ws_bytes)
+                           : launch_gemm_t<XT, 2, 1, 4, 1, 2 * LK>(x, w, c, m, n, n, k, alpha, beta,
+                                                                   bias, s, ws, ws_bytes);
+        return rows128 ? launch_gemm_t<XT, 1, 2, 4, 1, 2 * LK>(x, w, c, m, n, n, k, alpha, beta,
+                                                               bias, s, ws, ws_bytes)
+                       : launch_gemm_t<XT, 2, 2, 4, 1, 2 * LK>(x, w, c, m, n, n, k, alpha, beta,
+                                                               bias, s, ws, ws_bytes);
     }
     if (m <= 32)
         return launch_gemm_t<XT, 2, 1, 4, 1, LK>(x, w, c, m, n, n, k, alpha, beta, bias, s, ws,
@@ -1290,12 +1310,16 @@ int64_t gemm_t_workspace(int64_t m, int64_t n, int64_t k) {
 
 template <int XT>
 int64_t gemm_workspace_x(int64_t m, int64_t n, int64_t k) {
-    if (m <= 32)
-        return gemm_small_long_k(m, k) ? gemm_t_workspace<XT, 2, 1, 4, 1, 4>(m, n, k)
-                                       : gemm_t_workspace<XT, 2, 1, 4, 1>(m, n, k);
-    if (m <= 64)
-        return gemm_small_long_k(m, k) ? gemm_t_workspace<XT, 2, 2, 4, 1, 4>(m, n, k)
-                                       : gemm_t_workspace<XT, 2, 2, 4, 1>(m, n, k);
+    if (m <= 64 && gemm_small_long_k(m, k)) {
+        const bool rows128 = gemm_small_rows<XT>(m, n);
+        if (m <= 32)
+            return rows128 ? gemm_t_workspace<XT, 1, 1, 4, 1, 4>(m, n, k)
+                           : gemm_t_workspace<XT, 2, 1, 4, 1, 4>(m, n, k);
+        return rows128 ? gemm_t_workspace<XT, 1, 2, 4, 1, 4>(m, n, k)
+                       : gemm_t_workspace<XT, 2, 2, 4, 1, 4>(m, n, k);
+    }
+    if (m <= 32) return gemm_t_workspace<XT, 2, 1, 4, 1>(m, n, k);
+    if (m <= 64) return gemm_t_workspace<XT, 2, 2, 4, 1>(m, n, k);
     if constexpr (XT == kDtypeF32) {
         return gemm_t_workspace<XT, 2, 4, 4, 1>(m, n, k);
     } else {

@@ -146,6 +146,53 @@ def test_two_block_integer_bf16_bit_exact(gpu, orc, name, M, K, N):
         assert_bits(out.cpu().numpy(), want, f"alpha={alpha} beta={beta} bias={use_bias}")
 
 
+SMALL_LONG_K = [
+    # M, K, N: 49..64 tokens over K > 8192, which the column-block kernel leaves to the
+    # eight-wave kernel: four limbs per k-step, 128-row tiles two per CU below 16384 rows
+    # (256-row tiles from 16384), the K split over the workspace; ragged K and N
+    (49, 14336, 4096), (64, 11008, 4096), (64, 14336, 16384), (57, 9000, 1000),
+]
+
+
+@pytest.mark.parametrize("M,K,N", SMALL_LONG_K)
+@pytest.mark.parametrize("dt", ["bf16", "int8"])
+def test_small_m_long_k_bit_exact(gpu, orc, M, K, N, dt):
+    """bf16 (integer values) and int8 activations, with the workspace (split K) and without
+    it (one launch over all of K): every output equals the int64 oracle."""
+    announce(f"exact small-M long-K {dt} M={M} K={K} N={N}")
+    lib = _lib.lib()
+    code = _lib.DTYPE_BF16 if dt == "bf16" else _lib.DTYPE_I8
+    assert lib.t81_hip_ternary_matmul_workspace_size(M, N, K, code) > 0
+    w, x, c, bias = int_problem(M, N, K, seed=M * 7 + K + N)
+    packed = ops.quantize_pack(w.to(gpu), 0.45, _lib.THR_CPP)
+    acc = orc.trit_matmul_i64(x.to(torch.int8).numpy(), packed.cpu().numpy(), K)
+    xg = (x.to(torch.bfloat16) if dt == "bf16" else x.to(torch.int8)).to(gpu)
+    s = torch.cuda.current_stream().cuda_stream
+    if dt == "bf16":
+        cg = c.to(gpu)
+        for alpha, beta, use_bias in ((1.0, 0.0, False), (0.5, 1.0, True)):
+            want = expected(acc, alpha, beta, c.numpy(), bias.numpy() if use_bias else None)
+            out = ops.ternary_matmul(xg, packed, K, alpha=alpha, beta=beta,
+                                     c=cg.clone() if beta else None,
+                                     bias=bias.to(gpu) if use_bias else None, kernel=3)
+            assert_bits(out.cpu().numpy(), want, f"split alpha={alpha} beta={beta}")
+            plain = cg.clone()
+            _lib.check(lib.t81_hip_ternary_matmul(
+                xg.data_ptr(), code, packed.data_ptr(), plain.data_ptr(), M, N, K, alpha, beta,
+                bias.to(gpu).data_ptr() if use_bias else None, s))
+            assert_bits(plain.cpu().numpy(), want, f"no workspace alpha={alpha} beta={beta}")
+    else:
+        ci = torch.randint(-(1 << 20), 1 << 20, (M, N), dtype=torch.int32)
+        out = ops.ternary_matmul(xg, packed, K, kernel=3)
+        np.testing.assert_array_equal(out.cpu().numpy().astype(np.int64), acc)
+        out = ops.ternary_matmul(xg, packed, K, beta=1.0, c=ci.to(gpu), kernel=3)
+        np.testing.assert_array_equal(out.cpu().numpy().astype(np.int64), acc + ci.numpy())
+        plain = ci.to(gpu)
+        _lib.check(lib.t81_hip_ternary_matmul(xg.data_ptr(), code, packed.data_ptr(),
+                                              plain.data_ptr(), M, N, K, 1.0, 1.0, None, s))
+        np.testing.assert_array_equal(plain.cpu().numpy().astype(np.int64), acc + ci.numpy())
+
+
 # --------------------------------------------------------------------- K3 --
 def _sample(M, N, n1, seed, tokens=48, rows=96):
     """Tokens from every 256-token tile; rows from both the whole-tile region [0, n1)
