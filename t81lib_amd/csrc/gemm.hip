@@ -1154,8 +1154,14 @@ SplitPlan gemm_t_plan(int64_t m, int64_t n, int64_t k) {
 // tokens (M = 17 on 8192 -> 8192 31.4 -> 27.6), not at 33..64 tokens over K = 8192 (8192 ->
 // 3072 M = 64 30.9 -> 31.6) nor over K = 4096 (4096 -> 6144 M = 48 22.3 -> 34.8, the
 // float32 tiles then fill 102 KB of LDS and a CU holds one workgroup); six measured slower
-// than four except on 8192 -> 8192.
-bool gemm_small_long_k(int64_t m, int64_t k) { return m <= 32 ? k >= 8192 : k > 8192; }
+// than four except on 8192 -> 8192.  At <= 32 tokens the same form (with the 128-row tiles
+// below) also wins over a short K on 8192 or more rows (float32 4096 -> 14336 at 17 / 32
+// tokens 26.5 / 29.0 -> 21.7 / 25.4 us, 3072 -> 9216 18.6 / 20.5 -> 15.8 / 18.6, 3072 ->
+// 16384 19.0 / 22.9 -> 18.9 / 23.2) and loses on 4096 -> 6144 (14.8 / 15.8 -> 16.2 / 19.1)
+// and 4096 -> 4096 (12.8 / 14.0 -> 14.2 / 16.4).
+bool gemm_small_long_k(int64_t m, int64_t n, int64_t k) {
+    return m <= 32 ? k >= 8192 || n >= 8192 : k > 8192;
+}
 
 // On that path, 128-row tiles (two workgroups per CU) instead of 256-row ones where the
 // 256-row grid has fewer than 64 tiles: more workgroups share the K split, and two per CU
@@ -1219,8 +1225,9 @@ hipError_t launch_gemm_x(const void *x, const uint8_t *w, void *c, int64_t m, in
         if (handled || e != hipSuccess) return e;
     }
     // 17..64 tokens that the column-block kernel does not take (float32, long K, unaligned
-    // x): the eight-wave kernel, four limbs per k-step over a long K (gemm_small_long_k)
-    if (m <= 64 && gemm_small_long_k(m, k)) {
+    // x): the eight-wave kernel, four limbs per k-step over a long K, or over many rows at
+    // <= 32 tokens (gemm_small_long_k)
+    if (m <= 64 && gemm_small_long_k(m, n, k)) {
         const bool rows128 = gemm_small_rows<XT>(m, n);
         if (m <= 32)
             return rows128 ? launch_gemm_t<XT, 1, 1, 4, 1, 2 * LK>(x, w, c, m, n, n, k, alpha, beta,
@@ -1310,7 +1317,7 @@ int64_t gemm_t_workspace(int64_t m, int64_t n, int64_t k) {
 
 template <int XT>
 int64_t gemm_workspace_x(int64_t m, int64_t n, int64_t k) {
-    if (m <= 64 && gemm_small_long_k(m, k)) {
+    if (m <= 64 && gemm_small_long_k(m, n, k)) {
         const bool rows128 = gemm_small_rows<XT>(m, n);
         if (m <= 32)
             return rows128 ? gemm_t_workspace<XT, 1, 1, 4, 1, 4>(m, n, k)

@@ -136,15 +136,16 @@ ALIGNED = [(17, 4100, 3000), (24, 3072, 3072), (32, 4096, 14336), (32, 14336, 40
 @pytest.mark.parametrize("M,K,N", ALIGNED)
 def test_k3_small_m_aligned_f32_bit_exact(gpu, orc, M, K, N):
     """17..64 tokens at a 16-byte aligned x: the eight-wave kernel's vector-load path, two
-    limbs per k-step, four over K >= 8192 (<= 32 tokens) or K > 8192, split over the
-    workspace."""
+    limbs per k-step, four (and 128-row tiles below 16384 rows) over K > 8192, or at <= 32
+    tokens over K >= 8192 or N >= 8192; split over the workspace."""
     announce(f"exact f32 K3 aligned M={M} K={K} N={N}")
     run_cases(gpu, orc, M, N, K, seed=M * 53 + K + N, kernel=3, what="aligned")
 
 
 # ------------------------------------------------------ K3 eight-wave, 17..64 --
 EIGHT = [(48, 4104, 1000), (32, 3000, 4096), (64, 4096, 6144), (17, 4100, 3000),
-         (20, 14336, 4096), (33, 3072, 9216), (64, 8192, 3072), (17, 8192, 8192)]
+         (20, 14336, 4096), (33, 3072, 9216), (64, 8192, 3072), (17, 8192, 8192),
+         (24, 3072, 9216)]
 
 
 @pytest.mark.parametrize("M,K,N", EIGHT)
