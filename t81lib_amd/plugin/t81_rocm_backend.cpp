@@ -241,7 +241,10 @@ void gemm_ternary(const void *X, TritActivation x_type, std::span<const core::li
     detail::DeviceView x(X, xb, true), w(W.data(), W.size_bytes(), true);
     detail::DeviceView c(C, cb, beta != 0.0f), b(bias, bias ? static_cast<std::size_t>(N) * 4 : 0, true);
     hipStream_t s = static_cast<hipStream_t>(stream);
-    // K3's split-K workspace for shapes with few output tiles, stream-ordered
+    // K3's split-K workspace for shapes with few output tiles, from the stream-ordered pool
+    // (a pool allocation, freed in stream order): calls on different streams may run at the
+    // same time, which t81_hip_ternary_matmul_noalloc's one static scratch per device does
+    // not allow
     const std::int64_t wsb = t81_hip_ternary_matmul_workspace_size(M, N, K, code);
     void *ws = nullptr;
     if (wsb > 0) detail::check_hip(hipMallocAsync(&ws, static_cast<std::size_t>(wsb), s), "hipMallocAsync");
