@@ -618,12 +618,14 @@ DECODE_SHAPES = [("phi3.qkv", 3072, 9216), ("phi3.o", 3072, 3072), ("phi3.gate_u
 
 def run_decode(torch, ops, lib, dev, only_case=None) -> dict:
     """Config 3 (Phi-3 decode shapes) and the Llama-3-8B gate / down shapes at 1, 4, 8 and
-    16 tokens, and at 32 (config 5's decode batch) and 48, through the product path
+    16 tokens, and at 32 (config 5's decode batch), 48 and 64, through the product path
     (ops.ternary_matmul: K2 up to 16 tokens, with the workspace its K splits use; the K3
-    entry at 32 and 48, whose bf16 calls run K2's column-block stream kernel with two and
-    three 16-token blocks): median microseconds
-    per call over rotating weight copies (> 2 x MALL, so every call streams from HBM), GB/s
-    of algorithmic bytes, and each shape's 16-token time over its one-token time."""
+    entry from 17, whose bf16 calls run K2's column-block stream kernel with two and three
+    16-token blocks, two launches at 49..64, or the eight-wave kernel at 49..64 over K >
+    8192): median microseconds per call over rotating weight copies (> 2 x MALL, so every
+    call streams from HBM), GB/s of algorithmic bytes, and each shape's 16-token time over
+    its one-token time.  The Llama shapes also with float32 activations at 16..64 tokens
+    (keys f32_M*), the form t8.nn.Linear's float inputs take."""
     shapes = {}
     todo = DECODE_SHAPES if only_case is None else [("case", only_case[0], only_case[1])]
     for name, k, n in todo:
@@ -631,25 +633,31 @@ def run_decode(torch, ops, lib, dev, only_case=None) -> dict:
         copies = max(4, -(-2 * MALL_BYTES // wbytes) + 2)
         wb = make_weights(torch, ops, lib, n, k, copies, dev, seed=3)
         row = {"K": k, "N": n}
-        for m in ((1, 4, 8, 16, 32, 48) if only_case is None else (only_case[2],)):
-            x = torch.randn((m, k), device=dev).to(torch.bfloat16)
+        runs = [("", torch.bfloat16, m) for m in
+                ((1, 4, 8, 16, 32, 48, 64) if only_case is None else (only_case[2],))]
+        if only_case is None and name.startswith("llama"):
+            runs += [("f32_", torch.float32, m) for m in (16, 32, 48, 64)]
+        for tag, dt, m in runs:
+            x = torch.randn((m, k), device=dev).to(dt)
             out = torch.empty((m, n), device=dev)
             d = time_graph(torch, lambda w: ops.ternary_matmul(x, w, k, c=out), wb, 256, 32,
                            dist=True, min_launches=100, min_ms=20.0)
             us = d["median_ms"] * 1e3
-            row[f"M{m}_us"] = round(us, 3)
-            row[f"M{m}_GBps"] = round(gemv_bytes(m, n, k) / (us * 1e-6) / 1e9, 1)
-            log(f"decode {name:13s} M={m:2d} {k:5d}->{n:5d}: {us:7.2f} us")
+            row[f"{tag}M{m}_us"] = round(us, 3)
+            row[f"{tag}M{m}_GBps"] = round(gemv_bytes(m, n, k, 4 if tag else 2) / (us * 1e-6)
+                                           / 1e9, 1)
+            log(f"decode {name:13s} {tag or 'bf16_'}M={m:2d} {k:5d}->{n:5d}: {us:7.2f} us")
             del x, out
         if only_case is None:
             row["M16_over_M1"] = round(row["M16_us"] / row["M1_us"], 3)
         shapes[name] = row
         del wb
         torch.cuda.empty_cache()
-    return {"workload": "K2 decode at 1-16 tokens (32, 48: the K3 entry, K2's column-block "
-                        "kernel), "
+    return {"workload": "K2 decode at 1-16 tokens (32, 48, 64: the K3 entry -- K2's "
+                        "column-block kernel, or the eight-wave kernel at 64 over K > 8192), "
                         "bf16 x, fp32 out, alpha=1 beta=0, median over rotating weight copies; "
-                        "config 3 (Phi-3) plus the Llama-3-8B gate / down shapes",
+                        "config 3 (Phi-3) plus the Llama-3-8B gate / down shapes, those also "
+                        "with float32 x at 16-64 tokens (f32_M*)",
             "shapes": shapes}
 
 

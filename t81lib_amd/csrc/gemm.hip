@@ -1358,14 +1358,16 @@ int64_t gemm_workspace_bytes(int64_t m, int64_t n, int64_t k, int x_dtype) {
     if (m <= 0 || n <= 0 || k <= 0) return 0;
     switch (x_dtype) {
         case kDtypeBF16:
-            // 17..48 tokens (64 with K <= 8192) with K % 8 == 0 take the column-block stream
-            // kernel: no workspace
-            if (m >= 17 && m <= (k <= 8192 ? 64 : 48) && k % 8 == 0) return 0;
+            // the column-block stream kernel's shapes (17..gemv_column_blocks_max_tokens
+            // tokens, K % 8 == 0): no workspace
+            if (m >= 17 && m <= gemv_column_blocks_max_tokens(k, x_dtype) && k % 8 == 0)
+                return 0;
             return gemm_workspace_x<kDtypeBF16>(m, n, k);
         case kDtypeF32: return gemm_workspace_x<kDtypeF32>(m, n, k);
         default:
             // int8 the same with K % 16 == 0
-            if (m >= 17 && m <= (k <= 8192 ? 64 : 48) && k % 16 == 0) return 0;
+            if (m >= 17 && m <= gemv_column_blocks_max_tokens(k, x_dtype) && k % 16 == 0)
+                return 0;
             return gemm_workspace_x<kDtypeI8>(m, n, k);
     }
 }

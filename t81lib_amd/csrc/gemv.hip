@@ -1238,8 +1238,9 @@ hipError_t launch_gemv_x(const void *x, const uint8_t *w, void *c, int m, int64_
 
 }  // namespace
 
-// 17..48 tokens (64 with K <= 8192) with aligned bf16 activations (called by the K3
-// launcher, which owns M > 16): the column-block stream kernel, no workspace.  17..32
+// 17..48 tokens (64 with K <= 8192, bf16 32 from K = 12288: gemv_column_blocks_max_tokens)
+// with aligned bf16 activations (called by the K3 launcher, which owns M > 16): the
+// column-block stream kernel, no workspace.  17..32
 // tokens, two blocks: row groups per workgroup and waves from a sweep of 1, 2, 4 groups x
 // 4, 8 waves at 17, 24 and 32 tokens on the config-3/4 shapes, against the eight-wave GEMM
 // kernel with its K split: at 32 tokens llama.qkv 15.8 -> 9.9 us, 4096 -> 4096 13.9 ->
@@ -1298,12 +1299,24 @@ hipError_t launch_gemv_column_blocks(bool *handled, const void *x, int x_dtype,
     return shape(std::integral_constant<int, kDtypeBF16>());
 }
 
+int64_t gemv_column_blocks_max_tokens(int64_t k, int x_dtype) {
+    // 64 up to K = 8192 (49..64 as two launches), else 48; bf16 32 from K = 12288: over the
+    // longest K the eight-wave kernel's four-limb, 128-row form is faster at 33..48 bf16
+    // tokens (14336 -> 4096 at 33 / 48 tokens 26.5 / 27.6 -> 25.0 / 25.0 us, 14336 -> 8192
+    // 33.9 / 34.9 -> 29.6 / 31.3) while over 11008 it is not (20.9 / 21.1 -> 23.2 / 23.6),
+    // nor at 17..32 tokens (14336 -> 4096 at 32 19.1 against 22.6), nor for int8, whose
+    // column blocks stage a third of the bytes (14336 -> 4096 at 48 29.2 us against 37.4 at
+    // 49 in the eight-wave kernel)
+    if (k <= 8192) return 64;
+    return x_dtype == kDtypeBF16 && k >= 12288 ? 32 : 48;
+}
+
 bool gemv_column_blocks_fits(const void *x, int x_dtype, int64_t m, int64_t n, int64_t k) {
     // 16-byte pieces of whole 8-value (bf16) or 16-value (int8) chunks; block offsets
     // (16 rows x N) and grid in range
     const int64_t chunk = x_dtype == kDtypeI8 ? 16 : 8;
     return (x_dtype == kDtypeBF16 || x_dtype == kDtypeI8) && m >= 17 &&
-           m <= (k <= 8192 ? 64 : 48) && n > 0 && k > 0 && k % chunk == 0 &&
+           m <= gemv_column_blocks_max_tokens(k, x_dtype) && n > 0 && k > 0 && k % chunk == 0 &&
            reinterpret_cast<uintptr_t>(x) % 16 == 0 && (n + 15) / 16 < (int64_t(1) << 31) &&
            k < (int64_t(1) << 31);
 }

@@ -35,9 +35,11 @@ hipError_t launch_validate(const uint8_t *packed, int64_t count, int32_t *bad, h
 // gemv.hip (K2): M <= 16.  ws (ws_bytes of device memory, may be null) lets 9..16 tokens
 // over a long K split it over workgroups (float32 activations, int8 with K % 16 != 0,
 // bf16 with K % 8 != 0); gemv_workspace_bytes says how much a shape uses.
-// 17..48 tokens (64 with K <= 8192), bf16 (K % 8 == 0) or int8 (K % 16 == 0) activations
-// at a 16-byte aligned x: the column-block stream kernel of gemv.hip (two or three 16-token
-// blocks; 49..64 tokens as two launches); the K3 launcher tries it first.
+// 17..gemv_column_blocks_max_tokens(K, dtype) tokens (64 up to K = 8192, else 48; bf16 32
+// from K = 12288), bf16 (K % 8 == 0) or int8 (K % 16 == 0) activations at a 16-byte aligned
+// x: the column-block stream kernel of gemv.hip (two or three 16-token blocks; 49..64 tokens
+// as two launches); the K3 launcher tries it first.
+int64_t gemv_column_blocks_max_tokens(int64_t k, int x_dtype);
 bool gemv_column_blocks_fits(const void *x, int x_dtype, int64_t m, int64_t n, int64_t k);
 hipError_t launch_gemv_column_blocks(bool *handled, const void *x, int x_dtype,
                                      const uint8_t *w, void *c, int m, int64_t n, int64_t k,

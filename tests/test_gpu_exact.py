@@ -119,9 +119,9 @@ TWO_BLOCK_CASES = [
     ("llama.down", 17, 14336, 4096), ("llama.gate", 24, 4096, 14336), ("llama.qkv", 32, 4096, 6144),
     ("phi3.o", 32, 3072, 3072), ("phi3.down", 32, 8192, 3072), ("phi3.gate_up", 32, 3072, 16384),
     ("ragged", 29, 4104, 333),
-    # 33..48 tokens: three blocks, eight waves (one row group per workgroup up to 4096 rows,
-    # two above); a third block of one token, of 16, and ragged shapes
-    ("llama.down", 33, 14336, 4096), ("llama.gate", 48, 4096, 14336), ("llama.qkv", 40, 4096, 6144),
+    # 33..48 tokens below K = 12288: three blocks, eight waves (one row group per workgroup
+    # up to 4096 rows, two above); a third block of one token, of 16, and ragged shapes
+    ("llama2.down", 33, 11008, 4096), ("llama.gate", 48, 4096, 14336), ("llama.qkv", 40, 4096, 6144),
     ("phi3.o", 48, 3072, 3072), ("phi3.down", 45, 8192, 3072), ("ragged", 37, 4104, 4133),
     # 49..64 tokens: two launches (tokens 0..31, then the rest: 17..32 of them)
     ("llama.gate", 64, 4096, 14336), ("phi3.o", 49, 3072, 3072), ("ragged", 57, 4104, 4133),
@@ -147,15 +147,19 @@ def test_two_block_integer_bf16_bit_exact(gpu, orc, name, M, K, N):
 
 
 SMALL_LONG_K = [
-    # M, K, N: 49..64 tokens over K > 8192, which the column-block kernel leaves to the
-    # eight-wave kernel: four limbs per k-step, 128-row tiles two per CU below 16384 rows
-    # (256-row tiles from 16384), the K split over the workspace; ragged K and N
-    (49, 14336, 4096), (64, 11008, 4096), (64, 14336, 16384), (57, 9000, 1000),
+    # M, K, N, dtypes: 49..64 tokens over K > 8192 (and bf16 33..48 over K >= 12288), which
+    # the column-block kernel leaves to the eight-wave kernel: four limbs per k-step, 128-row
+    # tiles two per CU below 16384 rows (256-row tiles from 16384), the K split over the
+    # workspace; ragged K and N
+    (49, 14336, 4096, "bf16"), (64, 11008, 4096, "bf16"), (64, 14336, 16384, "bf16"),
+    (57, 9000, 1000, "bf16"), (33, 14336, 4096, "bf16"), (48, 12288, 8192, "bf16"),
+    (40, 13000, 999, "bf16"),
+    (49, 14336, 4096, "int8"), (64, 11008, 4096, "int8"), (64, 14336, 16384, "int8"),
+    (57, 9000, 1000, "int8"),
 ]
 
 
-@pytest.mark.parametrize("M,K,N", SMALL_LONG_K)
-@pytest.mark.parametrize("dt", ["bf16", "int8"])
+@pytest.mark.parametrize("M,K,N,dt", SMALL_LONG_K)
 def test_small_m_long_k_bit_exact(gpu, orc, M, K, N, dt):
     """bf16 (integer values) and int8 activations, with the workspace (split K) and without
     it (one launch over all of K): every output equals the int64 oracle."""

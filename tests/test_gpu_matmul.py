@@ -473,7 +473,8 @@ def test_k2_tile_kernel_plans(gpu, orc, M, N, K, dtype, splits):
                                          (20, 20000, 2008, torch.int8)])
 def test_k3_eight_wave_split_k_full_check(gpu, orc, M, N, K, dtype):
     """Launches of the eight-wave kernel with few tiles (17 <= M <= 64: fp32 activations,
-    int8 with K % 16 != 0, bf16 with K % 8 != 0 or, past 48 tokens, K > 8192) split K: each
+    int8 with K % 16 != 0, bf16 with K % 8 != 0 or, past 48 tokens, K > 8192, past 32
+    tokens, K >= 12288 for bf16) split K: each
     split writes its raw sums (int32 for int8, exact) as a row-major M x N matrix in the
     workspace and a second kernel adds them in split order.  Every output against the
     oracle, with and without the workspace; int8 bit-exact."""
