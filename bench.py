@@ -375,7 +375,10 @@ class DecoderStack:
     """Random-init ternary decoder: weights ~ N(0, 1) (the effective W / 0.02, so the
     0.45 threshold leaves ~1/3 zero trits; literal N(0, 0.02) weights would all be zero),
     embedding and lm_head ~ N(0, 0.02) in bf16.  ``reference=True`` replaces each packed
-    linear by F.linear in float32 with the same trits (the test oracle of the stack)."""
+    linear by F.linear in float32 with the same trits (the test oracle of the stack);
+    ``reference="split"`` does the same with K summed as two halves, a second float32
+    summation order (the tests use its distance from the first as the scale of rounding
+    drift through the stack)."""
 
     def __init__(self, torch, dev, layers, hidden, heads, kv_heads, ffn, vocab, max_batch,
                  max_tokens, seed=0, reference=False):
@@ -423,6 +426,10 @@ class DecoderStack:
         self.cos, self.sin = ang.cos(), ang.sin()            # (T, hd / 2)
 
     def _linear(self, blk, name, x2d):
+        if self.reference == "split":
+            h = x2d.shape[-1] // 2
+            xf, wt = x2d.float(), blk[name]
+            return self.F.linear(xf[:, :h], wt[:, :h]) + self.F.linear(xf[:, h:], wt[:, h:])
         if self.reference:
             return self.F.linear(x2d.float(), blk[name])
         return blk[name](x2d)
