@@ -125,14 +125,23 @@ __device__ __forceinline__ float strip_keep(floatx4 v, int j) {
 // 14336 -> 4096 9.38 -> 8.57 us, 8192 -> 3072 6.27 -> 6.01 us; slower where every wave
 // streams one range (4096 -> 14336 at one token 6.45 -> 8.73 us: the LDS round trip then
 // sits at the start of every wave's critical path).
+//
+// kSplit (float32, M <= 2): the hi and lo bf16 planes of each token are two B token
+// columns (2 m: hi, 2 m + 1: lo) instead of a second MFMA per operand, so one MFMA
+// serves both planes; each output adds its token's two columns at the end.  The launch
+// takes S = 8 for one token and 4 for two, as bf16 takes for two and four tokens.
 template <int XT, int S, int NW, int R, bool kNat = false, bool kNt = false,
-          int DEPTH = kStripDepth, bool kStageB = false>
+          int DEPTH = kStripDepth, bool kStageB = false, bool kSplit = false>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void gemv_strip_kernel(
     const void *__restrict__ x, const uint8_t *__restrict__ w, void *__restrict__ c, int M,
     int64_t N, int64_t K, int L, int nranges, int x_aligned, float alpha, float beta,
     const float *__restrict__ bias) {
     static_assert(S == 4 || S == 8 || S == 16, "one matched entry per lane needs S >= 4");
     static_assert(!kStageB || (XT == kDtypeBF16 && !kNat), "staged B: bf16, padded order");
+    static_assert(!kSplit || (XT == kDtypeF32 && S <= 8 && !kStageB),
+                  "planes as token columns: float32, two columns per token");
+    // the MFMA's operand type: one bf16 plane (bf16, int8, float32 planes as columns)
+    constexpr int XM = kSplit ? kDtypeBF16 : XT;
     constexpr int RPI = 16 / S;  // rows per load (and tokens per MFMA)
     constexpr int H = R * RPI;   // rows per workgroup
     constexpr int D = R < DEPTH ? R : DEPTH;
@@ -169,8 +178,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     for (int rg = wave; rg < nranges; rg += NW) {
         const int limb = rg * 4 * S + sub;
         const bool in_row = limb < L;
-        // ---- B: activations of token i / S for the lane's limb ----
-        const int mb = i / S;
+        // ---- B: activations of token i / S for the lane's limb (kSplit: column i / S is
+        // plane (i / S) % 2 of token i / S / 2) ----
+        const int mb = kSplit ? (i / S) >> 1 : i / S;
         const bool bvalid = mb < M && in_row;
         const int64_t xrow = static_cast<int64_t>(mb < M ? mb : 0) * K;
         const int64_t kb = static_cast<int64_t>(limb) * kTrits;
@@ -239,6 +249,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
         bf16x8 nh[6], nl[6], bh[kOps], bl[kOps];
 #pragma unroll
         for (int j = 0; j < 6; ++j) cvt_x8<XT>(xr[j], nh[j], nl[j]);
+        if constexpr (kSplit) {
+            // the lane's column carries one plane
+            const bool lo_col = ((i / S) & 1) != 0;
+#pragma unroll
+            for (int j = 0; j < 6; ++j) nh[j] = lo_col ? nl[j] : nh[j];
+        }
         if constexpr (kNat) {
 #pragma unroll
             for (int j = 0; j < 6; ++j) {
@@ -247,7 +263,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
             }
         } else {
             strip_pad(nh, bh);
-            if constexpr (XT == kDtypeF32) strip_pad(nl, bl);
+            if constexpr (XM == kDtypeF32) strip_pad(nl, bl);
         }
         auto decode = [&](uint32_t wd, uint32_t *out) {
             if constexpr (kNat) decode_dword(lut, wd, out);
@@ -271,7 +287,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
                 __builtin_amdgcn_sched_barrier(0);
                 if (t + 1 + D < R) ring[(t + 1) % D] = fetch(t + 1 + D);
             }
-            const floatx4 acc = strip_mfma<XT, kOps>(cur, bh, bl);
+            const floatx4 acc = strip_mfma<XM, kOps>(cur, bh, bl);
             if (t > 0) kept[t - 1] += strip_keep(prev, i);
             prev = acc;
 #pragma unroll
@@ -299,7 +315,13 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
 #pragma unroll
             for (int ss = 0; ss < S; ++ss) {
                 // entry D[ra*S + ss][m*S + ss] sits in lane (m*S + ss) + 16 * ((ra*S + ss) / 4)
-                val += red[ww][t][m * S + ss + 16 * ((ra * S + ss) >> 2)];
+                if constexpr (kSplit) {
+                    // token m's hi column 2 m and lo column 2 m + 1
+                    val += red[ww][t][2 * m * S + ss + 16 * ((ra * S + ss) >> 2)];
+                    val += red[ww][t][(2 * m + 1) * S + ss + 16 * ((ra * S + ss) >> 2)];
+                } else {
+                    val += red[ww][t][m * S + ss + 16 * ((ra * S + ss) >> 2)];
+                }
             }
         }
         if constexpr (XT == kDtypeI8) {
@@ -331,19 +353,32 @@ struct StripArgs {
 };
 
 template <int XT, int S, int NW, int R, bool kNat = false, bool kNt = false,
-          int DEPTH = kStripDepth, bool kStageB = false>
+          int DEPTH = kStripDepth, bool kStageB = false, bool kSplit = false>
 hipError_t launch_strip(const StripArgs &a) {
     constexpr int H = R * (16 / S);
     const int64_t blocks = (a.n + H - 1) / H;
-    gemv_strip_kernel<XT, S, NW, R, kNat, kNt, DEPTH, kStageB><<<dim3(static_cast<unsigned>(blocks)), dim3(64 * NW), 0,
-                                       a.s>>>(a.x, a.w, a.c, a.m, a.n, a.k, a.L, a.nranges,
-                                              a.aligned ? 1 : 0, a.alpha, a.beta, a.bias);
+    gemv_strip_kernel<XT, S, NW, R, kNat, kNt, DEPTH, kStageB, kSplit>
+        <<<dim3(static_cast<unsigned>(blocks)), dim3(64 * NW), 0, a.s>>>(
+            a.x, a.w, a.c, a.m, a.n, a.k, a.L, a.nranges, a.aligned ? 1 : 0, a.alpha, a.beta,
+            a.bias);
     return hipGetLastError();
 }
 
-template <int XT, int S, int R, bool kNt = false, bool kStageB = false>
+template <int XT, int S, int R, bool kNt = false, bool kStageB = false, bool kSplit = false>
 hipError_t launch_strip_nw(int nw, const StripArgs &a) {
     constexpr int D = kStripDepth;
+    if constexpr (kSplit) {
+        switch (nw) {
+            case 1: return launch_strip<XT, S, 1, R, false, kNt, D, false, true>(a);
+            case 2: return launch_strip<XT, S, 2, R, false, kNt, D, false, true>(a);
+            case 3: return launch_strip<XT, S, 3, R, false, kNt, D, false, true>(a);
+            case 4: return launch_strip<XT, S, 4, R, false, kNt, D, false, true>(a);
+            case 5: return launch_strip<XT, S, 5, R, false, kNt, D, false, true>(a);
+            case 6: return launch_strip<XT, S, 6, R, false, kNt, D, false, true>(a);
+            case 7: return launch_strip<XT, S, 7, R, false, kNt, D, false, true>(a);
+            default: return launch_strip<XT, S, 8, R, false, kNt, D, false, true>(a);
+        }
+    }
     if constexpr (kStageB) {
         // staged B runs only where waves stream several ranges: five waves or more
         switch (nw) {
@@ -369,33 +404,33 @@ hipError_t launch_strip_nw(int nw, const StripArgs &a) {
 // seven loads keep three of them in flight, not four: 4096 -> 14336 (seven loads)
 // 6.69 -> 6.45 us, 3072 -> 9216 (four) 4.94 -> 4.69 us; eight loads (3072 -> 16384)
 // measured 1 % slower with three.
-template <int S, int R, bool kNt>
+template <int S, int R, bool kNt, int XT = kDtypeBF16, bool kSplit = false>
 hipError_t launch_strip_nat_nw(int nw, const StripArgs &a) {
     constexpr int kD = R <= 7 ? 3 : kStripDepth;
     switch (nw) {
-        case 1: return launch_strip<kDtypeBF16, S, 1, R, true, kNt, kD>(a);
-        case 2: return launch_strip<kDtypeBF16, S, 2, R, true, kNt, kD>(a);
-        default: return launch_strip<kDtypeBF16, S, 3, R, true, kNt, kD>(a);
+        case 1: return launch_strip<XT, S, 1, R, true, kNt, kD, false, kSplit>(a);
+        case 2: return launch_strip<XT, S, 2, R, true, kNt, kD, false, kSplit>(a);
+        default: return launch_strip<XT, S, 3, R, true, kNt, kD, false, kSplit>(a);
     }
 }
-template <int S, bool kNt>
+template <int S, bool kNt, int XT = kDtypeBF16, bool kSplit = false>
 hipError_t launch_strip_nat(int nw, int r, const StripArgs &a) {
-    if (r == 14) return launch_strip_nat_nw<S, 14, kNt>(nw, a);
-    if (r == 7) return launch_strip_nat_nw<S, 7, kNt>(nw, a);
-    if (r >= 16) return launch_strip_nat_nw<S, 16, kNt>(nw, a);
-    if (r >= 8) return launch_strip_nat_nw<S, 8, kNt>(nw, a);
-    return launch_strip_nat_nw<S, 4, kNt>(nw, a);
+    if (r == 14) return launch_strip_nat_nw<S, 14, kNt, XT, kSplit>(nw, a);
+    if (r == 7) return launch_strip_nat_nw<S, 7, kNt, XT, kSplit>(nw, a);
+    if (r >= 16) return launch_strip_nat_nw<S, 16, kNt, XT, kSplit>(nw, a);
+    if (r >= 8) return launch_strip_nat_nw<S, 8, kNt, XT, kSplit>(nw, a);
+    return launch_strip_nat_nw<S, 4, kNt, XT, kSplit>(nw, a);
 }
 
-template <int XT, int S, bool kNt = false, bool kStageB = false>
+template <int XT, int S, bool kNt = false, bool kStageB = false, bool kSplit = false>
 hipError_t launch_strip_nr(int nw, int r, const StripArgs &a) {
-    if constexpr (XT == kDtypeBF16) {
-        if (r == 14) return launch_strip_nw<XT, S, 14, kNt, kStageB>(nw, a);
-        if (r == 7) return launch_strip_nw<XT, S, 7, kNt, kStageB>(nw, a);
+    if constexpr (XT == kDtypeBF16 || kSplit) {
+        if (r == 14) return launch_strip_nw<XT, S, 14, kNt, kStageB, kSplit>(nw, a);
+        if (r == 7) return launch_strip_nw<XT, S, 7, kNt, kStageB, kSplit>(nw, a);
     }
-    if (r >= 16) return launch_strip_nw<XT, S, 16, kNt, kStageB>(nw, a);
-    if (r >= 8) return launch_strip_nw<XT, S, 8, kNt, kStageB>(nw, a);
-    return launch_strip_nw<XT, S, 4, kNt, kStageB>(nw, a);
+    if (r >= 16) return launch_strip_nw<XT, S, 16, kNt, kStageB, kSplit>(nw, a);
+    if (r >= 8) return launch_strip_nw<XT, S, 8, kNt, kStageB, kSplit>(nw, a);
+    return launch_strip_nw<XT, S, 4, kNt, kStageB, kSplit>(nw, a);
 }
 
 // The weight loads of bf16 launches over at least this many packed bytes carry the
@@ -416,11 +451,20 @@ hipError_t launch_strip_x(bool *handled, const void *x, const uint8_t *w, void *
     *handled = false;
     const int64_t L = (k + kTrits - 1) / kTrits;
     if (m < 1 || m > 4 || n <= 0 || L <= 0) return hipSuccess;
+    // float32 at one or two tokens: hi and lo planes as B token columns (kSplit), so the
+    // launch is shaped as bf16 at mc = 2 m tokens.  Against a second MFMA per operand
+    // (same box): one token 4096 -> 14336 10.03 -> 7.39 us, 14336 -> 4096 10.63 -> 9.44,
+    // 3072 -> 9216 6.45 -> 5.66, 3072 -> 16384 7.25 -> 6.25, but 8192 -> 3072 6.72 -> 8.77
+    // and 3072 -> 3072 4.10 -> 4.43, so one token takes it from 4096 rows; two tokens
+    // everywhere (4096 -> 14336 9.34 -> 7.85, 8192 -> 3072 9.71 -> 7.19, 3072 -> 3072 4.70
+    // -> 3.99).
+    const bool split = XT == kDtypeF32 && (m == 2 || (m == 1 && n >= 4096));
+    const int mc = split ? 2 * m : m;
     // S = 16 (one row x 64 limbs per load) for one token when it pads the row no more
     // than S = 8 does; S = 8 (2 rows x 32 limbs) up to 2 tokens; S = 4 up to 4.
     const int64_t pad16 = (L + 63) / 64 * 64;
     const int64_t pad8 = (L + 31) / 32 * 32;
-    const int S = m == 1 && pad16 <= pad8 ? 16 : (m <= 2 ? 8 : 4);
+    const int S = mc == 1 && pad16 <= pad8 ? 16 : (mc <= 2 ? 8 : 4);
     // buffer offsets within a workgroup's rows must stay below 2^31
     constexpr int64_t kElem = XT == kDtypeF32 ? 4 : (XT == kDtypeBF16 ? 2 : 1);
     if (64 * L * kTrytes >= 0x7FFFFFFF) return hipSuccess;
@@ -447,20 +491,31 @@ hipError_t launch_strip_x(bool *handled, const void *x, const uint8_t *w, void *
     // weights, so R starts at the first of 8, 16 that keeps that ratio (bf16 bytes) at
     // or below 0.4; then it halves, down to 4, while the launch has fewer than 1200
     // waves (longer strips also lengthen the compute tail after the last load).
-    const double x_ratio8 = 4.0 * S * m * kTrits * 2 / (8 * 1024.0);
+    const double x_ratio8 = 4.0 * S * mc * kTrits * 2 / (8 * 1024.0);
     int r = x_ratio8 <= 0.4 ? 8 : 16;
     auto waves = [&](int rr) { return (n + rr * (16 / S) - 1) / (rr * (16 / S)) * nw; };
     while (r > 4 && waves(r) < kStripMinWaves) r /= 2;
     // bf16 (the decode case): one load fewer per strip when that evens out the
     // workgroups per CU, the busiest CU then streaming fewer rows (4096 x 14336:
     // 896 workgroups, 3.5 per CU, become 1024, 4 per CU, 7.3 -> 7.1 us).
-    if (XT == kDtypeBF16 && (r == 8 || r == 16)) {
+    if ((XT == kDtypeBF16 || split) && (r == 8 || r == 16)) {
         const int64_t cus = cu_count();
         auto busiest = [&](int rr) {
             const int64_t blocks = (n + rr * (16 / S) - 1) / (rr * (16 / S));
             return (blocks + cus - 1) / cus * rr;
         };
         if (busiest(r - r / 8) < busiest(r)) r -= r / 8;
+    }
+    if constexpr (XT == kDtypeF32) {
+        if (split) {
+            // as bf16 at mc = 2 or 4 tokens: padded order, S = 8 / 4, the same hint
+            const bool nt = n * L * kTrytes >= kStripNtMinBytes;
+            if (S == 8)
+                return nt ? launch_strip_nr<XT, 8, true, false, true>(nw, r, a)
+                          : launch_strip_nr<XT, 8, false, false, true>(nw, r, a);
+            return nt ? launch_strip_nr<XT, 4, true, false, true>(nw, r, a)
+                      : launch_strip_nr<XT, 4, false, false, true>(nw, r, a);
+        }
     }
     if constexpr (XT == kDtypeBF16) {
         const bool nt = n * L * kTrytes >= kStripNtMinBytes;

@@ -12,7 +12,8 @@ alpha = 0.5 / -1.25, beta = 0.5 / 1 keep the epilogue exact as well.
 
 Paths covered (the north-star fp32 tolerance of 1e-3 relative is met with room to spare
 by a bit-exact result; float activations enter at t81/torch/__init__.py:241-246):
-* K2 column-strip kernel (M <= 4) at 4096 -> 14336, 14336 -> 4096, 8192 -> 3072;
+* K2 column-strip kernel (M <= 4) at 4096 -> 14336, 14336 -> 4096, 8192 -> 3072, with the
+  two planes as separate MFMAs or (one token from 4096 rows, two tokens) as B columns;
 * K2 wave / stream kernels at 5..8 tokens;
 * K2 tile kernel at 9..16 tokens over K >= 6144 with its split sum in the workspace,
   and the stream kernel for the wider shapes it leaves;
@@ -90,6 +91,9 @@ def run_cases(gpu, orc, M, N, K, seed, kernel, what, offset=0):
 
 # ------------------------------------------------------------------- K2 strip --
 STRIP = [(M, K, N) for (K, N) in ((4096, 14336), (14336, 4096), (8192, 3072)) for M in (1, 2, 3, 4)]
+# the hi / lo planes as B token columns (one token from 4096 rows, two tokens): ragged K
+# (element loads), ragged N, a short K
+STRIP += [(1, 1000, 4100), (2, 999, 37), (2, 3072, 3072), (1, 48, 5000)]
 
 
 @pytest.mark.parametrize("M,K,N", STRIP)
