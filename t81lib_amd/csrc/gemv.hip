@@ -38,10 +38,9 @@ namespace {
 // Applies alpha / beta / bias to a finished 16x16 tile and stores it.  Lane (m, q)
 // holds rows n0 + 4q + i (i < 4) of token m.
 template <int XT>
-__device__ __forceinline__ void store_tile(floatx4 v, int lane, int M, int64_t N, int64_t n0,
-                                           void *c, float alpha, float beta, const float *bias) {
-    const int r = lane & 15;
-    const int q = lane >> 4;
+__device__ __forceinline__ void store_tile_rq(floatx4 v, int r, int q, int M, int64_t N,
+                                              int64_t n0, void *c, float alpha, float beta,
+                                              const float *bias) {
     if (r >= M) return;
     const int64_t nb = n0 + 4 * q;
     if constexpr (XT == kDtypeI8) {
@@ -77,8 +76,16 @@ __device__ __forceinline__ void store_tile(floatx4 v, int lane, int M, int64_t N
     }
 }
 
-// Sums the per-wave partial tiles of G 16-row groups and stores them.
-template <int XT, int G, int KS>
+template <int XT>
+__device__ __forceinline__ void store_tile(floatx4 v, int lane, int M, int64_t N, int64_t n0,
+                                           void *c, float alpha, float beta, const float *bias) {
+    store_tile_rq<XT>(v, lane & 15, lane >> 4, M, N, n0, c, alpha, beta, bias);
+}
+
+// Sums the per-wave partial tiles of G 16-row groups and stores them.  kSplit: B column
+// 2 t holds token t's hi plane and 2 t + 1 its lo plane; the two are added (the lane
+// pair next to each other) and the even lane stores token t.
+template <int XT, int G, int KS, bool kSplit = false>
 __device__ __forceinline__ void reduce_store(floatx4 (&acc)[G], floatx4 *red, int wave, int lane,
                                              int M, int64_t N, int64_t n0, void *c, float alpha,
                                              float beta, const float *bias) {
@@ -89,7 +96,15 @@ __device__ __forceinline__ void reduce_store(floatx4 (&acc)[G], floatx4 *red, in
         floatx4 v = red[g * 64 + lane];
 #pragma unroll
         for (int ww = 1; ww < KS; ++ww) v += red[(ww * G + g) * 64 + lane];
-        store_tile<XT>(v, lane, M, N, n0 + 16 * g, c, alpha, beta, bias);
+        if constexpr (kSplit) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] += __shfl_xor(v[e], 1);
+            if ((lane & 1) == 0)
+                store_tile_rq<XT>(v, (lane & 15) >> 1, lane >> 4, M, N, n0 + 16 * g, c, alpha,
+                                  beta, bias);
+        } else {
+            store_tile<XT>(v, lane, M, N, n0 + 16 * g, c, alpha, beta, bias);
+        }
     }
 }
 
@@ -385,22 +400,31 @@ __global__ __launch_bounds__(64 * W) void gemv_wave_kernel(
 // split K round-robin; each activation fragment serves its G 16-row groups.  kStage
 // (bf16, kAligned): the activations of a sub-block are loaded as pieces and become
 // fragments through the wave's LDS region (load_x_pieces).
-template <int XT, int G, bool kAligned, int KS, bool kStage, bool kDeep = false>
+template <int XT, int G, bool kAligned, int KS, bool kStage, bool kDeep = false,
+          bool kSplit = false>
 __global__ __launch_bounds__(64 * KS) void gemv_stream_kernel(const void *__restrict__ x,
                                                           const uint8_t *__restrict__ w,
                                                           void *__restrict__ c, int M, int64_t N,
                                                           int64_t K, int64_t L, float alpha,
                                                           float beta,
                                                           const float *__restrict__ bias) {
-    static_assert(!kStage || ((XT == kDtypeBF16 || XT == kDtypeI8) && kAligned),
-                  "pieces are aligned bf16, or int8 widened to bf16 as they are staged");
+    static_assert(!kStage || ((XT == kDtypeBF16 || XT == kDtypeI8 || kSplit) && kAligned),
+                  "pieces are aligned bf16, int8 widened to bf16 as they are staged, or "
+                  "float32 split into two columns");
     static_assert(!kDeep || kStage, "two sub-blocks in flight: the staged form only");
-    // a piece: 16 bytes of one token's activations, 8 bf16 or 16 int8 values (the int8
-    // launch also needs K % 16 == 0 and a 16-byte aligned x)
-    constexpr int kVals = XT == kDtypeI8 ? 16 : 8;
-    constexpr int kPieces = 4 * kTrits / kVals;        // per token and sub-block: 24 or 12
-    constexpr int kLanePieces = 16 * kPieces / 64;     // per lane: 6 or 3
-    constexpr int kElemB = XT == kDtypeI8 ? 1 : 2;
+    static_assert(!kSplit || (XT == kDtypeF32 && kStage && !kDeep),
+                  "planes as columns: float32, staged");
+    // a piece: 16 bytes of one token's activations, 8 bf16, 16 int8 or 4 float32 values
+    // (the int8 launch also needs K % 16 == 0 and a 16-byte aligned x; float32, K % 4 ==
+    // 0).  kSplit (float32, up to 8 tokens): token t's piece becomes 4 bf16 of its hi plane
+    // in staging row 2 t and 4 of its lo plane in row 2 t + 1, so the B operand's 16
+    // columns are 8 tokens' two planes and one MFMA serves both.
+    constexpr int kVals = XT == kDtypeI8 ? 16 : (kSplit ? 4 : 8);
+    constexpr int kPieces = 4 * kTrits / kVals;        // per token and sub-block: 24, 12, 48
+    constexpr int kTok = kSplit ? 8 : 16;              // tokens with pieces
+    constexpr int kLanePieces = kTok * kPieces / 64;   // per lane: 6 or 3
+    constexpr int kElemB = XT == kDtypeI8 ? 1 : (kSplit ? 4 : 2);
+    constexpr int XM = kSplit ? kDtypeBF16 : XT;       // the MFMA's operand type
     __shared__ __attribute__((aligned(16))) uint8_t lut[kLutBytes];
     __shared__ __attribute__((aligned(16))) floatx4 red[KS * G * 64];
     __shared__ __attribute__((aligned(16))) uint8_t xst[kStage ? KS * kXStageBytes : 16];
@@ -437,6 +461,26 @@ __global__ __launch_bounds__(64 * KS) void gemv_stream_kernel(const void *__rest
         for (int i = 0; i < kLanePieces; ++i) {
             const int P = 64 * i + lane;
             const int t = P / kPieces;
+            if constexpr (kSplit) {
+                // 4 float32 -> 4 bf16 of the hi plane (row 2 t) and 4 of the lo plane
+                uint8_t *dst = xs + 2 * t * kXStagePitch + 8 * (P - kPieces * t);
+                uint32_t h[2], l[2];
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const float f0 = __uint_as_float(xp[i][2 * e]);
+                    const float f1 = __uint_as_float(xp[i][2 * e + 1]);
+                    const __bf16 h0 = static_cast<__bf16>(f0), h1 = static_cast<__bf16>(f1);
+                    const __bf16 l0 = static_cast<__bf16>(f0 - static_cast<float>(h0));
+                    const __bf16 l1 = static_cast<__bf16>(f1 - static_cast<float>(h1));
+                    h[e] = __builtin_bit_cast(uint16_t, h0) |
+                           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h1)) << 16);
+                    l[e] = __builtin_bit_cast(uint16_t, l0) |
+                           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, l1)) << 16);
+                }
+                *reinterpret_cast<uint2 *>(dst) = make_uint2(h[0], h[1]);
+                *reinterpret_cast<uint2 *>(dst + kXStagePitch) = make_uint2(l[0], l[1]);
+                continue;
+            }
             uint8_t *dst = xs + t * kXStagePitch + 16 * (kVals / 8) * (P - kPieces * t);
             if constexpr (XT == kDtypeI8) {
                 // 16 int8 -> 16 bf16 (exact: |v| <= 128 needs 8 significant bits)
@@ -500,7 +544,7 @@ __global__ __launch_bounds__(64 * KS) void gemv_stream_kernel(const void *__rest
         auto iter = [&](int64_t si, u32x4 (&xs_now)[6], u32x4 (&xs_next)[6], u32x4 (&wn)[G]) {
             pieces_to(si + 2 * KS, xs_now);
 #pragma unroll
-            for (int g = 0; g < G; ++g) acc[g] = mfma_limb<XT>(lut, wn[g], bh, bl, acc[g]);
+            for (int g = 0; g < G; ++g) acc[g] = mfma_limb<XM>(lut, wn[g], bh, bl, acc[g]);
             weights_to(si + 2 * KS, wn);
             stage_from(xs_next);
         };
@@ -509,7 +553,7 @@ __global__ __launch_bounds__(64 * KS) void gemv_stream_kernel(const void *__rest
             if (s + KS >= S) break;
             iter(s + KS, xb, xa, wb);
         }
-        reduce_store<XT, G, KS>(acc, red, wave, lane, M, N, n0, c, alpha, beta, bias);
+        reduce_store<XT, G, KS, kSplit>(acc, red, wave, lane, M, N, n0, c, alpha, beta, bias);
         return;
     }
     if constexpr (kStage) {
@@ -547,7 +591,7 @@ __global__ __launch_bounds__(64 * KS) void gemv_stream_kernel(const void *__rest
         for (int g = 0; g < G; ++g) wnext[g] = load_limb(w, n0 + 16 * g + r, 4 * sn + q, N, L, L);
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-            acc[g] = mfma_limb<XT>(lut, wcur[g], bh, bl, acc[g]);
+            acc[g] = mfma_limb<XM>(lut, wcur[g], bh, bl, acc[g]);
             wcur[g] = wnext[g];
         }
         if constexpr (kStage) {
@@ -560,7 +604,7 @@ __global__ __launch_bounds__(64 * KS) void gemv_stream_kernel(const void *__rest
             }
         }
     }
-    reduce_store<XT, G, KS>(acc, red, wave, lane, M, N, n0, c, alpha, beta, bias);
+    reduce_store<XT, G, KS, kSplit>(acc, red, wave, lane, M, N, n0, c, alpha, beta, bias);
 }
 
 // ---------------------------------------------------------------------------------
@@ -1176,9 +1220,41 @@ hipError_t launch_wave_su(int su, int run, const WaveArgs &a) {
 // Waves in flight the wave kernel aims for before it splits K finer.
 constexpr int64_t kTargetWaves = 1024;
 
+// float32 at 5..8 tokens (K % 4 == 0, 16-byte aligned x): the staged stream kernel with
+// each token's hi and lo planes as two of the 16 B columns, row groups per workgroup as for
+// bf16 at 8+ tokens.  Against the wave / stream kernels' second MFMA per operand (same
+// box): 8 tokens 14336 -> 4096 26.65 -> 15.91 us, 4096 -> 14336 17.30 -> 10.96, 3072 ->
+// 16384 14.31 -> 9.03, 3072 -> 3072 7.75 -> 6.07; 5 tokens 22.98 -> 15.93, 14.10 ->
+// 10.90, 18.19 -> 9.06.  At 3 and 4 tokens the strip kernel stays faster (14336 -> 4096
+// 11.41 / 13.98 against 15.97 / 15.98 this way).
+hipError_t launch_stream_split(const void *x, const uint8_t *w, void *c, int m, int64_t n,
+                               int64_t k, int64_t L, float alpha, float beta, const float *bias,
+                               hipStream_t s) {
+    auto go = [&](auto gc) {
+        constexpr int G = decltype(gc)::value;
+        const int64_t blocks = (n + 16 * G - 1) / (16 * G);
+        gemv_stream_kernel<kDtypeF32, G, true, 8, true, false, true>
+            <<<dim3(static_cast<unsigned>(blocks)), dim3(64 * 8), 0, s>>>(x, w, c, m, n, k, L,
+                                                                        alpha, beta, bias);
+        return hipGetLastError();
+    };
+    if (n <= 4096) return go(std::integral_constant<int, 1>());
+    if (n < 9216) return go(std::integral_constant<int, 2>());
+    return go(std::integral_constant<int, 4>());
+}
+
+bool stream_split_fits(const void *x, int m, int64_t k) {
+    return m >= 5 && m <= 8 && k % 4 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
+}
+
 template <int XT>
 hipError_t launch_gemv_x(const void *x, const uint8_t *w, void *c, int m, int64_t n, int64_t k,
                          float alpha, float beta, const float *bias, hipStream_t s) {
+    if constexpr (XT == kDtypeF32) {
+        if (stream_split_fits(x, m, k))
+            return launch_stream_split(x, w, c, m, n, k, (k + kTrits - 1) / kTrits, alpha, beta,
+                                       bias, s);
+    }
     using LY = WaveLayout<XT>;
     const int elem = LY::kElem;
     const int64_t L = (k + kTrits - 1) / kTrits;

@@ -14,7 +14,8 @@ Paths covered (the north-star fp32 tolerance of 1e-3 relative is met with room t
 by a bit-exact result; float activations enter at t81/torch/__init__.py:241-246):
 * K2 column-strip kernel (M <= 4) at 4096 -> 14336, 14336 -> 4096, 8192 -> 3072, with the
   two planes as separate MFMAs or (one token from 4096 rows, two tokens) as B columns;
-* K2 wave / stream kernels at 5..8 tokens;
+* K2 at 5..8 tokens: the staged stream kernel with the planes as B columns, and (x off
+  16-byte alignment) the wave / stream kernels;
 * K2 tile kernel at 9..16 tokens over K >= 6144 with its split sum in the workspace,
   and the stream kernel for the wider shapes it leaves;
 * K3 eight-wave kernel at 17..64 tokens, on aligned x (vector loads) and on x one element
@@ -103,14 +104,17 @@ def test_strip_f32_bit_exact(gpu, orc, M, K, N):
 
 
 # ------------------------------------------------------ K2 wave / stream, 5..8 --
-FEW = [(5, 8192, 3072), (8, 4096, 14336), (6, 14336, 4096), (7, 3072, 3072), (8, 3072, 9216),
-       (5, 1000, 333)]
+# offset 0: the staged stream kernel with each token's planes as two B columns (16-byte
+# aligned x, K % 4 == 0); offset 1: the wave / stream kernels' two MFMAs per operand
+FEW = [(5, 8192, 3072, 0), (8, 4096, 14336, 0), (6, 14336, 4096, 0), (7, 3072, 3072, 0),
+       (8, 3072, 9216, 0), (5, 1000, 333, 0), (8, 14336, 4096, 0), (7, 4100, 20000, 0),
+       (5, 8192, 3072, 1), (8, 4096, 14336, 1), (6, 14336, 4096, 1), (7, 1000, 333, 1)]
 
 
-@pytest.mark.parametrize("M,K,N", FEW)
-def test_gemv_few_tokens_f32_bit_exact(gpu, orc, M, K, N):
-    announce(f"exact f32 K2 M={M} K={K} N={N}")
-    run_cases(gpu, orc, M, N, K, seed=M * 37 + K + N, kernel=2, what="K2")
+@pytest.mark.parametrize("M,K,N,offset", FEW)
+def test_gemv_few_tokens_f32_bit_exact(gpu, orc, M, K, N, offset):
+    announce(f"exact f32 K2 M={M} K={K} N={N} offset={offset}")
+    run_cases(gpu, orc, M, N, K, seed=M * 37 + K + N, kernel=2, what="K2", offset=offset)
 
 
 # --------------------------------------------------- K2 tile kernel, 9..16 tokens --
