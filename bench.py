@@ -631,8 +631,8 @@ def run_decode(torch, ops, lib, dev, only_case=None) -> dict:
     16-token blocks, two launches at 49..64, or the eight-wave kernel at 49..64 over K >
     8192): median microseconds per call over rotating weight copies (> 2 x MALL, so every
     call streams from HBM), GB/s of algorithmic bytes, and each shape's 16-token time over
-    its one-token time.  The Llama shapes also with float32 activations at 16..64 tokens
-    (keys f32_M*), the form t8.nn.Linear's float inputs take."""
+    its one-token time.  The Llama shapes also with float32 activations at 1, 8 and 16..64
+    tokens (keys f32_M*), the form t8.nn.Linear's float inputs take."""
     shapes = {}
     todo = DECODE_SHAPES if only_case is None else [("case", only_case[0], only_case[1])]
     for name, k, n in todo:
@@ -643,7 +643,7 @@ def run_decode(torch, ops, lib, dev, only_case=None) -> dict:
         runs = [("", torch.bfloat16, m) for m in
                 ((1, 4, 8, 16, 32, 48, 64) if only_case is None else (only_case[2],))]
         if only_case is None and name.startswith("llama"):
-            runs += [("f32_", torch.float32, m) for m in (16, 32, 48, 64)]
+            runs += [("f32_", torch.float32, m) for m in (1, 8, 16, 32, 48, 64)]
         for tag, dt, m in runs:
             x = torch.randn((m, k), device=dev).to(dt)
             out = torch.empty((m, n), device=dev)
@@ -664,7 +664,7 @@ def run_decode(torch, ops, lib, dev, only_case=None) -> dict:
                         "column-block kernel, or the eight-wave kernel at 64 over K > 8192), "
                         "bf16 x, fp32 out, alpha=1 beta=0, median over rotating weight copies; "
                         "config 3 (Phi-3) plus the Llama-3-8B gate / down shapes, those also "
-                        "with float32 x at 16-64 tokens (f32_M*)",
+                        "with float32 x at 1, 8 and 16-64 tokens (f32_M*)",
             "shapes": shapes}
 
 
