@@ -1212,11 +1212,110 @@ hipError_t launch_gemm_t(const void *x, const uint8_t *w, void *c, int64_t m, in
     return hipGetLastError();
 }
 
+// ---- float32 activations past 64 tokens, given a workspace ----
+// The tokens are cut into equal chunks; each chunk is split into its bf16 planes in the
+// workspace (x = hi + lo, hi = bf16(x), lo = bf16(x - hi), |x - hi - lo| <= 2^-18 |x|),
+// and the chunk's rows of C are two bf16 launches: C = alpha * hi T + beta * C + bias,
+// then C = alpha * lo T + C.  The bf16 launches run the big-tile kernel, against the
+// float32 eight-wave kernel that stages both planes for 256 x 128 tiles: gate_up M = 2048
+// 1604 -> 794 us, M = 8192 6701 -> 3100, M = 512 456 -> 220; qkv M = 2048 458 -> 203.
+// A chunk's two planes fit kF32PlaneBytes (so the workspace stays within the
+// no-allocation entry's static scratch), and the path is taken only where the bf16
+// launches of its chunks need no split-K workspace of their own: with one (down 14336 ->
+// 4096 at M = 2048: 1024-token chunks of 64 tiles) the two launches measured slower than
+// the eight-wave kernel (834 -> 1126 us), as at 65 tokens.
+constexpr int64_t kF32PlaneBytes = int64_t{64} << 20;
+
+template <int XT>
+int64_t gemm_workspace_x(int64_t m, int64_t n, int64_t k);
+
+struct F32Chunks {
+    int64_t rows = 0;    // tokens per chunk (the last may hold fewer)
+    int64_t count = 0;   // 0: the planes path does not take the shape
+};
+
+F32Chunks f32_chunks(int64_t m, int64_t n, int64_t k) {
+    F32Chunks ch;
+    if (m <= 64 || k % 8 != 0 || n <= 0) return ch;
+    const int64_t cap = kF32PlaneBytes / (4 * k);   // tokens whose planes fit
+    if (cap < 256) return ch;
+    const int64_t count = (m + cap - 1) / cap;
+    const int64_t rows = (m + count - 1) / count;
+    const int64_t last = m - (count - 1) * rows;
+    if (gemm_workspace_x<kDtypeBF16>(rows, n, k) != 0 ||
+        gemm_workspace_x<kDtypeBF16>(last, n, k) != 0)
+        return ch;
+    ch.rows = rows;
+    ch.count = count;
+    return ch;
+}
+
+// The workspace the planes path needs (0: it does not take the shape).
+int64_t f32_planes_bytes(int64_t m, int64_t n, int64_t k) {
+    const F32Chunks ch = f32_chunks(m, n, k);
+    return ch.count > 0 ? 4 * ch.rows * k : 0;
+}
+
+__global__ __launch_bounds__(256) void f32_planes_kernel(const float *__restrict__ x,
+                                                         uint32_t *__restrict__ hi,
+                                                         uint32_t *__restrict__ lo,
+                                                         int64_t pairs) {
+    // pairs of consecutive values (K % 8 == 0 keeps a pair inside a row)
+    for (int64_t p = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; p < pairs;
+         p += static_cast<int64_t>(gridDim.x) * 256) {
+        const float f0 = x[2 * p], f1 = x[2 * p + 1];
+        const __bf16 h0 = static_cast<__bf16>(f0), h1 = static_cast<__bf16>(f1);
+        const __bf16 l0 = static_cast<__bf16>(f0 - static_cast<float>(h0));
+        const __bf16 l1 = static_cast<__bf16>(f1 - static_cast<float>(h1));
+        hi[p] = __builtin_bit_cast(uint16_t, h0) |
+                (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h1)) << 16);
+        lo[p] = __builtin_bit_cast(uint16_t, l0) |
+                (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, l1)) << 16);
+    }
+}
+
+template <int XT>
+hipError_t launch_gemm_x(const void *x, const uint8_t *w, void *c, int64_t m, int64_t n,
+                         int64_t k, float alpha, float beta, const float *bias, hipStream_t s,
+                         void *ws, int64_t ws_bytes);
+
+hipError_t launch_gemm_f32_planes(const float *x, const uint8_t *w, float *c, int64_t m,
+                                  int64_t n, int64_t k, float alpha, float beta,
+                                  const float *bias, hipStream_t s, void *ws) {
+    const int64_t mc = f32_chunks(m, n, k).rows;
+    uint16_t *hi = static_cast<uint16_t *>(ws);
+    for (int64_t t0 = 0; t0 < m; t0 += mc) {
+        const int64_t rows = m - t0 < mc ? m - t0 : mc;
+        uint16_t *lo = hi + rows * k;
+        const int64_t pairs = rows * k / 2;
+        int64_t blocks = (pairs + 255) / 256;
+        if (blocks > 4096) blocks = 4096;
+        f32_planes_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s>>>(
+            x + t0 * k, reinterpret_cast<uint32_t *>(hi), reinterpret_cast<uint32_t *>(lo), pairs);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        float *cc = c + t0 * n;
+        e = launch_gemm_x<kDtypeBF16>(hi, w, cc, rows, n, k, alpha, beta, bias, s, nullptr, 0);
+        if (e != hipSuccess) return e;
+        e = launch_gemm_x<kDtypeBF16>(lo, w, cc, rows, n, k, alpha, 1.0f, nullptr, s, nullptr, 0);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
 template <int XT>
 hipError_t launch_gemm_x(const void *x, const uint8_t *w, void *c, int64_t m, int64_t n,
                          int64_t k, float alpha, float beta, const float *bias, hipStream_t s,
                          void *ws, int64_t ws_bytes) {
     constexpr int LK = 2;  // limbs per k-step
+    if constexpr (XT == kDtypeF32) {
+        const int64_t planes = f32_planes_bytes(m, n, k);
+        if (planes > 0 && ws != nullptr && ws_bytes >= planes &&
+            reinterpret_cast<uintptr_t>(ws) % 16 == 0)
+            return launch_gemm_f32_planes(static_cast<const float *>(x), w,
+                                          static_cast<float *>(c), m, n, k, alpha, beta, bias, s,
+                                          ws);
+    }
     if constexpr (XT == kDtypeBF16 || XT == kDtypeI8) {
         // 17..64 tokens, aligned: the column-block stream kernel of K2 (gemv.hip)
         bool handled = false;
@@ -1317,6 +1416,15 @@ int64_t gemm_t_workspace(int64_t m, int64_t n, int64_t k) {
 
 template <int XT>
 int64_t gemm_workspace_x(int64_t m, int64_t n, int64_t k) {
+    if constexpr (XT == kDtypeF32) {
+        // the bf16 planes of float32 activations past 64 tokens (f32_planes_bytes), or the
+        // eight-wave kernel's split where a misaligned workspace leaves the planes out
+        const int64_t planes = f32_planes_bytes(m, n, k);
+        if (planes > 0) {
+            const int64_t eight = gemm_t_workspace<XT, 2, 4, 4, 1>(m, n, k);
+            return planes > eight ? planes : eight;
+        }
+    }
     if (m <= 64 && gemm_small_long_k(m, n, k)) {
         const bool rows128 = gemm_small_rows<XT>(m, n);
         if (m <= 32)

@@ -23,7 +23,8 @@ by a bit-exact result; float activations enter at t81/torch/__init__.py:241-246)
   K), with the K split over a workspace and without;
 * K3 at M > 64, including the config-4 shape 4096 -> 6144 at M = 512, every output
   against a float64 product of the unpacked trits on the GPU (exact) and a sample
-  against the C oracle.
+  against the C oracle; and the path that runs the activations as two bf16 launches of
+  their planes, chunk by chunk, from the workspace.
 """
 
 from __future__ import annotations
@@ -227,5 +228,64 @@ def test_k3_config4_f32_sampled_and_full(gpu, orc):
                                       c.numpy()[toks][:, rows] if beta else None,
                                       bias.numpy()[rows] if use_bias else None)
         assert_bits(got_s, want_s, f"sample alpha={alpha} beta={beta}")
+    del exact
+    torch.cuda.empty_cache()
+
+
+# ------------------------------------------- K3 float32 as two bf16 launches --
+PLANES = [
+    # M, K, N, chunks: float32 activations past 64 tokens whose bf16 launches need no split
+    # of their own run as the bf16 planes in the workspace, chunk by chunk (a chunk's two
+    # planes within 64 MiB): one chunk, and three of 700 tokens over K = 16384
+    (2048, 4096, 6144, 1), (700, 2048, 16384, 1), (2100, 16384, 14336, 3),
+]
+
+
+@pytest.mark.parametrize("M,K,N,chunks", PLANES)
+def test_k3_f32_planes_bit_exact(gpu, orc, M, K, N, chunks):
+    """Every output against a float64 product of the unpacked trits on the GPU (exact), that
+    product against the C oracle on a sample, with the workspace (the planes path: beta and
+    bias in the first launch, the lo plane added by the second) and without it (the
+    eight-wave kernel)."""
+    announce(f"exact f32 K3 planes M={M} K={K} N={N}")
+    lib = _lib.lib()
+    rows = -(-M // chunks)
+    assert lib.t81_hip_ternary_matmul_workspace_size(M, N, K, _lib.DTYPE_F32) == 4 * rows * K
+    _, a, b, x, c, bias = problem(M, N, K, seed=M + K + N)
+    g = torch.Generator("cpu").manual_seed(7)
+    w = torch.randn((N, K), generator=g)
+    packed = ops.quantize_pack(w.to(gpu), 0.45, _lib.THR_CPP)
+    del w
+    xg, cg, bg = x.to(gpu), c.to(gpu), bias.to(gpu)
+    tt = ops.unpack(packed, N, K).to(torch.float64).t().contiguous()
+    exact = torch.matmul(xg.double(), tt)
+    del tt
+    rng = np.random.default_rng(8)
+    toks = np.unique(np.concatenate([[0, M - 1, rows - 1, min(rows, M - 1)],
+                                     rng.choice(M, 12, replace=False)]))
+    cols = np.unique(np.concatenate([[0, N - 1], rng.choice(N, 24, replace=False)]))
+    acc_s = fixed_point_acc256(orc, a[toks], b[toks], packed.cpu().numpy()[cols], K)
+    tsel, csel = torch.from_numpy(toks).to(gpu), torch.from_numpy(cols).to(gpu)
+    np.testing.assert_array_equal(exact[tsel][:, csel].cpu().numpy() * 256.0,
+                                  acc_s.astype(np.float64), err_msg="GPU float64 vs oracle")
+    s = torch.cuda.current_stream().cuda_stream
+    for alpha, beta, use_bias in EPILOGUES:
+        want = alpha * exact
+        if beta:
+            want = want + beta * cg.double()
+        if use_bias:
+            want = want + bg.double()
+        assert float(want.abs().max()) < 2 ** 13, "epilogue must stay exact in float32"
+        out = ops.ternary_matmul(xg, packed, K, alpha=alpha, beta=beta,
+                                 c=cg.clone() if beta else None,
+                                 bias=bg if use_bias else None, kernel=3)
+        bad = int((out.double() != want).sum())
+        assert bad == 0, f"planes alpha={alpha} beta={beta}: {bad} of {M * N} outputs differ"
+        plain = cg.clone()
+        _lib.check(lib.t81_hip_ternary_matmul(xg.data_ptr(), _lib.DTYPE_F32, packed.data_ptr(),
+                                              plain.data_ptr(), M, N, K, alpha, beta,
+                                              bg.data_ptr() if use_bias else None, s))
+        bad = int((plain.double() != want).sum())
+        assert bad == 0, f"eight-wave alpha={alpha} beta={beta}: {bad} outputs differ"
     del exact
     torch.cuda.empty_cache()
