@@ -70,6 +70,8 @@ def _run_pair(gpu, M, N, K, dtype, seed):
     # int8 and float32: eight-wave splits of few tiles (int32 partials exact for int8)
     (torch.int8, [(20, 3000, 9000), (20, 1200, 4008)]),
     (torch.float32, [(48, 1000, 4104), (40, 700, 2000)]),
+    # float32 past 64 tokens as the bf16 planes in the scratch, two bf16 launches per chunk
+    (torch.float32, [(2048, 6144, 4096), (700, 16384, 2048)]),
     # K2 with 9..16 tokens over a long K (float32 and int8 activations; aligned bf16 runs
     # in one launch, as does int8 with K % 16 == 0): K split over workgroups, partials summed
     # in split order
