@@ -114,8 +114,11 @@ int t81_hip_ternary_matmul_kernel(int which, const void *x, int x_dtype, const u
  * multiple of 16, or bf16 ones with K not a multiple of 8, and workspace_bytes is at least
  * t81_hip_ternary_matmul_workspace_size(...), K is split over several workgroups
  * per tile: each writes its partial tile to the workspace and a second kernel sums
- * the partials in split order (deterministic).  NULL / 0 bytes: no split.  The
- * workspace must be 16-byte aligned and not used by another call at the same time.
+ * the partials in split order (deterministic).  With float32 activations past 64 tokens
+ * (K % 8 == 0) the workspace may instead hold the activations' bf16 hi and lo planes,
+ * chunk by chunk, and each chunk runs as two bf16 launches (the second adding the lo
+ * plane's product to C).  NULL / 0 bytes: no split, no planes.  The workspace must be
+ * 16-byte aligned and not used by another call at the same time.
  * Replaces: the same reference interfaces as t81_hip_ternary_matmul; the
  *           reference's CPU path needs no workspace, so it has no such argument. */
 int t81_hip_ternary_matmul_ws(int which, const void *x, int x_dtype, const uint8_t *w, void *c,
@@ -136,7 +139,7 @@ int64_t t81_hip_ternary_matmul_workspace_size(int64_t m, int64_t n, int64_t k, i
  * split plan and results, bit for bit -- but allocating nothing: the workspace is a
  * static 64 MiB device array in the library, one copy per device, reserved when the
  * library's code object is loaded on that device and held until the process ends.
- * Shapes whose split needs more than 64 MiB are rejected (T81_HIP_EINVAL_SHAPE, nothing
+ * Shapes whose workspace needs more than 64 MiB are rejected (T81_HIP_EINVAL_SHAPE, nothing
  * launched).  Every call on a device shares that array: calls that may overlap on one
  * device (other streams or threads) race and must be serialised by the caller.
  * No counterpart in the reference: it is for callers that cannot allocate device memory

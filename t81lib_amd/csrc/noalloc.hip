@@ -1,8 +1,8 @@
 // t81lib_amd/csrc/noalloc.hip -- t81_hip_ternary_matmul_noalloc: the trit-dot matmul with
-// its split-K workspace (K3's partial tiles, K2's partials for 9..16 tokens over a long K
-// with float32 or int8 activations) taken from a static device array, for callers that
-// cannot allocate device memory (code under HIP graph capture, serving loops that forbid
-// it).
+// its workspace (K3's split-K partial tiles, K2's partials for 9..16 tokens over a long K
+// with float32 or int8 activations, the bf16 planes of float32 activations past 64 tokens)
+// taken from a static device array, for callers that cannot allocate device memory (code
+// under HIP graph capture, serving loops that forbid it).
 //
 // `scratch` is a file-scope device array, reserved when the code object is loaded on a
 // device and held until the process ends, one copy per device at its own address.  In
@@ -11,7 +11,8 @@
 // kernels receive.  Every call on a device shares the array: calls that overlap on one
 // device (different streams, or threads) race and must be serialised by the caller.
 // Nothing in it needs to start at zero -- a split launch writes every partial it later
-// reads -- so the last call's contents are simply overwritten.
+// reads, the planes path every plane value -- so the last call's contents are simply
+// overwritten.
 #include <hip/hip_runtime.h>
 
 #include <mutex>
