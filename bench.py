@@ -735,7 +735,7 @@ def run_prefill(torch, ops, lib, dev) -> dict:
     workspace the shape asks for): exactly 100 timed launches issued one by one after 20
     untimed ones, over two weight copies, plus >= 50 ms of spread samples.  TFLOP/s of 2 M N K and the fraction of the bf16
     matrix-core peak, from the mean over the 100 timed launches (median alongside)."""
-    cases = []
+    cases, f32_cases = [], []
     for name, k, n in PREFILL_SHAPES:
         wb = make_weights(torch, ops, lib, n, k, 2, dev, seed=4)
         for m in (512, 2048, 8192):
@@ -756,12 +756,26 @@ def run_prefill(torch, ops, lib, dev) -> dict:
                     f"(median {d['median_ms'] * 1e3:8.1f})  {tf:7.1f} TFLOP/s  "
                     f"{tf / BF16_PEAK_TFLOPS:.3f}")
             del x, c
+        # float32 activations at M = 2048, alpha 1 beta 0 (t8.nn.Linear's float inputs):
+        # the planes through the workspace where they pay, else the eight-wave kernel
+        m = 2048
+        x = torch.randn((m, k), device=dev)
+        c = torch.randn((m, n), device=dev)
+        d = time_eager(torch, abi_launch(lib, x, lib.DTYPE_F32, wb, c, m, n, k, which=3,
+                                         torch=torch), len(wb), 100, 20, ahead=4)
+        tf = 2.0 * m * n * k / (d["ms"] * 1e-3) / 1e12
+        f32_cases.append({"shape": name, "M": m, "K": k, "N": n, "ms": round(d["ms"], 5),
+                          "median_ms": round(d["median_ms"], 5), "tflops": round(tf, 1),
+                          "frac_of_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)})
+        log(f"prefill {name:14s} M={m:5d} float32 x: {d['ms'] * 1e3:8.1f} us  {tf:7.1f} TFLOP/s")
+        del x, c
         del wb
         torch.cuda.empty_cache()
     return {"workload": "config 4: K3 prefill GEMM on the Llama-3-8B qkv / gate_up / down shapes "
                         "at M = 512, 2048, 8192, bf16 x, fp32 C, (alpha, beta) = (1, 0) and "
-                        "(0.5, 1); 100 timed launches each",
-            "peak_tflops": BF16_PEAK_TFLOPS, "cases": cases}
+                        "(0.5, 1); 100 timed launches each; float32_x: the same shapes at "
+                        "M = 2048 with float32 activations, alpha 1 beta 0",
+            "peak_tflops": BF16_PEAK_TFLOPS, "cases": cases, "float32_x": f32_cases}
 
 
 def run_limb(torch, ops, lib, dev, cpu_budget: float, with_cpu: bool) -> dict:
