@@ -1,10 +1,11 @@
-// t81lib_amd/csrc/gemv_strip.hip -- K2 for M <= 4 tokens: column strips, activations
-// fixed in registers, wide contiguous weight loads.
+// t81lib_amd/csrc/gemv_strip.hip -- K2 for M <= 4 tokens (bf16 up to 8 over wide, short-K
+// shapes): column strips, activations fixed in registers, wide contiguous weight loads.
 //
 //   C[m, n] = alpha * sum_k X[m, k] * T[n, k] + beta * C[m, n] + bias[n]
 //
 // The limbs of a row are cut into ranges of 4*S consecutive limbs (S = 16 or 8 for one
-// token, 8 for two, 4 for up to four).  A workgroup owns H = R * RPI consecutive rows
+// token, 8 for two, 4 for up to four, 2 for up to eight).  A workgroup owns H = R * RPI
+// consecutive rows
 // (RPI = 16 / S); wave w of it streams range w of all of them (a column "strip"), so the activations
 // a lane needs never change: they are loaded once, as the B operand of
 // v_mfma_f32_16x16x32_bf16, and stay in registers.  One load instruction covers RPI
@@ -19,8 +20,10 @@
 // entry is row a's partial sum over the limbs l0 + q*S + s (q = 0..3) for token j / S.
 // The other entries mix limbs and are never read.  Each load has its own accumulator
 // (started at zero); lane (j, q) holds D[4q + e][j] for e < 4 and keeps element j % 4,
-// which for S in {4, 8, 16} is the one matched entry it holds, if any.  The MFMA count
-// per weight byte is the same for every M <= RPI; tokens past M have zero activations.
+// which for S in {4, 8, 16} is the one matched entry it holds, if any; for S = 2 it keeps
+// elements j % 2 and j % 2 + 2, its two matched entries (rows 2q and 2q + 1).  The MFMA
+// count per weight byte is the same for every M <= RPI; tokens past M have zero
+// activations.
 //
 // The weights are decoded in padded order (each tryte -> bf16 t0, t1, t2, 0 through
 // one 8-byte table read), eight MFMAs per limb; the activations carry a zero in every
@@ -106,8 +109,12 @@ __device__ __forceinline__ float strip_keep(floatx4 v, int j) {
     const float hi = (j & 1) ? v[3] : v[2];
     return (j & 2) ? hi : lo;
 }
+// S = 2: elements j % 2 and j % 2 + 2 (rows 4q + j % 2 and 4q + j % 2 + 2).
+__device__ __forceinline__ float strip_keep2(floatx4 v, int j, int kp) {
+    return (j & 1) ? (kp ? v[3] : v[1]) : (kp ? v[2] : v[0]);
+}
 
-// S: sub-positions per quarter (range = 4*S limbs, S in {4, 8, 16}); NW: waves, one range
+// S: sub-positions per quarter (range = 4*S limbs, S in {2, 4, 8, 16}); NW: waves, one range
 // each at a time; R: loads per range, i.e. R * (16 / S) rows per workgroup.  kNt: weight
 // loads carry the non-temporal hint (see launch_strip_x).  DEPTH: loads in flight per
 // wave (kStripDepth, three for the short natural-order strips).  kNat: limbs
@@ -136,7 +143,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     const void *__restrict__ x, const uint8_t *__restrict__ w, void *__restrict__ c, int M,
     int64_t N, int64_t K, int L, int nranges, int x_aligned, float alpha, float beta,
     const float *__restrict__ bias) {
-    static_assert(S == 4 || S == 8 || S == 16, "one matched entry per lane needs S >= 4");
+    static_assert(S == 2 || S == 4 || S == 8 || S == 16,
+                  "matched entries per lane: one for S >= 4, two for S = 2");
     static_assert(!kStageB || (XT == kDtypeBF16 && !kNat), "staged B: bf16, padded order");
     static_assert(!kSplit || (XT == kDtypeF32 && S <= 8 && !kStageB),
                   "planes as token columns: float32, two columns per token");
@@ -146,7 +154,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     constexpr int H = R * RPI;   // rows per workgroup
     constexpr int D = R < DEPTH ? R : DEPTH;
     __shared__ __attribute__((aligned(16))) uint8_t lut[kLutBytes];
-    __shared__ float red[NW][R][64];
+    constexpr int KP = S == 2 ? 2 : 1;   // matched entries a lane keeps per load
+    __shared__ float red[NW][R][KP][64];
     constexpr int kSlot = 112;
     __shared__ __attribute__((aligned(16))) uint8_t xst[kStageB ? NW * 64 * kSlot : 16];
 
@@ -170,9 +179,19 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
         __syncthreads();
     };
 
-    float kept[R];
+    float kept[R][KP];
 #pragma unroll
-    for (int t = 0; t < R; ++t) kept[t] = 0.0f;
+    for (int t = 0; t < R; ++t)
+#pragma unroll
+        for (int kp = 0; kp < KP; ++kp) kept[t][kp] = 0.0f;
+    auto keep = [&](int t, floatx4 v) {
+        if constexpr (S == 2) {
+            kept[t][0] += strip_keep2(v, i, 0);
+            kept[t][1] += strip_keep2(v, i, 1);
+        } else {
+            kept[t][0] += strip_keep(v, i);
+        }
+    };
 
     bool first = true;
     for (int rg = wave; rg < nranges; rg += NW) {
@@ -288,18 +307,20 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
                 if (t + 1 + D < R) ring[(t + 1) % D] = fetch(t + 1 + D);
             }
             const floatx4 acc = strip_mfma<XM, kOps>(cur, bh, bl);
-            if (t > 0) kept[t - 1] += strip_keep(prev, i);
+            if (t > 0) keep(t - 1, prev);
             prev = acc;
 #pragma unroll
             for (int e = 0; e < 4 * kOps; ++e) cur[e] = nxt[e];
         }
-        kept[R - 1] += strip_keep(prev, i);
+        keep(R - 1, prev);
     }
     if (first) publish_lut();  // a wave with no range still takes part in the barriers
 
     // ---- kept values to LDS; each output sums S sub-sums per wave, waves in order ----
 #pragma unroll
-    for (int t = 0; t < R; ++t) red[wave][t][lane] = kept[t];
+    for (int t = 0; t < R; ++t)
+#pragma unroll
+        for (int kp = 0; kp < KP; ++kp) red[wave][t][kp][lane] = kept[t][kp];
     __syncthreads();
 
     const int nw_used = nranges < NW ? nranges : NW;
@@ -315,12 +336,15 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
 #pragma unroll
             for (int ss = 0; ss < S; ++ss) {
                 // entry D[ra*S + ss][m*S + ss] sits in lane (m*S + ss) + 16 * ((ra*S + ss) / 4)
+                // (S = 2: lane j's two kept entries are rows 4q + j % 2 (kp 0) and
+                // 4q + j % 2 + 2 (kp 1), i.e. kp = ra % 2)
+                const int kp = S == 2 ? (ra & 1) : 0;
                 if constexpr (kSplit) {
                     // token m's hi column 2 m and lo column 2 m + 1
-                    val += red[ww][t][2 * m * S + ss + 16 * ((ra * S + ss) >> 2)];
-                    val += red[ww][t][(2 * m + 1) * S + ss + 16 * ((ra * S + ss) >> 2)];
+                    val += red[ww][t][kp][2 * m * S + ss + 16 * ((ra * S + ss) >> 2)];
+                    val += red[ww][t][kp][(2 * m + 1) * S + ss + 16 * ((ra * S + ss) >> 2)];
                 } else {
-                    val += red[ww][t][m * S + ss + 16 * ((ra * S + ss) >> 2)];
+                    val += red[ww][t][kp][m * S + ss + 16 * ((ra * S + ss) >> 2)];
                 }
             }
         }
@@ -450,7 +474,15 @@ hipError_t launch_strip_x(bool *handled, const void *x, const uint8_t *w, void *
                           hipStream_t s) {
     *handled = false;
     const int64_t L = (k + kTrits - 1) / kTrits;
-    if (m < 1 || m > 4 || n <= 0 || L <= 0) return hipSuccess;
+    if (m < 1 || m > 8 || n <= 0 || L <= 0) return hipSuccess;
+    // bf16 at 5..8 tokens over >= 12288 rows and K <= 4096: S = 2 (8 rows x 8 limbs per
+    // load, two kept entries per lane).  Against the stream kernel, same box: 4096 -> 14336
+    // at 5 / 6 / 8 tokens 9.40 / 9.52 / 9.57 -> 8.68 / 8.74 / 8.83 us, 3072 -> 16384 7.88 /
+    // 8.05 / 8.00 -> 6.29 / 6.31 / 6.70; even on 3072 -> 9216 (6.81 / 7.00 / 7.42 -> 6.70 /
+    // 7.10 / 7.61); slower over a long K, where every wave streams several ranges (14336
+    // -> 4096 11.24 -> 12.99 / 13.11 / 13.48, 8192 -> 3072 7.38 -> 8.74), and on 3072 ->
+    // 3072.
+    if (m > 4 && !(XT == kDtypeBF16 && n >= 12288 && k <= 4096)) return hipSuccess;
     // float32 at one or two tokens: hi and lo planes as B token columns (kSplit), so the
     // launch is shaped as bf16 at mc = 2 m tokens.  Against a second MFMA per operand
     // (same box): one token 4096 -> 14336 10.03 -> 7.39 us, 14336 -> 4096 10.63 -> 9.44,
@@ -464,7 +496,7 @@ hipError_t launch_strip_x(bool *handled, const void *x, const uint8_t *w, void *
     // than S = 8 does; S = 8 (2 rows x 32 limbs) up to 2 tokens; S = 4 up to 4.
     const int64_t pad16 = (L + 63) / 64 * 64;
     const int64_t pad8 = (L + 31) / 32 * 32;
-    const int S = mc == 1 && pad16 <= pad8 ? 16 : (mc <= 2 ? 8 : 4);
+    const int S = mc == 1 && pad16 <= pad8 ? 16 : (mc <= 2 ? 8 : (mc <= 4 ? 4 : 2));
     // buffer offsets within a workgroup's rows must stay below 2^31
     constexpr int64_t kElem = XT == kDtypeF32 ? 4 : (XT == kDtypeBF16 ? 2 : 1);
     if (64 * L * kTrytes >= 0x7FFFFFFF) return hipSuccess;
@@ -526,9 +558,12 @@ hipError_t launch_strip_x(bool *handled, const void *x, const uint8_t *w, void *
             return S == 16 ? launch_strip_nat<16, false>(nw, r, a)
                            : launch_strip_nat<8, false>(nw, r, a);
         }
-        // staged B where waves stream several ranges (see gemv_strip_kernel); two to four
-        // tokens (S = 8, 4)
+        // staged B where waves stream several ranges (see gemv_strip_kernel); two to eight
+        // tokens (S = 8, 4, 2)
         if (a.aligned && per_wave > 1 && S != 16) {
+            if (S == 2)
+                return nt ? launch_strip_nr<XT, 2, true, true>(nw, r, a)
+                          : launch_strip_nr<XT, 2, false, true>(nw, r, a);
             if (nt)
                 return S == 8 ? launch_strip_nr<XT, 8, true, true>(nw, r, a)
                               : launch_strip_nr<XT, 4, true, true>(nw, r, a);
@@ -539,9 +574,11 @@ hipError_t launch_strip_x(bool *handled, const void *x, const uint8_t *w, void *
             switch (S) {
                 case 16: return launch_strip_nr<XT, 16, true>(nw, r, a);
                 case 8: return launch_strip_nr<XT, 8, true>(nw, r, a);
-                default: return launch_strip_nr<XT, 4, true>(nw, r, a);
+                case 4: return launch_strip_nr<XT, 4, true>(nw, r, a);
+                default: return launch_strip_nr<XT, 2, true>(nw, r, a);
             }
         }
+        if (S == 2) return launch_strip_nr<XT, 2>(nw, r, a);
     }
     switch (S) {
         case 16: return launch_strip_nr<XT, 16>(nw, r, a);

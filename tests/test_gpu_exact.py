@@ -91,6 +91,10 @@ K2_CASES = (
     + [("phi3.down", 5, 8192, 3072), ("phi3.o", 12, 3072, 3072), ("wide", 10, 3072, 6144)]
     + [("llama.qkv", 1, 4096, 6144), ("ragged", 1, 4100, 77), ("ragged", 3, 1000, 333),
        ("ragged", 13, 5767, 300)]
+    # the strip kernel at 5..8 tokens (S = 2, two kept entries per lane): >= 12288 rows and
+    # K <= 4096, one range per wave or several (staged B), ragged N and K
+    + [("phi3.gate_up", M, 3072, 16384) for M in (5, 6, 7)]
+    + [("ragged", 7, 4000, 12300), ("ragged", 6, 1000, 13000), ("ragged", 5, 4099, 12289)]
 )
 
 
