@@ -128,7 +128,7 @@ int t81_hip_ternary_matmul_ws(int which, const void *x, int x_dtype, const uint8
 
 /* Bytes of workspace t81_hip_ternary_matmul_ws uses for this shape on the current
  * device (0: the shape does not split).  Never fails.  It does not look at x's
- * alignment: int8 activations at 8+ tokens with K % 16 == 0 report 0, and such a call
+ * alignment: int8 activations at 5+ tokens with K % 16 == 0 report 0, and such a call
  * runs in one launch with no split whether or not x is 16-byte aligned (bf16 likewise at
  * the column-block kernel's 17..48 tokens, where an unaligned x runs K3 unsplit).  For
  * M <= 16 it is K2's workspace: K3 forced there (which = 3) runs unsplit. */

@@ -923,7 +923,7 @@ hipError_t launch_gemv_tile(bool *handled, const void *x, const uint8_t *w, void
     // aligned bf16: the stream kernel with staged activation pieces, one launch, is faster
     // (llama.down M = 16 13.2 us against 14.4 with the split sum; phi3.down 7.9 against 9.4)
     if (XT == kDtypeBF16 && aligned) return hipSuccess;
-    // int8 at 8+ tokens with 16-value pieces: the same staged stream kernel
+    // int8 at 5+ tokens with 16-value pieces: the same staged stream kernel
     if (XT == kDtypeI8 && m >= 8 && k % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0)
         return hipSuccess;
     *handled = true;
@@ -949,13 +949,13 @@ hipError_t launch_stream(const void *x, const uint8_t *w, void *c, int m, int64_
         }
     }
     if constexpr (XT == kDtypeI8 && kAligned) {
-        // int8, 8+ tokens: the same staging, the values widened to bf16 (16-value pieces).
+        // int8, 5+ tokens: the same staging, the values widened to bf16 (16-value pieces).
         // One row group per workgroup (<= 4096 rows) keeps two sub-blocks in flight: with
         // three pieces per lane the second slot is cheap (llama.down M = 8 14.5 -> 12.6 us,
         // M = 16 14.5 -> 13.1, 3072 -> 3072 5.5 -> 5.4; the wider, two- and four-group
         // shapes measured slower, 10.1 -> 11.7 on llama.gate, as did bf16, whose six
         // pieces per lane double the slot: llama.down M = 16 13.2 -> 13.4)
-        if (m >= 8 && k % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0) {
+        if (m >= 5 && k % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0) {
             if constexpr (G == 1)
                 gemv_stream_kernel<XT, G, kAligned, KS, true, true>
                     <<<dim3(blocks), dim3(64 * KS), 0, s>>>(x, w, c, m, n, k, L, alpha, beta, bias);
@@ -1272,7 +1272,11 @@ hipError_t launch_gemv_x(const void *x, const uint8_t *w, void *c, int m, int64_
     // 16384 at M = 8: 10.5 -> 8.7 us; even at 3072 -> 9216), 5+ over >= 14336 (4096 ->
     // 14336 at M = 5: 11.2 -> 9.6 us; 3072 -> 9216 at M = 5 stays faster staged)
     // ... and 8+ tokens with aligned bf16 activations, staged (see launch_stream_shape)
-    const bool stage_i8 = XT == kDtypeI8 && m >= 8 && k % 16 == 0 &&
+    // int8 from 5 tokens (K % 16 == 0, aligned x) takes the staged stream kernel: against
+    // the wave kernel at 5..7 tokens 3072 -> 9216 12.25 / 10.49 / 11.35 -> 9.08 / 9.05 /
+    // 9.18 us, 8192 -> 3072 10.28 / 10.96 / 11.64 -> 8.18 / 8.16 / 8.18, 14336 -> 4096 13.3
+    // -> 12.4 (3072 -> 3072 at 5 tokens 5.57 -> 5.78)
+    const bool stage_i8 = XT == kDtypeI8 && m >= 5 && k % 16 == 0 &&
                           reinterpret_cast<uintptr_t>(x) % 16 == 0;
     const bool wide = (XT == kDtypeBF16 && ((m >= 8 && n >= 9216) || (m >= 5 && n >= 14336) ||
                                             (m >= 8 && aligned8))) ||
@@ -1401,7 +1405,7 @@ int64_t gemv_workspace_bytes(int64_t m, int64_t n, int64_t k, int x_dtype) {
     if (m < 5 || m > 16 || n <= 0 || k <= 0) return 0;
     // bf16 with K % 8 == 0 runs the staged stream kernel in one launch instead
     if (x_dtype == kDtypeBF16 && k % 8 == 0) return 0;
-    if (x_dtype == kDtypeI8 && m >= 8 && k % 16 == 0) return 0;   // the same, 16-value pieces
+    if (x_dtype == kDtypeI8 && m >= 5 && k % 16 == 0) return 0;   // the same, 16-value pieces
     return gemv_tile_workspace_bytes(static_cast<int>(m), n, k);   // float32 partials
 }
 

@@ -1,5 +1,6 @@
-// t81lib_amd/csrc/gemv_strip.hip -- K2 for M <= 4 tokens (bf16 up to 8 over wide, short-K
-// shapes): column strips, activations fixed in registers, wide contiguous weight loads.
+// t81lib_amd/csrc/gemv_strip.hip -- K2 for M <= 4 tokens (bf16 and int8 up to 8 over wide,
+// short-K shapes): column strips, activations fixed in registers, wide contiguous weight
+// loads.
 //
 //   C[m, n] = alpha * sum_k X[m, k] * T[n, k] + beta * C[m, n] + bias[n]
 //
@@ -482,7 +483,10 @@ hipError_t launch_strip_x(bool *handled, const void *x, const uint8_t *w, void *
     // 7.10 / 7.61); slower over a long K, where every wave streams several ranges (14336
     // -> 4096 11.24 -> 12.99 / 13.11 / 13.48, 8192 -> 3072 7.38 -> 8.74), and on 3072 ->
     // 3072.
-    if (m > 4 && !(XT == kDtypeBF16 && n >= 12288 && k <= 4096)) return hipSuccess;
+    // int8 the same (4096 -> 14336 at 5 / 8 tokens 16.48 / 9.92 -> 8.65 / 8.65 us, 3072 ->
+    // 16384 12.52 / 8.25 -> 6.34 / 6.50)
+    if (m > 4 && !((XT == kDtypeBF16 || XT == kDtypeI8) && n >= 12288 && k <= 4096))
+        return hipSuccess;
     // float32 at one or two tokens: hi and lo planes as B token columns (kSplit), so the
     // launch is shaped as bf16 at mc = 2 m tokens.  Against a second MFMA per operand
     // (same box): one token 4096 -> 14336 10.03 -> 7.39 us, 14336 -> 4096 10.63 -> 9.44,
@@ -490,7 +494,12 @@ hipError_t launch_strip_x(bool *handled, const void *x, const uint8_t *w, void *
     // and 3072 -> 3072 4.10 -> 4.43, so one token takes it from 4096 rows; two tokens
     // everywhere (4096 -> 14336 9.34 -> 7.85, 8192 -> 3072 9.71 -> 7.19, 3072 -> 3072 4.70
     // -> 3.99).
-    const bool split = XT == kDtypeF32 && (m == 2 || (m == 1 && n >= 4096));
+    // (three and four tokens, as S = 2, on the wide short-K shapes the S = 2 form takes:
+    // 4096 -> 14336 at 3 / 4 tokens 9.54 / 10.26 -> 9.15 / 9.33 us, 3072 -> 16384 8.01 /
+    // 8.92 -> 6.53 / 6.70; elsewhere slower, 14336 -> 4096 11.46 -> 14.09)
+    const bool wide_short = n >= 12288 && k <= 4096;
+    const bool split = XT == kDtypeF32 &&
+                       (m == 2 || (m == 1 && n >= 4096) || (m <= 4 && wide_short));
     const int mc = split ? 2 * m : m;
     // S = 16 (one row x 64 limbs per load) for one token when it pads the row no more
     // than S = 8 does; S = 8 (2 rows x 32 limbs) up to 2 tokens; S = 4 up to 4.
@@ -545,6 +554,9 @@ hipError_t launch_strip_x(bool *handled, const void *x, const uint8_t *w, void *
             if (S == 8)
                 return nt ? launch_strip_nr<XT, 8, true, false, true>(nw, r, a)
                           : launch_strip_nr<XT, 8, false, false, true>(nw, r, a);
+            if (S == 2)
+                return nt ? launch_strip_nr<XT, 2, true, false, true>(nw, r, a)
+                          : launch_strip_nr<XT, 2, false, false, true>(nw, r, a);
             return nt ? launch_strip_nr<XT, 4, true, false, true>(nw, r, a)
                       : launch_strip_nr<XT, 4, false, false, true>(nw, r, a);
         }
@@ -583,7 +595,8 @@ hipError_t launch_strip_x(bool *handled, const void *x, const uint8_t *w, void *
     switch (S) {
         case 16: return launch_strip_nr<XT, 16>(nw, r, a);
         case 8: return launch_strip_nr<XT, 8>(nw, r, a);
-        default: return launch_strip_nr<XT, 4>(nw, r, a);
+        case 4: return launch_strip_nr<XT, 4>(nw, r, a);
+        default: return launch_strip_nr<XT, 2>(nw, r, a);
     }
 }
 

@@ -49,8 +49,9 @@ hipError_t launch_gemv(const void *x, int x_dtype, const uint8_t *w, void *c, in
                        void *ws = nullptr, int64_t ws_bytes = 0);
 int64_t gemv_workspace_bytes(int64_t m, int64_t n, int64_t k, int x_dtype);
 
-// gemv_strip.hip (K2, M <= 4; bf16 at 5..8 tokens over >= 12288 rows and K <= 4096): sets
-// *handled = false (and launches nothing) when the shape is outside what it covers
+// gemv_strip.hip (K2, M <= 4; bf16 and int8 at 5..8 tokens over >= 12288 rows and K <=
+// 4096): sets *handled = false (and launches nothing) when the shape is outside what it
+// covers
 hipError_t launch_gemv_strip(bool *handled, const void *x, int x_dtype, const uint8_t *w,
                              void *c, int m, int64_t n, int64_t k, float alpha, float beta,
                              const float *bias, hipStream_t s);

@@ -472,12 +472,13 @@ def test_k3_int8_config4_bit_exact(gpu, orc, name, M, K, N):
 
 
 I8_STREAM_CASES = [
-    # M, N, K: int8 activations at 8..16 tokens through K2 (K % 16 == 0, 16-byte aligned x:
-    # the staged stream kernel), at the 8-token switch-over and at 9..15 tokens with masked
-    # token columns, for one, two and four row groups per workgroup; K = 14400 ends inside
-    # a sub-block
+    # M, N, K: int8 activations at 5..16 tokens through K2 (K % 16 == 0, 16-byte aligned x:
+    # the staged stream kernel; the strip kernel at 5..8 over >= 12288 rows and K <= 4096),
+    # at the 5-token switch-over and at 6..15 tokens with masked token columns, for one,
+    # two and four row groups per workgroup; K = 14400 ends inside a sub-block
     (8, 14336, 4096), (8, 4096, 14336), (12, 4100, 3072), (9, 257, 14400), (15, 9216, 3072),
-    (11, 3072, 8192),
+    (11, 3072, 8192), (5, 4096, 14336), (6, 9216, 3072), (7, 3072, 8192), (5, 16384, 3072),
+    (7, 12300, 4000),
 ]
 
 
