@@ -337,8 +337,13 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_kernel(
 // A workgroup of four waves computes a 256 x 256 tile of C^T; wave (wn, wm) owns
 // 128 weight rows x 128 tokens, i.e. 4 x 4 blocks of v_mfma_f32_32x32x16_bf16
 // (256 accumulator registers).  (RB = 3: 192-row tiles, three row blocks per wave, for
-// shapes whose 256-row tiles leave CUs idle; whole tiles only.)  A k-step is two limbs
-// (96 trits):
+// shapes whose 256-row tiles leave CUs idle; whole tiles only.)  WR = 4 ("tall" tiles):
+// the four waves side by side along the rows instead of 2 x 2, a 512 x 128 tile -- each
+// wave's MFMAs, decode and B reads as before, but the workgroup's activation tile is
+// half as large, so a step issues half the global -> LDS tile loads (7 per wave instead
+// of 13; gate_up M = 2048 367 -> 356 us, M = 8192 1398 -> 1356 us, qkv / down at M =
+// 8192 -3 % / -2 %, bit-identical), for twice the weight bytes per token tile (read from
+// L2 and the MALL).  A k-step is two limbs (96 trits):
 //  * lane (r, h) loads all 16 bytes of limb 2s + h of row 32 rb + r, so one
 //    32-trit slice of the MFMA pairs trits 8J..8J+7 of limb 2s (h = 0) with the
 //    same trits of limb 2s + 1 (h = 1), J = 0..5; B lane (c, h) reads
@@ -377,18 +382,18 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void *base,
         reinterpret_cast<void *>((static_cast<uint64_t>(hi) << 32) | lo), 0, n, 0x00020000);
 }
 
-// Work items.  Weight rows [0, n1) run as whole 256 x 256 tiles (all k-steps, result
-// to C).  Rows [n1, N) run either as split-K items (nsplit > 0): item (split sp, tile t of
+// Work items.  Weight rows [0, n1) run as whole 256 x 256 tiles (512 x 128 for WR = 4;
+// all k-steps, result to C).  Rows [n1, N) run either as split-K items (nsplit > 0): item (split sp, tile t of
 // that region) runs k-steps [sp * sps, (sp + 1) * sps) and stores its raw accumulators
 // (no alpha, beta, bias) to part in the order (sp, t, wave, block, a4, lane) as float4s
 // -- every store is 1 KB contiguous; gemm_split_reduce_kernel then sums the splits in
-// order -- or (half != 0) as half-width tiles of 256 rows x 128 tokens over all k-steps,
-// result to C: when those fill about one round of the CUs they need no workspace and no
+// order (WR = 2 only) -- or (half != 0) as half-width tiles of 256 rows x 128 tokens
+// (512 x 64) over all k-steps, result to C: when those fill about one round of the CUs they need no workspace and no
 // second launch.  Half of the remainder's items come first and half last in the item
 // order, so the workgroups that start with a (shorter) remainder item finish their whole
 // tiles half a tile out of step with the others, and the C stores of the two halves do
 // not all land at once.
-template <int XT, int RB, bool kBeta>
+template <int XT, int RB, bool kBeta, int WR = 2>
 __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
     const void *__restrict__ x, const uint8_t *__restrict__ w, void *__restrict__ c, int M, int N,
     int ldc, int K, int L, float alpha, float beta, const float *__restrict__ bias, int n1,
@@ -401,11 +406,15 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
         nsplit = 0;
         half = 0;
     }
-    constexpr int kRows = 64 * RB;   // weight rows per tile
+    static_assert(WR == 2 || (WR == 4 && RB == 4), "waves 2 x 2, or 4 along the rows");
+    if constexpr (WR == 4) nsplit = 0;   // no split-K items (their sum assumes 2 x 2)
+    constexpr int WT = 4 / WR;            // waves along the tokens
+    constexpr int kRows = 32 * RB * WR;   // weight rows per tile
+    constexpr int kTokW = 128 * WT;       // tokens per whole tile
     // Two separate tile objects (not one array indexed by a run-time parity): the
     // loads into one buffer then provably do not alias the reads of the other, and
     // the compiler need not wait for them before every LDS read.  A half-width item
-    // uses the first half of each.
+    // (and every WR = 4 item) uses the first half of each, or less.
     // (The table's larger alignment places it at LDS address 0, so a table address is
     // just the byte field, with no base to add.)
     __shared__ __attribute__((aligned(1024))) uint8_t lut[kLutBytes];
@@ -430,8 +439,8 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
 
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wn = wave & 1;
-    const int wm = wave >> 1;
+    const int wn = WR == 4 ? wave : wave & 1;
+    const int wm = WR == 4 ? 0 : wave >> 1;
 
     // Items walk the weight-row tiles fastest: items running together share their
     // activation rows.  (Tile indices are uniform: readfirstlane keeps them, and the
@@ -439,8 +448,8 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
     // persistent, one workgroup per CU taking items blockIdx.x, + gridDim.x, ...: a
     // new workgroup per tile started only after the C stores of the whole previous
     // round had drained (~15 us a round at M = 2048).
-    const int tiles_m = (M + kW4Tokens - 1) / kW4Tokens;
-    const int tiles_mh = (M + kW4Tokens / 2 - 1) / (kW4Tokens / 2);   // half-width tiles
+    const int tiles_m = (M + kTokW - 1) / kTokW;
+    const int tiles_mh = (M + kTokW / 2 - 1) / (kTokW / 2);   // half-width tiles
     const int tn1 = (n1 + kRows - 1) / kRows;        // row tiles of whole tiles
     const int tn2 = (N - n1 + kRows - 1) / kRows;    // row tiles of the remainder
     const int full_items = tn1 * tiles_m;
@@ -451,18 +460,20 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
     const int all_steps = (L + 1) / 2;
     lut_fill(lut, tid, kW4Threads);  // published by the first item's barrier
 
-    // One item: 64 RB weight rows (nwg..) x 64 CB tokens (m0..) over k-steps
+    // One item: 32 RB WR weight rows (nwg..) x 32 CB WT tokens (m0..) over k-steps
     // [s_begin, s_end); wave (wn, wm) owns 32 RB rows x 32 CB tokens.  CB = 4: whole or
     // split-K tiles; CB = 2: half-width tiles.
     auto run_item = [&](auto cbc, int nwg, int m0, int s_begin, int s_end, bool split, int sp,
                         int tt) {
         constexpr int CB = decltype(cbc)::value;      // 32-token blocks per wave
-        constexpr int kTok = 64 * CB;                  // tokens per workgroup
+        constexpr int kTok = 32 * CB * WT;             // tokens per workgroup
         // every wave is past the previous item's epilogue (staged in xs0) before this
         // item's tile loads
         __syncthreads();
-        constexpr int kTL = kTok * kW4RowSlots / 64;   // tile loads per workgroup (52, 26)
-        constexpr int LPW = (kTL + 3) / 4;             // per wave (13; 7, the last wave 5)
+        // tile loads per workgroup (52, 26, 13) and per wave (13; 7, the last wave 5; 4, the
+        // last wave 1)
+        constexpr int kTL = kTok * kW4RowSlots / 64;
+        constexpr int LPW = (kTL + 3) / 4;
         constexpr int NCH = 6 * CB;                    // chunks of four MFMAs per step
         constexpr int HALF = 3 * CB;                   // chunks per half step
         constexpr int NF = CB == 4 ? 2 * RB : RB;      // chunks of a half that read the table
@@ -629,8 +640,9 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
         // each also carries its share of the decode -- the first NF chunks of the first
         // half: half 1 of wcur into a1; of the second half: half 0 of wnxt (the next
         // step) into a0; table reads two chunks ahead of their merge -- and of the loads.
-        // Whole tiles (CB = 4): the tile of the next step (chunks 0-11), then the weights
-        // of the step after it (chunk 12); issued after the tile loads, the weight loads
+        // Whole tiles (CB = 4): the tile of the next step (chunks 0 .. LPW - 2, two loads
+        // in the last), then the weights of the step after it (chunk LPW - 1); issued
+        // after the tile loads, the weight loads
         // can stay in flight across the step's wait (vmcnt(RB)), so they have a step and a
         // half to land, not half a step.  Half-width tiles (CB = 2): the weights of the
         // step after next (chunk 0), and, past the barrier, the tile of the step after
@@ -670,24 +682,24 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
                     }
                 }
                 if constexpr (CB == 4) {
-                    if (g < 12) load_tile_part(step + 1, otherc, g);
-                    if (g == 11) load_tile_part(step + 1, otherc, 12);
-                    if (g == 12) fetch_w(step + 2, wnn);
+                    if (g < LPW - 1) load_tile_part(step + 1, otherc, g);
+                    if (g == LPW - 2) load_tile_part(step + 1, otherc, LPW - 1);
+                    if (g == LPW - 1) fetch_w(step + 2, wnn);
                 } else {
                     if (g == 0) fetch_w(step + 2, wnn);
                     if (step + 1 < s_end) {
                         if (g == 9) {
                             load_tile_part(step + 2, bufc, 0);
-                            load_tile_part(step + 2, bufc, 1);
-                            load_tile_part(step + 2, bufc, 2);
+                            if (LPW > 1) load_tile_part(step + 2, bufc, 1);
+                            if (LPW > 2) load_tile_part(step + 2, bufc, 2);
                         }
                         if (g == 10) {
-                            load_tile_part(step + 2, bufc, 3);
-                            load_tile_part(step + 2, bufc, 4);
+                            if (LPW > 3) load_tile_part(step + 2, bufc, 3);
+                            if (LPW > 4) load_tile_part(step + 2, bufc, 4);
                         }
                         if (g == 11) {
-                            load_tile_part(step + 2, bufc, 5);
-                            load_tile_part(step + 2, bufc, 6);
+                            if (LPW > 5) load_tile_part(step + 2, bufc, 5);
+                            if (LPW > 6) load_tile_part(step + 2, bufc, 6);
                         }
                     }
                 }
@@ -872,7 +884,7 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
             if constexpr (RB == 4) {
                 const int tn = __builtin_amdgcn_readfirstlane(item % tn2);
                 const int tm = __builtin_amdgcn_readfirstlane(item / tn2);
-                run_item(std::integral_constant<int, 2>(), n1 + tn * kRows, tm * (kW4Tokens / 2),
+                run_item(std::integral_constant<int, 2>(), n1 + tn * kRows, tm * (kTokW / 2),
                          0, all_steps, false, 0, 0);
             }
         } else {
@@ -885,7 +897,7 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
             const int s_begin = split ? sp * sps : 0;
             const int s_end = split && s_begin + sps < all_steps ? s_begin + sps : all_steps;
             run_item(std::integral_constant<int, 4>(), (split ? n1 : 0) + tn * kRows,
-                     tm * kW4Tokens, s_begin, s_end, split, sp, tt);
+                     tm * kTokW, s_begin, s_end, split, sp, tt);
         }
     }  // work items
 }
@@ -1085,6 +1097,48 @@ hipError_t launch_gemm_w4(const void *x, const uint8_t *w, void *c, int64_t m, i
         static_cast<const float4 *>(part), static_cast<float *>(c) + n1, m, n - n1, ldc,
         static_cast<int>(tiles), static_cast<int>(plan->nsplit), alpha, beta,
         bias ? bias + n1 : nullptr);
+    return hipGetLastError();
+}
+
+// Tall tiles (the big-tile kernel's WR = 4 instance: 512 weight rows x 128 tokens) for
+// shapes with at least a round of them: when whole rounds cover the rows, or whole rounds
+// and then one round of their 512 x 64 half-width tiles (three quarters of the CUs or
+// more), as for 256 x 256 tiles.  Otherwise (fewer tiles, or a remainder that fits
+// neither) the 256 x 256 rules below.  Also needs the 32-bit buffer offsets of a
+// workgroup's 512 weight rows.
+bool gemm_tall_plan(int64_t m, int64_t n, int64_t k, int64_t *n1_out, bool *half_out) {
+    const int64_t L = (k + kTrits - 1) / kTrits;
+    const int64_t cus = cu_count();
+    const int64_t tiles_m = (m + 127) / 128;
+    const int64_t tiles = ((n + 511) / 512) * tiles_m;
+    if (m <= 64 || tiles < cus || int64_t(512) * L * kTrytes >= 0x7FFFFFFF) return false;
+    const int64_t rem = tiles % cus;
+    if (rem == 0) {
+        *n1_out = n;
+        *half_out = false;
+        return true;
+    }
+    const int64_t n1 = (tiles - rem) / tiles_m * 512;
+    if (n1 <= 0 || n1 >= n) return false;
+    const int64_t t = ((n - n1 + 511) / 512) * ((m + 63) / 64);
+    if (t > cus || 4 * t < 3 * cus) return false;
+    *n1_out = n1;
+    *half_out = true;
+    return true;
+}
+hipError_t launch_gemm_w4_tall(const void *x, const uint8_t *w, void *c, int64_t m, int64_t n,
+                               int64_t n1, bool half, int64_t k, float alpha, float beta,
+                               const float *bias, hipStream_t s) {
+    const int64_t L = (k + kTrits - 1) / kTrits;
+    const int64_t items = ((n1 + 511) / 512) * ((m + 127) / 128) +
+                          (half ? ((n - n1 + 511) / 512) * ((m + 63) / 64) : 0);
+    const int64_t cus = cu_count();
+    auto kernel = beta != 0.0f ? gemm_w4_kernel<kDtypeBF16, 4, true, 4>
+                               : gemm_w4_kernel<kDtypeBF16, 4, false, 4>;
+    kernel<<<dim3(items < cus ? items : cus), dim3(kW4Threads), 0, s>>>(
+        x, w, c, static_cast<int>(m), static_cast<int>(n), static_cast<int>(n),
+        static_cast<int>(k), static_cast<int>(L), alpha, beta, bias, static_cast<int>(n1), 0,
+        nullptr, 0, half ? 1 : 0);
     return hipGetLastError();
 }
 
@@ -1359,6 +1413,11 @@ hipError_t launch_gemm_x(const void *x, const uint8_t *w, void *c, int64_t m, in
         const int64_t n1 = gemm_rows_whole_rounds(m, n);
         const int64_t L = (k + kTrits - 1) / kTrits;
         const bool w4 = XT == kDtypeBF16 && gemm_w4_fits(x, m, n, k);
+        int64_t tn1 = 0;
+        bool thalf = false;
+        if (w4 && gemm_tall_plan(m, n, k, &tn1, &thalf))
+            // one launch of 512 x 128 tiles for rows [0, tn1), 512 x 64 for the rest
+            return launch_gemm_w4_tall(x, w, c, m, n, tn1, thalf, k, alpha, beta, bias, s);
         if (w4 && gemm_use_192(m, n))
             return launch_gemm_w4_192(x, w, c, m, n, n, k, alpha, beta, bias, s);
         if (w4 && gemm_use_half(m, n, n1))

@@ -232,6 +232,26 @@ def whole_round_rows(M: int, N: int) -> int:
     return N
 
 
+def tall_rows(M: int, N: int, K: int):
+    """Weight rows the K3 launcher runs as whole 512 x 128 tiles when it takes the tall
+    form (the rest as one round of 512 x 64 half-width tiles), or None when it does not
+    (the launcher's rule for aligned bf16 activations)."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    tiles_m = -(-M // 128)
+    tiles = -(-N // 512) * tiles_m
+    L = -(-K // 48)
+    if M <= 64 or tiles < cus or 512 * L * 16 >= 0x7FFFFFFF:
+        return None
+    rem = tiles % cus
+    if rem == 0:
+        return N
+    n1 = (tiles - rem) // tiles_m * 512
+    if not 0 < n1 < N:
+        return None
+    t = -(-(N - n1) // 512) * -(-M // 64)
+    return n1 if 4 * t >= 3 * cus and t <= cus else None
+
+
 def _gpu_exact_product(xg_f64: torch.Tensor, packed: torch.Tensor, N: int, K: int) -> torch.Tensor:
     """x @ T^T in float64 on the GPU from the unpacked trits (exact for these integers)."""
     tt = ops.unpack(packed, N, K).to(torch.float64).t().contiguous()   # (K, N)
@@ -324,26 +344,42 @@ def test_k3_big_tile_integer_bf16_bit_exact(gpu, orc, M, N, K):
 
 
 K3_HALF = [
-    # M, N, K: whole rounds of 256 x 256 tiles for the first 16384 rows, the rest as one
-    # round of half-width 256 x 128 tiles (on 256 CUs: 200 / 192 / 192 of them) in the
-    # same launch; one, three (K past the last whole step) and four steps; ragged N
+    # M, N, K: whole rounds of 256 x 256 tiles for the first 8192 rows, the rest as one
+    # round of half-width 256 x 128 tiles (on 256 CUs: 195 of them) in the same launch,
+    # where the tall tiles' remainder (180 of 512 x 64) would not fill a round; one and
+    # four steps; ragged M and N
+    (1900, 256 * 44 + 13, 96), (1900, 256 * 44 + 13, 384),
+]
+K3_TALL = [
+    # M, N, K: tall 512 x 128 tiles (four waves along the rows).  Whole rounds only (on 256
+    # CUs): one round with ragged M and N, two rounds with three steps (K past the last
+    # whole step), one token in the last token tile; then whole rounds for the first 16384
+    # rows and the rest as one round of 512 x 64 half-width tiles (208 / 192 / 192 of them):
+    # one, three and four steps, ragged N
+    (1000, 512 * 32 - 5, 96), (1000, 512 * 64, 200), (129, 512 * 128, 96),
     (1000, 256 * 88 + 7, 96), (1000, 256 * 88, 200), (1000, 256 * 88 - 5, 384),
 ]
 
 
-@pytest.mark.parametrize("M,N,K", K3_HALF)
-def test_k3_half_width_integer_bf16_bit_exact(gpu, orc, M, N, K):
+@pytest.mark.parametrize("M,N,K,tall", [c + (False,) for c in K3_HALF] +
+                         [c + (True,) for c in K3_TALL])
+def test_k3_half_width_integer_bf16_bit_exact(gpu, orc, M, N, K, tall):
     """Every output against the float64 product of the unpacked trits on the GPU, a sample
     from both regions against the C oracle, alpha / beta / bias, and no workspace asked
-    for (the half-width tiles need none)."""
-    announce(f"exact K3 half-width M={M} N={N} K={K}")
+    for (the half-width and tall tiles need none)."""
+    announce(f"exact K3 {'tall' if tall else 'half-width'} M={M} N={N} K={K}")
     lib = _lib.lib()
     assert lib.t81_hip_ternary_matmul_workspace_size(M, N, K, _lib.DTYPE_BF16) == 0
     w, x, c, bias = int_problem(M, N, K, seed=M + N + K)
     packed = ops.quantize_pack(w.to(gpu), 0.45, _lib.THR_CPP)
     exact = _gpu_exact_product(x.to(torch.float64).to(gpu), packed, N, K)
-    n1 = whole_round_rows(M, N)
-    assert 0 < n1 < N, "shape expected to leave rows past whole rounds"
+    if tall:
+        n1 = tall_rows(M, N, K)
+        assert n1 is not None, "shape expected to take the tall tiles"
+    else:
+        assert tall_rows(M, N, K) is None, "shape expected to keep the 256 x 256 tiles"
+        n1 = whole_round_rows(M, N)
+        assert 0 < n1 < N, "shape expected to leave rows past whole rounds"
     toks, rows = _sample(M, N, n1, seed=K)
     acc_s = orc.trit_matmul_i64(x[torch.from_numpy(toks)].to(torch.int8).numpy(),
                                 packed.cpu().numpy()[rows], K)
