@@ -1100,7 +1100,9 @@ hipError_t launch_gemm_w4(const void *x, const uint8_t *w, void *c, int64_t m, i
     return hipGetLastError();
 }
 
-// Tall tiles (the big-tile kernel's WR = 4 instance: 512 weight rows x 128 tokens) for
+}  // namespace
+
+// Tall tiles (the big-tile kernels' WR = 4 instances: 512 weight rows x 128 tokens) for
 // shapes with at least a round of them: when whole rounds cover the rows, or whole rounds
 // and then one round of their 512 x 64 half-width tiles (three quarters of the CUs or
 // more), as for 256 x 256 tiles.  Otherwise (fewer tiles, or a remainder that fits
@@ -1126,6 +1128,8 @@ bool gemm_tall_plan(int64_t m, int64_t n, int64_t k, int64_t *n1_out, bool *half
     *half_out = true;
     return true;
 }
+namespace {
+
 hipError_t launch_gemm_w4_tall(const void *x, const uint8_t *w, void *c, int64_t m, int64_t n,
                                int64_t n1, bool half, int64_t k, float alpha, float beta,
                                const float *bias, hipStream_t s) {

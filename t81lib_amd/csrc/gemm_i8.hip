@@ -8,8 +8,9 @@
 // int32 result can hold (|sum| <= 128 K), at twice the bf16 rate (5 POP/s dense).
 //
 // Tiling (as the bf16 kernel): a workgroup of four waves, one per SIMD, computes a
-// 256 x 256 tile of C^T; wave (wn, wm) owns 128 weight rows x 128 tokens, 4 x 4 blocks
-// of 32 x 32 int32 accumulators (all 256 AGPRs).  A k-step is two limbs (96 trits):
+// 256 x 256 tile of C^T (or a tall 512 x 128 one, the waves along the rows); wave (wn, wm)
+// owns 128 weight rows x 128 tokens, 4 x 4 blocks of 32 x 32 int32 accumulators (all 256
+// AGPRs).  A k-step is two limbs (96 trits):
 //  * lane (r, h) loads the 16 bytes of limb 2s + h of row 32 rb + r and decodes it into
 //    three 16-trit operands (J = 0, 1, 2: trits 16J .. 16J + 15 of the limb, one int8
 //    each); B lane (c, h) reads X[c, 96 s + 48 h + 16 J .. + 16], 16 bytes of the
@@ -95,7 +96,10 @@ __device__ __forceinline__ void i8_lut_fill(uint8_t *lds, int tid, int nthreads)
 // kHalf: the instance with the half-width path (compiled apart, so that the whole-tile
 // instance keeps its register allocation: the combined one spills 27 scalar registers and
 // ran M = 8192 gate_up 1.2 % slower).
-template <bool kHalf, bool kAcc>
+// WR = 4: tall 512 x 128 tiles (the four waves side by side along the rows, each still
+// 128 rows x 128 tokens; half the activation-tile loads per step), half-width 512 x 64,
+// no split-K items (their sum assumes 2 x 2 waves).
+template <bool kHalf, bool kAcc, int WR = 2>
 __global__ __launch_bounds__(kI8Threads) void gemm_w4_i8_kernel(
     const int8_t *__restrict__ x, const uint8_t *__restrict__ w, int32_t *__restrict__ c, int M,
     int N, int ldc, int K, int L, int accumulate, int n1, int sps, i32x4 *__restrict__ part,
@@ -125,13 +129,18 @@ __global__ __launch_bounds__(kI8Threads) void gemm_w4_i8_kernel(
 
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wn = wave & 1;
-    const int wm = wave >> 1;
+    static_assert(WR == 2 || WR == 4, "waves 2 x 2, or 4 along the rows");
+    if constexpr (WR == 4) nsplit = 0;
+    constexpr int WT = 4 / WR;           // waves along the tokens
+    constexpr int kRowsT = 128 * WR;     // weight rows per tile
+    constexpr int kTokT = 128 * WT;      // tokens per whole tile
+    const int wn = WR == 4 ? wave : wave & 1;
+    const int wm = WR == 4 ? 0 : wave >> 1;
 
-    const int tiles_m = (M + kI8Tokens - 1) / kI8Tokens;
-    const int tiles_mh = (M + kI8Tokens / 2 - 1) / (kI8Tokens / 2);   // half-width tiles
-    const int tn1 = (n1 + kI8Rows - 1) / kI8Rows;
-    const int tn2 = (N - n1 + kI8Rows - 1) / kI8Rows;
+    const int tiles_m = (M + kTokT - 1) / kTokT;
+    const int tiles_mh = (M + kTokT / 2 - 1) / (kTokT / 2);   // half-width tiles
+    const int tn1 = (n1 + kRowsT - 1) / kRowsT;
+    const int tn2 = (N - n1 + kRowsT - 1) / kRowsT;
     const int full_items = tn1 * tiles_m;
     const int tiles2 = tn2 * tiles_m;
     const int rem_items = half ? tn2 * tiles_mh : (nsplit > 0 ? tiles2 * nsplit : 0);
@@ -140,14 +149,16 @@ __global__ __launch_bounds__(kI8Threads) void gemm_w4_i8_kernel(
     const int all_steps = (L + 1) / 2;
     i8_lut_fill(lut, tid, kI8Threads);  // published by the first item's barrier
 
-    // One item: 256 weight rows (nwg..) x 64 CB tokens (m0..) over k-steps [s_begin, s_end);
-    // wave (wn, wm) owns 128 rows x 32 CB tokens.  CB = 4: whole or split-K tiles; CB = 2:
-    // half-width tiles.
+    // One item: 128 WR weight rows (nwg..) x 32 CB WT tokens (m0..) over k-steps
+    // [s_begin, s_end); wave (wn, wm) owns 128 rows x 32 CB tokens.  CB = 4: whole or
+    // split-K tiles; CB = 2: half-width tiles.
     auto run_item = [&](auto cbc, int nwg, int m0, int s_begin, int s_end, bool split, int sp,
                         int tt) {
         constexpr int CB = decltype(cbc)::value;          // 32-token blocks per wave
-        constexpr int kTL = 64 * CB * kI8RowSlots / 64;    // tile loads per workgroup (28, 14)
-        constexpr int LPW = (kTL + 3) / 4;                 // per wave (7; 4, the last wave 2)
+        // tile loads per workgroup (28, 14, 7) and per wave (7; 4, the last wave 2; 2, the
+        // last wave 1)
+        constexpr int kTL = 32 * CB * WT * kI8RowSlots / 64;
+        constexpr int LPW = (kTL + 3) / 4;
         constexpr int NCH = 3 * CB;                        // chunks of four MFMAs per step
         constexpr int NFC = CB == 4 ? 8 : 4;               // chunks that issue table reads
         constexpr int kWLoads = 4;                         // loads of fetch_w: one per row block
@@ -197,8 +208,9 @@ __global__ __launch_bounds__(kI8Threads) void gemm_w4_i8_kernel(
             tbase[i] = slot < kI8RowSlots - 1 ? row * static_cast<uint32_t>(K) + 16 * slot : kI8Oob;
             tslot[i / 4] |= (16 * slot) << (8 * (i % 4));
         }
-        // The last wave's spare loads of a half-width tile (LDS bytes 14336..16383, inside
-        // the buffer and never read) load zeros through an out-of-range offset, not a branch.
+        // The last wave's spare loads of a half-width or tall tile (LDS bytes 14336..16383 or
+        // 7168..8191, inside the buffer and never read) load zeros through an out-of-range
+        // offset, not a branch.
         auto load_tile_part = [&](int step, auto bufc, int i) {
             const bool spare = LPW * 4 != kTL && i >= kTL - 3 * LPW && LPW * wave + i >= kTL;
             const int k0 = step * kI8StepK;
@@ -463,8 +475,8 @@ __global__ __launch_bounds__(kI8Threads) void gemm_w4_i8_kernel(
             if (rem) {
                 const int tn = __builtin_amdgcn_readfirstlane(item % tn2);
                 const int tm = __builtin_amdgcn_readfirstlane(item / tn2);
-                run_item(std::integral_constant<int, 2>(), n1 + tn * kI8Rows,
-                         tm * (kI8Tokens / 2), 0, all_steps, false, 0, 0);
+                run_item(std::integral_constant<int, 2>(), n1 + tn * kRowsT,
+                         tm * (kTokT / 2), 0, all_steps, false, 0, 0);
                 continue;
             }
         }
@@ -477,8 +489,8 @@ __global__ __launch_bounds__(kI8Threads) void gemm_w4_i8_kernel(
             const int tm = __builtin_amdgcn_readfirstlane(tt / tiles_n);
             const int s_begin = split ? sp * sps : 0;
             const int s_end = split && s_begin + sps < all_steps ? s_begin + sps : all_steps;
-            run_item(std::integral_constant<int, 4>(), (split ? n1 : 0) + tn * kI8Rows,
-                     tm * kI8Tokens, s_begin, s_end, split, sp, tt);
+            run_item(std::integral_constant<int, 4>(), (split ? n1 : 0) + tn * kRowsT,
+                     tm * kTokT, s_begin, s_end, split, sp, tt);
         }
     }  // work items
 }
@@ -608,6 +620,26 @@ int64_t gemm_i8_workspace_bytes(int64_t m, int64_t n, int64_t k) {
 hipError_t launch_gemm_i8(const void *x, const uint8_t *w, int32_t *c, int64_t m, int64_t n,
                           int64_t k, bool accumulate, hipStream_t s, void *ws, int64_t ws_bytes) {
     const int64_t L = (k + kTrits - 1) / kTrits;
+    const int64_t cus = cu_count();
+    // Tall tiles (gemm_tall_plan) up to K = 8192: gate_up M = 2048 249.7 -> 242.7 us, M =
+    // 8192 946.7 -> 923.6 us, qkv M = 8192 208.2 -> 204.8 us; down (K = 14336) at M = 8192
+    // measured 453.2 -> 457.4 us and keeps the 256 x 256 tiles.
+    int64_t tn1 = 0;
+    bool thalf = false;
+    if (k <= 8192 && gemm_tall_plan(m, n, k, &tn1, &thalf)) {
+        const int64_t items = ((tn1 + 511) / 512) * ((m + 127) / 128) +
+                              (thalf ? ((n - tn1 + 511) / 512) * ((m + 63) / 64) : 0);
+        const dim3 grid(static_cast<unsigned>(items < cus ? items : cus));
+        auto kernel = thalf ? (accumulate ? gemm_w4_i8_kernel<true, true, 4>
+                                          : gemm_w4_i8_kernel<true, false, 4>)
+                            : (accumulate ? gemm_w4_i8_kernel<false, true, 4>
+                                          : gemm_w4_i8_kernel<false, false, 4>);
+        kernel<<<grid, dim3(kI8Threads), 0, s>>>(
+            static_cast<const int8_t *>(x), w, c, static_cast<int>(m), static_cast<int>(n),
+            static_cast<int>(n), static_cast<int>(k), static_cast<int>(L), accumulate ? 1 : 0,
+            static_cast<int>(tn1), 0, nullptr, 0);
+        return hipGetLastError();
+    }
     I8Plan p = i8_plan(m, n, k);
     const bool split = !p.half && p.nsplit > 1 && ws != nullptr &&
                        ws_bytes >= p.nsplit * p.tiles * kI8Rows * kI8Tokens * 4;
@@ -619,7 +651,6 @@ hipError_t launch_gemm_i8(const void *x, const uint8_t *w, int32_t *c, int64_t m
     const int64_t items = ((p.n1 + kI8Rows - 1) / kI8Rows) * tiles_m +
                           (split ? p.nsplit * p.tiles : 0) + half_items;
     if (items <= 0) return hipSuccess;
-    const int64_t cus = cu_count();
     const dim3 grid(static_cast<unsigned>(items < cus ? items : cus));
     // (split items store raw partials; the split sum adds C)
     if (p.half) {

@@ -118,6 +118,10 @@ hipError_t launch_gemm_i8(const void *x, const uint8_t *w, int32_t *c, int64_t m
 // Compute units of the current device (256 on MI355X), cached per device.
 int cu_count();
 
+// Whether the big-tile kernels run a shape as tall 512 x 128 tiles (gemm.hip): rows
+// [0, *n1) as whole tiles, and with *half the rest as one round of 512 x 64 tiles.
+bool gemm_tall_plan(int64_t m, int64_t n, int64_t k, int64_t *n1, bool *half);
+
 // limb.hip (K4)
 hipError_t launch_gemm_limb(const uint8_t *a, const uint8_t *b, float *c, int m, int n,
                             int k_limbs, float alpha, float beta, hipStream_t s);

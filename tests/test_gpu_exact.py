@@ -418,8 +418,14 @@ I8_SMALL = [
     # whole step, even and odd step counts, more tiles than CUs, few tiles (split-K)
     (300, 256 * 160 + 13, 208), (260, 256 * 81 + 7, 480), (512, 256 * 200 - 5, 96),
     (65, 1000, 4096), (300, 1000, 4112), (100, 2000, 4800), (257, 700, 16),
-    # whole rounds for the first 16384 rows, the rest as one round of half-width tiles
-    # (200 / 192 of them on 256 CUs): two and three steps, ragged N
+    # whole rounds of 256 x 256 tiles for the first 8192 rows, the rest as one round of
+    # 256 x 128 half-width tiles (195 of them on 256 CUs, where the tall tiles' remainder
+    # would not fill a round): one and three steps, ragged M and N
+    (1900, 256 * 44 + 13, 96), (1900, 256 * 44 + 13, 208),
+    # tall 512 x 128 tiles (on 256 CUs): one round with ragged M and N, two rounds, one
+    # token in the last token tile; whole rounds for the first 16384 rows and the rest as
+    # one round of 512 x 64 half-width tiles (208 / 192 of them): one and three steps
+    (1000, 512 * 32 - 5, 96), (1000, 512 * 64, 208), (129, 512 * 128, 96),
     (1000, 256 * 88 + 7, 96), (1000, 256 * 88 - 5, 208),
 ]
 
