@@ -336,14 +336,15 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_kernel(
 //
 // A workgroup of four waves computes a 256 x 256 tile of C^T; wave (wn, wm) owns
 // 128 weight rows x 128 tokens, i.e. 4 x 4 blocks of v_mfma_f32_32x32x16_bf16
-// (256 accumulator registers).  (RB = 3: 192-row tiles, three row blocks per wave, for
-// shapes whose 256-row tiles leave CUs idle; whole tiles only.)  WR = 4 ("tall" tiles):
+// (256 accumulator registers).  WR = 4 ("tall" tiles):
 // the four waves side by side along the rows instead of 2 x 2, a 512 x 128 tile -- each
 // wave's MFMAs, decode and B reads as before, but the workgroup's activation tile is
 // half as large, so a step issues half the global -> LDS tile loads (7 per wave instead
 // of 13; gate_up M = 2048 367 -> 356 us, M = 8192 1398 -> 1356 us, qkv / down at M =
 // 8192 -3 % / -2 %, bit-identical), for twice the weight bytes per token tile (read from
-// L2 and the MALL).  A k-step is two limbs (96 trits):
+// L2 and the MALL).  (RB = 3, WR = 4: 384 x 128 tiles, three row blocks per wave, for
+// shapes whose 256-row tiles leave CUs idle; whole tiles only.)  A k-step is two limbs
+// (96 trits):
 //  * lane (r, h) loads all 16 bytes of limb 2s + h of row 32 rb + r, so one
 //    32-trit slice of the MFMA pairs trits 8J..8J+7 of limb 2s (h = 0) with the
 //    same trits of limb 2s + 1 (h = 1), J = 0..5; B lane (c, h) reads
@@ -401,12 +402,12 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
     static_assert(XT == kDtypeBF16, "the LDS tile is filled straight from bf16 activations");
     static_assert(RB == 3 || RB == 4, "three or four 32-row blocks per wave");
     if constexpr (RB == 3) {
-        // the 192-row instance has no remainder path: every row is in a whole tile
+        // the 384-row instance has no remainder path: every row is in a whole tile
         n1 = N;
         nsplit = 0;
         half = 0;
     }
-    static_assert(WR == 2 || (WR == 4 && RB == 4), "waves 2 x 2, or 4 along the rows");
+    static_assert((WR == 2 && RB == 4) || WR == 4, "waves 2 x 2, or 4 along the rows");
     if constexpr (WR == 4) nsplit = 0;   // no split-K items (their sum assumes 2 x 2)
     constexpr int WT = 4 / WR;            // waves along the tokens
     constexpr int kRows = 32 * RB * WR;   // weight rows per tile
@@ -1036,25 +1037,29 @@ int64_t split_workspace_bytes(const SplitPlan &p) {
     return p.nsplit > 1 ? p.nsplit * p.tiles * kW4Rows * kW4Tokens * 4 : 0;
 }
 
-// 192-row tiles (three 32-row blocks per wave) when a shape has fewer 256-row tiles than
-// CUs but 160 or more (no split), and its 192-row tiles still fit one round: every CU
-// then runs one tile of three quarters the work instead of three quarters of the CUs
-// one tile each (qkv at M = 2048: 192 -> 256 tiles).
-bool gemm_use_192(int64_t m, int64_t n) {
-    const int64_t tiles_m = (m + kW4Tokens - 1) / kW4Tokens;
-    const int64_t t4 = ((n + kW4Rows - 1) / kW4Rows) * tiles_m;
-    const int64_t t3 = ((n + 191) / 192) * tiles_m;
+// 384 x 128 tiles (three 32-row blocks per wave, the waves along the rows: the RB = 3,
+// WR = 4 instance) when a shape has fewer 256 x 256 tiles than CUs but 160 or more (no
+// split), and its 384 x 128 tiles still fit one round: every CU then runs one tile of
+// about three quarters the work instead of three quarters of the CUs one tile each (qkv
+// at M = 2048: 192 -> 256 tiles).  The 2 x 2 form of the same tiles (192 x 256) measured
+// slower: qkv M = 2048 83.2 -> 80.7 us, with beta = 1 95.4 -> 89.8 us, 3072 -> 3072 at
+// M = 4096 66.2 -> 64.7 us, a ragged 2000 x 4104 -> 6000 95.9 -> 90.9 us.
+bool gemm_use_384(int64_t m, int64_t n, int64_t k) {
+    const int64_t L = (k + kTrits - 1) / kTrits;
+    const int64_t t4 = ((n + kW4Rows - 1) / kW4Rows) * ((m + kW4Tokens - 1) / kW4Tokens);
+    const int64_t t3 = ((n + 383) / 384) * ((m + 127) / 128);
     const int64_t cus = cu_count();
-    return m > 64 && t4 >= 160 && t4 < cus && t3 <= cus;
+    return m > 64 && t4 >= 160 && t4 < cus && t3 <= cus &&
+           int64_t(384) * L * kTrytes < 0x7FFFFFFF;
 }
-hipError_t launch_gemm_w4_192(const void *x, const uint8_t *w, void *c, int64_t m, int64_t n,
+hipError_t launch_gemm_w4_384(const void *x, const uint8_t *w, void *c, int64_t m, int64_t n,
                               int64_t ldc, int64_t k, float alpha, float beta, const float *bias,
                               hipStream_t s) {
     const int64_t L = (k + kTrits - 1) / kTrits;
-    const int64_t items = ((n + 191) / 192) * ((m + kW4Tokens - 1) / kW4Tokens);
+    const int64_t items = ((n + 383) / 384) * ((m + 127) / 128);
     const int64_t cus = cu_count();
-    auto kernel = beta != 0.0f ? gemm_w4_kernel<kDtypeBF16, 3, true>
-                               : gemm_w4_kernel<kDtypeBF16, 3, false>;
+    auto kernel = beta != 0.0f ? gemm_w4_kernel<kDtypeBF16, 3, true, 4>
+                               : gemm_w4_kernel<kDtypeBF16, 3, false, 4>;
     kernel<<<dim3(items < cus ? items : cus), dim3(kW4Threads), 0, s>>>(
         x, w, c, static_cast<int>(m), static_cast<int>(n), static_cast<int>(ldc),
         static_cast<int>(k), static_cast<int>(L), alpha, beta, bias, static_cast<int>(n), 0,
@@ -1422,8 +1427,8 @@ hipError_t launch_gemm_x(const void *x, const uint8_t *w, void *c, int64_t m, in
         if (w4 && gemm_tall_plan(m, n, k, &tn1, &thalf))
             // one launch of 512 x 128 tiles for rows [0, tn1), 512 x 64 for the rest
             return launch_gemm_w4_tall(x, w, c, m, n, tn1, thalf, k, alpha, beta, bias, s);
-        if (w4 && gemm_use_192(m, n))
-            return launch_gemm_w4_192(x, w, c, m, n, n, k, alpha, beta, bias, s);
+        if (w4 && gemm_use_384(m, n, k))
+            return launch_gemm_w4_384(x, w, c, m, n, n, k, alpha, beta, bias, s);
         if (w4 && gemm_use_half(m, n, n1))
             // one launch: whole tiles for rows [0, n1), one round of half-width tiles for
             // the rest

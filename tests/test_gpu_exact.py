@@ -321,8 +321,9 @@ K3_SMALL = [
     # whole rounds of 256 x 256 tiles, the remaining rows as one round of half-width
     # 256 x 128 tiles (on 256 CUs: 192-256 of them), ragged M and N
     (1900, 256 * 44 + 13, 200),
-    # 160-255 tiles of 256 rows whose 192-row tiles fit one round (on 256 CUs): 192-row
-    # tiles; a last tile of 7 rows (three steps), ragged M over two token tiles (16 steps)
+    # 160-255 tiles of 256 x 256 whose 384 x 128 tiles fit one round (on 256 CUs: 252 and
+    # 192 of them): 384 x 128 tiles; a last tile of 7 rows (three steps), ragged M over
+    # three token tiles (16 steps)
     (200, 192 * 250 + 7, 200), (300, 192 * 128 - 5, 1536),
 ]
 
