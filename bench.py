@@ -991,18 +991,25 @@ def summarize_trace_by_grid(d: str, kernel_sub: str, cmd: str, runs: bool = Fals
     kernel and launch shape (grid x workgroup size, which tells apart the shapes one kernel
     instance serves), for the kernels whose name contains kernel_sub, in first-launch order.
     runs: one row per run of consecutive such dispatches with the same key (in start order),
-    so that two shapes with one launch shape, timed one after the other, stay apart."""
+    so that two shapes with one launch shape, timed one after the other, stay apart; two
+    keys whose dispatches strictly alternate (two epilogues of one shape timed in turn) keep
+    one row each for the stretch they alternate over."""
     rows = [r for r in _read_csv(_find(d, "kernel_trace.csv")) if kernel_sub in r["Kernel_Name"]]
     rows.sort(key=lambda r: int(r["Start_Timestamp"]))
     groups: list = []
     index: dict = {}
+    keys: list = []
     for r in rows:
         key = (r["Kernel_Name"], int(r["Grid_Size_X"]), int(r["Workgroup_Size_X"]))
         us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        keys.append(key)
         if runs:
-            if not groups or groups[-1][0] != key:
-                groups.append((key, []))
-            groups[-1][1].append(us)
+            if groups and groups[-1][0] == key:
+                groups[-1][1].append(us)
+            elif len(groups) >= 2 and groups[-2][0] == key and len(keys) >= 3 and keys[-3] == key:
+                groups[-2][1].append(us)
+            else:
+                groups.append((key, [us]))
         else:
             if key not in index:
                 index[key] = len(groups)
