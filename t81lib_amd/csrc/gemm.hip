@@ -384,13 +384,13 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void *base,
 }
 
 // Work items.  Weight rows [0, n1) run as whole 256 x 256 tiles (512 x 128 for WR = 4;
-// all k-steps, result to C).  Rows [n1, N) run either as split-K items (nsplit > 0): item (split sp, tile t of
-// that region) runs k-steps [sp * sps, (sp + 1) * sps) and stores its raw accumulators
-// (no alpha, beta, bias) to part in the order (sp, t, wave, block, a4, lane) as float4s
-// -- every store is 1 KB contiguous; gemm_split_reduce_kernel then sums the splits in
-// order (WR = 2 only) -- or (half != 0) as half-width tiles of 256 rows x 128 tokens
-// (512 x 64) over all k-steps, result to C: when those fill about one round of the CUs they need no workspace and no
-// second launch.  Half of the remainder's items come first and half last in the item
+// all k-steps, result to C).  Rows [n1, N) run either as split-K items (nsplit > 0): item
+// (split sp, tile t of that region) runs k-steps [sp * sps, (sp + 1) * sps) and stores its
+// raw accumulators (no alpha, beta, bias) to part in the order (sp, t, wave, block, a4,
+// lane) as float4s -- every store is 1 KB contiguous; gemm_split_reduce_kernel<WR> then
+// sums the splits in order -- or (half != 0) as half-width tiles of 256 rows x 128 tokens
+// (512 x 64) over all k-steps, result to C: when those fill about one round of the CUs
+// they need no workspace and no second launch.  Half of the remainder's items come first and half last in the item
 // order, so the workgroups that start with a (shorter) remainder item finish their whole
 // tiles half a tile out of step with the others, and the C stores of the two halves do
 // not all land at once.
@@ -408,7 +408,6 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
         half = 0;
     }
     static_assert((WR == 2 && RB == 4) || WR == 4, "waves 2 x 2, or 4 along the rows");
-    if constexpr (WR == 4) nsplit = 0;   // no split-K items (their sum assumes 2 x 2)
     constexpr int WT = 4 / WR;            // waves along the tokens
     constexpr int kRows = 32 * RB * WR;   // weight rows per tile
     constexpr int kTokW = 128 * WT;       // tokens per whole tile
@@ -923,6 +922,8 @@ bool gemm_w4_fits(const void *x, int64_t m, int64_t n, int64_t k) {
 // kernel's own epilogue does.
 constexpr int kReducePitch = 132;   // floats per staged token row: 128 + 4 pad
 
+// WR = 4: the partials of tall split items (512 x 128 tiles, wave w on rows 128 w ..).
+template <int WR = 2>
 __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(
     const float4 *__restrict__ part, float *__restrict__ c, int64_t M, int64_t N, int64_t ldc,
     int tiles, int nsplit, float alpha, float beta, const float *__restrict__ bias) {
@@ -930,9 +931,9 @@ __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(
     const int tt = static_cast<int>(blockIdx.x >> 4);
     const int wave = static_cast<int>((blockIdx.x >> 2) & 3);
     const int cb = static_cast<int>(blockIdx.x & 3);
-    const int wn = wave & 1, wm = wave >> 1;
-    const int tiles_n = static_cast<int>((N + kW4Rows - 1) / kW4Rows);
-    const int64_t m0 = static_cast<int64_t>(tt / tiles_n) * kW4Tokens + 128 * wm + 32 * cb;
+    const int wn = WR == 4 ? wave : wave & 1, wm = WR == 4 ? 0 : wave >> 1;
+    const int tiles_n = static_cast<int>((N + 128 * WR - 1) / (128 * WR));
+    const int64_t m0 = static_cast<int64_t>(tt / tiles_n) * (512 / WR) + 128 * wm + 32 * cb;
     if (m0 >= M) return;
     const int64_t per_split = static_cast<int64_t>(tiles) * 4 * 64 * 64;
     const float4 *src = part + (static_cast<int64_t>(tt) * 4 + wave) * 4096;
@@ -953,7 +954,7 @@ __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(
         *reinterpret_cast<float4 *>(&st[r * kReducePitch + 32 * rb + 8 * a4 + 4 * h]) = v;
     }
     __syncthreads();
-    const int64_t n0 = static_cast<int64_t>(tt % tiles_n) * kW4Rows + 128 * wn;
+    const int64_t n0 = static_cast<int64_t>(tt % tiles_n) * (128 * WR) + 128 * wn;
     const bool vec4 = ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(c) & 15u) == 0;
     for (int i = threadIdx.x; i < 32 * 32; i += 256) {
         const int tok = i >> 5, c4 = i & 31;
@@ -1098,7 +1099,7 @@ hipError_t launch_gemm_w4(const void *x, const uint8_t *w, void *c, int64_t m, i
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int64_t tiles = plan->tiles;
-    gemm_split_reduce_kernel<<<dim3(static_cast<unsigned>(tiles * 16)), dim3(256), 0, s>>>(
+    gemm_split_reduce_kernel<2><<<dim3(static_cast<unsigned>(tiles * 16)), dim3(256), 0, s>>>(
         static_cast<const float4 *>(part), static_cast<float *>(c) + n1, m, n - n1, ldc,
         static_cast<int>(tiles), static_cast<int>(plan->nsplit), alpha, beta,
         bias ? bias + n1 : nullptr);
@@ -1148,6 +1149,45 @@ hipError_t launch_gemm_w4_tall(const void *x, const uint8_t *w, void *c, int64_t
         x, w, c, static_cast<int>(m), static_cast<int>(n), static_cast<int>(n),
         static_cast<int>(k), static_cast<int>(L), alpha, beta, bias, static_cast<int>(n1), 0,
         nullptr, 0, half ? 1 : 0);
+    return hipGetLastError();
+}
+
+// Split-K over tall tiles, for shapes whose rows all split (fewer than 160 big tiles): the
+// plan of gemm_split_plan over 512 x 128 tiles, each split item storing its raw sums as a
+// 2 x 2 item does (1 KB per wave per block), summed by gemm_split_reduce_kernel<4>.  Half
+// the tile loads per step, the same partial traffic: down 14336 -> 4096 at M = 2048 193.9
+// -> 189.2 us, at M = 512 69.3 -> 68.5 us, qkv at M = 512 the same (43.5 us); bit-identical
+// to the 2 x 2 split (each output's splits hold the same k-steps).
+SplitPlan gemm_split_plan_tall(int64_t m, int64_t n, int64_t k) {
+    const int64_t L = (k + kTrits - 1) / kTrits;
+    const int64_t nsteps = (L + 1) / 2;
+    const int64_t tiles = ((n + 511) / 512) * ((m + 127) / 128);
+    SplitPlan p{1, nsteps, tiles};
+    if (m <= 64 || tiles >= 160 || tiles <= 0 || int64_t(512) * L * kTrytes >= 0x7FFFFFFF)
+        return p;
+    int64_t ns = (cu_count() + tiles / 2) / tiles;
+    if (ns > nsteps / 4) ns = nsteps / 4;
+    if (ns < 2) return p;
+    p.sps = (nsteps + ns - 1) / ns;
+    p.nsplit = (nsteps + p.sps - 1) / p.sps;
+    return p;
+}
+hipError_t launch_gemm_w4_tall_split(const void *x, const uint8_t *w, void *c, int64_t m,
+                                     int64_t n, int64_t k, float alpha, float beta,
+                                     const float *bias, hipStream_t s, const SplitPlan &plan,
+                                     void *part) {
+    const int64_t L = (k + kTrits - 1) / kTrits;
+    const int64_t items = plan.nsplit * plan.tiles;
+    const int64_t cus = cu_count();
+    gemm_w4_kernel<kDtypeBF16, 4, false, 4><<<dim3(items < cus ? items : cus), dim3(kW4Threads), 0, s>>>(
+        x, w, c, static_cast<int>(m), static_cast<int>(n), static_cast<int>(n),
+        static_cast<int>(k), static_cast<int>(L), alpha, beta, bias, 0,
+        static_cast<int>(plan.sps), static_cast<float4 *>(part), static_cast<int>(plan.nsplit), 0);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    gemm_split_reduce_kernel<4><<<dim3(static_cast<unsigned>(plan.tiles * 16)), dim3(256), 0, s>>>(
+        static_cast<const float4 *>(part), static_cast<float *>(c), m, n, n,
+        static_cast<int>(plan.tiles), static_cast<int>(plan.nsplit), alpha, beta, bias);
     return hipGetLastError();
 }
 
@@ -1434,6 +1474,12 @@ hipError_t launch_gemm_x(const void *x, const uint8_t *w, void *c, int64_t m, in
             // the rest
             return launch_gemm_w4(x, w, c, m, n, n1, n, k, alpha, beta, bias, s, nullptr, nullptr,
                                   true);
+        if (w4 && ws != nullptr && n1 == 0) {
+            // every row split over the workspace: tall split-K items, then their sum
+            const SplitPlan tp = gemm_split_plan_tall(m, n, k);
+            if (tp.nsplit > 1 && ws_bytes >= split_workspace_bytes(tp))
+                return launch_gemm_w4_tall_split(x, w, c, m, n, k, alpha, beta, bias, s, tp, ws);
+        }
         if (w4 && ws != nullptr && n1 < n) {
             // one launch: whole tiles for rows [0, n1), split-K items for the rest
             const SplitPlan plan = gemm_split_plan(m, n - n1, k);
@@ -1521,9 +1567,14 @@ int64_t gemm_workspace_x(int64_t m, int64_t n, int64_t k) {
         if constexpr (XT != kDtypeBF16) return eight;
         // aligned activations whose remaining rows fill a round of half-width tiles run
         // without a workspace
-        const int64_t big = k % 8 == 0 && !gemm_use_half(m, n, n1)
-                                ? split_workspace_bytes(gemm_split_plan(m, n - n1, k))
-                                : 0;
+        int64_t big = k % 8 == 0 && !gemm_use_half(m, n, n1)
+                          ? split_workspace_bytes(gemm_split_plan(m, n - n1, k))
+                          : 0;
+        if (k % 8 == 0 && n1 == 0) {
+            // (the tall split's plan, which its tile count can change)
+            const int64_t t = split_workspace_bytes(gemm_split_plan_tall(m, n, k));
+            if (t > big) big = t;
+        }
         return big > eight ? big : eight;
     }
 }

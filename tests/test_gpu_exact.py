@@ -314,13 +314,18 @@ def test_k3_config4_integer_bf16_bit_exact(gpu, orc, name, M, K, N):
 
 K3_SMALL = [
     # M, N, K: >= 160 big tiles (whole-tile kernel), odd and even step counts, K past
-    # the last whole step, ragged M / N, more tiles than CUs; then few tiles (split-K)
+    # the last whole step, ragged M / N, more tiles than CUs; then few tiles (split-K over
+    # tall 512 x 128 tiles when the workspace is given, else the eight-wave kernel)
     (300, 256 * 160 + 13, 200), (512, 256 * 80, 192), (260, 256 * 81 + 7, 480),
     (512, 256 * 200 - 5, 96), (300, 1000, 4104), (260, 4096, 2000), (200, 700, 1536),
     (300, 256 * 160, 1536),
     # whole rounds of 256 x 256 tiles, the remaining rows as one round of half-width
     # 256 x 128 tiles (on 256 CUs: 192-256 of them), ragged M and N
     (1900, 256 * 44 + 13, 200),
+    # whole rounds of 256 x 256 tiles for the first 32768 rows, the rest (88 half-width
+    # tiles, too few for a round) as 2 x 2 split-K items over the workspace, where the tall
+    # tiles' remainder fits neither (two splits of four k-steps)
+    (512, 256 * 150, 768),
     # 160-255 tiles of 256 x 256 whose 384 x 128 tiles fit one round (on 256 CUs: 252 and
     # 192 of them): 384 x 128 tiles; a last tile of 7 rows (three steps), ragged M over
     # three token tiles (16 steps)
