@@ -986,27 +986,36 @@ def summarize_trace(d: str, cmd: str, top: int = 8) -> str:
     return "\n".join(out) + "\n"
 
 
-def summarize_trace_by_grid(d: str, kernel_sub: str, cmd: str, runs: bool = False) -> str:
+def summarize_trace_by_grid(d: str, kernel_sub: str, cmd: str, runs: bool = False,
+                            gap_ms: float = 1.0) -> str:
     """Per-dispatch table of a `rocprofv3 --kernel-trace --output-format csv` run, grouped by
     kernel and launch shape (grid x workgroup size, which tells apart the shapes one kernel
     instance serves), for the kernels whose name contains kernel_sub, in first-launch order.
     runs: one row per run of consecutive such dispatches with the same key (in start order),
-    so that two shapes with one launch shape, timed one after the other, stay apart; two
-    keys whose dispatches strictly alternate (two epilogues of one shape timed in turn) keep
-    one row each for the stretch they alternate over."""
+    so that two shapes with one launch shape, timed one after the other, stay apart; a run
+    also ends where the GPU ran none of these kernels for more than gap_ms (the host setting
+    up the next timed case); two keys whose dispatches strictly alternate (two launches per
+    call, as float32 activations' two planes) keep one row each for the stretch they
+    alternate over."""
     rows = [r for r in _read_csv(_find(d, "kernel_trace.csv")) if kernel_sub in r["Kernel_Name"]]
     rows.sort(key=lambda r: int(r["Start_Timestamp"]))
     groups: list = []
     index: dict = {}
     keys: list = []
+    last_end = None
     for r in rows:
         key = (r["Kernel_Name"], int(r["Grid_Size_X"]), int(r["Workgroup_Size_X"]))
         us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        gap = last_end is not None and int(r["Start_Timestamp"]) - last_end > gap_ms * 1e6
+        last_end = int(r["End_Timestamp"])
+        if gap:
+            keys = []
         keys.append(key)
         if runs:
-            if groups and groups[-1][0] == key:
+            if groups and groups[-1][0] == key and not gap:
                 groups[-1][1].append(us)
-            elif len(groups) >= 2 and groups[-2][0] == key and len(keys) >= 3 and keys[-3] == key:
+            elif (len(groups) >= 2 and groups[-2][0] == key and len(keys) >= 3 and
+                  keys[-3] == key):
                 groups[-2][1].append(us)
             else:
                 groups.append((key, [us]))
