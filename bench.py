@@ -994,9 +994,10 @@ def summarize_trace_by_grid(d: str, kernel_sub: str, cmd: str, runs: bool = Fals
     runs: one row per run of consecutive such dispatches with the same key (in start order),
     so that two shapes with one launch shape, timed one after the other, stay apart; a run
     also ends where the GPU ran none of these kernels for more than gap_ms (the host setting
-    up the next timed case); two keys whose dispatches strictly alternate (two launches per
-    call, as float32 activations' two planes) keep one row each for the stretch they
-    alternate over."""
+    up the next timed case) or where a dispatch takes more than 1.6 x or less than 1 / 1.6 x
+    the run's mean so far (the next shape on the same launch shape); two keys whose
+    dispatches strictly alternate (two launches per call, as float32 activations' two
+    planes) keep one row each for the stretch they alternate over."""
     rows = [r for r in _read_csv(_find(d, "kernel_trace.csv")) if kernel_sub in r["Kernel_Name"]]
     rows.sort(key=lambda r: int(r["Start_Timestamp"]))
     groups: list = []
@@ -1012,10 +1013,13 @@ def summarize_trace_by_grid(d: str, kernel_sub: str, cmd: str, runs: bool = Fals
             keys = []
         keys.append(key)
         if runs:
-            if groups and groups[-1][0] == key and not gap:
+            def near(ts):
+                mean = sum(ts) / len(ts)
+                return mean / 1.6 <= us <= 1.6 * mean
+            if groups and groups[-1][0] == key and not gap and near(groups[-1][1]):
                 groups[-1][1].append(us)
             elif (len(groups) >= 2 and groups[-2][0] == key and len(keys) >= 3 and
-                  keys[-3] == key):
+                  keys[-3] == key and near(groups[-2][1])):
                 groups[-2][1].append(us)
             else:
                 groups.append((key, [us]))
