@@ -390,10 +390,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void *base,
 // lane) as float4s -- every store is 1 KB contiguous; gemm_split_reduce_kernel<WR> then
 // sums the splits in order -- or (half != 0) as half-width tiles of 256 rows x 128 tokens
 // (512 x 64) over all k-steps, result to C: when those fill about one round of the CUs
-// they need no workspace and no second launch.  Half of the remainder's items come first and half last in the item
-// order, so the workgroups that start with a (shorter) remainder item finish their whole
-// tiles half a tile out of step with the others, and the C stores of the two halves do
-// not all land at once.
+// they need no workspace and no second launch.  Half of the remainder's items come first
+// and half last in the item order, so the workgroups that start with a (shorter)
+// remainder item finish their whole tiles half a tile out of step with the others, and
+// the C stores of the two halves do not all land at once.
 template <int XT, int RB, bool kBeta, int WR = 2>
 __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
     const void *__restrict__ x, const uint8_t *__restrict__ w, void *__restrict__ c, int M, int N,
@@ -1179,7 +1179,8 @@ hipError_t launch_gemm_w4_tall_split(const void *x, const uint8_t *w, void *c, i
     const int64_t L = (k + kTrits - 1) / kTrits;
     const int64_t items = plan.nsplit * plan.tiles;
     const int64_t cus = cu_count();
-    gemm_w4_kernel<kDtypeBF16, 4, false, 4><<<dim3(items < cus ? items : cus), dim3(kW4Threads), 0, s>>>(
+    const dim3 grid(static_cast<unsigned>(items < cus ? items : cus));
+    gemm_w4_kernel<kDtypeBF16, 4, false, 4><<<grid, dim3(kW4Threads), 0, s>>>(
         x, w, c, static_cast<int>(m), static_cast<int>(n), static_cast<int>(n),
         static_cast<int>(k), static_cast<int>(L), alpha, beta, bias, 0,
         static_cast<int>(plan.sps), static_cast<float4 *>(part), static_cast<int>(plan.nsplit), 0);
