@@ -12,8 +12,11 @@
 // trytes the reference's 48x48 trit convolution and carry passes
 // (simd_impl.hpp:185-223) produce, and the double sums below -- same table, same
 // order, no FMA contraction -- are bit-identical to gemm_cpu.cpp:8-71.
-// This kernel is the parity path, not the roofline-graded one: one thread per
-// output, l ascending.
+// The convolution runs as signed 4-byte dot products (v_dot4_i32_i8) of a's digits
+// against b's digits reversed, and the carry sweep as a multiply-shift; the table lives
+// in LDS.  Several lanes per output each form one product, and the output's first lane
+// adds them in limb order -- the reference's order, so the same bits.  This is the parity
+// path, not the roofline-graded one.
 #include "pack_common.hpp"
 #include "t81_device.hpp"
 #include "t81_kernels.hpp"
@@ -51,65 +54,115 @@ __constant__ TrTable kTable = make_tryte_table();
 constexpr TrTable kHostTable = make_tryte_table();
 constexpr double kRadix = make_radix();
 
-__device__ __forceinline__ double limb_value_double(const int (&digit)[32], int base) {
+constexpr int kTableEntries = kTrytes * 27;
+
+// The tryte table in the workgroup's LDS (tab[27 p + u] = table[p][u]); published by the
+// caller's next barrier.
+__device__ __forceinline__ void tryte_table_fill(double *tab) {
+    for (int e = threadIdx.x; e < kTableEntries; e += blockDim.x)
+        tab[e] = kTable.v[e / 27][e % 27];
+}
+
+// include/t81/linalg/gemm.hpp:48-56: the 16 tryte contributions of one limb, in order.
+__device__ __forceinline__ double limb_value_double(const double *tab, const int (&digit)[32],
+                                                    int base) {
     double r = 0.0;
 #pragma unroll
-    for (int p = 0; p < kTrytes; ++p) r = r + kTable.v[p][digit[base + p] + 13];
+    for (int p = 0; p < kTrytes; ++p) r = r + tab[27 * p + digit[base + p] + 13];
     return r;
 }
 
-__device__ __forceinline__ double multiply_to_double(const uint4 &a4, const uint4 &b4) {
-    int a[kTrytes], b[kTrytes];
+// Four trytes (bytes < 27) -> their digits u - 13 as signed bytes: with bit 7 of every
+// byte set, the per-byte subtraction never borrows across bytes.
+__device__ __forceinline__ uint32_t tryte_digits(uint32_t w) {
+    return ((w | 0x80808080u) - 0x0D0D0D0Du) ^ 0x80808080u;
+}
+
+__device__ __forceinline__ double multiply_to_double(const double *tab, const uint4 &a4,
+                                                     const uint4 &b4) {
     const uint32_t aw[4] = {a4.x, a4.y, a4.z, a4.w};
     const uint32_t bw[4] = {b4.x, b4.y, b4.z, b4.w};
+    // ad: a's digits; pb: b's digits reversed (b[15 - x] at byte x of dwords 4..7) with
+    // four zero dwords either side
+    uint32_t ad[4], pb[12];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            a[4 * i + j] = static_cast<int>((aw[i] >> (8 * j)) & 0xFFu) - 13;
-            b[4 * i + j] = static_cast<int>((bw[i] >> (8 * j)) & 0xFFu) - 13;
-        }
+        ad[i] = tryte_digits(aw[i]);
+        pb[4 + i] = __builtin_bswap32(tryte_digits(bw[3 - i]));
+        pb[i] = 0u;
+        pb[8 + i] = 0u;
     }
+    // conv[s] = sum_p a[p] b[s - p] (|conv| <= 16 * 169): per 4-digit block k of a, the
+    // reversed b's bytes from offset 31 - s + 4k (compile-time offsets)
+    auto window = [&](int off) -> int {
+        const int d = off >> 2, r = off & 3;
+        return static_cast<int>(r == 0 ? pb[d] : __builtin_amdgcn_alignbyte(pb[d + 1], pb[d], r));
+    };
     int conv[32];
 #pragma unroll
-    for (int s = 0; s < 32; ++s) conv[s] = 0;
+    for (int s = 0; s < 31; ++s) {
+        int acc = 0;
 #pragma unroll
-    for (int p = 0; p < kTrytes; ++p)
-#pragma unroll
-        for (int q = 0; q < kTrytes; ++q) conv[p + q] += a[p] * b[q];
-    // balanced base-27 carry sweep: digit in -13..13
+        for (int k = 0; k < 4; ++k)
+            acc = __builtin_amdgcn_sdot4(static_cast<int>(ad[k]), window(31 - s + 4 * k), acc,
+                                         false);
+        conv[s] = acc;
+    }
+    conv[31] = 0;
+    // balanced base-27 carry sweep, digit in -13..13: |v| < 2810, so n = v + 5413 lies in
+    // [2603, 8223] and floor((v + 13) / 27) = floor(n / 27) - 200 = (n * 38837 >> 20) - 200
+    // (the multiply-shift is exact for 0 <= n < 45590)
     int carry = 0;
 #pragma unroll
     for (int s = 0; s < 32; ++s) {
         const int v = conv[s] + carry;
-        // floor((v + 13) / 27) without relying on the sign of integer division
-        const int c = (v + 13 >= 0) ? (v + 13) / 27 : -((-(v + 13) + 26) / 27);
+        const int c = static_cast<int>((static_cast<uint32_t>(v + 5413) * 38837u) >> 20) - 200;
         conv[s] = v - 27 * c;
         carry = c;
     }
-    const double low = limb_value_double(conv, 0);
-    const double high = limb_value_double(conv, kTrytes);
+    const double low = limb_value_double(tab, conv, 0);
+    const double high = limb_value_double(tab, conv, kTrytes);
     const double scaled = high * kRadix;
     return low + scaled;
 }
 
+// LPO lanes per output: each forms one limb product (scaled by alpha) per pass of LPO
+// limbs, and the output's first lane adds them to its sum in limb order -- the
+// operations and order of gemm_cpu.cpp:8-71.
+template <int LPO>
 __global__ __launch_bounds__(256) void gemm_limb_kernel(const uint8_t *__restrict__ a,
                                                         const uint8_t *__restrict__ b,
                                                         float *__restrict__ c, int M, int N,
                                                         int KL, float alpha, float beta) {
-    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (t >= static_cast<int64_t>(M) * N) return;
-    const int64_t i = t / N;
-    const int64_t j = t - i * N;
-    double acc = static_cast<double>(c[t]) * static_cast<double>(beta);
+    __shared__ double prod[256];
+    __shared__ double tab[kTableEntries];
+    tryte_table_fill(tab);
+    __syncthreads();
+    const int g = threadIdx.x / LPO;   // output within the workgroup
+    const int ln = threadIdx.x % LPO;  // limb lane
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * (256 / LPO) + g;
+    const bool live = t < static_cast<int64_t>(M) * N;
+    const int64_t i = live ? t / N : 0;
+    const int64_t j = live ? t - i * N : 0;
+    double acc = live && ln == 0 ? static_cast<double>(c[t]) * static_cast<double>(beta) : 0.0;
     const uint4 *arow = reinterpret_cast<const uint4 *>(a) + i * KL;
     const uint4 *bcol = reinterpret_cast<const uint4 *>(b) + j;
-    for (int l = 0; l < KL; ++l) {
-        const double p = multiply_to_double(arow[l], bcol[static_cast<int64_t>(l) * N]);
-        const double scaled = p * static_cast<double>(alpha);
-        acc = acc + scaled;
+    for (int l0 = 0; l0 < KL; l0 += LPO) {
+        const int l = l0 + ln;
+        double scaled = 0.0;
+        if (live && l < KL) {
+            const double p = multiply_to_double(tab, arow[l], bcol[static_cast<int64_t>(l) * N]);
+            scaled = p * static_cast<double>(alpha);
+        }
+        prod[threadIdx.x] = scaled;
+        __syncthreads();
+        if (live && ln == 0) {
+            const int cnt = KL - l0 < LPO ? KL - l0 : LPO;
+            for (int q = 0; q < cnt; ++q) acc = acc + prod[g * LPO + q];
+        }
+        __syncthreads();
     }
-    c[t] = static_cast<float>(acc);
+    if (live && ln == 0) c[t] = static_cast<float>(acc);
 }
 
 // The reference's literal matmul_input in one pass (t81/torch/__init__.py:241-276):
@@ -129,6 +182,8 @@ __global__ __launch_bounds__(256) void gemm_limb_fused_kernel(
     int64_t K, int KL, float thr, float alpha, float beta) {
     __shared__ uint4 xs[kFuseTile][kFuseChunk];
     __shared__ uint4 as[kFuseTile][kFuseChunk];
+    __shared__ double tab[kTableEntries];
+    tryte_table_fill(tab);   // published by the first chunk's barrier
     const int tid = threadIdx.x;
     const int ti = tid / kFuseTile;
     const int tj = tid % kFuseTile;
@@ -163,7 +218,7 @@ __global__ __launch_bounds__(256) void gemm_limb_fused_kernel(
         __syncthreads();
         if (live) {
             for (int l = 0; l < cl; ++l) {
-                const double p = multiply_to_double(as[ti][l], xs[tj][l]);
+                const double p = multiply_to_double(tab, as[ti][l], xs[tj][l]);
                 const double scaled = p * static_cast<double>(alpha);
                 acc = acc + scaled;
             }
@@ -204,8 +259,18 @@ hipError_t launch_gemm_limb(const uint8_t *a, const uint8_t *b, float *c, int m,
                             int k_limbs, float alpha, float beta, hipStream_t s) {
     const int64_t total = static_cast<int64_t>(m) * n;
     if (total == 0) return hipSuccess;
-    gemm_limb_kernel<<<dim3((total + 255) / 256), dim3(256), 0, s>>>(a, b, c, m, n, k_limbs,
-                                                                     alpha, beta);
+    // lanes per output: the limb count rounded up to 16, 32 or 64 (config 1: 22 limbs, 32
+    // lanes: 70.5 -> 30.6 us against one thread per output with the convolution as
+    // multiply-adds and a branching carry sweep; 512 x 128 x 100 limbs 313.6 -> 114.4 us)
+    if (k_limbs <= 16)
+        gemm_limb_kernel<16><<<dim3((total + 15) / 16), dim3(256), 0, s>>>(a, b, c, m, n, k_limbs,
+                                                                          alpha, beta);
+    else if (k_limbs <= 32)
+        gemm_limb_kernel<32><<<dim3((total + 7) / 8), dim3(256), 0, s>>>(a, b, c, m, n, k_limbs,
+                                                                         alpha, beta);
+    else
+        gemm_limb_kernel<64><<<dim3((total + 3) / 4), dim3(256), 0, s>>>(a, b, c, m, n, k_limbs,
+                                                                         alpha, beta);
     return hipGetLastError();
 }
 
