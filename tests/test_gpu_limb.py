@@ -51,7 +51,11 @@ def test_mul_wide_pairs_bit_exact(gpu, golden):
 
 
 @pytest.mark.parametrize("M,N,KL,nz", [(1, 1, 1, 16), (33, 17, 5, 6), (64, 40, 22, 9),
-                                        (7, 129, 3, 16), (16, 16, 0, 1)])
+                                        (7, 129, 3, 16), (16, 16, 0, 1),
+                                        # lanes per output 16 / 32 / 64 at their edges, and
+                                        # several passes of 64 limbs
+                                        (4, 4, 16, 16), (9, 11, 17, 16), (5, 7, 33, 16),
+                                        (3, 5, 100, 16), (2, 3, 130, 12)])
 def test_random_vs_oracle(gpu, orc, M, N, KL, nz):
     announce(f"K4 random M={M} N={N} KL={KL} nz={nz}")
     rng = np.random.default_rng(M * N + KL)
