@@ -618,6 +618,61 @@ def run_spmm(torch, dev) -> list:
     return out
 
 
+def run_aux(torch, ops, _lib, dev) -> list:
+    """The HBM-bound kernels off the GEMM path: the backend contract's elementwise ops
+    (where / clamp / lerp / addcmul over 32 Mi float32 elements, 16 / 8 / 16 / 16 bytes per
+    element) and the reference's TQ1_0 row codec on 8192 x 3072 float32 (quantize: 4 bytes
+    per value in, 2 per 8 values out; dequantize: the reverse).  Two buffer sets, each
+    larger than the MALL, alternate, so every launch streams from HBM; graph-timed, GB/s of
+    algorithmic bytes and the fraction of 8 TB/s."""
+    from t81lib_amd import gguf
+    out = []
+    n = 32 << 20
+    sets = []
+    for i in range(2):
+        g = torch.Generator(dev).manual_seed(20 + i)
+        sets.append([torch.randn(n, device=dev, generator=g) for _ in range(4)])
+
+    def one(name, fn, nbytes, bufs):
+        ms = time_graph(torch, fn, bufs, 200, 8)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out.append({"kernel": name, "us": ms * 1e3, "bytes": nbytes, "GBps": gbs,
+                    "frac_hbm": gbs / HBM_PEAK_GBPS})
+        log(f"aux {name}: {ms * 1e3:8.2f} us  {gbs:7.1f} GB/s  {gbs / HBM_PEAK_GBPS:.3f} of peak")
+
+    one("where 32Mi float32", lambda b: ops.where(b[0], b[1], b[2], out=b[3]), 16 * n, sets)
+    one("clamp 32Mi float32", lambda b: ops.clamp(b[0], -0.5, 0.5, out=b[3]), 8 * n, sets)
+    one("lerp 32Mi float32", lambda b: ops.lerp(b[0], b[1], b[2], out=b[3]), 16 * n, sets)
+    one("addcmul 32Mi float32", lambda b: ops.addcmul(b[0], b[1], b[2], 0.75, out=b[3]),
+        16 * n, sets)
+    del sets
+    rows, cols = 8192, 3072
+    L = _lib.lib()
+    # per copy: source, scales, words, dequantized output (preallocated: the graphs hold the
+    # kernels alone)
+    bufs = []
+    for _ in range(4):
+        src = torch.randn((rows, cols), device=dev)
+        sc, wd = gguf.quantize_rows_tq1_0(src)
+        bufs.append((src, sc, wd, torch.empty((rows, cols), device=dev)))
+    qb = 4 * rows * cols + 2 * rows * (cols // 8) + 4 * rows
+
+    def quant(b):
+        _lib.check(L.t81_hip_tq1_quantize_rows(b[0].data_ptr(), rows, cols, 0.45, None,
+                                               b[1].data_ptr(), b[2].data_ptr(),
+                                               torch.cuda.current_stream().cuda_stream))
+
+    def dequant(b):
+        _lib.check(L.t81_hip_tq1_dequantize_rows(b[2].data_ptr(), rows, cols, b[1].data_ptr(),
+                                                 b[3].data_ptr(),
+                                                 torch.cuda.current_stream().cuda_stream))
+    one("TQ1_0 quantize rows 8192x3072 float32", quant, qb, bufs)
+    one("TQ1_0 dequantize rows 8192x3072 float32", dequant, qb, bufs)
+    del bufs
+    torch.cuda.empty_cache()
+    return out
+
+
 DECODE_SHAPES = [("phi3.qkv", 3072, 9216), ("phi3.o", 3072, 3072), ("phi3.gate_up", 3072, 16384),
                  ("phi3.down", 8192, 3072), ("llama.gate", 4096, 14336),
                  ("llama.down", 14336, 4096)]
@@ -1141,7 +1196,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", choices=["gemv", "gemm", "pack", "copy", "read", "spmm", "launch",
                                        "stack", "decode", "backward", "prefill", "limb",
-                                       "pack3072", "gemv_valu"],
+                                       "pack3072", "gemv_valu", "aux"],
                     default=None,
                     help="time one kernel only (for profiling runs); 'copy' times a plain "
                          "elementwise copy of the GEMV weight size, the calibration kernel "
@@ -1426,6 +1481,7 @@ def main() -> int:
         if only in (None, "decode") else None
     sweep = run_sweep(torch, ops, _lib, dev) if args.sweep else None
     spmm = run_spmm(torch, dev) if only == "spmm" else None
+    aux = run_aux(torch, ops, _lib, dev) if only == "aux" else None
     backward = run_backward(torch, ops, _lib, dev) if only == "backward" else None
     stack = run_stack(torch, dev) if only == "stack" or (only is None and not args.no_stack) \
         else None
@@ -1524,6 +1580,8 @@ def main() -> int:
         line["sweep"] = sweep
     if spmm:
         line["spmm"] = spmm
+    if aux:
+        line["aux"] = aux
     if backward:
         line["backward"] = backward
     if stack:

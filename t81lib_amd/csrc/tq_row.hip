@@ -17,8 +17,11 @@
 // quantizes each row with the scale float(h), as a caller of quantize_row_tq1_0
 // would.
 //
-// All three kernels are bound by HBM: a word is 32 bytes of float32 on one side and
-// 2 bytes on the other.  One thread per word, consecutive threads on consecutive words.
+// All the kernels are bound by HBM: a word is 32 bytes of float32 on one side and
+// 2 bytes on the other.  Quantize runs two lanes per word (float4 loads where the row is
+// 16-byte aligned); the rows dequantize does too, with float4 stores, when the row
+// length is a multiple of 8 and the output 16-byte aligned; the other dequantize paths
+// run one lane per word, consecutive lanes on consecutive words.
 #include <hip/hip_runtime.h>
 
 #include "t81_device.hpp"
@@ -82,36 +85,60 @@ __device__ __forceinline__ float block_max(float m, float *red) {
     return r;
 }
 
+// Max of non-NaN |v| over this thread's values: float4 loads over the 16-byte aligned
+// whole quads when the row starts aligned, single loads for the rest.
 __device__ __forceinline__ float abs_max_strided(const float *v, int64_t n) {
     float m = 0.0f;
-    for (int64_t i = threadIdx.x; i < n; i += 256) {
+    int64_t head = 0;
+    if ((reinterpret_cast<uintptr_t>(v) & 15u) == 0) {
+        const int64_t quads = n >> 2;
+        for (int64_t i = threadIdx.x; i < quads; i += 256) {
+            const floatx4 a = *reinterpret_cast<const floatx4 *>(v + 4 * i);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float b = fabsf(a[j]);
+                m = b > m ? b : m;
+            }
+        }
+        head = quads << 2;
+    }
+    for (int64_t i = head + threadIdx.x; i < n; i += 256) {
         const float a = fabsf(v[i]);
         m = a > m ? a : m;
     }
     return m;
 }
 
-// Word w of a row: trits of v[8w .. 8w + 8) (those below n), digit 0 least significant.
-__device__ __forceinline__ uint32_t quantize_word(const float *v, int64_t n, int64_t w,
-                                                  float scale, float inv, float thr) {
-    float x[kWordTrits];
-    const int64_t k0 = w * kWordTrits;
-    if (k0 + kWordTrits <= n && (reinterpret_cast<uintptr_t>(v + k0) & 15u) == 0) {
-        const floatx4 a = *reinterpret_cast<const floatx4 *>(v + k0);
-        const floatx4 b = *reinterpret_cast<const floatx4 *>(v + k0 + 4);
+// The words of a row, two lanes per word: lane 2w + h turns values 8w + 4h .. 8w + 4h + 4
+// (pad trits 0) into the half word sum_i d_i 3^i, and the even lane hands its half plus
+// 81 times its neighbour's to store(w, word), so a wavefront reads 1 KiB of the row
+// contiguously.  Both lanes of a pair run the same iterations (256 is even), so the
+// partner is always live.
+template <typename Store>
+__device__ __forceinline__ void quantize_words(const float *v, int64_t n, int64_t words,
+                                               float scale, float inv, float thr,
+                                               Store store) {
+    const bool vec = (reinterpret_cast<uintptr_t>(v) & 15u) == 0;
+    for (int64_t q = threadIdx.x; q < 2 * words; q += 256) {
+        const int64_t k0 = 4 * q;
+        float x[4];
+        if (vec && k0 + 4 <= n) {
+            const floatx4 a = *reinterpret_cast<const floatx4 *>(v + k0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) x[i] = a[i], x[4 + i] = b[i];
-    } else {
+            for (int i = 0; i < 4; ++i) x[i] = a[i];
+        } else {
 #pragma unroll
-        for (int i = 0; i < kWordTrits; ++i) x[i] = k0 + i < n ? v[k0 + i] : 0.0f;
+            for (int i = 0; i < 4; ++i) x[i] = k0 + i < n ? v[k0 + i] : 0.0f;
+        }
+        uint32_t half = 0;
+#pragma unroll
+        for (int i = 3; i >= 0; --i) {
+            const int t = (k0 + i < n && scale > 0.0f) ? tq1r_trit(x[i] * inv, thr) : 0;
+            half = half * 3u + tq1r_digit(t);
+        }
+        const uint32_t hi = __shfl_xor(half, 1, 64);
+        if ((q & 1) == 0) store(q >> 1, half + 81u * hi);
     }
-    uint32_t word = 0;
-#pragma unroll
-    for (int i = kWordTrits - 1; i >= 0; --i) {
-        const int t = (k0 + i < n && scale > 0.0f) ? tq1r_trit(x[i] * inv, thr) : 0;
-        word = word * 3u + tq1r_digit(t);
-    }
-    return word & 0x1FFFu;
 }
 
 // Trit i (0..7) of a word's low 8 base-3 digits times scale.
@@ -141,8 +168,9 @@ __global__ __launch_bounds__(256) void tq1r_quantize_rows_kernel(
     const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
     const int64_t words = (n + kWordTrits - 1) / kWordTrits;
     uint16_t *out = dst + row * words;
-    for (int64_t w = threadIdx.x; w < words; w += 256)
-        out[w] = static_cast<uint16_t>(quantize_word(v, n, w, scale, inv, thr));
+    quantize_words(v, n, words, scale, inv, thr, [out](int64_t w, uint32_t word) {
+        out[w] = static_cast<uint16_t>(word);
+    });
 }
 
 __global__ __launch_bounds__(256) void tq1r_dequantize_rows_kernel(
@@ -160,6 +188,33 @@ __global__ __launch_bounds__(256) void tq1r_dequantize_rows_kernel(
 #pragma unroll
     for (int i = 0; i < kWordTrits; ++i)
         if (i < count) o[i] = out[i];
+}
+
+// Rows whose length is a multiple of 8 into a 16-byte aligned output: the output is the
+// flat run of all words' values, and thread t writes values 4t .. 4t + 4 (half t & 1 of
+// word t >> 1) with one float4 store, 1 KiB per wavefront contiguously.
+__global__ __launch_bounds__(256) void tq1r_dequantize_rows_vec_kernel(
+    const uint16_t *__restrict__ src, int64_t total_words, int64_t words,
+    const float *__restrict__ scales, float *__restrict__ dst) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    const int64_t w = t >> 1;
+    if (w >= total_words) return;
+    const int64_t row = total_words <= 0xFFFFFFFFll
+                            ? static_cast<int64_t>(static_cast<uint32_t>(w) /
+                                                   static_cast<uint32_t>(words))
+                            : w / words;
+    const float scale = scales[row];
+    uint32_t word = src[w];
+    if (t & 1) word /= 81u;
+    floatx4 o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t d = word % 3u;
+        word /= 3u;
+        const float tv = d == 0 ? 1.0f : (d == 2 ? -1.0f : 0.0f);
+        o[i] = scale == 0.0f ? 0.0f : tv * scale;
+    }
+    *reinterpret_cast<floatx4 *>(dst + 4 * t) = o;
 }
 
 struct PayloadLayout {
@@ -227,11 +282,10 @@ __global__ __launch_bounds__(256) void tq1r_payload_rows_kernel(
     const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
     const int64_t words = (n + kWordTrits - 1) / kWordTrits;
     uint8_t *out = grp + lay.header + (row - g * lay.group) * lay.row_bytes;
-    for (int64_t w = threadIdx.x; w < words; w += 256) {
-        const uint32_t word = quantize_word(v, n, w, scale, inv, thr);
+    quantize_words(v, n, words, scale, inv, thr, [out](int64_t w, uint32_t word) {
         out[2 * w] = static_cast<uint8_t>(word & 0xFFu);
         out[2 * w + 1] = static_cast<uint8_t>(word >> 8);
-    }
+    });
 }
 
 PayloadLayout layout(int64_t rows, int64_t n, int64_t block_rows, bool refinements) {
@@ -290,8 +344,12 @@ hipError_t launch_tq1r_dequantize_rows(const uint16_t *src, int64_t rows, int64_
                                        const float *scales, float *dst, hipStream_t s) {
     const int64_t words = (n + kWordTrits - 1) / kWordTrits;
     if (rows * words == 0) return hipSuccess;
-    tq1r_dequantize_rows_kernel<<<grid_of(rows * words), 256, 0, s>>>(src, rows, n, words,
-                                                                       scales, dst);
+    if (n % kWordTrits == 0 && (reinterpret_cast<uintptr_t>(dst) & 15u) == 0)
+        tq1r_dequantize_rows_vec_kernel<<<grid_of(2 * rows * words), 256, 0, s>>>(
+            src, rows * words, words, scales, dst);
+    else
+        tq1r_dequantize_rows_kernel<<<grid_of(rows * words), 256, 0, s>>>(src, rows, n, words,
+                                                                           scales, dst);
     return hipGetLastError();
 }
 
