@@ -19,7 +19,7 @@
 //
 // All the kernels are bound by HBM: a word is 32 bytes of float32 on one side and
 // 2 bytes on the other.  Quantize runs two lanes per word (float4 loads where the row is
-// 16-byte aligned); the rows dequantize does too, with float4 stores, when the row
+// 16-byte aligned, rows of up to 8192 values held in registers and read once); the rows dequantize does too, with float4 stores, when the row
 // length is a multiple of 8 and the output 16-byte aligned; the other dequantize paths
 // run one lane per word, consecutive lanes on consecutive words.
 #include <hip/hip_runtime.h>
@@ -171,6 +171,51 @@ __global__ __launch_bounds__(256) void tq1r_quantize_rows_kernel(
     quantize_words(v, n, words, scale, inv, thr, [out](int64_t w, uint32_t word) {
         out[w] = static_cast<uint16_t>(word);
     });
+}
+
+// Rows of n <= 1024 R values, n a multiple of 4 and the matrix 16-byte aligned: the row
+// is read once, R float4 per lane (quad q = lane + 256 j), and quantized from registers;
+// lane q and lane q ^ 1 hold the two halves of word q >> 1 at every j.
+template <int R>
+__global__ __launch_bounds__(256) void tq1r_quantize_rows_reg_kernel(
+    const float *__restrict__ values, int64_t n, float thr, const float *__restrict__ scales_in,
+    float *__restrict__ scales_out, uint16_t *__restrict__ dst) {
+    __shared__ float red[4];
+    const int64_t row = blockIdx.x;
+    const float *v = values + row * n;
+    const int quads = static_cast<int>(n >> 2);
+    floatx4 x[R];
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+        const int q = threadIdx.x + 256 * j;
+        x[j] = q < quads ? *reinterpret_cast<const floatx4 *>(v + 4 * q) : floatx4{0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float a = fabsf(x[j][i]);
+            m = a > m ? a : m;
+        }
+    }
+    float scale = scales_in != nullptr ? scales_in[row] : 0.0f;
+    if (!(scale > 0.0f)) scale = block_max(m, red);
+    if (scales_out != nullptr && threadIdx.x == 0) scales_out[row] = scale;
+    const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+    const int words = static_cast<int>((n + kWordTrits - 1) / kWordTrits);
+    uint16_t *out = dst + row * words;
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+        const int q = threadIdx.x + 256 * j;
+        if (q < 2 * words) {
+            uint32_t half = 0;
+#pragma unroll
+            for (int i = 3; i >= 0; --i) {
+                const int t = (4 * q + i < n && scale > 0.0f) ? tq1r_trit(x[j][i] * inv, thr) : 0;
+                half = half * 3u + tq1r_digit(t);
+            }
+            const uint32_t hi = __shfl_xor(half, 1, 64);
+            if ((q & 1) == 0) out[q >> 1] = static_cast<uint16_t>(half + 81u * hi);
+        }
+    }
 }
 
 __global__ __launch_bounds__(256) void tq1r_dequantize_rows_kernel(
@@ -335,8 +380,24 @@ hipError_t launch_tq1r_quantize_rows(const float *values, int64_t rows, int64_t 
                                      const float *scales_in, float *scales_out, uint16_t *dst,
                                      hipStream_t s) {
     if (rows == 0 || n == 0) return hipSuccess;
-    tq1r_quantize_rows_kernel<<<dim3(static_cast<unsigned>(rows)), 256, 0, s>>>(
-        values, n, clamp_threshold(thr), scales_in, scales_out, dst);
+    const dim3 grid(static_cast<unsigned>(rows));
+    const float t = clamp_threshold(thr);
+    if (n % 4 == 0 && n <= 8192 && (reinterpret_cast<uintptr_t>(values) & 15u) == 0) {
+        if (n <= 1024)
+            tq1r_quantize_rows_reg_kernel<1><<<grid, 256, 0, s>>>(values, n, t, scales_in,
+                                                                  scales_out, dst);
+        else if (n <= 2048)
+            tq1r_quantize_rows_reg_kernel<2><<<grid, 256, 0, s>>>(values, n, t, scales_in,
+                                                                  scales_out, dst);
+        else if (n <= 4096)
+            tq1r_quantize_rows_reg_kernel<4><<<grid, 256, 0, s>>>(values, n, t, scales_in,
+                                                                  scales_out, dst);
+        else
+            tq1r_quantize_rows_reg_kernel<8><<<grid, 256, 0, s>>>(values, n, t, scales_in,
+                                                                  scales_out, dst);
+    } else {
+        tq1r_quantize_rows_kernel<<<grid, 256, 0, s>>>(values, n, t, scales_in, scales_out, dst);
+    }
     return hipGetLastError();
 }
 

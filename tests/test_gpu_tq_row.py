@@ -136,7 +136,8 @@ def test_dequant_tensor_truncation_messages(gpu, g):
         t81lib.dequant_tq1_0(np.zeros(8, np.uint16), 1, 8)
 
 
-@pytest.mark.parametrize("rows,cols", [(1, 1), (37, 100), (300, 4096), (64, 14336), (1000, 9)])
+@pytest.mark.parametrize("rows,cols", [(1, 1), (37, 100), (300, 4096), (64, 14336), (1000, 9),
+                                       (5, 2052), (3, 1028), (8, 8192), (4, 8196)])
 def test_quantize_rows_vs_oracle(gpu, rows, cols):
     announce(f"tq1 rows {rows}x{cols}")
     rng = np.random.default_rng(rows + cols)
