@@ -668,7 +668,39 @@ def run_aux(torch, ops, _lib, dev) -> list:
                                                  torch.cuda.current_stream().cuda_stream))
     one("TQ1_0 quantize rows 8192x3072 float32", quant, qb, bufs)
     one("TQ1_0 dequantize rows 8192x3072 float32", dequant, qb, bufs)
-    del bufs
+    # the tensor payload behind t81lib.dequant_tq1_0 (groups of 32 rows, half scales), and
+    # the GGUF TQ1_0 / TQ2_0 blocks of 256 weights
+    pb = int(L.t81_hip_tq1_payload_bytes(rows, cols, 32, 0))
+    pays = []
+    for b in bufs:
+        pay = torch.empty(pb, dtype=torch.uint8, device=dev)
+        _lib.check(L.t81_hip_tq1_quantize_payload(b[0].data_ptr(), rows, cols, 32, 0, 0.45,
+                                                  pay.data_ptr(),
+                                                  torch.cuda.current_stream().cuda_stream))
+        pays.append((pay, b[3]))
+
+    def dequant_payload(b):
+        _lib.check(L.t81_hip_tq1_dequantize_payload(b[0].data_ptr(), pb, rows, cols, 32, 0,
+                                                    b[1].data_ptr(),
+                                                    torch.cuda.current_stream().cuda_stream))
+    one("TQ1_0 dequantize payload 8192x3072 float32", dequant_payload, 4 * rows * cols + pb,
+        pays)
+    for quant, name in ((34, "TQ1_0"), (35, "TQ2_0")):
+        gb = rows * (cols // 256) * int(L.t81_hip_tq_block_bytes(quant))
+        blks = []
+        for b in bufs:
+            blk = torch.empty(gb, dtype=torch.uint8, device=dev)
+            _lib.check(L.t81_hip_tq_quantize(b[0].data_ptr(), blk.data_ptr(), rows, cols, 0.45,
+                                             quant, torch.cuda.current_stream().cuda_stream))
+            blks.append((blk, b[3]))
+
+        def dequant_blocks(b, quant=quant):
+            _lib.check(L.t81_hip_tq_dequantize(b[0].data_ptr(), b[1].data_ptr(), rows, cols,
+                                               quant, torch.cuda.current_stream().cuda_stream))
+        one(f"GGUF {name} dequantize 8192x3072 float32", dequant_blocks,
+            4 * rows * cols + gb, blks)
+        del blks
+    del bufs, pays
     torch.cuda.empty_cache()
     return out
 

@@ -13,7 +13,9 @@
 //   digits weighted 81, 27, 9, 3 over 240 + i*4 + c; a number v < 243 is stored as
 //   (v * 256 + 242) / 243, so digit n reads back as ((uint8)(byte * 3^n) * 3) >> 8.
 // All float arithmetic is float32 with separate roundings (no contraction), as numpy
-// evaluates it.  Rows are zero-padded to whole blocks.
+// evaluates it.  Rows are zero-padded to whole blocks.  Dequantize writes with the
+// non-temporal hint (every output byte is written once); whole-block rows into an
+// aligned output as one float4 per lane.
 #include <hip/hip_fp16.h>
 
 #include "t81_device.hpp"
@@ -132,7 +134,7 @@ __global__ __launch_bounds__(256) void tq_dequantize_kernel(const uint8_t *__res
     float *row = dst + r * cols;
     auto put = [&](int j, int digit) {
         const int64_t col = col0 + j;
-        if (col < cols) row[col] = d * static_cast<float>(digit - 1);
+        if (col < cols) __builtin_nontemporal_store(d * static_cast<float>(digit - 1), row + col);
     };
     if constexpr (Q == kTq2) {
         const uint32_t b = in[lane];
@@ -162,6 +164,54 @@ __global__ __launch_bounds__(256) void tq_dequantize_kernel(const uint8_t *__res
     }
 }
 
+// Whole blocks (cols a multiple of 256) into a 16-byte aligned output, where block b's
+// weights are outputs 256 b .. 256 b + 255: lane l writes weights 4 l .. 4 l + 3 with one
+// non-temporal float4.  Those four share a digit position: TQ2_0 bits 2s of four
+// consecutive bytes; TQ1_0 digit n of four consecutive bytes (n = e / 32 below 160,
+// (e - 160) / 16 below 240, (e - 240) / 4 after, e = 4 l).
+template <int Q>
+__global__ __launch_bounds__(256) void tq_dequantize_vec_kernel(const uint8_t *__restrict__ src,
+                                                                float *__restrict__ dst,
+                                                                int64_t blocks) {
+    const int lane = threadIdx.x & 63;
+    const int64_t blk =
+        static_cast<int64_t>(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (blk >= blocks) return;
+    const uint8_t *in = src + blk * tq_bytes(Q);
+    const uint16_t h = static_cast<uint16_t>(in[tq_bytes(Q) - 2] | (in[tq_bytes(Q) - 1] << 8));
+    const float d = __half2float(__ushort_as_half(h));
+    const int e = 4 * lane;
+    int digit[4];
+    if constexpr (Q == kTq2) {
+        const int base = (e >> 7) * 32 + (e & 31);
+        const int sh = 2 * ((e >> 5) & 3);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) digit[j] = (in[base + j] >> sh) & 3;
+    } else {
+        int base, n;
+        if (e < 160) {
+            base = e & 31, n = e >> 5;
+        } else if (e < 240) {
+            base = 32 + ((e - 160) & 15), n = (e - 160) >> 4;
+        } else {
+            base = 48, n = (e - 240) >> 2;
+        }
+        uint32_t p = 1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (i < n) p *= 3;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t q = (static_cast<uint32_t>(in[base + j]) * p) & 0xFFu;
+            digit[j] = static_cast<int>((q * 3u) >> 8);
+        }
+    }
+    floatx4 o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = d * static_cast<float>(digit[j] - 1);
+    __builtin_nontemporal_store(o, reinterpret_cast<floatx4 *>(dst + blk * kQK + e));
+}
+
 }  // namespace
 
 hipError_t launch_tq_quantize(const float *src, uint8_t *dst, int64_t rows, int64_t cols,
@@ -183,10 +233,16 @@ hipError_t launch_tq_dequantize(const uint8_t *src, float *dst, int64_t rows, in
     const int64_t blocks = rows * nb;
     if (blocks == 0) return hipSuccess;
     const dim3 grid(static_cast<unsigned>((blocks + 3) / 4));
-    if (quant == kTq2)
+    if (cols % kQK == 0 && (reinterpret_cast<uintptr_t>(dst) & 15u) == 0) {
+        if (quant == kTq2)
+            tq_dequantize_vec_kernel<kTq2><<<grid, 256, 0, s>>>(src, dst, blocks);
+        else
+            tq_dequantize_vec_kernel<kTq1><<<grid, 256, 0, s>>>(src, dst, blocks);
+    } else if (quant == kTq2) {
         tq_dequantize_kernel<kTq2><<<grid, 256, 0, s>>>(src, dst, rows, cols, nb);
-    else
+    } else {
         tq_dequantize_kernel<kTq1><<<grid, 256, 0, s>>>(src, dst, rows, cols, nb);
+    }
     return hipGetLastError();
 }
 

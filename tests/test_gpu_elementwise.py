@@ -38,7 +38,8 @@ def _run(ops, op, a, b, c, kw, out=None):
     return ops.addcmul(a, b, c, kw["p0"], out=out)
 
 
-@pytest.mark.parametrize("n", [0, 1, 3, 4, 5, 257, 100003])
+# (1 << 20) + 3: the non-temporal vector path and its scalar tail
+@pytest.mark.parametrize("n", [0, 1, 3, 4, 5, 257, 100003, (1 << 20) + 3])
 def test_elementwise_vs_oracle(gpu, orc, n):
     import torch
 
@@ -67,6 +68,13 @@ def test_elementwise_unaligned_and_in_place(gpu, orc):
         inplace = ta.clone()
         _run(ops, op, inplace, tb, tc, kw, out=inplace)
         assert _same_or_both_nan(inplace.cpu().numpy(), want), (op, "in place")
+    # in place on the non-temporal path
+    a, b, c = _inputs(1 << 20, 6)
+    for op, kw in EW_CASES:
+        want = orc.elementwise(op, a, b, c, **kw)
+        inplace, tb, tc = (torch.from_numpy(v).to(gpu) for v in (a, b, c))
+        _run(ops, op, inplace, tb, tc, kw, out=inplace)
+        assert _same_or_both_nan(inplace.cpu().numpy(), want), (op, "in place, 1 Mi")
 
 
 def test_elementwise_argument_errors(gpu):

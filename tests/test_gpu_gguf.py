@@ -43,7 +43,7 @@ def weights(rows, cols, seed, specials=False):
 @pytest.mark.parametrize("quant", list(QUANTS))
 @pytest.mark.parametrize("threshold", [0.45, 0.25, 0.0, 1.0, 3.0])
 @pytest.mark.parametrize("shape", [(3, 4), (64, 128), (7, 600), (33, 1000), (5, 256), (1, 1),
-                                   (2, 513), (0, 10), (4, 0)])
+                                   (2, 513), (0, 10), (4, 0), (6, 768), (3, 4096)])
 def test_codecs_bit_exact(gpu, quant, threshold, shape):
     announce(f"tq codec {quant} thr={threshold} shape={shape}")
     rows, cols = shape
@@ -56,11 +56,13 @@ def test_codecs_bit_exact(gpu, quant, threshold, shape):
     np.testing.assert_array_equal(dec_got.view(np.uint32), dec_want.view(np.uint32))
 
 
+@pytest.mark.parametrize("cols", [1000, 1024])
 @pytest.mark.parametrize("quant", list(QUANTS))
-def test_dequantize_any_bytes(gpu, quant):
-    """Every byte value decodes (TQ2_0 digit 3 -> 2, TQ1_0 bytes >= 243 wrap) as the oracle."""
-    announce(f"tq dequant random bytes {quant}")
-    rows, cols = 17, 1000
+def test_dequantize_any_bytes(gpu, quant, cols):
+    """Every byte value decodes (TQ2_0 digit 3 -> 2, TQ1_0 bytes >= 243 wrap) as the oracle
+    (cols 1024: whole blocks, the float4 path)."""
+    announce(f"tq dequant random bytes {quant} cols={cols}")
+    rows = 17
     nbytes = gguf.row_bytes(cols, quant)
     g = np.random.default_rng(5)
     payload = g.integers(0, 256, (rows, nbytes), dtype=np.uint8)
