@@ -671,13 +671,17 @@ def run_aux(torch, ops, _lib, dev) -> list:
     # the tensor payload behind t81lib.dequant_tq1_0 (groups of 32 rows, half scales), and
     # the GGUF TQ1_0 / TQ2_0 blocks of 256 weights
     pb = int(L.t81_hip_tq1_payload_bytes(rows, cols, 32, 0))
-    pays = []
-    for b in bufs:
-        pay = torch.empty(pb, dtype=torch.uint8, device=dev)
-        _lib.check(L.t81_hip_tq1_quantize_payload(b[0].data_ptr(), rows, cols, 32, 0, 0.45,
-                                                  pay.data_ptr(),
+    pays = [(torch.empty(pb, dtype=torch.uint8, device=dev), b[3], b[0]) for b in bufs]
+
+    def quant_payload(b):
+        _lib.check(L.t81_hip_tq1_quantize_payload(b[2].data_ptr(), rows, cols, 32, 0, 0.45,
+                                                  b[0].data_ptr(),
                                                   torch.cuda.current_stream().cuda_stream))
-        pays.append((pay, b[3]))
+    for b in pays:
+        quant_payload(b)
+    # the writer has no reference counterpart (the reference only reads payloads)
+    one("TQ1_0 quantize payload 8192x3072 float32 (writer)", quant_payload,
+        4 * rows * cols + pb, pays)
 
     def dequant_payload(b):
         _lib.check(L.t81_hip_tq1_dequantize_payload(b[0].data_ptr(), pb, rows, cols, 32, 0,

@@ -93,7 +93,23 @@ __device__ __forceinline__ float abs_max_strided(const float *v, int64_t n) {
     int64_t head = 0;
     if ((reinterpret_cast<uintptr_t>(v) & 15u) == 0) {
         const int64_t quads = n >> 2;
-        for (int64_t i = threadIdx.x; i < quads; i += 256) {
+        int64_t i = threadIdx.x;
+        // four loads in flight per lane over long spans (a 32-row group of the payload
+        // writer: 256 -> 49.9 us for 8192 x 3072 with one)
+        for (; i + 768 < quads; i += 1024) {
+            floatx4 a[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                a[u] = *reinterpret_cast<const floatx4 *>(v + 4 * (i + 256 * u));
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float b = fabsf(a[u][j]);
+                    m = b > m ? b : m;
+                }
+        }
+        for (; i < quads; i += 256) {
             const floatx4 a = *reinterpret_cast<const floatx4 *>(v + 4 * i);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
