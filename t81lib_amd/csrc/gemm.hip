@@ -804,8 +804,13 @@ __global__ __launch_bounds__(kW4Threads) void gemm_w4_kernel(
                 const int tok = 4 * i + tq;
                 const int m = m0 + 32 * CB * wm + 32 * cb + tok;
                 const bool ok = vec4 && m < M && tc < prow && nb + 3 < nv;
-                cv[i] = ok ? *reinterpret_cast<const float4 *>(cdst + static_cast<int64_t>(m) * ldv + nb)
-                           : make_float4(0.f, 0.f, 0.f, 0.f);
+                // non-temporal: each C value is read once (gate_up beta = 1 M = 2048
+                // 394.0 -> 384.3 us, M = 8192 1518 -> 1496)
+                f32x4 t = {0.f, 0.f, 0.f, 0.f};
+                if (ok)
+                    t = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(
+                        cdst + static_cast<int64_t>(m) * ldv + nb));
+                cv[i] = make_float4(t[0], t[1], t[2], t[3]);
             }
         };
         float4 cva[8], cvb[8];

@@ -412,8 +412,13 @@ __global__ __launch_bounds__(kI8Threads) void gemm_w4_i8_kernel(
             for (int i = 0; i < 8; ++i) {
                 const int m = m0 + 32 * CB * wm + 32 * cb + 4 * i + tq;
                 const bool ok = vec4 && m < M && nb + 3 < N;
-                cv[i] = ok ? *reinterpret_cast<const i32x4 *>(c + static_cast<int64_t>(m) * ldc + nb)
-                           : i32x4{0, 0, 0, 0};
+                // non-temporal, as the bf16 kernel's C reads (gate_up M = 2048 with C
+                // accumulated: 283.0 -> 270.9 us)
+                i32x4 t = {0, 0, 0, 0};
+                if (ok)
+                    t = __builtin_nontemporal_load(
+                        reinterpret_cast<const i32x4 *>(c + static_cast<int64_t>(m) * ldc + nb));
+                cv[i] = t;
             }
         };
         i32x4 cva[8], cvb[8];
