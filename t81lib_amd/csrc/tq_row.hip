@@ -311,33 +311,34 @@ __global__ __launch_bounds__(256) void tq1r_dequantize_payload_kernel(
 }
 
 // Rows whose length is a multiple of 8 into a 16-byte aligned output, as
-// tq1r_dequantize_rows_vec_kernel: thread t decodes half t & 1 of word t >> 1 (words
-// numbered over all rows) and writes one non-temporal float4.  kEven: the payload starts
-// at an even address, so every word does (headers, rows and groups have even sizes) and
-// is read with one 16-bit load.
+// tq1r_dequantize_rows_vec_kernel.  A group's rows of words are contiguous in the payload
+// (a row is exactly its words) and its rows contiguous in the output, so workgroup b takes
+// chunk b % chunks of group b / chunks (a division of uniform values), and its thread t'
+// decodes half t' & 1 of the group's word t' >> 1 into one non-temporal float4 at output
+// 4 t' of the group -- no per-lane division.  kEven: the payload starts at an even
+// address, so every word does (headers, rows and groups have even sizes) and is read with
+// one 16-bit load.
 template <bool kEven>
 __global__ __launch_bounds__(256) void tq1r_dequantize_payload_vec_kernel(
-    const uint8_t *__restrict__ payload, int64_t total_words, int64_t words, PayloadLayout lay,
-    float *__restrict__ dst) {
-    const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    const int64_t w = t >> 1;
-    if (w >= total_words) return;
-    int64_t row, g;
-    if (total_words <= 0xFFFFFFFFll) {
-        row = static_cast<uint32_t>(w) / static_cast<uint32_t>(words);
-        g = static_cast<uint32_t>(row) / static_cast<uint32_t>(lay.group);
-    } else {
-        row = w / words;
-        g = row / lay.group;
-    }
+    const uint8_t *__restrict__ payload, int64_t rows, int64_t n, int64_t words,
+    uint32_t chunks, PayloadLayout lay, float *__restrict__ dst) {
+    const uint32_t g = blockIdx.x / chunks;
+    const int64_t q = static_cast<int64_t>(blockIdx.x - g * chunks) * 256 + threadIdx.x;
+    const int64_t r0 = static_cast<int64_t>(g) * lay.group;
+    const int64_t nr = rows - r0 < lay.group ? rows - r0 : lay.group;
+    if (q >= 2 * nr * words) return;
     const uint8_t *grp = payload + g * lay.stride;
-    const float scale = half_bits_to_float(static_cast<uint32_t>(grp[0]) |
-                                           (static_cast<uint32_t>(grp[1]) << 8));
-    const uint8_t *p =
-        grp + lay.header + (row - g * lay.group) * lay.row_bytes + 2 * (w - row * words);
+    // both loads ahead of the scale's conversion, whose branches would otherwise hold the
+    // word's load behind the scale's (two memory latencies per wave; 8192 x 3072:
+    // 20.0 -> 16.9 us)
+    const uint8_t *p = grp + lay.header + 2 * (q >> 1);
     uint32_t word = kEven ? *reinterpret_cast<const uint16_t *>(p)
                           : static_cast<uint32_t>(p[0]) | (static_cast<uint32_t>(p[1]) << 8);
-    if (t & 1) word /= 81u;
+    const uint32_t hbits = kEven ? *reinterpret_cast<const uint16_t *>(grp)
+                                 : static_cast<uint32_t>(grp[0]) |
+                                       (static_cast<uint32_t>(grp[1]) << 8);
+    if (q & 1) word /= 81u;
+    const float scale = half_bits_to_float(hbits);
     floatx4 o;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -346,7 +347,7 @@ __global__ __launch_bounds__(256) void tq1r_dequantize_payload_vec_kernel(
         const float tv = d == 0 ? 1.0f : (d == 2 ? -1.0f : 0.0f);
         o[i] = scale == 0.0f ? 0.0f : tv * scale;
     }
-    __builtin_nontemporal_store(o, reinterpret_cast<floatx4 *>(dst + 4 * t));
+    __builtin_nontemporal_store(o, reinterpret_cast<floatx4 *>(dst + r0 * n + 4 * q));
 }
 
 // One workgroup per group: h = half(max |v| over the group's rows, contiguous in the
@@ -477,13 +478,17 @@ hipError_t launch_tq1r_dequantize_payload(const uint8_t *payload, int64_t rows, 
     const int64_t words = (n + kWordTrits - 1) / kWordTrits;
     if (rows * words == 0) return hipSuccess;
     const PayloadLayout lay = layout(rows, n, block_rows, refinements);
-    if (n % kWordTrits == 0 && (reinterpret_cast<uintptr_t>(dst) & 15u) == 0) {
+    const int64_t groups = (rows + lay.group - 1) / lay.group;
+    const int64_t chunks = (2 * lay.group * words + 255) / 256;
+    if (n % kWordTrits == 0 && (reinterpret_cast<uintptr_t>(dst) & 15u) == 0 &&
+        groups * chunks <= 0xFFFFFFFFll / 256) {
+        const dim3 grid(static_cast<unsigned>(groups * chunks));
         if ((reinterpret_cast<uintptr_t>(payload) & 1u) == 0)
-            tq1r_dequantize_payload_vec_kernel<true><<<grid_of(2 * rows * words), 256, 0, s>>>(
-                payload, rows * words, words, lay, dst);
+            tq1r_dequantize_payload_vec_kernel<true><<<grid, 256, 0, s>>>(
+                payload, rows, n, words, static_cast<uint32_t>(chunks), lay, dst);
         else
-            tq1r_dequantize_payload_vec_kernel<false><<<grid_of(2 * rows * words), 256, 0, s>>>(
-                payload, rows * words, words, lay, dst);
+            tq1r_dequantize_payload_vec_kernel<false><<<grid, 256, 0, s>>>(
+                payload, rows, n, words, static_cast<uint32_t>(chunks), lay, dst);
     } else
         tq1r_dequantize_payload_kernel<<<grid_of(rows * words), 256, 0, s>>>(payload, rows, n,
                                                                               words, lay, dst);
