@@ -206,7 +206,9 @@ __global__ __launch_bounds__(256) void tq1r_quantize_rows_reg_kernel(
 #pragma unroll
     for (int j = 0; j < R; ++j) {
         const int q = threadIdx.x + 256 * j;
-        x[j] = q < quads ? *reinterpret_cast<const floatx4 *>(v + 4 * q) : floatx4{0, 0, 0, 0};
+        // non-temporal: the row is read once (8192 x 3072: 24.8 -> 23.9 us in an A/B)
+        x[j] = q < quads ? __builtin_nontemporal_load(reinterpret_cast<const floatx4 *>(v + 4 * q))
+                         : floatx4{0, 0, 0, 0};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const float a = fabsf(x[j][i]);
