@@ -298,10 +298,11 @@ __global__ __launch_bounds__(256) void tq1r_dequantize_payload_kernel(
     const int64_t w = idx - row * words;
     const int64_t g = row / lay.group;
     const uint8_t *grp = payload + g * lay.stride;
-    const float scale = half_bits_to_float(static_cast<uint32_t>(grp[0]) |
-                                           (static_cast<uint32_t>(grp[1]) << 8));
+    // the word's bytes are loaded with the scale's, ahead of the scale's conversion
     const uint8_t *p = grp + lay.header + (row - g * lay.group) * lay.row_bytes + 2 * w;
     const uint32_t word = static_cast<uint32_t>(p[0]) | (static_cast<uint32_t>(p[1]) << 8);
+    const float scale = half_bits_to_float(static_cast<uint32_t>(grp[0]) |
+                                           (static_cast<uint32_t>(grp[1]) << 8));
     const int64_t k0 = w * kWordTrits;
     const int count = static_cast<int>(n - k0 < kWordTrits ? n - k0 : kWordTrits);
     float out[kWordTrits];
