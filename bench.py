@@ -696,11 +696,17 @@ def run_aux(torch, ops, _lib, dev) -> list:
             blk = torch.empty(gb, dtype=torch.uint8, device=dev)
             _lib.check(L.t81_hip_tq_quantize(b[0].data_ptr(), blk.data_ptr(), rows, cols, 0.45,
                                              quant, torch.cuda.current_stream().cuda_stream))
-            blks.append((blk, b[3]))
+            blks.append((blk, b[3], b[0]))
+
+        def quant_blocks(b, quant=quant):
+            _lib.check(L.t81_hip_tq_quantize(b[2].data_ptr(), b[0].data_ptr(), rows, cols, 0.45,
+                                             quant, torch.cuda.current_stream().cuda_stream))
 
         def dequant_blocks(b, quant=quant):
             _lib.check(L.t81_hip_tq_dequantize(b[0].data_ptr(), b[1].data_ptr(), rows, cols,
                                                quant, torch.cuda.current_stream().cuda_stream))
+        one(f"GGUF {name} quantize 8192x3072 float32", quant_blocks, 4 * rows * cols + gb,
+            blks)
         one(f"GGUF {name} dequantize 8192x3072 float32", dequant_blocks,
             4 * rows * cols + gb, blks)
         del blks

@@ -51,6 +51,76 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// Whole blocks of a 16-byte aligned matrix (cols a multiple of 256): lane l reads values
+// 4 l .. 4 l + 3 of its wavefront's block with one non-temporal float4 (each value is read
+// once), takes the block max from those, turns them into digits (trit + 1) and writes the
+// four digits to the wavefront's 256-byte LDS slot; each lane then gathers the digits its
+// output byte packs, in the layouts described at the top.  The slot is private to the
+// wavefront, whose LDS operations complete in order, so no barrier is needed.
+// (8192 x 3072: TQ1_0 63.5 -> 26.1 us, TQ2_0 57.7 -> 24.3 against tq_quantize_kernel.)
+template <int Q>
+__global__ __launch_bounds__(256) void tq_quantize_vec_kernel(const float *__restrict__ src,
+                                                              uint8_t *__restrict__ dst,
+                                                              int64_t blocks, float thr,
+                                                              int use_thr) {
+    __shared__ uint32_t slots[4][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t blk = static_cast<int64_t>(blockIdx.x) * 4 + wave;
+    if (blk >= blocks) return;  // whole wavefront
+    const floatx4 x =
+        __builtin_nontemporal_load(reinterpret_cast<const floatx4 *>(src + blk * kQK) + lane);
+    float mx = 0.0f;
+    bool nan = false;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const float a = fabsf(x[u]);
+        nan |= a != a;
+        mx = fmaxf(mx, a);
+    }
+    mx = wave_max(mx);
+    const float d = __builtin_amdgcn_ballot_w64(nan) != 0 ? __builtin_nanf("") : mx;
+    const float inv_d = d == 0.0f ? 0.0f : 1.0f / d;
+    uint32_t dig = 0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+        dig |= static_cast<uint32_t>(tq_trit(x[u] * inv_d, use_thr, thr) + 1) << (8 * u);
+    slots[wave][lane] = dig;
+    __builtin_amdgcn_wave_barrier();
+    const uint8_t *sd = reinterpret_cast<const uint8_t *>(slots[wave]);
+    uint8_t *out = dst + blk * tq_bytes(Q);
+    if constexpr (Q == kTq2) {
+        const int a = lane >> 5;
+        const int c = lane & 31;
+        uint32_t b = 0;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) b |= static_cast<uint32_t>(sd[a * 128 + s * 32 + c]) << (2 * s);
+        out[lane] = static_cast<uint8_t>(b);
+    } else {
+        if (lane < 52) {
+            int first, stride, ndig;
+            if (lane < 32) {
+                first = lane, stride = 32, ndig = 5;
+            } else if (lane < 48) {
+                first = 160 + (lane - 32), stride = 16, ndig = 5;
+            } else {
+                first = 240 + (lane - 48), stride = 4, ndig = 4;
+            }
+            uint32_t v = 0;
+#pragma unroll
+            for (int i = 0; i < 5; ++i)
+                if (i < ndig) v = v * 3 + sd[first + i * stride];
+            if (ndig == 4) v *= 3;  // four digits weighted 81, 27, 9, 3
+            out[lane] = static_cast<uint8_t>((v * 256u + 242u) / 243u);
+        }
+    }
+    if (lane == 0) {
+        const uint16_t h = __half_as_ushort(__float2half_rn(d));
+        out[tq_bytes(Q) - 2] = static_cast<uint8_t>(h & 0xFFu);
+        out[tq_bytes(Q) - 1] = static_cast<uint8_t>(h >> 8);
+    }
+}
+
 template <int Q>
 __global__ __launch_bounds__(256) void tq_quantize_kernel(const float *__restrict__ src,
                                                           uint8_t *__restrict__ dst,
@@ -220,7 +290,12 @@ hipError_t launch_tq_quantize(const float *src, uint8_t *dst, int64_t rows, int6
     const int64_t blocks = rows * nb;
     if (blocks == 0) return hipSuccess;
     const dim3 grid(static_cast<unsigned>((blocks + 3) / 4));
-    if (quant == kTq2)
+    if (cols % kQK == 0 && (reinterpret_cast<uintptr_t>(src) & 15u) == 0) {
+        if (quant == kTq2)
+            tq_quantize_vec_kernel<kTq2><<<grid, 256, 0, s>>>(src, dst, blocks, thr, use_thr);
+        else
+            tq_quantize_vec_kernel<kTq1><<<grid, 256, 0, s>>>(src, dst, blocks, thr, use_thr);
+    } else if (quant == kTq2)
         tq_quantize_kernel<kTq2><<<grid, 256, 0, s>>>(src, dst, rows, cols, nb, thr, use_thr);
     else
         tq_quantize_kernel<kTq1><<<grid, 256, 0, s>>>(src, dst, rows, cols, nb, thr, use_thr);
