@@ -71,7 +71,9 @@ __host__ __device__ __forceinline__ float half_bits_to_float(uint32_t h) {
     return __builtin_bit_cast(float, bits);
 }
 
-// Max of non-NaN |v| over the workgroup (256 threads), from per-thread maxima >= 0.
+// Max of non-NaN |v| over the workgroup (kT threads, red[kT / 64]), from per-thread
+// maxima >= 0.
+template <int kT = 256>
 __device__ __forceinline__ float block_max(float m, float *red) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
@@ -82,25 +84,27 @@ __device__ __forceinline__ float block_max(float m, float *red) {
     __syncthreads();
     float r = red[0];
 #pragma unroll
-    for (int w = 1; w < 4; ++w) r = red[w] > r ? red[w] : r;
+    for (int w = 1; w < kT / 64; ++w) r = red[w] > r ? red[w] : r;
     return r;
 }
 
-// Max of non-NaN |v| over this thread's values: float4 loads over the 16-byte aligned
-// whole quads when the row starts aligned, single loads for the rest.
+// Max of non-NaN |v| over this thread's values (thread t of kT takes every kT-th quad):
+// float4 loads over the 16-byte aligned whole quads when the row starts aligned, single
+// loads for the rest.
+template <int kT = 256>
 __device__ __forceinline__ float abs_max_strided(const float *v, int64_t n) {
     float m = 0.0f;
     int64_t head = 0;
     if ((reinterpret_cast<uintptr_t>(v) & 15u) == 0) {
         const int64_t quads = n >> 2;
         int64_t i = threadIdx.x;
-        // four loads in flight per lane over long spans (a 32-row group of the payload
-        // writer: 256 -> 49.9 us for 8192 x 3072 with one)
-        for (; i + 768 < quads; i += 1024) {
+        // four loads in flight per lane over long spans (the payload writer's scale
+        // pass over 8192 x 3072 took 49.9 us with one, 30.9 with four)
+        for (; i + 3 * kT < quads; i += 4 * kT) {
             floatx4 a[4];
 #pragma unroll
             for (int u = 0; u < 4; ++u)
-                a[u] = *reinterpret_cast<const floatx4 *>(v + 4 * (i + 256 * u));
+                a[u] = *reinterpret_cast<const floatx4 *>(v + 4 * (i + kT * u));
 #pragma unroll
             for (int u = 0; u < 4; ++u)
 #pragma unroll
@@ -109,7 +113,7 @@ __device__ __forceinline__ float abs_max_strided(const float *v, int64_t n) {
                     m = b > m ? b : m;
                 }
         }
-        for (; i < quads; i += 256) {
+        for (; i < quads; i += kT) {
             const floatx4 a = *reinterpret_cast<const floatx4 *>(v + 4 * i);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -119,7 +123,7 @@ __device__ __forceinline__ float abs_max_strided(const float *v, int64_t n) {
         }
         head = quads << 2;
     }
-    for (int64_t i = head + threadIdx.x; i < n; i += 256) {
+    for (int64_t i = head + threadIdx.x; i < n; i += kT) {
         const float a = fabsf(v[i]);
         m = a > m ? a : m;
     }
@@ -355,14 +359,16 @@ __global__ __launch_bounds__(256) void tq1r_dequantize_payload_vec_kernel(
 
 // One workgroup per group: h = half(max |v| over the group's rows, contiguous in the
 // input), round to nearest even; the reserved bytes are zeroed.
-__global__ __launch_bounds__(256) void tq1r_payload_scales_kernel(
+// (1024 threads: one workgroup per group leaves a grid of rows / 32 workgroups; 256
+// threads each took 30.9 us for 8192 x 3072.)
+__global__ __launch_bounds__(1024) void tq1r_payload_scales_kernel(
     const float *__restrict__ values, int64_t rows, int64_t n, PayloadLayout lay,
     uint8_t *__restrict__ payload) {
-    __shared__ float red[4];
+    __shared__ float red[16];
     const int64_t g = blockIdx.x;
     const int64_t r0 = g * lay.group;
     const int64_t nr = rows - r0 < lay.group ? rows - r0 : lay.group;
-    const float m = block_max(abs_max_strided(values + r0 * n, nr * n), red);
+    const float m = block_max<1024>(abs_max_strided<1024>(values + r0 * n, nr * n), red);
     uint8_t *grp = payload + g * lay.stride;
     if (threadIdx.x == 0) {
         const uint16_t h = __builtin_bit_cast(uint16_t, static_cast<_Float16>(m));
@@ -504,7 +510,7 @@ hipError_t launch_tq1r_quantize_payload(const float *values, int64_t rows, int64
     if (rows == 0) return hipSuccess;
     const PayloadLayout lay = layout(rows, n, block_rows, refinements);
     const int64_t groups = (rows + lay.group - 1) / lay.group;
-    tq1r_payload_scales_kernel<<<dim3(static_cast<unsigned>(groups)), 256, 0, s>>>(
+    tq1r_payload_scales_kernel<<<dim3(static_cast<unsigned>(groups)), 1024, 0, s>>>(
         values, rows, n, lay, payload);
     if (n > 0)
         tq1r_payload_rows_kernel<<<dim3(static_cast<unsigned>(rows)), 256, 0, s>>>(
